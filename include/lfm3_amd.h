@@ -1,0 +1,267 @@
+/*
+ * lfm3_amd: the C-ABI boundary of the MI355X (gfx950) LFM3 continuous
+ * batching step. Plain pointers, sizes and hipStream_t (passed as void*);
+ * every call returns LFM3_OK or a negative status, with the message kept
+ * per thread (lfm3_last_error). Kernel entry points are stream-ordered and
+ * own nothing: weights, activations, state and workspaces are passed in,
+ * as with the reference's ops (hip/ops.hpp:12-151).
+ *
+ * Status mapping to the reference's conventions:
+ *   LFM3_E_INVALID  std::invalid_argument for unsupported shapes/inputs
+ *                   (hip/ops.hip:2293-2294, 2402-2403; engine.cpp:908-914)
+ *   LFM3_E_HIP      std::runtime_error(hipGetErrorString) from Check
+ *                   (engine.cpp:23-26)
+ *   LFM3_E_STATE    a poisoned session, which refuses work until Reset
+ *                   (engine.cpp:905-907)
+ */
+#ifndef LFM3_AMD_H_
+#define LFM3_AMD_H_
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LFM3_OK 0
+#define LFM3_E_INVALID (-1)
+#define LFM3_E_HIP (-2)
+#define LFM3_E_STATE (-3)
+#define LFM3_E_NOMEM (-4)
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* lfm3_last_error(void);
+
+/* ---------------------------------------------------------------------
+ * Q8_0 weights in the device tile layout.
+ *
+ * GGUF Q8_0 rows (34-byte blocks: fp16 d, 32 x int8 q; weights.cpp:101-125)
+ * are repacked once at load into tiles of 16 rows x 64 columns: 1024 code
+ * bytes + 32 fp16 scales per tile, rows padded to 16 and columns to 64 with
+ * zero codes and zero scales. Codes and scales are separate arrays.
+ * Replaces: DeviceWeights::Add/Upload (upload.cpp:29-72), which copies the
+ * GGUF bytes verbatim.
+ * ------------------------------------------------------------------- */
+/* Bytes of the tiled codes and scales of a rows x cols matrix. */
+void lfm3_q8_tiled_bytes(uint32_t rows, uint32_t cols, size_t* code_bytes,
+                         size_t* scale_bytes);
+/* Host repack of GGUF Q8_0 rows into tiles. Source row tile i goes to
+   destination row tile (tile_offset + i * tile_stride): stride 1 with an
+   offset concatenates matrices; stride 2 interleaves two (FFN gate/up).
+   cols must be a multiple of 32. */
+int lfm3_q8_pack_host(const void* gguf, uint32_t rows, uint32_t cols,
+                      void* codes, void* scales, uint32_t tile_offset,
+                      uint32_t tile_stride);
+/* The same repack on the device, from GGUF bytes already uploaded. */
+int lfm3_q8_pack_device(const void* gguf, uint32_t rows, uint32_t cols,
+                        void* codes, void* scales, uint32_t tile_offset,
+                        uint32_t tile_stride, void* stream);
+
+/* ---------------------------------------------------------------------
+ * Q8_0 skinny GEMV for 1..8 FP32 rows: y[b][r] = sum_k W[r][k] x[b][k].
+ * Replaces: gpu::LaunchGEMV (hip/ops.hip:1799-1825, B = 1) and
+ * gpu::LaunchBatchedQuantGEMMFp32 (hip/ops.hip:1827-1915, B = 2..8), the
+ * decode projections behind gpu::Dense / gpu::Project (hip/ops.hpp:44-64).
+ * x: batch rows of ldx floats (ldx % 4 == 0, 16-byte aligned); y: batch
+ * rows of ldy floats. The workspace (lfm3_gemv_workspace_bytes) must be
+ * zeroed once when allocated; calls leave it zeroed.
+ * ------------------------------------------------------------------- */
+size_t lfm3_gemv_workspace_bytes(uint32_t rows, uint32_t cols,
+                                 uint32_t batch);
+int lfm3_q8_gemv(const void* codes, const void* scales, uint32_t rows,
+                 uint32_t cols, const float* x, uint32_t ldx, float* y,
+                 uint32_t ldy, uint32_t batch, void* workspace,
+                 size_t workspace_bytes, void* stream);
+/* FFN gate/up with the SwiGLU epilogue over a stride-2 interleaved pair
+   (rows = rows of each of gate and up): y[b][r] = silu(g) * u.
+   Replaces: gpu::ProjectSwiGLU (hip/ops.hip:2187-2204) and the decode half
+   of gpu::ProjectFfn (hip/ops.hip:2205-2229). */
+int lfm3_q8_gemv_swiglu(const void* codes, const void* scales, uint32_t rows,
+                        uint32_t cols, const float* x, uint32_t ldx, float* y,
+                        uint32_t ldy, uint32_t batch, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------
+ * Row operations.
+ * ------------------------------------------------------------------- */
+/* x[i] += post_norm(branch[i]) (branch/post may be NULL), then
+   z[i] = RMSNorm(x[i]) * norm (norm may be NULL: x only). FP32.
+   Replaces: gpu::ResidualNorm FP32 branch (hip/ops.hip:2158-2169) and
+   gpu::LaunchBatchedRMSNorm (hip/ops.hip:1752-1764). */
+int lfm3_residual_norm(const float* branch, const float* post_norm, float* x,
+                       const float* norm, float* z, uint32_t rows,
+                       uint32_t hidden, float eps, void* stream);
+/* out[i] = d * q of row tokens[i] (tokens in device memory).
+   Replaces: gpu::Embed (hip/ops.hip:2007-2011). */
+int lfm3_embed(const void* codes, const void* scales, uint32_t vocab,
+               uint32_t hidden, const uint32_t* tokens, uint32_t n,
+               float* out, void* stream);
+/* Greedy ids: first index of each row's maximum, as std::max_element
+   (tests/session_test.cpp:32-34). ids in device memory. The workspace
+   (lfm3_argmax_workspace_bytes) must be zeroed once; calls leave it
+   zeroed. Replaces: the host sampler's temperature-0 pick. */
+size_t lfm3_argmax_workspace_bytes(uint32_t rows);
+int lfm3_argmax(const float* logits, uint32_t rows, uint32_t cols,
+                uint32_t* ids, void* workspace, size_t workspace_bytes,
+                void* stream);
+
+/* ---------------------------------------------------------------------
+ * Ragged decode rows: every row belongs to its own session; per-row
+ * pointers and positions come from device index tables.
+ * ------------------------------------------------------------------- */
+/* One gated short-convolution step per row: p = [B | C | x] (row stride
+   ldp), history[i] -> that row's [hidden][width - 1] FP32 history.
+   Replaces: gpu::ShortConv with n == 1 (hip/ops.hip:2250-2255) called once
+   per session (engine.cpp:394-400). */
+int lfm3_conv_step_ragged(const float* p, uint32_t ldp, const float* taps,
+                          float* const* history, float* y, uint32_t ldy,
+                          uint32_t rows, uint32_t hidden, uint32_t width,
+                          void* stream);
+/* Per-head Q/K RMSNorm, paired RoPE at positions[i] and the F16 K/V store
+   to ring slot positions[i] % capacity[i] of cache_k[i] / cache_v[i]
+   ([capacity][kv_heads][dim] F16). q/k/v rows have stride ld floats.
+   frequencies: dim / 2 floats; factors: NULL on sliding layers.
+   Replaces: gpu::DecodeHeads (hip/ops.hip:2397-2407) per session
+   (engine.cpp:424-429). */
+int lfm3_decode_heads_ragged(float* q, float* k, const float* v, uint32_t ld,
+                             const float* q_norm, const float* k_norm,
+                             const float* frequencies, const float* factors,
+                             uint16_t* const* cache_k,
+                             uint16_t* const* cache_v,
+                             const uint32_t* positions,
+                             const uint32_t* capacity, uint32_t rows,
+                             uint32_t heads, uint32_t kv_heads, uint32_t dim,
+                             float eps, void* stream);
+
+/* Work list of ragged decode attention: one item per (row, key span). */
+typedef struct {
+  uint32_t row;        /* query row */
+  uint32_t key_begin;  /* first key position of the span */
+  uint32_t key_end;    /* one past the last key position */
+  uint32_t first_item; /* index of this row's first item */
+  uint32_t parts;      /* number of spans of this row */
+  uint32_t reserved[3];
+} lfm3_attention_item;
+/* Host planning: positions[i] is row i's position (keys [first, position],
+   first = max(0, position + 1 - window) when window > 0). Writes up to
+   max_items items and returns their count, or a negative status. */
+int lfm3_attention_plan(const uint32_t* positions, uint32_t rows,
+                        uint32_t window, lfm3_attention_item* items,
+                        uint32_t max_items);
+size_t lfm3_attention_workspace_bytes(uint32_t items, uint32_t rows,
+                                      uint32_t heads, uint32_t kv_heads,
+                                      uint32_t dim);
+/* Gated GQA of one query per row over its session's F16 ring:
+   out[i][h] = (softmax(q_h . K / sqrt(dim)) V) / (1 + exp(-gate[i][h])).
+   q/gate/out rows have strides ldq/ldg/ldo floats; items and the per-row
+   tables are in device memory. The workspace must be zeroed once; calls
+   leave its counters zeroed. dim 64 or 128; heads % kv_heads == 0 with a
+   group of 2, 4 or 8.
+   Replaces: gpu::Attention with n == 1 (hip/ops.hip:2289-2315:
+   DecodeWaves + DecodeCombine) per session (engine.cpp:430-434). */
+int lfm3_decode_attention_ragged(
+    const float* q, uint32_t ldq, const float* gate, uint32_t ldg,
+    const uint16_t* const* cache_k, const uint16_t* const* cache_v,
+    const uint32_t* capacity, const lfm3_attention_item* items,
+    uint32_t n_items, float* out, uint32_t ldo, uint32_t rows, uint32_t heads,
+    uint32_t kv_heads, uint32_t dim, void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/* ---------------------------------------------------------------------
+ * Engine: Model / Session (engine.hpp:17-163).
+ * ------------------------------------------------------------------- */
+enum { LFM3_LAYER_CONV = 0, LFM3_LAYER_FULL = 1, LFM3_LAYER_SLIDING = 2 };
+enum { LFM3_TYPE_F32 = 0, LFM3_TYPE_Q8_0 = 8 };
+
+/* config.hpp:9-20. */
+typedef struct {
+  uint32_t hidden, intermediate, vocab, context, heads, head_dim, window,
+      conv_width, n_layers;
+  float eps, theta, theta_swa;
+  const uint32_t* kv_heads;  /* per layer; 0 for convolution layers */
+  const uint8_t* layer_type; /* LFM3_LAYER_* per layer */
+} lfm3_config;
+
+/* weights.hpp:7-12 tensor view in host memory (GGUF layout). */
+typedef struct {
+  const void* data;
+  uint32_t type; /* LFM3_TYPE_F32 / LFM3_TYPE_Q8_0 */
+  uint32_t cols, rows;
+} lfm3_tensor;
+
+/* Tensor order: embedding, output, output_norm, rope_freqs, then per layer
+   norm, ffn_norm, post_norm, post_ffn_norm, gate, up, down, conv, in_proj,
+   out_proj, q, k, v, q_norm, k_norm, attn_gate, attn_out (weights.hpp:13-22;
+   absent tensors have data == NULL). */
+#define LFM3_GLOBAL_TENSORS 4
+#define LFM3_LAYER_TENSORS 17
+
+typedef struct lfm3_model lfm3_model;
+typedef struct lfm3_session lfm3_session;
+
+/* Binds and uploads the weights (Model::Load, engine.cpp:117-170, with the
+   GGUF mapping replaced by caller-provided tensor views). */
+int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
+                    size_t count, lfm3_model** out);
+void lfm3_model_destroy(lfm3_model* model);
+/* Model::CreateSession (engine.cpp:195-236). */
+int lfm3_session_create(lfm3_model* model, uint32_t context,
+                        lfm3_session** out);
+void lfm3_session_destroy(lfm3_session* session);
+uint32_t lfm3_session_position(const lfm3_session* session);
+int lfm3_session_reset(lfm3_session* session);
+int lfm3_session_is_coherent(const lfm3_session* session);
+uint32_t lfm3_session_ring_capacity(const lfm3_session* session,
+                                    uint32_t layer);
+
+/* Session state in device memory (Session::ContinuationData,
+   engine.cpp:1341-1358): kind 0 logits (vocab f32), 1 frontier (hidden
+   f32), 2 conv history (hidden * (width - 1) f32), 3 K ring, 4 V ring
+   ([capacity][kv_heads][head_dim] F16). */
+enum {
+  LFM3_STATE_LOGITS = 0,
+  LFM3_STATE_FRONTIER = 1,
+  LFM3_STATE_CONV = 2,
+  LFM3_STATE_KEY = 3,
+  LFM3_STATE_VALUE = 4
+};
+int lfm3_session_state(lfm3_session* session, int kind, uint32_t layer,
+                       void** data, size_t* bytes);
+/* Restores a position after the caller wrote state rows directly
+   (Session::FinishRestore, engine.cpp:1380-1386). */
+int lfm3_session_set_position(lfm3_session* session, uint32_t position);
+
+/* Session::ForwardBatch (engine.cpp:1160-1216): one token per distinct
+   session (at most 8), logits copied to host rows logits[i] (vocab floats
+   each). On a device failure every session of the batch is poisoned. */
+int lfm3_forward_batch(lfm3_session* const* sessions, size_t n,
+                       const uint32_t* tokens, float* const* logits);
+/* The same round with logits left in each session's device state and the
+   greedy ids of the rows written to ids (host). The serving loop's form:
+   no logits cross PCIe. */
+int lfm3_forward_batch_greedy(lfm3_session* const* sessions, size_t n,
+                              const uint32_t* tokens, uint32_t* ids);
+/* Session::ReadLogits (engine.cpp) into host memory (vocab floats). */
+int lfm3_session_read_logits(const lfm3_session* session, float* logits);
+/* Stream of the model's batch rounds (Session::DeviceStream). */
+void* lfm3_model_stream(lfm3_model* model);
+
+/* ---------------------------------------------------------------------
+ * Deterministic synthetic inputs (benchmarks and parity tests). No
+ * counterpart in the reference: they stand in for a GGUF checkpoint and
+ * prefilled session state. Each value is a function of (seed, stream name,
+ * index) only: SplitMix64 counters, Box-Muller normals in double precision.
+ * ------------------------------------------------------------------- */
+uint64_t lfm3_synth_key(uint64_t seed, const char* name);
+void lfm3_synth_normal(uint64_t key, float mean, float stddev, float* out,
+                       size_t n);
+void lfm3_synth_uniform_u32(uint64_t key, uint32_t lo, uint32_t hi,
+                            uint32_t* out, size_t n);
+void lfm3_synth_half_normal(uint64_t key, uint16_t* out, size_t n);
+/* GGUF Q8_0 rows: q uniform in [-127, 127], d = fp16(|N(0, d_std)| / 127). */
+void lfm3_synth_q8(uint64_t key, uint32_t rows, uint32_t cols, float d_std,
+                   void* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

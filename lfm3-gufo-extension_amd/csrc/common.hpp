@@ -1,0 +1,93 @@
+// Shared device helpers and status plumbing for the gfx950 LFM3 kernels.
+#ifndef LFM3_AMD_COMMON_HPP_
+#define LFM3_AMD_COMMON_HPP_
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/lfm3_amd.h"
+
+namespace lfm3amd {
+
+using Half = std::uint16_t;
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Q8_0 tile geometry of the device weight layout: a tile is 16 weight rows
+// by one 64-column chunk (two Q8_0 blocks). Its 1024 code bytes are one
+// 16-byte load per lane of a wave: lane L = 16 g + n holds row n, bytes
+// [0, 8) = elements 8g..8g+7 of the chunk's first block and bytes [8, 16)
+// = elements 8g..8g+7 of its second block, which is the B operand of two
+// v_mfma_f32_16x16x32_f16 (one per Q8_0 block). Its 32 fp16 scales follow
+// the same tile order as [row][block].
+constexpr int kTileRows = 16;
+constexpr int kChunk = 64;
+constexpr int kTileCodeBytes = kTileRows * kChunk;     // 1024
+constexpr int kTileScales = kTileRows * 2;             // 32 halves
+
+inline std::uint32_t RowTiles(std::uint32_t rows) {
+  return (rows + kTileRows - 1) / kTileRows;
+}
+inline std::uint32_t Chunks(std::uint32_t cols) {
+  return (cols + kChunk - 1) / kChunk;
+}
+
+// Thread-local message of the last failed C-ABI call.
+void SetError(const std::string& message);
+int Fail(int status, const std::string& message);
+int HipStatus(hipError_t e, const char* what);
+
+__device__ __forceinline__ float HalfBitsToFloat(unsigned bits) {
+  return float(__builtin_bit_cast(_Float16, static_cast<unsigned short>(bits)));
+}
+__device__ __forceinline__ Half FloatToHalfBits(float x) {
+  return __builtin_bit_cast(Half, static_cast<_Float16>(x));
+}
+
+// Four Q8_0 codes (one dword) -> four exact fp16 values. v_perm_b32 places
+// each code byte (biased by 128) under an 0x64 high byte, which reads as
+// 1024 + q + 128; subtracting 1152 leaves q exactly.
+__device__ __forceinline__ void CodesToHalves(unsigned codes, h2& lo, h2& hi) {
+  codes ^= 0x80808080u;
+  const unsigned p0 = __builtin_amdgcn_perm(codes, 0x64646464u, 0x01050004u);
+  const unsigned p1 = __builtin_amdgcn_perm(codes, 0x64646464u, 0x03070206u);
+  const h2 bias = {static_cast<_Float16>(-1152.0f),
+                   static_cast<_Float16>(-1152.0f)};
+  lo = __builtin_bit_cast(h2, p0) + bias;
+  hi = __builtin_bit_cast(h2, p1) + bias;
+}
+// Eight codes (two dwords) -> one MFMA operand of eight fp16 values.
+__device__ __forceinline__ h8 EightCodes(unsigned a, unsigned b) {
+  h2 v0, v1, v2, v3;
+  CodesToHalves(a, v0, v1);
+  CodesToHalves(b, v2, v3);
+  h8 out;
+  out[0] = v0[0];
+  out[1] = v0[1];
+  out[2] = v1[0];
+  out[3] = v1[1];
+  out[4] = v2[0];
+  out[5] = v2[1];
+  out[6] = v3[0];
+  out[7] = v3[1];
+  return out;
+}
+
+__device__ __forceinline__ float WaveSum(float v) {
+#pragma unroll
+  for (int m = 32; m; m >>= 1)
+    v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ float WaveMax(float v) {
+#pragma unroll
+  for (int m = 32; m; m >>= 1)
+    v = fmaxf(v, __shfl_xor(v, m, 64));
+  return v;
+}
+
+}  // namespace lfm3amd
+#endif

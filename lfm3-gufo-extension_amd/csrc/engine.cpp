@@ -1,0 +1,747 @@
+// Model / Session of the LFM3 continuous-batching step on one MI355X.
+//
+// Mirrors the reference engine (engine.hpp:17-163, engine.cpp): a model
+// owns packed device weights shared by sessions; a session owns its
+// recurrent state (convolution history, F16 K/V rings), logits and
+// frontier row; ForwardBatch advances up to eight sessions by one token in
+// one round that shares every projection across rows. Where the reference
+// loops per session for the convolution and attention launches
+// (engine.cpp:394-400, 424-436), a round here uploads one device index
+// table (tokens, positions, per-layer state pointers, ring capacities and
+// attention work lists) and every launch covers all rows.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace lfm3amd {
+namespace {
+
+constexpr std::uint32_t kMaxBatch = 8;  // engine.hpp:48
+
+struct Error : std::runtime_error {
+  int status;
+  Error(int s, const std::string& m) : std::runtime_error(m), status(s) {}
+};
+void Check(hipError_t e, const char* what) {
+  if (e != hipSuccess)
+    throw Error(LFM3_E_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+void CheckStatus(int status) {
+  if (status != LFM3_OK)
+    throw Error(status, lfm3_last_error());
+}
+[[noreturn]] void Invalid(const std::string& m) { throw Error(LFM3_E_INVALID, m); }
+
+struct Buffer {
+  void* p = nullptr;
+  std::size_t bytes = 0;
+  Buffer() = default;
+  explicit Buffer(std::size_t n, bool zero = true) : bytes(n) {
+    if (n) {
+      Check(hipMalloc(&p, n), "hipMalloc");
+      if (zero)
+        Check(hipMemset(p, 0, n), "hipMemset");
+    }
+  }
+  ~Buffer() {
+    if (p)
+      (void)hipFree(p);
+  }
+  Buffer(Buffer&& b) noexcept : p(b.p), bytes(b.bytes) { b.p = nullptr; b.bytes = 0; }
+  Buffer& operator=(Buffer&& b) noexcept {
+    std::swap(p, b.p);
+    std::swap(bytes, b.bytes);
+    return *this;
+  }
+  Buffer(const Buffer&) = delete;
+  template<class T> T* as() const { return static_cast<T*>(p); }
+};
+
+struct PinnedBuffer {
+  void* p = nullptr;
+  explicit PinnedBuffer(std::size_t n) { Check(hipHostMalloc(&p, n, 0), "hipHostMalloc"); }
+  ~PinnedBuffer() {
+    if (p)
+      (void)hipHostFree(p);
+  }
+  PinnedBuffer(const PinnedBuffer&) = delete;
+};
+
+// A tiled Q8_0 matrix of rows x cols (several sources may share it).
+struct Matrix {
+  Buffer codes, scales;
+  std::uint32_t rows = 0, cols = 0;
+};
+
+Buffer UploadFloats(const float* host, std::size_t n) {
+  Buffer b(n * 4, false);
+  Check(hipMemcpy(b.p, host, n * 4, hipMemcpyHostToDevice), "hipMemcpy");
+  return b;
+}
+
+struct Part {
+  const lfm3_tensor* t;
+  std::uint32_t tile_offset, tile_stride;
+};
+// Packs sources into one tiled matrix of `tiles` row tiles.
+Matrix PackMatrix(std::initializer_list<Part> parts, std::uint32_t tiles,
+                  std::uint32_t rows, std::uint32_t cols) {
+  Matrix m;
+  m.rows = rows;
+  m.cols = cols;
+  const std::size_t chunks = Chunks(cols);
+  const std::size_t code_bytes = std::size_t(tiles) * chunks * kTileCodeBytes;
+  const std::size_t scale_bytes = std::size_t(tiles) * chunks * kTileScales * 2;
+  std::vector<std::uint8_t> codes(code_bytes, 0);
+  std::vector<std::uint8_t> scales(scale_bytes, 0);
+  for (const auto& part : parts)
+    CheckStatus(lfm3_q8_pack_host(part.t->data, part.t->rows, part.t->cols,
+                                  codes.data(), scales.data(), part.tile_offset,
+                                  part.tile_stride));
+  m.codes = Buffer(code_bytes, false);
+  m.scales = Buffer(scale_bytes, false);
+  Check(hipMemcpy(m.codes.p, codes.data(), code_bytes, hipMemcpyHostToDevice), "hipMemcpy");
+  Check(hipMemcpy(m.scales.p, scales.data(), scale_bytes, hipMemcpyHostToDevice), "hipMemcpy");
+  return m;
+}
+
+struct Layer {
+  int type = LFM3_LAYER_CONV;
+  std::uint32_t kv = 0;
+  Buffer norm, ffn_norm, post_norm, post_ffn_norm, conv, q_norm, k_norm;
+  Matrix ffn;      // gate/up, interleaved by row tile (SwiGLU pairs)
+  Matrix down;
+  Matrix in_proj, out_proj;
+  Matrix qkvg;     // q | k | v | gate, concatenated by row tile
+  Matrix attn_out;
+  std::uint32_t q_off = 0, k_off = 0, v_off = 0, g_off = 0, qkvg_ld = 0;
+};
+
+// Device index table of one round (uploaded once per round).
+struct RoundTable {
+  std::uint32_t tokens[kMaxBatch];
+  std::uint32_t positions[kMaxBatch];
+  float* logits[kMaxBatch];
+  float* frontier[kMaxBatch];
+};
+
+std::size_t Align(std::size_t n) { return (n + 255) / 256 * 256; }
+
+}  // namespace
+}  // namespace lfm3amd
+
+using namespace lfm3amd;
+
+struct lfm3_session;
+
+struct lfm3_model {
+  std::vector<std::uint32_t> kv_heads;
+  std::vector<std::uint8_t> layer_type;
+  lfm3_config config{};
+  std::vector<Layer> layers;
+  Matrix embedding, output;
+  bool tied = true;
+  Buffer output_norm, factors, freq_global, freq_sliding;
+  hipStream_t stream = nullptr;
+  // Round scratch, shared by the model's rounds (calls are serialized, as
+  // the Gufo scheduler serializes sessions: engine.cpp:101-113).
+  Buffer x, z, proj, a, hidden, out, logits, gemv_ws, argmax_ws, ids;
+  std::size_t proj_ld = 0, gemv_ws_bytes = 0;
+  // Per-round device tables: RoundTable, per-layer pointer rows, items.
+  Buffer table;
+  std::unique_ptr<PinnedBuffer> staging;
+  std::size_t table_bytes = 0, items_capacity = 0;
+  Buffer attn_ws;
+  std::size_t attn_ws_bytes = 0;
+  std::uint32_t max_context = 0;
+
+  ~lfm3_model() {
+    if (stream)
+      (void)hipStreamDestroy(stream);
+  }
+  const Matrix& head() const { return tied ? embedding : output; }
+};
+
+struct lfm3_session {
+  lfm3_model* model = nullptr;
+  std::uint32_t context = 0, position = 0;
+  bool poisoned = false, logits_ready = false;
+  struct State {
+    Buffer conv, k, v;
+    std::uint32_t capacity = 0;
+  };
+  std::vector<State> states;
+  Buffer logits, frontier;
+};
+
+namespace lfm3amd {
+namespace {
+
+void ValidateConfig(const lfm3_config& c) {
+  if (!c.hidden || !c.intermediate || !c.vocab || !c.context || !c.heads ||
+      !c.head_dim || !c.window || !c.n_layers || c.conv_width < 2 ||
+      c.conv_width > 32 || !c.kv_heads || !c.layer_type ||
+      (c.head_dim != 64 && c.head_dim != 128) || c.hidden % 64 ||
+      c.intermediate % 64 || c.hidden > 4096 || !(c.eps > 0) ||
+      !(c.theta > 0) || !(c.theta_swa > 0))
+    Invalid("unsupported LFM3 dimensions");
+  for (std::uint32_t i = 0; i < c.n_layers; ++i) {
+    const auto h = c.kv_heads[i];
+    const auto t = c.layer_type[i];
+    if (t > LFM3_LAYER_SLIDING || (t == LFM3_LAYER_CONV) != (h == 0) ||
+        (h && (c.heads % h || (c.heads / h != 2 && c.heads / h != 4 &&
+                               c.heads / h != 8))))
+      Invalid("invalid LFM3 layer heads/window");
+  }
+}
+
+void CheckTensor(const lfm3_tensor& t, std::uint32_t cols, std::uint32_t rows,
+                 bool q8, const char* name) {
+  if (!t.data || t.cols != cols || t.rows != rows ||
+      t.type != (q8 ? LFM3_TYPE_Q8_0 : LFM3_TYPE_F32))
+    Invalid(std::string("invalid LFM3 tensor: ") + name);
+}
+
+// weights.cpp:10-100 binding rules, checked before anything is uploaded.
+void ValidateTensors(const lfm3_config& c, const lfm3_tensor* tensors) {
+  const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
+  CheckTensor(tensors[0], H, c.vocab, true, "token_embd.weight");
+  if (tensors[1].data && tensors[1].data != tensors[0].data)
+    CheckTensor(tensors[1], H, c.vocab, true, "output.weight");
+  CheckTensor(tensors[2], H, 1, false, "output_norm.weight");
+  CheckTensor(tensors[3], D / 2, 1, false, "rope_freqs.weight");
+  for (std::uint32_t i = 0; i < D / 2; ++i) {
+    const float f = static_cast<const float*>(tensors[3].data)[i];
+    if (!std::isfinite(f) || !(f > 0))
+      Invalid("invalid LFM3 RoPE factor");
+  }
+  for (std::uint32_t i = 0; i < c.n_layers; ++i) {
+    const lfm3_tensor* t = tensors + LFM3_GLOBAL_TENSORS + std::size_t(i) * LFM3_LAYER_TENSORS;
+    CheckTensor(t[0], H, 1, false, "attn_norm.weight");
+    CheckTensor(t[1], H, 1, false, "ffn_norm.weight");
+    if (bool(t[2].data) != bool(t[3].data))
+      Invalid("LFM3 requires both post norms or neither");
+    if (t[2].data) {
+      CheckTensor(t[2], H, 1, false, "post_attention_norm.weight");
+      CheckTensor(t[3], H, 1, false, "post_ffw_norm.weight");
+    }
+    CheckTensor(t[4], H, F, true, "ffn_gate.weight");
+    CheckTensor(t[5], H, F, true, "ffn_up.weight");
+    CheckTensor(t[6], F, H, true, "ffn_down.weight");
+    if (c.layer_type[i] == LFM3_LAYER_CONV) {
+      CheckTensor(t[7], c.conv_width, H, false, "shortconv.conv.weight");
+      CheckTensor(t[8], H, 3 * H, true, "shortconv.in_proj.weight");
+      CheckTensor(t[9], H, H, true, "shortconv.out_proj.weight");
+    } else {
+      const std::uint32_t qr = c.heads * D, kr = c.kv_heads[i] * D;
+      CheckTensor(t[10], H, qr, true, "attn_q.weight");
+      CheckTensor(t[11], H, kr, true, "attn_k.weight");
+      CheckTensor(t[12], H, kr, true, "attn_v.weight");
+      CheckTensor(t[13], D, 1, false, "attn_q_norm.weight");
+      CheckTensor(t[14], D, 1, false, "attn_k_norm.weight");
+      CheckTensor(t[15], H, c.heads, true, "attn_gate.weight");
+      CheckTensor(t[16], qr, H, true, "attn_output.weight");
+    }
+  }
+}
+
+void EnsureRoundBuffers(lfm3_model& m, std::uint32_t max_context) {
+  const auto& c = m.config;
+  if (max_context <= m.max_context)
+    return;
+  // Attention work items: at most ceil(context / 256) spans per row.
+  const std::size_t per_row = (max_context + 255) / 256 + 1;
+  m.items_capacity = per_row * kMaxBatch;
+  const std::size_t L = c.n_layers;
+  m.table_bytes = Align(sizeof(RoundTable)) +
+                  Align(L * kMaxBatch * sizeof(void*)) * 3 +   // conv / k / v
+                  Align(L * kMaxBatch * 4) +                   // capacity
+                  Align(m.items_capacity * sizeof(lfm3_attention_item)) * 2;
+  m.table = Buffer(m.table_bytes);
+  m.staging = std::make_unique<PinnedBuffer>(m.table_bytes);
+  m.attn_ws_bytes = lfm3_attention_workspace_bytes(
+      std::uint32_t(m.items_capacity), kMaxBatch, c.heads, c.heads, c.head_dim);
+  m.attn_ws = Buffer(m.attn_ws_bytes);
+  m.max_context = max_context;
+}
+
+}  // namespace
+}  // namespace lfm3amd
+
+extern "C" {
+
+int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
+                    std::size_t count, lfm3_model** out) {
+  if (!out)
+    return Fail(LFM3_E_INVALID, "null model output");
+  *out = nullptr;
+  try {
+    if (!config || !tensors)
+      Invalid("null LFM3 config or tensors");
+    const lfm3_config& c = *config;
+    ValidateConfig(c);
+    if (count != LFM3_GLOBAL_TENSORS + std::size_t(c.n_layers) * LFM3_LAYER_TENSORS)
+      Invalid("LFM3 tensor list must describe every layer");
+    auto m = std::make_unique<lfm3_model>();
+    m->kv_heads.assign(c.kv_heads, c.kv_heads + c.n_layers);
+    m->layer_type.assign(c.layer_type, c.layer_type + c.n_layers);
+    m->config = c;
+    m->config.kv_heads = m->kv_heads.data();
+    m->config.layer_type = m->layer_type.data();
+    const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
+    ValidateTensors(c, tensors);
+    Check(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "hipStreamCreate");
+
+    const lfm3_tensor& emb = tensors[0];
+    CheckTensor(emb, H, c.vocab, true, "token_embd.weight");
+    m->embedding = PackMatrix({{&emb, 0, 1}}, RowTiles(c.vocab), c.vocab, H);
+    const lfm3_tensor& outw = tensors[1];
+    m->tied = !outw.data || outw.data == emb.data;
+    if (!m->tied) {
+      CheckTensor(outw, H, c.vocab, true, "output.weight");
+      m->output = PackMatrix({{&outw, 0, 1}}, RowTiles(c.vocab), c.vocab, H);
+    }
+    CheckTensor(tensors[2], H, 1, false, "output_norm.weight");
+    m->output_norm = UploadFloats(static_cast<const float*>(tensors[2].data), H);
+    CheckTensor(tensors[3], D / 2, 1, false, "rope_freqs.weight");
+    const auto* factors = static_cast<const float*>(tensors[3].data);
+    for (std::uint32_t i = 0; i < D / 2; ++i)
+      if (!std::isfinite(factors[i]) || !(factors[i] > 0))
+        Invalid("invalid LFM3 RoPE factor");
+    m->factors = UploadFloats(factors, D / 2);
+    // reference.cpp:29-43: theta^(-2i/D) in FP32, as the oracle forms it.
+    std::vector<float> fg(D / 2), fs(D / 2);
+    for (std::uint32_t i = 0; i < D / 2; ++i) {
+      fg[i] = std::pow(c.theta, -2.0F * float(i) / float(D));
+      fs[i] = std::pow(c.theta_swa, -2.0F * float(i) / float(D));
+    }
+    m->freq_global = UploadFloats(fg.data(), D / 2);
+    m->freq_sliding = UploadFloats(fs.data(), D / 2);
+
+    std::uint32_t proj_rows = 3 * H;
+    for (std::uint32_t i = 0; i < c.n_layers; ++i) {
+      const lfm3_tensor* t = tensors + LFM3_GLOBAL_TENSORS + std::size_t(i) * LFM3_LAYER_TENSORS;
+      Layer l;
+      l.type = c.layer_type[i];
+      l.kv = c.kv_heads[i];
+      CheckTensor(t[0], H, 1, false, "attn_norm.weight");
+      CheckTensor(t[1], H, 1, false, "ffn_norm.weight");
+      l.norm = UploadFloats(static_cast<const float*>(t[0].data), H);
+      l.ffn_norm = UploadFloats(static_cast<const float*>(t[1].data), H);
+      if (bool(t[2].data) != bool(t[3].data))
+        Invalid("LFM3 requires both post norms or neither");
+      if (t[2].data) {
+        CheckTensor(t[2], H, 1, false, "post_attention_norm.weight");
+        CheckTensor(t[3], H, 1, false, "post_ffw_norm.weight");
+        l.post_norm = UploadFloats(static_cast<const float*>(t[2].data), H);
+        l.post_ffn_norm = UploadFloats(static_cast<const float*>(t[3].data), H);
+      }
+      CheckTensor(t[4], H, F, true, "ffn_gate.weight");
+      CheckTensor(t[5], H, F, true, "ffn_up.weight");
+      CheckTensor(t[6], F, H, true, "ffn_down.weight");
+      l.ffn = PackMatrix({{&t[4], 0, 2}, {&t[5], 1, 2}}, 2 * RowTiles(F), F, H);
+      l.down = PackMatrix({{&t[6], 0, 1}}, RowTiles(H), H, F);
+      if (l.type == LFM3_LAYER_CONV) {
+        CheckTensor(t[7], c.conv_width, H, false, "shortconv.conv.weight");
+        CheckTensor(t[8], H, 3 * H, true, "shortconv.in_proj.weight");
+        CheckTensor(t[9], H, H, true, "shortconv.out_proj.weight");
+        l.conv = UploadFloats(static_cast<const float*>(t[7].data),
+                              std::size_t(H) * c.conv_width);
+        l.in_proj = PackMatrix({{&t[8], 0, 1}}, RowTiles(3 * H), 3 * H, H);
+        l.out_proj = PackMatrix({{&t[9], 0, 1}}, RowTiles(H), H, H);
+      } else {
+        const std::uint32_t qr = c.heads * D, kr = l.kv * D;
+        CheckTensor(t[10], H, qr, true, "attn_q.weight");
+        CheckTensor(t[11], H, kr, true, "attn_k.weight");
+        CheckTensor(t[12], H, kr, true, "attn_v.weight");
+        CheckTensor(t[13], D, 1, false, "attn_q_norm.weight");
+        CheckTensor(t[14], D, 1, false, "attn_k_norm.weight");
+        CheckTensor(t[15], H, c.heads, true, "attn_gate.weight");
+        CheckTensor(t[16], qr, H, true, "attn_output.weight");
+        const std::uint32_t tq = RowTiles(qr), tk = RowTiles(kr), tg = RowTiles(c.heads);
+        l.q_off = 0;
+        l.k_off = tq * kTileRows;
+        l.v_off = (tq + tk) * kTileRows;
+        l.g_off = (tq + 2 * tk) * kTileRows;
+        l.qkvg_ld = (tq + 2 * tk + tg) * kTileRows;
+        l.qkvg = PackMatrix({{&t[10], 0, 1}, {&t[11], tq, 1}, {&t[12], tq + tk, 1},
+                             {&t[15], tq + 2 * tk, 1}},
+                            tq + 2 * tk + tg, l.qkvg_ld, H);
+        l.attn_out = PackMatrix({{&t[16], 0, 1}}, RowTiles(H), H, qr);
+        l.q_norm = UploadFloats(static_cast<const float*>(t[13].data), D);
+        l.k_norm = UploadFloats(static_cast<const float*>(t[14].data), D);
+        proj_rows = std::max(proj_rows, l.qkvg_ld);
+      }
+      m->layers.push_back(std::move(l));
+    }
+    // Round scratch for up to kMaxBatch rows.
+    m->proj_ld = (proj_rows + 3) / 4 * 4;
+    const std::size_t B = kMaxBatch;
+    m->x = Buffer(B * H * 4);
+    m->z = Buffer(B * H * 4);
+    m->proj = Buffer(B * m->proj_ld * 4);
+    m->a = Buffer(B * std::max<std::size_t>(H, std::size_t(c.heads) * D) * 4);
+    m->hidden = Buffer(B * F * 4);
+    m->out = Buffer(B * H * 4);
+    m->logits = Buffer(B * std::size_t(c.vocab) * 4);
+    std::size_t ws = lfm3_gemv_workspace_bytes(c.vocab, H, B);
+    for (const auto& l : m->layers) {
+      ws = std::max(ws, lfm3_gemv_workspace_bytes(F, H, B));
+      ws = std::max(ws, lfm3_gemv_workspace_bytes(H, F, B));
+      if (l.type == LFM3_LAYER_CONV) {
+        ws = std::max(ws, lfm3_gemv_workspace_bytes(3 * H, H, B));
+        ws = std::max(ws, lfm3_gemv_workspace_bytes(H, H, B));
+      } else {
+        ws = std::max(ws, lfm3_gemv_workspace_bytes(l.qkvg_ld, H, B));
+        ws = std::max(ws, lfm3_gemv_workspace_bytes(H, c.heads * D, B));
+      }
+    }
+    m->gemv_ws_bytes = std::max<std::size_t>(ws, 256);
+    m->gemv_ws = Buffer(m->gemv_ws_bytes);
+    m->argmax_ws = Buffer(lfm3_argmax_workspace_bytes(B));
+    m->ids = Buffer(B * 4);
+    Check(hipDeviceSynchronize(), "model upload");
+    *out = m.release();
+    return LFM3_OK;
+  } catch (const Error& e) {
+    return Fail(e.status, e.what());
+  } catch (const std::bad_alloc&) {
+    return Fail(LFM3_E_NOMEM, "out of host memory");
+  } catch (const std::exception& e) {
+    return Fail(LFM3_E_INVALID, e.what());
+  }
+}
+
+void lfm3_model_destroy(lfm3_model* model) { delete model; }
+
+void* lfm3_model_stream(lfm3_model* model) { return model ? model->stream : nullptr; }
+
+int lfm3_session_create(lfm3_model* m, std::uint32_t context, lfm3_session** out) {
+  if (!out)
+    return Fail(LFM3_E_INVALID, "null session output");
+  *out = nullptr;
+  try {
+    if (!m || !context || context > m->config.context)
+      Invalid("invalid LFM3 context");
+    const auto& c = m->config;
+    auto s = std::make_unique<lfm3_session>();
+    s->model = m;
+    s->context = context;
+    for (std::uint32_t i = 0; i < c.n_layers; ++i) {
+      lfm3_session::State st;
+      if (c.layer_type[i] == LFM3_LAYER_CONV) {
+        st.conv = Buffer(std::size_t(c.hidden) * (c.conv_width - 1) * 4);
+      } else {
+        // engine.cpp:60-77: sliding rings keep min(context, window) rows.
+        st.capacity = c.layer_type[i] == LFM3_LAYER_SLIDING
+                          ? std::min(context, c.window)
+                          : context;
+        const std::size_t n = std::size_t(st.capacity) * c.kv_heads[i] * c.head_dim * 2;
+        st.k = Buffer(n);
+        st.v = Buffer(n);
+      }
+      s->states.push_back(std::move(st));
+    }
+    s->logits = Buffer(std::size_t(c.vocab) * 4);
+    s->frontier = Buffer(std::size_t(c.hidden) * 4);
+    EnsureRoundBuffers(*m, context);
+    *out = s.release();
+    return LFM3_OK;
+  } catch (const Error& e) {
+    return Fail(e.status, e.what());
+  } catch (const std::exception& e) {
+    return Fail(LFM3_E_NOMEM, e.what());
+  }
+}
+
+void lfm3_session_destroy(lfm3_session* s) { delete s; }
+
+std::uint32_t lfm3_session_position(const lfm3_session* s) { return s ? s->position : 0; }
+
+int lfm3_session_is_coherent(const lfm3_session* s) { return s && !s->poisoned; }
+
+std::uint32_t lfm3_session_ring_capacity(const lfm3_session* s, std::uint32_t layer) {
+  return s && layer < s->states.size() ? s->states[layer].capacity : 0;
+}
+
+// engine.cpp:1300-1332: zero the convolution history, position 0, healthy.
+int lfm3_session_reset(lfm3_session* s) {
+  if (!s)
+    return Fail(LFM3_E_INVALID, "null session");
+  const auto& c = s->model->config;
+  for (auto& st : s->states)
+    if (st.conv.p) {
+      const int e = HipStatus(
+          hipMemset(st.conv.p, 0, std::size_t(c.hidden) * (c.conv_width - 1) * 4),
+          "reset");
+      if (e)
+        return e;
+    }
+  s->position = 0;
+  s->logits_ready = false;
+  s->poisoned = false;
+  return LFM3_OK;
+}
+
+int lfm3_session_state(lfm3_session* s, int kind, std::uint32_t layer,
+                       void** data, std::size_t* bytes) {
+  if (!s || !data)
+    return Fail(LFM3_E_INVALID, "null session state query");
+  Buffer* b = nullptr;
+  switch (kind) {
+    case LFM3_STATE_LOGITS: b = &s->logits; break;
+    case LFM3_STATE_FRONTIER: b = &s->frontier; break;
+    case LFM3_STATE_CONV:
+    case LFM3_STATE_KEY:
+    case LFM3_STATE_VALUE:
+      if (layer >= s->states.size())
+        return Fail(LFM3_E_INVALID, "LFM3 layer out of range");
+      b = kind == LFM3_STATE_CONV ? &s->states[layer].conv
+          : kind == LFM3_STATE_KEY ? &s->states[layer].k
+                                   : &s->states[layer].v;
+      break;
+    default:
+      return Fail(LFM3_E_INVALID, "unknown LFM3 state kind");
+  }
+  *data = b->p;
+  if (bytes)
+    *bytes = b->bytes;
+  return b->p ? LFM3_OK : Fail(LFM3_E_INVALID, "LFM3 layer has no such state");
+}
+
+int lfm3_session_set_position(lfm3_session* s, std::uint32_t position) {
+  if (!s || position > s->context)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 position");
+  s->position = position;
+  s->poisoned = false;
+  s->logits_ready = false;
+  return LFM3_OK;
+}
+
+int lfm3_session_read_logits(const lfm3_session* s, float* logits) {
+  if (!s || !logits)
+    return Fail(LFM3_E_INVALID, "null logits");
+  if (!s->logits_ready)
+    return Fail(LFM3_E_STATE, "LFM3 session has no logits");
+  return HipStatus(hipMemcpy(logits, s->logits.p, std::size_t(s->model->config.vocab) * 4,
+                             hipMemcpyDeviceToHost),
+                   "read logits");
+}
+
+}  // extern "C"
+
+namespace lfm3amd {
+namespace {
+
+// One decode round of n rows (engine.cpp:257-527, batch branch).
+void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
+              const std::uint32_t* tokens, bool greedy) {
+  const auto& c = m.config;
+  const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
+  const std::uint32_t L = c.n_layers;
+  const hipStream_t s = m.stream;
+  std::uint32_t max_context = 0;
+  for (std::uint32_t i = 0; i < n; ++i)
+    max_context = std::max(max_context, sessions[i]->context);
+  EnsureRoundBuffers(m, max_context);
+
+  // Host side of the round's index tables, then one upload.
+  auto* host = static_cast<std::uint8_t*>(m.staging->p);
+  std::memset(host, 0, m.table_bytes);
+  auto* rt = reinterpret_cast<RoundTable*>(host);
+  std::size_t off = Align(sizeof(RoundTable));
+  const std::size_t conv_off = off;
+  off += Align(L * kMaxBatch * sizeof(void*));
+  const std::size_t k_off = off;
+  off += Align(L * kMaxBatch * sizeof(void*));
+  const std::size_t v_off = off;
+  off += Align(L * kMaxBatch * sizeof(void*));
+  const std::size_t cap_off = off;
+  off += Align(L * kMaxBatch * 4);
+  const std::size_t items_full_off = off;
+  off += Align(m.items_capacity * sizeof(lfm3_attention_item));
+  const std::size_t items_swa_off = off;
+  auto** conv_ptr = reinterpret_cast<float**>(host + conv_off);
+  auto** k_ptr = reinterpret_cast<Half**>(host + k_off);
+  auto** v_ptr = reinterpret_cast<Half**>(host + v_off);
+  auto* cap = reinterpret_cast<std::uint32_t*>(host + cap_off);
+  for (std::uint32_t i = 0; i < n; ++i) {
+    lfm3_session& se = *sessions[i];
+    rt->tokens[i] = tokens[i];
+    rt->positions[i] = se.position;
+    rt->logits[i] = se.logits.as<float>();
+    rt->frontier[i] = se.frontier.as<float>();
+    for (std::uint32_t l = 0; l < L; ++l) {
+      conv_ptr[l * kMaxBatch + i] = se.states[l].conv.as<float>();
+      k_ptr[l * kMaxBatch + i] = se.states[l].k.as<Half>();
+      v_ptr[l * kMaxBatch + i] = se.states[l].v.as<Half>();
+      cap[l * kMaxBatch + i] = se.states[l].capacity;
+    }
+  }
+  const int n_full = lfm3_attention_plan(
+      rt->positions, n, 0,
+      reinterpret_cast<lfm3_attention_item*>(host + items_full_off),
+      std::uint32_t(m.items_capacity));
+  const int n_swa = lfm3_attention_plan(
+      rt->positions, n, c.window,
+      reinterpret_cast<lfm3_attention_item*>(host + items_swa_off),
+      std::uint32_t(m.items_capacity));
+  if (n_full < 0 || n_swa < 0)
+    throw Error(LFM3_E_INVALID, lfm3_last_error());
+  auto* dev = m.table.as<std::uint8_t>();
+  Check(hipMemcpyAsync(dev, host, m.table_bytes, hipMemcpyHostToDevice, s), "table upload");
+  const auto* d_rt = reinterpret_cast<const RoundTable*>(dev);
+
+  float* x = m.x.as<float>();
+  float* z = m.z.as<float>();
+  float* proj = m.proj.as<float>();
+  float* a = m.a.as<float>();
+  float* hid = m.hidden.as<float>();
+  float* out = m.out.as<float>();
+  const std::uint32_t pld = std::uint32_t(m.proj_ld);
+  const auto gemv = [&](const Matrix& w, const float* in, std::uint32_t ldx,
+                        float* y, std::uint32_t ldy) {
+    CheckStatus(lfm3_q8_gemv(w.codes.p, w.scales.p, w.rows, w.cols, in, ldx, y,
+                             ldy, n, m.gemv_ws.p, m.gemv_ws_bytes, s));
+  };
+
+  CheckStatus(lfm3_embed(m.embedding.codes.p, m.embedding.scales.p, c.vocab, H,
+                         d_rt->tokens, n, x, s));
+  CheckStatus(lfm3_residual_norm(nullptr, nullptr, x, m.layers[0].norm.as<float>(),
+                                 z, n, H, c.eps, s));
+  for (std::uint32_t il = 0; il < L; ++il) {
+    const Layer& l = m.layers[il];
+    if (l.type == LFM3_LAYER_CONV) {
+      gemv(l.in_proj, z, H, proj, pld);
+      CheckStatus(lfm3_conv_step_ragged(
+          proj, pld, l.conv.as<float>(),
+          reinterpret_cast<float* const*>(dev + conv_off) + il * kMaxBatch, a, H,
+          n, H, c.conv_width, s));
+      gemv(l.out_proj, a, H, out, H);
+    } else {
+      const bool swa = l.type == LFM3_LAYER_SLIDING;
+      gemv(l.qkvg, z, H, proj, pld);
+      const auto* kp = reinterpret_cast<std::uint16_t* const*>(dev + k_off) + il * kMaxBatch;
+      const auto* vp = reinterpret_cast<std::uint16_t* const*>(dev + v_off) + il * kMaxBatch;
+      const auto* cp = reinterpret_cast<const std::uint32_t*>(dev + cap_off) + il * kMaxBatch;
+      CheckStatus(lfm3_decode_heads_ragged(
+          proj + l.q_off, proj + l.k_off, proj + l.v_off, pld,
+          l.q_norm.as<float>(), l.k_norm.as<float>(),
+          swa ? m.freq_sliding.as<float>() : m.freq_global.as<float>(),
+          swa ? nullptr : m.factors.as<float>(), kp, vp, d_rt->positions, cp, n,
+          c.heads, l.kv, D, c.eps, s));
+      const auto* items = reinterpret_cast<const lfm3_attention_item*>(
+          dev + (swa ? items_swa_off : items_full_off));
+      CheckStatus(lfm3_decode_attention_ragged(
+          proj + l.q_off, pld, proj + l.g_off, pld, kp, vp, cp, items,
+          std::uint32_t(swa ? n_swa : n_full), a, c.heads * D, n, c.heads, l.kv,
+          D, m.attn_ws.p, m.attn_ws_bytes, s));
+      gemv(l.attn_out, a, c.heads * D, out, H);
+    }
+    CheckStatus(lfm3_residual_norm(out, l.post_norm.as<float>(), x,
+                                   l.ffn_norm.as<float>(), z, n, H, c.eps, s));
+    CheckStatus(lfm3_q8_gemv_swiglu(l.ffn.codes.p, l.ffn.scales.p, F, H, z, H,
+                                    hid, F, n, m.gemv_ws.p, m.gemv_ws_bytes, s));
+    gemv(l.down, hid, F, out, H);
+    const float* next = il + 1 < L ? m.layers[il + 1].norm.as<float>()
+                                   : m.output_norm.as<float>();
+    CheckStatus(lfm3_residual_norm(out, l.post_ffn_norm.as<float>(), x, next, z,
+                                   n, H, c.eps, s));
+  }
+  // z holds the final-normed rows (engine.cpp:505): LM head, then each
+  // session's logits and frontier rows.
+  const Matrix& head = m.head();
+  gemv(head, z, H, m.logits.as<float>(), c.vocab);
+  CheckStatus(LaunchScatterRows(m.logits.as<float>(), c.vocab, d_rt->logits, n,
+                                c.vocab, s));
+  CheckStatus(LaunchScatterRows(z, H, d_rt->frontier, n, H, s));
+  if (greedy)
+    CheckStatus(lfm3_argmax(m.logits.as<float>(), n, c.vocab, m.ids.as<std::uint32_t>(),
+                            m.argmax_ws.p, m.argmax_ws.bytes, s));
+  Check(hipGetLastError(), "round launch");
+  Check(hipStreamSynchronize(s), "round");
+  for (std::uint32_t i = 0; i < n; ++i) {
+    ++sessions[i]->position;
+    sessions[i]->logits_ready = true;
+  }
+}
+
+// engine.cpp:1178-1195.
+void ValidateBatch(lfm3_session* const* sessions, std::size_t n,
+                   const std::uint32_t* tokens) {
+  if (!sessions || !tokens || n == 0 || n > kMaxBatch)
+    Invalid("invalid LFM3 decode batch shape");
+  for (std::size_t i = 0; i < n; ++i) {
+    lfm3_session* se = sessions[i];
+    if (!se || std::find(sessions, sessions + i, se) != sessions + i)
+      Invalid("duplicate or null LFM3 batch session");
+    if (se->poisoned || se->position >= se->context ||
+        tokens[i] >= se->model->config.vocab || se->model != sessions[0]->model)
+      Invalid("incompatible LFM3 batch session");
+  }
+}
+
+int BatchEntry(lfm3_session* const* sessions, std::size_t n,
+               const std::uint32_t* tokens, float* const* logits,
+               std::uint32_t* ids) {
+  try {
+    ValidateBatch(sessions, n, tokens);
+    if (logits)
+      for (std::size_t i = 0; i < n; ++i)
+        if (!logits[i])
+          Invalid("invalid LFM3 decode batch shape");
+  } catch (const Error& e) {
+    return Fail(e.status, e.what());
+  }
+  lfm3_model& m = *sessions[0]->model;
+  try {
+    RunRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr);
+    const std::size_t V = m.config.vocab;
+    if (logits)
+      for (std::size_t i = 0; i < n; ++i)
+        Check(hipMemcpy(logits[i], sessions[i]->logits.p, V * 4, hipMemcpyDeviceToHost),
+              "logits copy");
+    if (ids)
+      Check(hipMemcpy(ids, m.ids.p, n * 4, hipMemcpyDeviceToHost), "ids copy");
+    return LFM3_OK;
+  } catch (const Error& e) {
+    for (std::size_t i = 0; i < n; ++i)
+      sessions[i]->poisoned = true;  // engine.cpp:1205-1208
+    return Fail(e.status, e.what());
+  } catch (const std::exception& e) {
+    for (std::size_t i = 0; i < n; ++i)
+      sessions[i]->poisoned = true;
+    return Fail(LFM3_E_HIP, e.what());
+  }
+}
+
+}  // namespace
+}  // namespace lfm3amd
+
+extern "C" {
+
+int lfm3_forward_batch(lfm3_session* const* sessions, std::size_t n,
+                       const std::uint32_t* tokens, float* const* logits) {
+  if (!logits)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 decode batch shape");
+  return BatchEntry(sessions, n, tokens, logits, nullptr);
+}
+
+int lfm3_forward_batch_greedy(lfm3_session* const* sessions, std::size_t n,
+                              const std::uint32_t* tokens, std::uint32_t* ids) {
+  if (!ids)
+    return Fail(LFM3_E_INVALID, "null greedy ids");
+  return BatchEntry(sessions, n, tokens, nullptr, ids);
+}
+
+}  // extern "C"

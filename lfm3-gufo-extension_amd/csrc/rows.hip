@@ -1,0 +1,342 @@
+// Row operations of the decode round on gfx950: residual + RMSNorm, the
+// ragged gated short-convolution step, the ragged Q/K heads (per-head
+// RMSNorm, paired RoPE, F16 K/V ring store) and greedy argmax.
+#include <cmath>
+#include <string>
+
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace lfm3amd {
+
+namespace {
+thread_local std::string g_error;
+}
+void SetError(const std::string& message) { g_error = message; }
+int Fail(int status, const std::string& message) {
+  g_error = message;
+  return status;
+}
+int HipStatus(hipError_t e, const char* what) {
+  if (e == hipSuccess)
+    return LFM3_OK;
+  g_error = std::string(what) + ": " + hipGetErrorString(e);
+  return LFM3_E_HIP;
+}
+
+namespace {
+
+constexpr int kNormThreads = 256, kNormItems = 16;
+
+// Block sum of one value per thread: wave butterflies then the four wave
+// sums in wave order.
+__device__ float BlockSum(float v, float* scratch) {
+  v = WaveSum(v);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0)
+    scratch[wave] = v;
+  __syncthreads();
+  float total = 0.0f;
+  for (int w = 0; w < kNormThreads / 64; ++w)
+    total += scratch[w];
+  return total;
+}
+
+// reference.cpp:20-28 / hip/ops.hip:905-970 semantics: x += post(branch),
+// then z = x / sqrt(mean(x^2) + eps) * w, each product rounded as the
+// reference's x * scale * weight.
+__launch_bounds__(kNormThreads) __global__
+    void ResidualNormKernel(const float* __restrict__ branch,
+                            const float* __restrict__ post,
+                            float* __restrict__ x,
+                            const float* __restrict__ weight,
+                            float* __restrict__ z, int H, float eps) {
+  __shared__ float scratch[kNormThreads / 64];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const int items = (H + kNormThreads - 1) / kNormThreads;
+  float* xr = x + std::size_t(row) * H;
+  float v[kNormItems];
+#pragma unroll
+  for (int i = 0; i < kNormItems; ++i) {
+    const int k = tid + kNormThreads * i;
+    v[i] = i < items && k < H ? xr[k] : 0.0f;
+  }
+  if (branch) {
+    float b[kNormItems], squares = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormItems; ++i) {
+      const int k = tid + kNormThreads * i;
+      b[i] = i < items && k < H ? branch[std::size_t(row) * H + k] : 0.0f;
+      squares = fmaf(b[i], b[i], squares);
+    }
+    if (post) {
+      const float scale = 1.0f / sqrtf(BlockSum(squares, scratch) / float(H) + eps);
+#pragma unroll
+      for (int i = 0; i < kNormItems; ++i) {
+        const int k = tid + kNormThreads * i;
+        if (i < items && k < H)
+          b[i] = (b[i] * scale) * post[k];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kNormItems; ++i) {
+      const int k = tid + kNormThreads * i;
+      if (i < items && k < H) {
+        v[i] = v[i] + b[i];
+        xr[k] = v[i];
+      }
+    }
+  }
+  if (!weight)
+    return;
+  float squares = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormItems; ++i)
+    squares = fmaf(v[i], v[i], squares);
+  const float scale = 1.0f / sqrtf(BlockSum(squares, scratch) / float(H) + eps);
+#pragma unroll
+  for (int i = 0; i < kNormItems; ++i) {
+    const int k = tid + kNormThreads * i;
+    if (i < items && k < H)
+      z[std::size_t(row) * H + k] = (v[i] * scale) * weight[k];
+  }
+}
+
+// reference.cpp:85-101: one owner per (row, channel); the window sum keeps
+// the reference's order and separate roundings, so outputs and history are
+// bit-identical to it for the same projection rows.
+__global__ void ConvStepKernel(const float* __restrict__ p, int ldp,
+                               const float* __restrict__ taps,
+                               float* const* __restrict__ history,
+                               float* __restrict__ y, int ldy, int H, int L) {
+#pragma clang fp contract(off)
+  const int ch = blockIdx.x * blockDim.x + threadIdx.x, row = blockIdx.y;
+  if (ch >= H)
+    return;
+  const float* pr = p + std::size_t(row) * ldp;
+  float* own = history[row] + std::size_t(ch) * (L - 1);
+  const float bx = pr[ch] * pr[2 * H + ch];
+  const float* w = taps + std::size_t(ch) * L;
+  float sum = 0.0f;
+  for (int t = 0; t < L - 1; ++t)
+    sum += w[t] * own[t];
+  sum += w[L - 1] * bx;
+  for (int t = 1; t < L - 1; ++t)
+    own[t - 1] = own[t];
+  own[L - 2] = bx;
+  y[std::size_t(row) * ldy + ch] = sum * pr[H + ch];
+}
+
+// Per-head RMSNorm + paired RoPE + F16 store. A block is one row and the
+// dim / 2 threads of a head own the pairs (i, i + dim / 2); blockIdx.x walks
+// the query heads, then the KV heads, which also store K and V to the
+// row's ring slot. Sub-wave reductions cover one head (dim / 2 lanes).
+template<int D>
+__launch_bounds__(D / 2) __global__
+    void HeadsKernel(float* __restrict__ q, float* __restrict__ k,
+                     const float* __restrict__ v, int ld,
+                     const float* __restrict__ q_norm,
+                     const float* __restrict__ k_norm,
+                     const float* __restrict__ frequencies,
+                     const float* __restrict__ factors,
+                     Half* const* __restrict__ cache_k,
+                     Half* const* __restrict__ cache_v,
+                     const std::uint32_t* __restrict__ positions,
+                     const std::uint32_t* __restrict__ capacity, int heads,
+                     int kv_heads, float eps) {
+  constexpr int P = D / 2;
+  const int head = blockIdx.x, row = blockIdx.y, pair = threadIdx.x;
+  const bool is_key = head >= heads;
+  const int kvh = head - heads;
+  float* xh = is_key ? k + std::size_t(row) * ld + kvh * D
+                     : q + std::size_t(row) * ld + head * D;
+  const float* w = is_key ? k_norm : q_norm;
+  const float x0 = xh[pair], x1 = xh[pair + P];
+  float squares = fmaf(x0, x0, x1 * x1);
+#pragma unroll
+  for (int m = P / 2; m; m >>= 1)
+    squares += __shfl_xor(squares, m, P);
+  const float scale = 1.0f / sqrtf(squares / float(D) + eps);
+  const float a = (x0 * scale) * w[pair], b = (x1 * scale) * w[pair + P];
+  const std::uint32_t position = positions[row];
+  float angle = float(position) * frequencies[pair];
+  if (factors)
+    angle /= factors[pair];
+  float sn, cs;
+  sincosf(angle, &sn, &cs);
+  const float r0 = a * cs - b * sn, r1 = b * cs + a * sn;
+  xh[pair] = r0;
+  xh[pair + P] = r1;
+  if (!is_key)
+    return;
+  const std::size_t slot =
+      std::size_t(position % capacity[row]) * kv_heads * D + std::size_t(kvh) * D;
+  const float* vh = v + std::size_t(row) * ld + kvh * D;
+  Half* ck = cache_k[row];
+  Half* cv = cache_v[row];
+  ck[slot + pair] = FloatToHalfBits(r0);
+  ck[slot + pair + P] = FloatToHalfBits(r1);
+  cv[slot + pair] = FloatToHalfBits(vh[pair]);
+  cv[slot + pair + P] = FloatToHalfBits(vh[pair + P]);
+}
+
+// Greedy argmax: blocks reduce column ranges to a 64-bit key (ordered
+// value bits above the complemented index, so the largest key is the
+// largest value at its first index) merged with atomicMax; the last block
+// of a row writes the id and clears the key and its ticket for the next
+// call.
+constexpr int kArgmaxThreads = 256, kArgmaxPerBlock = 8192;
+
+__device__ __forceinline__ unsigned long long ArgKey(float value, unsigned index) {
+  unsigned bits = __float_as_uint(value);
+  bits = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+  return (static_cast<unsigned long long>(bits) << 32) | (0xffffffffu - index);
+}
+
+__launch_bounds__(kArgmaxThreads) __global__
+    void ArgmaxKernel(const float* __restrict__ logits, int cols,
+                      unsigned long long* __restrict__ keys,
+                      unsigned* __restrict__ tickets,
+                      std::uint32_t* __restrict__ ids) {
+  __shared__ unsigned long long best[kArgmaxThreads / 64];
+  __shared__ bool s_last;
+  const int row = blockIdx.y, tid = threadIdx.x;
+  const int begin = blockIdx.x * kArgmaxPerBlock;
+  const int end = min(begin + kArgmaxPerBlock, cols);
+  const float* lr = logits + std::size_t(row) * cols;
+  unsigned long long key = 0;
+  for (int c = begin + tid; c < end; c += kArgmaxThreads) {
+    const unsigned long long k = ArgKey(lr[c], unsigned(c));
+    key = k > key ? k : key;
+  }
+#pragma unroll
+  for (int m = 32; m; m >>= 1) {
+    const unsigned long long other = __shfl_xor(key, m, 64);
+    key = other > key ? other : key;
+  }
+  if ((tid & 63) == 0)
+    best[tid >> 6] = key;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArgmaxThreads / 64; ++w)
+      key = best[w] > key ? best[w] : key;
+    atomicMax(keys + row, key);
+    __threadfence();
+    const unsigned prev = atomicAdd(tickets + row, 1u);
+    s_last = prev == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last || tid != 0)
+    return;
+  __threadfence();
+  const unsigned long long final_key = atomicExch(keys + row, 0ull);
+  ids[row] = 0xffffffffu - unsigned(final_key & 0xffffffffu);
+  tickets[row] = 0;
+}
+
+__global__ void ScatterRowsKernel(const float* __restrict__ src, std::size_t ld,
+                                  float* const* __restrict__ dst,
+                                  std::size_t count) {
+  const int row = blockIdx.y;
+  const std::size_t i = (std::size_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  const float* s = src + row * ld;
+  float* d = dst[row];
+  if (i + 4 <= count) {
+    *reinterpret_cast<float4*>(d + i) = *reinterpret_cast<const float4*>(s + i);
+  } else {
+    for (std::size_t k = i; k < count; ++k)
+      d[k] = s[k];
+  }
+}
+
+}  // namespace
+
+int LaunchScatterRows(const float* src, std::size_t ld, float* const* dst,
+                      std::uint32_t rows, std::size_t count,
+                      hipStream_t stream) {
+  const std::size_t threads = (count + 3) / 4;
+  const dim3 grid(unsigned((threads + 255) / 256), rows);
+  ScatterRowsKernel<<<grid, 256, 0, stream>>>(src, ld, dst, count);
+  return HipStatus(hipGetLastError(), "LFM3 row scatter launch");
+}
+
+}  // namespace lfm3amd
+
+using namespace lfm3amd;
+
+extern "C" {
+
+const char* lfm3_last_error(void) { return g_error.c_str(); }
+
+int lfm3_residual_norm(const float* branch, const float* post_norm, float* x,
+                       const float* norm, float* z, std::uint32_t rows,
+                       std::uint32_t hidden, float eps, void* stream) {
+  if (!x || !rows || !hidden || hidden > kNormThreads * kNormItems ||
+      (norm && !z))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 residual norm shape");
+  ResidualNormKernel<<<rows, kNormThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      branch, branch ? post_norm : nullptr, x, norm, z, int(hidden), eps);
+  return HipStatus(hipGetLastError(), "LFM3 residual norm launch");
+}
+
+int lfm3_conv_step_ragged(const float* p, std::uint32_t ldp, const float* taps,
+                          float* const* history, float* y, std::uint32_t ldy,
+                          std::uint32_t rows, std::uint32_t hidden,
+                          std::uint32_t width, void* stream) {
+  if (!p || !taps || !history || !y || !rows || !hidden || width < 2 ||
+      width > 32 || ldp < 3 * hidden || ldy < hidden)
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 convolution shape");
+  const dim3 grid((hidden + 255) / 256, rows);
+  ConvStepKernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      p, int(ldp), taps, history, y, int(ldy), int(hidden), int(width));
+  return HipStatus(hipGetLastError(), "LFM3 convolution launch");
+}
+
+int lfm3_decode_heads_ragged(float* q, float* k, const float* v,
+                             std::uint32_t ld, const float* q_norm,
+                             const float* k_norm, const float* frequencies,
+                             const float* factors, std::uint16_t* const* cache_k,
+                             std::uint16_t* const* cache_v,
+                             const std::uint32_t* positions,
+                             const std::uint32_t* capacity, std::uint32_t rows,
+                             std::uint32_t heads, std::uint32_t kv_heads,
+                             std::uint32_t dim, float eps, void* stream) {
+  if (!q || !k || !v || !q_norm || !k_norm || !frequencies || !cache_k ||
+      !cache_v || !positions || !capacity || !rows || !heads || !kv_heads ||
+      heads % kv_heads || (dim != 64 && dim != 128))
+    return Fail(LFM3_E_INVALID, "LFM3 decode heads need dimension 64 or 128");
+  const dim3 grid(heads + kv_heads, rows);
+  const auto s = static_cast<hipStream_t>(stream);
+  if (dim == 128)
+    HeadsKernel<128><<<grid, 64, 0, s>>>(q, k, v, int(ld), q_norm, k_norm,
+                                         frequencies, factors, cache_k, cache_v,
+                                         positions, capacity, int(heads),
+                                         int(kv_heads), eps);
+  else
+    HeadsKernel<64><<<grid, 32, 0, s>>>(q, k, v, int(ld), q_norm, k_norm,
+                                        frequencies, factors, cache_k, cache_v,
+                                        positions, capacity, int(heads),
+                                        int(kv_heads), eps);
+  return HipStatus(hipGetLastError(), "LFM3 decode heads launch");
+}
+
+std::size_t lfm3_argmax_workspace_bytes(std::uint32_t rows) {
+  return std::size_t(rows) * (sizeof(unsigned long long) + sizeof(unsigned));
+}
+
+int lfm3_argmax(const float* logits, std::uint32_t rows, std::uint32_t cols,
+                std::uint32_t* ids, void* workspace, std::size_t workspace_bytes,
+                void* stream) {
+  if (!logits || !ids || !rows || !cols || !workspace ||
+      workspace_bytes < lfm3_argmax_workspace_bytes(rows))
+    return Fail(LFM3_E_INVALID, "invalid LFM3 argmax");
+  auto* keys = static_cast<unsigned long long*>(workspace);
+  auto* tickets = reinterpret_cast<unsigned*>(keys + rows);
+  const dim3 grid((cols + kArgmaxPerBlock - 1) / kArgmaxPerBlock, rows);
+  ArgmaxKernel<<<grid, kArgmaxThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      logits, int(cols), keys, tickets, ids);
+  return HipStatus(hipGetLastError(), "LFM3 argmax launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,432 @@
+"""ctypes binding of liblfm3_amd.so (the gfx950 LFM3 step) for tests and the
+benchmark. Device buffers come straight from the HIP runtime (plumbing
+only); every computation runs in the HIP library, and loading fails loudly
+when the library is missing.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "liblfm3_amd.so")
+
+OK, E_INVALID, E_HIP, E_STATE, E_NOMEM = 0, -1, -2, -3, -4
+LAYER_CONV, LAYER_FULL, LAYER_SLIDING = 0, 1, 2
+TYPE_F32, TYPE_Q8_0 = 0, 8
+STATE_LOGITS, STATE_FRONTIER, STATE_CONV, STATE_KEY, STATE_VALUE = range(5)
+GLOBAL_TENSORS, LAYER_TENSORS = 4, 17
+MAX_BATCH = 8
+
+vp, u32, u64, f32, sz, i32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_float, C.c_size_t, C.c_int
+
+
+class LFM3Error(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{status}] {message}")
+        self.status = status
+
+
+class Config(C.Structure):
+    _fields_ = [("hidden", u32), ("intermediate", u32), ("vocab", u32), ("context", u32),
+                ("heads", u32), ("head_dim", u32), ("window", u32), ("conv_width", u32),
+                ("n_layers", u32), ("eps", f32), ("theta", f32), ("theta_swa", f32),
+                ("kv_heads", C.POINTER(u32)), ("layer_type", C.POINTER(C.c_uint8))]
+
+
+class Tensor(C.Structure):
+    _fields_ = [("data", vp), ("type", u32), ("cols", u32), ("rows", u32)]
+
+
+class AttentionItem(C.Structure):
+    _fields_ = [("row", u32), ("key_begin", u32), ("key_end", u32),
+                ("first_item", u32), ("parts", u32), ("reserved", u32 * 3)]
+
+
+_SIGS = {
+    "lfm3_last_error": (C.c_char_p, []),
+    "lfm3_q8_tiled_bytes": (None, [u32, u32, C.POINTER(sz), C.POINTER(sz)]),
+    "lfm3_q8_pack_host": (i32, [vp, u32, u32, vp, vp, u32, u32]),
+    "lfm3_q8_pack_device": (i32, [vp, u32, u32, vp, vp, u32, u32, vp]),
+    "lfm3_gemv_workspace_bytes": (sz, [u32, u32, u32]),
+    "lfm3_q8_gemv": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, u32, vp, sz, vp]),
+    "lfm3_q8_gemv_swiglu": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, u32, vp, sz, vp]),
+    "lfm3_residual_norm": (i32, [vp, vp, vp, vp, vp, u32, u32, f32, vp]),
+    "lfm3_embed": (i32, [vp, vp, u32, u32, vp, u32, vp, vp]),
+    "lfm3_argmax_workspace_bytes": (sz, [u32]),
+    "lfm3_argmax": (i32, [vp, u32, u32, vp, vp, sz, vp]),
+    "lfm3_conv_step_ragged": (i32, [vp, u32, vp, vp, vp, u32, u32, u32, u32, vp]),
+    "lfm3_decode_heads_ragged": (i32, [vp, vp, vp, u32, vp, vp, vp, vp, vp, vp, vp, vp,
+                                       u32, u32, u32, u32, f32, vp]),
+    "lfm3_attention_plan": (i32, [vp, u32, u32, vp, u32]),
+    "lfm3_attention_workspace_bytes": (sz, [u32, u32, u32, u32, u32]),
+    "lfm3_decode_attention_ragged": (i32, [vp, u32, vp, u32, vp, vp, vp, vp, u32, vp, u32,
+                                           u32, u32, u32, u32, vp, sz, vp]),
+    "lfm3_model_load": (i32, [C.POINTER(Config), C.POINTER(Tensor), sz, C.POINTER(vp)]),
+    "lfm3_model_destroy": (None, [vp]),
+    "lfm3_model_stream": (vp, [vp]),
+    "lfm3_session_create": (i32, [vp, u32, C.POINTER(vp)]),
+    "lfm3_session_destroy": (None, [vp]),
+    "lfm3_session_position": (u32, [vp]),
+    "lfm3_session_reset": (i32, [vp]),
+    "lfm3_session_is_coherent": (i32, [vp]),
+    "lfm3_session_ring_capacity": (u32, [vp, u32]),
+    "lfm3_session_state": (i32, [vp, i32, u32, C.POINTER(vp), C.POINTER(sz)]),
+    "lfm3_session_set_position": (i32, [vp, u32]),
+    "lfm3_forward_batch": (i32, [vp, sz, vp, vp]),
+    "lfm3_forward_batch_greedy": (i32, [vp, sz, vp, vp]),
+    "lfm3_session_read_logits": (i32, [vp, vp]),
+    "lfm3_synth_key": (u64, [u64, C.c_char_p]),
+    "lfm3_synth_normal": (None, [u64, f32, f32, vp, sz]),
+    "lfm3_synth_uniform_u32": (None, [u64, u32, u32, vp, sz]),
+    "lfm3_synth_half_normal": (None, [u64, vp, sz]),
+    "lfm3_synth_q8": (None, [u64, u32, u32, f32, vp]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises if it was not built (no fallback path)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: build it (python -c 'import __graft_entry__ as g; g.build()')")
+        handle = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(status: int) -> int:
+    if status < 0:
+        raise LFM3Error(status, lib().lfm3_last_error().decode())
+    return status
+
+
+def ptr(a) -> int:
+    """Address of a numpy array or a DeviceBuffer (0 for None)."""
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    if a is None:
+        return 0
+    return a.addr
+
+
+# ---------------------------------------------------------------- synthetic
+
+def key(seed: int, name: str) -> int:
+    return lib().lfm3_synth_key(seed, name.encode())
+
+
+def normal(seed: int, name: str, n: int, mean=0.0, std=1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().lfm3_synth_normal(key(seed, name), mean, std, ptr(out), n)
+    return out
+
+
+def uniform_u32(seed: int, name: str, n: int, lo: int, hi: int) -> np.ndarray:
+    out = np.empty(n, np.uint32)
+    lib().lfm3_synth_uniform_u32(key(seed, name), lo, hi, ptr(out), n)
+    return out
+
+
+def half_normal(seed: int, name: str, n: int) -> np.ndarray:
+    out = np.empty(n, np.uint16)
+    lib().lfm3_synth_half_normal(key(seed, name), ptr(out), n)
+    return out
+
+
+def q8(seed: int, name: str, rows: int, cols: int, d_std=0.02) -> np.ndarray:
+    out = np.empty(rows * (cols // 32) * 34, np.uint8)
+    lib().lfm3_synth_q8(key(seed, name), rows, cols, d_std, ptr(out))
+    return out
+
+
+def q8_dequant(blob: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """float64 d * q of GGUF Q8_0 rows (test helper)."""
+    blocks = blob.reshape(rows, cols // 32, 34)
+    d = blocks[:, :, :2].copy().view(np.float16).astype(np.float64)
+    q = blocks[:, :, 2:].view(np.int8).astype(np.float64)
+    return (d * q).reshape(rows, cols)
+
+
+SEED = 20261201
+
+
+@dataclass
+class Dims:
+    """LFM3 text dims. Defaults: the reference checkpoint (config_test.cpp:82-92)."""
+    hidden: int = 2048
+    intermediate: int = 7680
+    vocab: int = 128000
+    context: int = 262144
+    heads: int = 16
+    head_dim: int = 128
+    kv_heads: int = 4
+    window: int = 256
+    conv_width: int = 7
+    eps: float = 1e-5
+    theta: float = 1e6
+    theta_swa: float = 1e4
+    # C conv, S sliding, G global: 13 / 5 / 6, last layer global.
+    pattern: str = "CCSCGCCSCGCCSCGCSCGCSCGG"
+
+    @property
+    def n_layers(self) -> int:
+        return len(self.pattern)
+
+    def layer_type(self, i: int) -> int:
+        return {"C": LAYER_CONV, "G": LAYER_FULL, "S": LAYER_SLIDING}[self.pattern[i]]
+
+
+NOMINAL = dict(intermediate=8192, vocab=65536, heads=32, head_dim=64, kv_heads=8)
+
+
+@dataclass
+class Weights:
+    dims: Dims
+    globals: list = field(default_factory=list)   # 4 (array|None, type, cols, rows)
+    layers: list = field(default_factory=list)    # per layer: 17 entries
+
+    def tensor_list(self):
+        return self.globals + [t for layer in self.layers for t in layer]
+
+
+def synth_weights(dims: Dims, seed: int = SEED, masked_rope=True) -> Weights:
+    """Random-init Q8_0 model of the given dims (GGUF layouts)."""
+    H, F, D, V = dims.hidden, dims.intermediate, dims.head_dim, dims.vocab
+    w = Weights(dims)
+    factors = np.ones(D // 2, np.float32)
+    if masked_rope:
+        factors[D // 4:] = 1e30
+    w.globals = [(q8(seed, "token_embd", V, H), TYPE_Q8_0, H, V), None,
+                 (normal(seed, "output_norm", H, 1.0, 0.02), TYPE_F32, H, 1),
+                 (factors, TYPE_F32, D // 2, 1)]
+    for i in range(dims.n_layers):
+        p = f"blk.{i}."
+        t = [None] * LAYER_TENSORS
+        for j, name in enumerate(["attn_norm", "ffn_norm", "post_attention_norm", "post_ffw_norm"]):
+            t[j] = (normal(seed, p + name, H, 1.0, 0.02), TYPE_F32, H, 1)
+        t[4] = (q8(seed, p + "ffn_gate", F, H), TYPE_Q8_0, H, F)
+        t[5] = (q8(seed, p + "ffn_up", F, H), TYPE_Q8_0, H, F)
+        t[6] = (q8(seed, p + "ffn_down", H, F), TYPE_Q8_0, F, H)
+        if dims.layer_type(i) == LAYER_CONV:
+            t[7] = (normal(seed, p + "shortconv.conv", H * dims.conv_width, 0.0, 0.1), TYPE_F32,
+                    dims.conv_width, H)
+            t[8] = (q8(seed, p + "shortconv.in_proj", 3 * H, H), TYPE_Q8_0, H, 3 * H)
+            t[9] = (q8(seed, p + "shortconv.out_proj", H, H), TYPE_Q8_0, H, H)
+        else:
+            kv = dims.kv_heads
+            t[10] = (q8(seed, p + "attn_q", dims.heads * D, H), TYPE_Q8_0, H, dims.heads * D)
+            t[11] = (q8(seed, p + "attn_k", kv * D, H), TYPE_Q8_0, H, kv * D)
+            t[12] = (q8(seed, p + "attn_v", kv * D, H), TYPE_Q8_0, H, kv * D)
+            t[13] = (normal(seed, p + "attn_q_norm", D, 1.0, 0.02), TYPE_F32, D, 1)
+            t[14] = (normal(seed, p + "attn_k_norm", D, 1.0, 0.02), TYPE_F32, D, 1)
+            t[15] = (q8(seed, p + "attn_gate", dims.heads, H), TYPE_Q8_0, H, dims.heads)
+            t[16] = (q8(seed, p + "attn_output", H, dims.heads * D), TYPE_Q8_0, dims.heads * D, H)
+        w.layers.append(t)
+    return w
+
+
+def make_config(dims: Dims):
+    kv = (u32 * dims.n_layers)(*[0 if dims.layer_type(i) == LAYER_CONV else dims.kv_heads
+                                 for i in range(dims.n_layers)])
+    lt = (C.c_uint8 * dims.n_layers)(*[dims.layer_type(i) for i in range(dims.n_layers)])
+    cfg = Config(dims.hidden, dims.intermediate, dims.vocab, dims.context, dims.heads,
+                 dims.head_dim, dims.window, dims.conv_width, dims.n_layers, dims.eps,
+                 dims.theta, dims.theta_swa, kv, lt)
+    return cfg, (kv, lt)
+
+
+def tensor_array(entries):
+    arr = (Tensor * len(entries))()
+    for i, e in enumerate(entries):
+        if e is not None:
+            data, typ, cols, rows = e
+            arr[i] = Tensor(ptr(data), typ, cols, rows)
+    return arr
+
+
+class Model:
+    """lfm3_model: device weights of one checkpoint (Model::Load)."""
+
+    def __init__(self, weights: Weights):
+        self.dims = weights.dims
+        cfg, self._keep = make_config(weights.dims)
+        self._tensors = tensor_array(weights.tensor_list())
+        handle = vp()
+        check(lib().lfm3_model_load(C.byref(cfg), self._tensors, len(self._tensors),
+                                    C.byref(handle)))
+        self.handle = handle
+
+    def close(self):
+        if self.handle:
+            lib().lfm3_model_destroy(self.handle)
+            self.handle = None
+
+    def stream(self) -> int:
+        return lib().lfm3_model_stream(self.handle) or 0
+
+    def session(self, context: int) -> "Session":
+        return Session(self, context)
+
+    def forward_batch(self, sessions, tokens, want_logits=True):
+        """Session::ForwardBatch: returns (n, vocab) float32 logits."""
+        n = len(sessions)
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        handles = (vp * max(n, 1))(*[s.handle for s in sessions])
+        if want_logits:
+            out = np.empty((n, self.dims.vocab), np.float32)
+            rows = (vp * max(n, 1))(*[out[i].ctypes.data for i in range(n)])
+            check(lib().lfm3_forward_batch(handles, n, ptr(toks), rows))
+            return out
+        ids = np.empty(n, np.uint32)
+        check(lib().lfm3_forward_batch_greedy(handles, n, ptr(toks), ptr(ids)))
+        return ids
+
+    def forward_batch_greedy(self, sessions, tokens):
+        return self.forward_batch(sessions, tokens, want_logits=False)
+
+
+class Session:
+    def __init__(self, model: Model, context: int):
+        self.model = model
+        handle = vp()
+        check(lib().lfm3_session_create(model.handle, context, C.byref(handle)))
+        self.handle = handle
+        self.context = context
+
+    def close(self):
+        if self.handle:
+            lib().lfm3_session_destroy(self.handle)
+            self.handle = None
+
+    @property
+    def position(self) -> int:
+        return lib().lfm3_session_position(self.handle)
+
+    def set_position(self, p: int):
+        check(lib().lfm3_session_set_position(self.handle, p))
+
+    def reset(self):
+        check(lib().lfm3_session_reset(self.handle))
+
+    def coherent(self) -> bool:
+        return bool(lib().lfm3_session_is_coherent(self.handle))
+
+    def capacity(self, layer: int) -> int:
+        return lib().lfm3_session_ring_capacity(self.handle, layer)
+
+    def state(self, kind: int, layer: int = 0):
+        data, nbytes = vp(), sz()
+        check(lib().lfm3_session_state(self.handle, kind, layer, C.byref(data), C.byref(nbytes)))
+        return data.value, nbytes.value
+
+    def read_logits(self) -> np.ndarray:
+        out = np.empty(self.model.dims.vocab, np.float32)
+        check(lib().lfm3_session_read_logits(self.handle, ptr(out)))
+        return out
+
+
+# ------------------------------------------------------------ device memory
+
+_hip = None
+
+
+def hip():
+    """The HIP runtime (libamdhip64) for allocations and copies."""
+    global _hip
+    if _hip is None:
+        h = C.CDLL("libamdhip64.so")
+        h.hipMalloc.argtypes = [C.POINTER(vp), sz]
+        h.hipFree.argtypes = [vp]
+        h.hipMemcpy.argtypes = [vp, vp, sz, i32]
+        h.hipMemset.argtypes = [vp, i32, sz]
+        h.hipDeviceSynchronize.argtypes = []
+        h.hipGetErrorString.restype = C.c_char_p
+        h.hipGetErrorString.argtypes = [i32]
+        h.hipGetDeviceCount.argtypes = [C.POINTER(i32)]
+        h.hipStreamSynchronize.argtypes = [vp]
+        _hip = h
+    return _hip
+
+
+def hip_check(e: int):
+    if e != 0:
+        raise LFM3Error(E_HIP, hip().hipGetErrorString(e).decode())
+
+
+H2D, D2H, D2D = 1, 2, 3
+
+
+class DeviceBuffer:
+    """hipMalloc'd bytes, zeroed, freed on close/GC."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = max(int(nbytes), 1)
+        p = vp()
+        hip_check(hip().hipMalloc(C.byref(p), self.nbytes))
+        self.addr = p.value
+        hip_check(hip().hipMemset(self.addr, 0, self.nbytes))
+
+    @classmethod
+    def of(cls, host: np.ndarray) -> "DeviceBuffer":
+        host = np.ascontiguousarray(host)
+        b = cls(host.nbytes)
+        b.upload(host)
+        return b
+
+    def upload(self, host: np.ndarray, offset: int = 0):
+        host = np.ascontiguousarray(host)
+        assert offset + host.nbytes <= self.nbytes
+        hip_check(hip().hipMemcpy(self.addr + offset, host.ctypes.data, host.nbytes, H2D))
+
+    def download(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype)
+        assert offset + out.nbytes <= self.nbytes
+        hip_check(hip().hipMemcpy(out.ctypes.data, self.addr + offset, out.nbytes, D2H))
+        return out
+
+    def close(self):
+        if self.addr:
+            hip().hipFree(self.addr)
+            self.addr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def upload_to(addr: int, host: np.ndarray):
+    host = np.ascontiguousarray(host)
+    hip_check(hip().hipMemcpy(addr, host.ctypes.data, host.nbytes, H2D))
+
+
+def download_from(addr: int, dtype, count: int) -> np.ndarray:
+    out = np.empty(count, dtype)
+    hip_check(hip().hipMemcpy(out.ctypes.data, addr, out.nbytes, D2H))
+    return out
+
+
+def synchronize():
+    hip_check(hip().hipDeviceSynchronize())
+
+
+def gpu_count() -> int:
+    n = i32(0)
+    try:
+        if hip().hipGetDeviceCount(C.byref(n)) != 0:
+            return 0
+    except OSError:
+        return 0
+    return n.value

@@ -1,0 +1,445 @@
+// CPU oracle for the LFM3 decode step: TEST INFRASTRUCTURE ONLY (see
+// oracle.h). A scalar FP32 restatement of reference.cpp built with
+// -ffp-contract=off so every expression rounds in source order, as the
+// reference's own scalar loops do. Nothing here is shipped or called by the
+// product library.
+#include "oracle.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <new>
+#include <vector>
+
+namespace {
+
+// Textbook IEEE binary16 decoding: sign, 5-bit exponent (bias 15), 10-bit
+// fraction; exponent 0 is subnormal (fraction * 2^-24), 31 is Inf/NaN.
+float HalfToFloat(uint16_t h) {
+  const uint32_t sign = uint32_t(h >> 15) << 31;
+  const uint32_t exponent = (h >> 10) & 31, fraction = h & 1023;
+  uint32_t bits;
+  if (exponent == 0) {
+    if (fraction == 0) {
+      bits = sign;
+    } else {
+      float value = std::ldexp(float(fraction), -24);
+      std::memcpy(&bits, &value, 4);
+      bits |= sign;
+    }
+  } else if (exponent == 31) {
+    bits = sign | 0x7f800000u | (fraction << 13);
+  } else {
+    bits = sign | ((exponent + 112) << 23) | (fraction << 13);
+  }
+  float out;
+  std::memcpy(&out, &bits, 4);
+  return out;
+}
+
+// Round-to-nearest-even binary32 -> binary16, including subnormals,
+// overflow to infinity and NaN preservation.
+uint16_t FloatToHalf(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint16_t sign = uint16_t((x >> 16) & 0x8000u);
+  const uint32_t abs = x & 0x7fffffffu;
+  if (abs >= 0x7f800000u)  // Inf or NaN
+    return sign | (abs > 0x7f800000u ? uint16_t(0x7e00u | ((abs >> 13) & 0x3ffu))
+                                     : uint16_t(0x7c00u));
+  const int exponent = int(abs >> 23) - 127;
+  if (exponent > 15)
+    return sign | 0x7c00u;
+  uint32_t mantissa = (abs & 0x7fffffu) | 0x800000u;  // 24 significant bits
+  int shift;                                          // bits dropped
+  uint32_t base;
+  if (exponent >= -14) {
+    shift = 13;
+    base = uint32_t(exponent + 15) << 10;
+    mantissa &= 0x7fffffu;  // implicit bit lives in the exponent field
+  } else {
+    if (abs == 0)
+      return sign;
+    shift = 13 + (-14 - exponent);
+    base = 0;
+    if (shift > 24)
+      return sign;  // below half the smallest subnormal
+  }
+  const uint32_t kept = mantissa >> shift;
+  const uint32_t rest = mantissa & ((1u << shift) - 1);
+  const uint32_t half = 1u << (shift - 1);
+  uint32_t out = base + kept;
+  if (rest > half || (rest == half && (kept & 1)))
+    ++out;  // may carry into the exponent, which is the correct result
+  return sign | uint16_t(out);
+}
+
+struct Q8Block {
+  uint16_t d;
+  int8_t q[32];
+};
+static_assert(sizeof(Q8Block) == 34, "Q8_0 block is 34 bytes");
+
+// weights.cpp:101-125 (Q8_0 via ggml's d * q, F32 by copy).
+bool DecodeRow(const orc_tensor& t, uint32_t row, float* out) {
+  if (row >= t.rows)
+    return false;
+  if (t.type == ORC_F32) {
+    std::memcpy(out, static_cast<const float*>(t.data) + size_t(row) * t.cols,
+                size_t(t.cols) * 4);
+    return true;
+  }
+  if (t.type == ORC_F16) {
+    const auto* h = static_cast<const uint16_t*>(t.data) + size_t(row) * t.cols;
+    for (uint32_t i = 0; i < t.cols; ++i)
+      out[i] = HalfToFloat(h[i]);
+    return true;
+  }
+  if (t.type == ORC_Q8_0 && t.cols % 32 == 0) {
+    const auto* blocks =
+        static_cast<const Q8Block*>(t.data) + size_t(row) * (t.cols / 32);
+    for (uint32_t b = 0; b < t.cols / 32; ++b) {
+      const float d = HalfToFloat(blocks[b].d);
+      for (int j = 0; j < 32; ++j)
+        out[b * 32 + j] = d * float(blocks[b].q[j]);
+    }
+    return true;
+  }
+  return false;
+}
+
+// reference.cpp:9-19.
+bool Mat(const orc_tensor& t, const float* x, float* y) {
+  std::vector<float> row(t.cols);
+  for (uint32_t r = 0; r < t.rows; ++r) {
+    if (!DecodeRow(t, r, row.data()))
+      return false;
+    float sum = 0;
+    for (uint32_t k = 0; k < t.cols; ++k)
+      sum += row[k] * x[k];
+    y[r] = sum;
+  }
+  return true;
+}
+
+// reference.cpp:20-28.
+void Norm(float* x, size_t n, const float* weight, float eps) {
+  float sum = 0;
+  for (size_t i = 0; i < n; ++i)
+    sum += x[i] * x[i];
+  const float scale = 1 / std::sqrt(sum / float(n) + eps);
+  for (size_t i = 0; i < n; ++i)
+    x[i] = x[i] * scale * weight[i];
+}
+
+// reference.cpp:29-43: pairs (i, i + D/2), angle = position * theta^(-2i/D),
+// divided by the factor on global layers.
+void Rope(float* x, size_t count, uint32_t D, uint32_t position, float theta,
+          bool sliding, const float* factors) {
+  for (size_t h = 0; h < count; ++h) {
+    float* head = x + h * D;
+    for (uint32_t i = 0; i < D / 2; ++i) {
+      float angle = float(position) * std::pow(theta, -2.0F * float(i) / float(D));
+      if (!sliding)
+        angle /= factors[i];
+      const float a = head[i], b = head[i + D / 2];
+      head[i] = a * std::cos(angle) - b * std::sin(angle);
+      head[i + D / 2] = b * std::cos(angle) + a * std::sin(angle);
+    }
+  }
+}
+
+// reference.cpp:85-101.
+void ConvStep(const float* p, const float* taps, float* history, float* y,
+              uint32_t H, uint32_t L) {
+  for (uint32_t ch = 0; ch < H; ++ch) {
+    float* own = history + size_t(ch) * (L - 1);
+    const float bx = p[ch] * p[2 * H + ch];
+    float sum = 0;
+    for (uint32_t t = 0; t < L; ++t)
+      sum += taps[ch * L + t] * (t + 1 == L ? bx : own[t]);
+    for (uint32_t t = 1; t < L - 1; ++t)
+      own[t - 1] = own[t];
+    if (L > 1)
+      own[L - 2] = bx;
+    y[ch] = sum * p[H + ch];
+  }
+}
+
+// reference.cpp:109-144 (the read half): gated GQA of one query row over
+// ring keys [first, position].
+void AttentionRead(const float* q, const float* gate, const float* ck,
+                   const float* cv, uint32_t heads, uint32_t kv_heads,
+                   uint32_t D, uint32_t position, uint32_t capacity,
+                   uint32_t window, float* out) {
+  const size_t stride = size_t(kv_heads) * D;
+  const uint32_t first =
+      window && position + 1 > window ? position + 1 - window : 0;
+  std::vector<float> scores(position + 1 - first);
+  for (uint32_t h = 0; h < heads; ++h) {
+    const uint32_t kh = h / (heads / kv_heads);
+    float max = -std::numeric_limits<float>::infinity();
+    for (uint32_t t = first; t <= position; ++t) {
+      float score = 0;
+      for (uint32_t d = 0; d < D; ++d)
+        score += q[h * D + d] * ck[(t % capacity) * stride + kh * D + d];
+      scores[t - first] = score / std::sqrt(float(D));
+      max = std::max(max, scores[t - first]);
+    }
+    float den = 0;
+    for (auto& score : scores) {
+      score = std::exp(score - max);
+      den += score;
+    }
+    for (uint32_t d = 0; d < D; ++d) {
+      float sum = 0;
+      for (uint32_t t = first; t <= position; ++t)
+        sum += (scores[t - first] / den) *
+               cv[(t % capacity) * stride + kh * D + d];
+      out[h * D + d] = sum / (1 + std::exp(-gate[h]));
+    }
+  }
+}
+
+}  // namespace
+
+struct orc_model {
+  orc_config config{};
+  std::vector<uint32_t> kv_heads;
+  std::vector<uint8_t> layer_type;
+  std::vector<orc_tensor> tensors;
+  const orc_tensor& global(int i) const { return tensors[i]; }
+  const orc_tensor& layer(uint32_t l, int i) const {
+    return tensors[ORC_GLOBALS + size_t(l) * ORC_PER_LAYER + i];
+  }
+};
+
+struct orc_session {
+  orc_model* model{};
+  uint32_t context{}, position{};
+  bool f16{};
+  struct State {
+    std::vector<float> conv, k, v;
+    uint32_t capacity{};
+  };
+  std::vector<State> states;
+};
+
+extern "C" {
+
+float orc_half_to_float(uint16_t h) { return HalfToFloat(h); }
+uint16_t orc_float_to_half(float f) { return FloatToHalf(f); }
+void orc_halves_to_floats(const uint16_t* h, float* f, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    f[i] = HalfToFloat(h[i]);
+}
+void orc_floats_to_halves(const float* f, uint16_t* h, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    h[i] = FloatToHalf(f[i]);
+}
+
+int orc_decode_row(const orc_tensor* t, uint32_t row, float* out) {
+  return DecodeRow(*t, row, out) ? 0 : -1;
+}
+int orc_mat(const orc_tensor* t, const float* x, float* y) {
+  return Mat(*t, x, y) ? 0 : -1;
+}
+int orc_mat_batch(const orc_tensor* t, const float* x, float* y,
+                  uint32_t batch) {
+  for (uint32_t b = 0; b < batch; ++b)
+    if (!Mat(*t, x + size_t(b) * t->cols, y + size_t(b) * t->rows))
+      return -1;
+  return 0;
+}
+void orc_norm(float* x, size_t n, const float* weight, float eps) {
+  Norm(x, n, weight, eps);
+}
+void orc_rope(float* x, size_t count, uint32_t dim, uint32_t position,
+              float theta, int sliding, const float* factors) {
+  Rope(x, count, dim, position, theta, sliding != 0, factors);
+}
+void orc_conv_step(const float* p, const float* taps, float* history, float* y,
+                   uint32_t hidden, uint32_t width) {
+  ConvStep(p, taps, history, y, hidden, width);
+}
+void orc_attention_read(const float* q, const float* gate, const float* ck,
+                        const float* cv, uint32_t heads, uint32_t kv_heads,
+                        uint32_t dim, uint32_t position, uint32_t capacity,
+                        uint32_t window, float* out) {
+  AttentionRead(q, gate, ck, cv, heads, kv_heads, dim, position, capacity,
+                window, out);
+}
+// reference.cpp:102-146.
+void orc_attention_step(float* q, float* k, const float* v, const float* gate,
+                        const float* q_norm, const float* k_norm,
+                        const float* factors, float* ck, float* cv,
+                        uint32_t heads, uint32_t kv_heads, uint32_t D,
+                        uint32_t position, uint32_t capacity, uint32_t window,
+                        float theta, int sliding, float eps, int f16,
+                        float* out) {
+  for (uint32_t h = 0; h < heads; ++h)
+    Norm(q + size_t(h) * D, D, q_norm, eps);
+  for (uint32_t h = 0; h < kv_heads; ++h)
+    Norm(k + size_t(h) * D, D, k_norm, eps);
+  Rope(q, heads, D, position, theta, sliding != 0, factors);
+  Rope(k, kv_heads, D, position, theta, sliding != 0, factors);
+  const size_t stride = size_t(kv_heads) * D;
+  const size_t slot = position % capacity;
+  for (size_t i = 0; i < stride; ++i) {
+    ck[slot * stride + i] = f16 ? HalfToFloat(FloatToHalf(k[i])) : k[i];
+    cv[slot * stride + i] = f16 ? HalfToFloat(FloatToHalf(v[i])) : v[i];
+  }
+  AttentionRead(q, gate, ck, cv, heads, kv_heads, D, position, capacity,
+                sliding ? window : 0, out);
+}
+void orc_swiglu(float* gate, const float* up, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    gate[i] = (gate[i] / (1 + std::exp(-gate[i]))) * up[i];
+}
+uint32_t orc_argmax(const float* x, size_t n) {
+  return uint32_t(std::max_element(x, x + n) - x);
+}
+
+orc_model* orc_model_create(const orc_config* config, const orc_tensor* tensors,
+                            size_t count) {
+  if (!config || count != ORC_GLOBALS + size_t(config->n_layers) * ORC_PER_LAYER)
+    return nullptr;
+  auto* m = new (std::nothrow) orc_model;
+  if (!m)
+    return nullptr;
+  m->config = *config;
+  m->kv_heads.assign(config->kv_heads, config->kv_heads + config->n_layers);
+  m->layer_type.assign(config->layer_type,
+                       config->layer_type + config->n_layers);
+  m->config.kv_heads = m->kv_heads.data();
+  m->config.layer_type = m->layer_type.data();
+  m->tensors.assign(tensors, tensors + count);
+  return m;
+}
+void orc_model_destroy(orc_model* m) { delete m; }
+
+orc_session* orc_session_create(orc_model* m, uint32_t context, int f16) {
+  if (!m || !context || context > m->config.context)
+    return nullptr;
+  auto* s = new (std::nothrow) orc_session;
+  if (!s)
+    return nullptr;
+  const auto& c = m->config;
+  s->model = m;
+  s->context = context;
+  s->f16 = f16 != 0;
+  s->states.resize(c.n_layers);
+  for (uint32_t i = 0; i < c.n_layers; ++i) {
+    auto& st = s->states[i];
+    if (c.layer_type[i] == ORC_CONV) {
+      st.conv.assign(size_t(c.hidden) * (c.conv_width - 1), 0.0F);
+    } else {
+      // reference.cpp:53-62: sliding rings hold min(context, window) rows.
+      st.capacity = c.layer_type[i] == ORC_SLIDING ? std::min(context, c.window)
+                                                   : context;
+      st.k.assign(size_t(st.capacity) * c.kv_heads[i] * c.head_dim, 0.0F);
+      st.v.assign(st.k.size(), 0.0F);
+    }
+  }
+  return s;
+}
+void orc_session_destroy(orc_session* s) { delete s; }
+void orc_session_reset(orc_session* s) {
+  s->position = 0;
+  for (auto& st : s->states) {
+    std::fill(st.conv.begin(), st.conv.end(), 0.0F);
+    std::fill(st.k.begin(), st.k.end(), 0.0F);
+    std::fill(st.v.begin(), st.v.end(), 0.0F);
+  }
+}
+uint32_t orc_session_position(const orc_session* s) { return s->position; }
+void orc_session_set_position(orc_session* s, uint32_t position) {
+  s->position = position;
+}
+uint32_t orc_session_capacity(const orc_session* s, uint32_t layer) {
+  return s->states[layer].capacity;
+}
+float* orc_session_conv(orc_session* s, uint32_t layer) {
+  return s->states[layer].conv.empty() ? nullptr : s->states[layer].conv.data();
+}
+float* orc_session_k(orc_session* s, uint32_t layer) {
+  return s->states[layer].k.empty() ? nullptr : s->states[layer].k.data();
+}
+float* orc_session_v(orc_session* s, uint32_t layer) {
+  return s->states[layer].v.empty() ? nullptr : s->states[layer].v.data();
+}
+
+// reference.cpp:72-168.
+int orc_session_step(orc_session* s, uint32_t token, float* logits,
+                     float* hidden) {
+  const orc_model& m = *s->model;
+  const auto& c = m.config;
+  if (token >= c.vocab || s->position >= s->context)
+    return -1;
+  const uint32_t H = c.hidden, D = c.head_dim;
+  std::vector<float> x(H), z(H), out(H);
+  DecodeRow(m.global(ORC_EMBEDDING), token, x.data());
+  for (uint32_t il = 0; il < c.n_layers; ++il) {
+    auto& st = s->states[il];
+    z = x;
+    Norm(z.data(), H, static_cast<const float*>(m.layer(il, ORC_L_NORM).data),
+         c.eps);
+    if (c.layer_type[il] == ORC_CONV) {
+      std::vector<float> p(3 * H), conv(H);
+      Mat(m.layer(il, ORC_L_IN_PROJ), z.data(), p.data());
+      ConvStep(p.data(),
+               static_cast<const float*>(m.layer(il, ORC_L_CONV).data),
+               st.conv.data(), conv.data(), H, c.conv_width);
+      Mat(m.layer(il, ORC_L_OUT_PROJ), conv.data(), out.data());
+    } else {
+      const uint32_t kv = c.kv_heads[il];
+      std::vector<float> q(size_t(c.heads) * D), k(size_t(kv) * D),
+          v(size_t(kv) * D), gate(c.heads), a(size_t(c.heads) * D);
+      Mat(m.layer(il, ORC_L_Q), z.data(), q.data());
+      Mat(m.layer(il, ORC_L_K), z.data(), k.data());
+      Mat(m.layer(il, ORC_L_V), z.data(), v.data());
+      Mat(m.layer(il, ORC_L_ATTN_GATE), z.data(), gate.data());
+      const bool sliding = c.layer_type[il] == ORC_SLIDING;
+      orc_attention_step(
+          q.data(), k.data(), v.data(), gate.data(),
+          static_cast<const float*>(m.layer(il, ORC_L_Q_NORM).data),
+          static_cast<const float*>(m.layer(il, ORC_L_K_NORM).data),
+          static_cast<const float*>(m.global(ORC_ROPE_FREQS).data),
+          st.k.data(), st.v.data(), c.heads, kv, D, s->position, st.capacity,
+          c.window, sliding ? c.theta_swa : c.theta, sliding, c.eps, s->f16,
+          a.data());
+      Mat(m.layer(il, ORC_L_ATTN_OUT), a.data(), out.data());
+    }
+    const auto& post = m.layer(il, ORC_L_POST_NORM);
+    if (post.data)
+      Norm(out.data(), H, static_cast<const float*>(post.data), c.eps);
+    for (uint32_t i = 0; i < H; ++i)
+      x[i] += out[i];
+    z = x;
+    Norm(z.data(), H,
+         static_cast<const float*>(m.layer(il, ORC_L_FFN_NORM).data), c.eps);
+    std::vector<float> gate(c.intermediate), up(c.intermediate);
+    Mat(m.layer(il, ORC_L_GATE), z.data(), gate.data());
+    Mat(m.layer(il, ORC_L_UP), z.data(), up.data());
+    for (uint32_t i = 0; i < c.intermediate; ++i)
+      gate[i] = (gate[i] / (1 + std::exp(-gate[i]))) * up[i];
+    Mat(m.layer(il, ORC_L_DOWN), gate.data(), out.data());
+    const auto& post_ffn = m.layer(il, ORC_L_POST_FFN_NORM);
+    if (post_ffn.data)
+      Norm(out.data(), H, static_cast<const float*>(post_ffn.data), c.eps);
+    for (uint32_t i = 0; i < H; ++i)
+      x[i] += out[i];
+  }
+  if (logits) {
+    Norm(x.data(), H, static_cast<const float*>(m.global(ORC_OUTPUT_NORM).data),
+         c.eps);
+    if (hidden)
+      std::copy(x.begin(), x.end(), hidden);
+    Mat(m.global(ORC_OUTPUT), x.data(), logits);
+  }
+  ++s->position;
+  return 0;
+}
+
+}  // extern "C"

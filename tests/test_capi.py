@@ -1,0 +1,175 @@
+"""CPU checks of the C-ABI library: it loads, exports every declared entry
+point, and its host-side logic (tile packing, attention work lists,
+synthetic inputs, input validation) follows its integer closed forms. No
+kernel runs here."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+import lfm3amd as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lfm3_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lfm3_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.lib()
+    names = declared_functions()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the binding covers all of them
+    assert set(names) <= set(L._SIGS)
+
+
+def test_synthetic_inputs_are_deterministic():
+    a = L.normal(L.SEED, "x", 300000)
+    b = L.normal(L.SEED, "x", 300000)
+    c = L.normal(L.SEED, "y", 300000)
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    assert abs(a.mean()) < 0.01 and abs(a.std() - 1) < 0.01
+    # element i does not depend on how many were drawn
+    assert np.array_equal(L.normal(L.SEED, "x", 1000), a[:1000])
+    w = L.q8(L.SEED, "w", 64, 256)
+    blocks = w.reshape(-1, 34)
+    q = blocks[:, 2:].view(np.int8)
+    assert q.min() >= -127 and q.max() <= 127 and len(np.unique(q)) > 250
+    d = blocks[:, :2].copy().view(np.float16).astype(np.float64)
+    assert (d >= 0).all() and abs(np.mean(d) * 127 - 0.02 * np.sqrt(2 / np.pi)) < 2e-3
+    u = L.uniform_u32(L.SEED, "u", 100000, 1, 4096)
+    assert u.min() >= 1 and u.max() <= 4096 and abs(u.mean() - 2048.5) < 30
+
+
+def unpack_tiles(codes, scales, rows, cols, tile_offset=0, tile_stride=1, tiles=None):
+    """Inverse of the documented tile layout: lane 16 g + n of tile
+    (r / 16, chunk) holds row n, bytes [0,8) block 2c elements 8g.., [8,16)
+    block 2c + 1 elements 8g..; scales [row][block] per tile."""
+    nchunks = (cols + 63) // 64
+    q = np.zeros((rows, nchunks * 64), np.int8)
+    d = np.zeros((rows, nchunks * 2), np.uint16)
+    t = codes.reshape(-1, nchunks, 4, 16, 16)      # tile, chunk, g, n, byte
+    s = scales.view(np.uint16).reshape(-1, nchunks, 16, 2)
+    for r in range(rows):
+        tile = tile_offset + (r // 16) * tile_stride
+        n = r % 16
+        for c in range(nchunks):
+            for g in range(4):
+                q[r, c * 64 + 8 * g:c * 64 + 8 * g + 8] = t[tile, c, g, n, :8].view(np.int8)
+                q[r, c * 64 + 32 + 8 * g:c * 64 + 32 + 8 * g + 8] = t[tile, c, g, n, 8:].view(np.int8)
+            d[r, 2 * c:2 * c + 2] = s[tile, c, n]
+    return q[:, :cols], d[:, :cols // 32], q[:, cols:], d[:, cols // 32:]
+
+
+@pytest.mark.parametrize("rows,cols", [(37, 96), (16, 64), (48, 2048), (5, 32)])
+def test_host_pack_round_trip(rows, cols):
+    src = L.q8(3, f"p{rows}x{cols}", rows, cols)
+    cb, sb = C.c_size_t(), C.c_size_t()
+    L.lib().lfm3_q8_tiled_bytes(rows, cols, C.byref(cb), C.byref(sb))
+    tiles = (rows + 15) // 16
+    nchunks = (cols + 63) // 64
+    assert cb.value == tiles * nchunks * 1024 and sb.value == tiles * nchunks * 64
+    codes = np.full(cb.value, 0x5a, np.uint8)
+    scales = np.full(sb.value, 0x5a, np.uint8)
+    L.check(L.lib().lfm3_q8_pack_host(L.ptr(src), rows, cols, L.ptr(codes), L.ptr(scales), 0, 1))
+    q, d, q_pad, d_pad = unpack_tiles(codes, scales, rows, cols)
+    blocks = src.reshape(rows, cols // 32, 34)
+    assert np.array_equal(q, blocks[:, :, 2:].view(np.int8).reshape(rows, cols))
+    assert np.array_equal(d, blocks[:, :, :2].copy().view(np.uint16).reshape(rows, cols // 32))
+    assert not q_pad.any() and not d_pad.any()
+    # padding rows of the last tile are zero too
+    t = codes.reshape(tiles, nchunks, 4, 16, 16)
+    if rows % 16:
+        assert not t[-1, :, :, rows % 16:, :].any()
+
+
+def test_host_pack_interleave_and_concat():
+    rows, cols = 32, 128
+    a = L.q8(4, "a", rows, cols)
+    b = L.q8(4, "b", rows, cols)
+    nchunks = 2
+    codes = np.zeros(4 * nchunks * 1024, np.uint8)
+    scales = np.zeros(4 * nchunks * 64, np.uint8)
+    L.check(L.lib().lfm3_q8_pack_host(L.ptr(a), rows, cols, L.ptr(codes), L.ptr(scales), 0, 2))
+    L.check(L.lib().lfm3_q8_pack_host(L.ptr(b), rows, cols, L.ptr(codes), L.ptr(scales), 1, 2))
+    qa, _, _, _ = unpack_tiles(codes, scales, rows, cols, 0, 2)
+    qb, _, _, _ = unpack_tiles(codes, scales, rows, cols, 1, 2)
+    assert np.array_equal(qa, a.reshape(rows, -1, 34)[:, :, 2:].view(np.int8).reshape(rows, cols))
+    assert np.array_equal(qb, b.reshape(rows, -1, 34)[:, :, 2:].view(np.int8).reshape(rows, cols))
+
+
+def plan(positions, window, capacity=4096):
+    pos = np.ascontiguousarray(positions, np.uint32)
+    items = (L.AttentionItem * capacity)()
+    n = L.check(L.lib().lfm3_attention_plan(L.ptr(pos), len(pos), window, items, capacity))
+    return [items[i] for i in range(n)]
+
+
+@pytest.mark.parametrize("window", [0, 256])
+def test_attention_plan_covers_each_row_exactly(window):
+    positions = L.uniform_u32(L.SEED, "ctx", 8, 1, 4096) - 1
+    positions = np.concatenate([positions, [0, 255, 256, 257, 511, 512]]).astype(np.uint32)
+    items = plan(positions, window)
+    by_row = {}
+    for idx, it in enumerate(items):
+        by_row.setdefault(it.row, []).append((idx, it))
+    assert sorted(by_row) == list(range(len(positions)))
+    for r, lst in by_row.items():
+        p = int(positions[r])
+        first = max(0, p + 1 - window) if window else 0
+        spans = [(it.key_begin, it.key_end) for _, it in lst]
+        assert spans[0][0] == first and spans[-1][1] == p + 1
+        for (b0, e0), (b1, e1) in zip(spans, spans[1:]):
+            assert e0 == b1
+        assert all(0 < e - b <= 256 for b, e in spans)
+        assert all(it.parts == len(lst) and it.first_item == lst[0][0] for _, it in lst)
+        if window:
+            assert len(lst) == 1
+
+
+def test_attention_plan_refuses_overflow():
+    with pytest.raises(L.LFM3Error):
+        plan([10000], 0, capacity=8)
+
+
+def test_model_load_rejects_bad_inputs_before_device_work():
+    dims = L.Dims(hidden=128, intermediate=192, vocab=300, context=64, heads=4, head_dim=64,
+                  kv_heads=2, window=8, pattern="CSG")
+    w = L.synth_weights(dims, seed=1)
+    bad = L.Dims(**{**dims.__dict__, "head_dim": 96})
+    with pytest.raises(L.LFM3Error) as e:
+        L.Model(L.Weights(bad, w.globals, w.layers))
+    assert e.value.status == L.E_INVALID
+    # a Q8 tensor with the wrong row count
+    layers = [list(t) for t in w.layers]
+    data, typ, cols, rows = layers[0][8]
+    layers[0][8] = (data, typ, cols, rows - 16)
+    with pytest.raises(L.LFM3Error) as e:
+        L.Model(L.Weights(dims, w.globals, layers))
+    assert e.value.status == L.E_INVALID and "in_proj" in str(e.value)
+    # a non-positive RoPE factor (weights.cpp:59-63)
+    g = list(w.globals)
+    g[3] = (np.zeros(32, np.float32), L.TYPE_F32, 32, 1)
+    with pytest.raises(L.LFM3Error) as e:
+        L.Model(L.Weights(dims, g, w.layers))
+    assert "RoPE" in str(e.value)
+
+
+def test_kernel_entry_points_refuse_unsupported_shapes():
+    lib = L.lib()
+    # Q8_0 needs cols % 32 == 0 and 1..8 rows; attention needs dim 64/128.
+    assert lib.lfm3_q8_gemv(1, 1, 16, 40, 16, 40, 1, 16, 1, None, 0, None) == L.E_INVALID
+    assert lib.lfm3_q8_gemv(1, 1, 16, 64, 16, 64, 1, 16, 9, None, 0, None) == L.E_INVALID
+    assert lib.lfm3_decode_attention_ragged(1, 8, 1, 8, 1, 1, 1, 1, 1, 1, 8, 1, 6, 2, 96,
+                                            1, 1 << 20, None) == L.E_INVALID
+    assert lib.lfm3_decode_attention_ragged(1, 8, 1, 8, 1, 1, 1, 1, 1, 1, 8, 1, 6, 2, 128,
+                                            1, 1 << 20, None) == L.E_INVALID  # group 3
+    assert b"attention" in lib.lfm3_last_error()

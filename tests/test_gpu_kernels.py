@@ -1,0 +1,332 @@
+"""Kernel parity on the GPU: every HIP entry point against the CPU oracle on
+the same seeded inputs, through the C-ABI.
+
+Gates: the reference's own (ops_test.cpp: projection 1e-4 vs FP64, conv
+1e-7 with exact history, decode attention 2e-6 vs FP64) where its vectors
+apply, and the BASELINE gates elsewhere (1e-3 relative / 1e-4 absolute for
+FP32 GEMV and attention outputs; bit-exact for indexing, ring slots and
+greedy ids)."""
+import numpy as np
+import pytest
+
+import lfm3amd as L
+import oracle as O
+from gpu_util import DeviceMatrix, gemv, pointer_table, within
+from test_oracle import attention_fp64, data, formula_q8
+
+pytestmark = pytest.mark.gpu
+SEED = L.SEED
+
+
+# -------------------------------------------------------------------- GEMV
+
+@pytest.mark.parametrize("B", [1, 2, 3, 8])
+def test_gemv_reference_projection_vectors(B):
+    """ops_test.cpp:46-89 (M = 37, K = 2048, formula weights, FP32 rows)."""
+    M, K = 37, 2048
+    w = formula_q8(M, K)
+    x = data(B * K, 0.07).reshape(B, K)
+    y = gemv(DeviceMatrix(w, M, K), x)
+    want64 = x.astype(np.float64) @ L.q8_dequant(w, M, K).T
+    assert np.max(np.abs(y - want64)) < 1e-4
+    ok, err = within(y, O.mat(O.q8_tensor(w, M, K), x))
+    assert ok, err
+
+
+@pytest.mark.parametrize("B", [1, 2, 4, 8])
+def test_gemv_decode_shape_8192x2048(B):
+    """The config-1 matrix: W 8192 x 2048 Q8_0, X ~ N(0, 1) rows."""
+    M, K = 8192, 2048
+    w = L.q8(SEED, "gemv.W", M, K)
+    x = L.normal(SEED, f"gemv.X{B}", B * K).reshape(B, K)
+    y = gemv(DeviceMatrix(w, M, K), x)
+    ok, err = within(y, O.mat(O.q8_tensor(w, M, K), x))
+    assert ok, err
+    want64 = x.astype(np.float64) @ L.q8_dequant(w, M, K).T
+    assert np.max(np.abs(y - want64)) < 2e-5
+
+
+@pytest.mark.parametrize("M,K,B", [(2048, 7680, 8), (128000, 2048, 4), (16, 2048, 5),
+                                   (3088, 2048, 8), (48, 96, 7), (512, 64, 8), (64, 64, 1), (6144, 2048, 8)])
+def test_gemv_model_shapes(M, K, B):
+    w = L.q8(SEED, f"shape.{M}x{K}", M, K)
+    x = (3.0 * L.normal(SEED, f"shape.x.{M}x{K}", B * K)).reshape(B, K)
+    y = gemv(DeviceMatrix(w, M, K), x)
+    ok, err = within(y, O.mat(O.q8_tensor(w, M, K), x))
+    assert ok, err
+
+
+def test_gemv_rows_are_independent_and_ragged_scales():
+    """Rows of very different magnitude share a launch; each row's result
+    equals its single-row result bit for bit."""
+    M, K = 2048, 2048
+    w = L.q8(SEED, "indep", M, K)
+    x = L.normal(SEED, "indep.x", 8 * K).reshape(8, K)
+    x *= np.array([1e-3, 1, 1e3, 7, 0.5, 1e-6, 30, 2], np.float32)[:, None]
+    m = DeviceMatrix(w, M, K)
+    y = gemv(m, x)
+    for b in (0, 2, 5):
+        assert np.array_equal(gemv(m, x[b:b + 1])[0], y[b])
+
+
+@pytest.mark.parametrize("F,K,B", [(7680, 2048, 8), (192, 128, 3), (8192, 2048, 1)])
+def test_gemv_swiglu(F, K, B):
+    g = L.q8(SEED, f"sw.g{F}", F, K)
+    u = L.q8(SEED, f"sw.u{F}", F, K)
+    x = L.normal(SEED, f"sw.x{F}", B * K).reshape(B, K)
+    y = gemv(DeviceMatrix(g, F, K, interleave_with=u), x, swiglu=True)
+    want = np.stack([O.swiglu(O.mat(O.q8_tensor(g, F, K), x[b]), O.mat(O.q8_tensor(u, F, K), x[b]))
+                     for b in range(B)])
+    ok, err = within(y, want)
+    assert ok, err
+
+
+def test_device_pack_matches_host_pack():
+    import ctypes as C
+    from gpu_util import packed
+    for rows, cols in ((37, 96), (512, 2048), (16, 7680)):
+        src = L.q8(SEED, f"dp{rows}", rows, cols)
+        codes, scales = packed(src, rows, cols)
+        dsrc = L.DeviceBuffer.of(src)
+        dc, ds = L.DeviceBuffer(codes.nbytes), L.DeviceBuffer(scales.nbytes)
+        L.check(L.lib().lfm3_q8_pack_device(dsrc.addr, rows, cols, dc.addr, ds.addr, 0, 1, None))
+        L.synchronize()
+        assert np.array_equal(dc.download(np.uint8, codes.size), codes)
+        assert np.array_equal(ds.download(np.uint8, scales.size), scales)
+
+
+def test_embed_is_exact_row_decode():
+    V, H = 1000, 2048
+    w = L.q8(SEED, "emb", V, H)
+    m = DeviceMatrix(w, V, H)
+    toks = np.array([0, 999, 17, 500, 17, 3], np.uint32)
+    dt = L.DeviceBuffer.of(toks)
+    out = L.DeviceBuffer(len(toks) * H * 4)
+    L.check(L.lib().lfm3_embed(m.codes.addr, m.scales.addr, V, H, dt.addr, len(toks), out.addr, None))
+    L.synchronize()
+    got = out.download(np.float32, len(toks) * H).reshape(len(toks), H)
+    t = O.q8_tensor(w, V, H)
+    for i, tok in enumerate(toks):
+        assert np.array_equal(got[i], O.decode_row(t, int(tok)))
+
+
+# ------------------------------------------------------------------- norms
+
+@pytest.mark.parametrize("H", [2048, 256, 4096])
+def test_residual_norm(H):
+    n = 8
+    x = L.normal(SEED, f"rn.x{H}", n * H, 0, 5).reshape(n, H)
+    br = L.normal(SEED, f"rn.b{H}", n * H, 0, 2).reshape(n, H)
+    post = L.normal(SEED, f"rn.p{H}", H, 1, 0.02)
+    wn = L.normal(SEED, f"rn.w{H}", H, 1, 0.02)
+    dx, db = L.DeviceBuffer.of(x), L.DeviceBuffer.of(br)
+    dp, dw = L.DeviceBuffer.of(post), L.DeviceBuffer.of(wn)
+    dz = L.DeviceBuffer(n * H * 4)
+    L.check(L.lib().lfm3_residual_norm(db.addr, dp.addr, dx.addr, dw.addr, dz.addr, n, H, 1e-5, None))
+    L.synchronize()
+    gx = dx.download(np.float32, n * H).reshape(n, H)
+    gz = dz.download(np.float32, n * H).reshape(n, H)
+    for r in range(n):
+        wx = x[r] + O.norm(br[r], post, 1e-5)
+        np.testing.assert_allclose(gx[r], wx, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(gz[r], O.norm(wx, wn, 1e-5), rtol=1e-5, atol=1e-6)
+
+
+# --------------------------------------------------------------------- conv
+
+def test_conv_step_ragged_bit_exact():
+    """Per-row histories through a pointer table (rows in scrambled session
+    order): outputs and histories equal the oracle's bit for bit given the
+    same projection rows."""
+    H, Lw, n = 2048, 7, 8
+    order = [3, 0, 7, 5, 1, 6, 2, 4]
+    ldp = 3 * H + 16
+    p = L.normal(SEED, "conv.p", n * ldp).reshape(n, ldp)
+    taps = L.normal(SEED, "conv.taps", H * Lw, 0, 0.1)
+    hists = [L.normal(SEED, f"conv.h{s}", H * (Lw - 1)) for s in range(8)]
+    dh = [L.DeviceBuffer.of(h) for h in hists]
+    table = pointer_table([dh[order[r]].addr for r in range(n)])
+    dp, dt = L.DeviceBuffer.of(p), L.DeviceBuffer.of(taps)
+    dy = L.DeviceBuffer(n * H * 4)
+    L.check(L.lib().lfm3_conv_step_ragged(dp.addr, ldp, dt.addr, table.addr, dy.addr, H, n, H, Lw, None))
+    L.synchronize()
+    y = dy.download(np.float32, n * H).reshape(n, H)
+    for r in range(n):
+        want_y, want_h = O.conv_step(p[r, :3 * H], taps, hists[order[r]], H, Lw)
+        assert np.array_equal(y[r], want_y)
+        assert np.array_equal(dh[order[r]].download(np.float32, H * (Lw - 1)), want_h)
+
+
+# --------------------------------------------------- heads and attention
+
+def ragged_case(heads, kv, D, window, ctx_hi=4096, n=8, tag="a", global_cap=4096):
+    rng = np.random.default_rng(abs(hash((heads, kv, D, window, tag))) % 2**32)
+    ctx = L.uniform_u32(SEED, f"att.ctx.{tag}", n, 1, ctx_hi)
+    positions = (ctx - 1).astype(np.uint32)
+    cap = window if window else global_cap
+    stride = kv * D
+    order = list(rng.permutation(n))
+    return ctx, positions, cap, stride, order
+
+
+@pytest.mark.parametrize("heads,kv,D", [(32, 8, 64), (16, 4, 128), (16, 8, 128), (16, 2, 128)])
+@pytest.mark.parametrize("window", [0, 256])
+def test_heads_and_attention_ragged(heads, kv, D, window):
+    """Config-2 shape: 8 sessions, contexts U[1, 4096], Q/K RMSNorm, paired
+    RoPE at theta 1e6, F16 ring store, gated GQA; sliding (256) and global."""
+    n = 8
+    ctx, positions, cap, stride, order = ragged_case(heads, kv, D, window)
+    theta = 1e6
+    factors = np.ones(D // 2, np.float32)
+    ld = (heads + 2 * kv) * D + heads + 4
+    qkv = L.normal(SEED, f"att.qkv.{heads}.{D}.{window}", n * ld).reshape(n, ld)
+    q_off, k_off, v_off, g_off = 0, heads * D, (heads + kv) * D, (heads + 2 * kv) * D
+    qn = L.normal(SEED, "att.qn", D, 1, 0.02)
+    kn = L.normal(SEED, "att.kn", D, 1, 0.02)
+    rings_k = [L.half_normal(SEED, f"att.k{s}.{D}", cap * stride) for s in range(n)]
+    rings_v = [L.half_normal(SEED, f"att.v{s}.{D}", cap * stride) for s in range(n)]
+    dk = [L.DeviceBuffer.of(r) for r in rings_k]
+    dv = [L.DeviceBuffer.of(r) for r in rings_v]
+    # row r belongs to session order[r]; its position is that session's
+    pos_rows = np.array([positions[order[r]] for r in range(n)], np.uint32)
+    tk = pointer_table([dk[order[r]].addr for r in range(n)])
+    tv = pointer_table([dv[order[r]].addr for r in range(n)])
+    caps = L.DeviceBuffer.of(np.full(n, cap, np.uint32))
+    dpos = L.DeviceBuffer.of(pos_rows)
+    i = np.arange(D // 2, dtype=np.float32)
+    from test_oracle import powf
+    freq = powf(theta, np.float32(-2.0) * i / np.float32(D))
+    dfreq, dfac = L.DeviceBuffer.of(freq), L.DeviceBuffer.of(factors)
+    dq = L.DeviceBuffer.of(qkv)
+    dqn, dkn = L.DeviceBuffer.of(qn), L.DeviceBuffer.of(kn)
+    L.check(L.lib().lfm3_decode_heads_ragged(
+        dq.addr + 4 * q_off, dq.addr + 4 * k_off, dq.addr + 4 * v_off, ld, dqn.addr, dkn.addr,
+        dfreq.addr, 0 if window else dfac.addr, tk.addr, tv.addr, dpos.addr, caps.addr, n,
+        heads, kv, D, 1e-5, None))
+    cap_items = 4096
+    items = (L.AttentionItem * cap_items)()
+    count = L.check(L.lib().lfm3_attention_plan(L.ptr(pos_rows), n, window, items, cap_items))
+    ditems = L.DeviceBuffer(count * C_ITEM)
+    L.hip_check(L.hip().hipMemcpy(ditems.addr, L.C.addressof(items), count * C_ITEM, L.H2D))
+    ws_bytes = L.lib().lfm3_attention_workspace_bytes(count, n, heads, kv, D)
+    ws = L.DeviceBuffer(ws_bytes)
+    dout = L.DeviceBuffer(n * heads * D * 4)
+    for repeat in range(2):  # the second call reuses the workspace tickets
+        L.check(L.lib().lfm3_decode_attention_ragged(
+            dq.addr + 4 * q_off, ld, dq.addr + 4 * g_off, ld, tk.addr, tv.addr, caps.addr,
+            ditems.addr, count, dout.addr, heads * D, n, heads, kv, D, ws.addr, ws_bytes, None))
+        L.synchronize()
+        out = dout.download(np.float32, n * heads * D).reshape(n, heads * D)
+        if repeat == 0:
+            first = out
+    assert np.array_equal(first, out)
+    for r in range(n):
+        s = order[r]
+        p = int(pos_rows[r])
+        ck = O.half_to_float(rings_k[s])
+        cv = O.half_to_float(rings_v[s])
+        want, qr, kr = O.attention_step(qkv[r, q_off:k_off], qkv[r, k_off:v_off],
+                                        qkv[r, v_off:g_off], qkv[r, g_off:g_off + heads], qn, kn,
+                                        None if window else factors, ck, cv, heads, kv, D, p, cap,
+                                        window, theta, bool(window), 1e-5, True)
+        ok, err = within(out[r], want)
+        assert ok, (r, err)
+        # ring: only slot p % cap changed; V bits exact; K within one ulp
+        gk = dk[s].download(np.uint16, cap * stride).reshape(cap, stride)
+        gv = dv[s].download(np.uint16, cap * stride).reshape(cap, stride)
+        slot = p % cap
+        keep = np.ones(cap, bool)
+        keep[slot] = False
+        assert np.array_equal(gk[keep], rings_k[s].reshape(cap, stride)[keep])
+        assert np.array_equal(gv[keep], rings_v[s].reshape(cap, stride)[keep])
+        assert np.array_equal(gv[slot], O.float_to_half(qkv[r, v_off:g_off]))
+        ulps = np.abs(gk[slot].astype(np.int32) - O.float_to_half(kr).astype(np.int32))
+        assert ulps.max() <= 1 and (ulps > 0).mean() < 0.02
+        # rotated q/k written back in place, as the reference's heads kernel does
+        gq = dq.download(np.float32, n * ld).reshape(n, ld)
+        np.testing.assert_allclose(gq[r, q_off:k_off], qr, rtol=1e-4, atol=2e-5)
+
+
+C_ITEM = L.C.sizeof(L.AttentionItem)
+
+
+@pytest.mark.parametrize("P,H,KH,window", [(259, 4, 2, 0), (259, 4, 2, 256), (4999, 4, 2, 0),
+                                           (4999, 4, 2, 256), (3000, 16, 4, 0),
+                                           (3000, 16, 4, 256)])
+def test_attention_reference_decode_vectors(P, H, KH, window):
+    """ops_test.cpp:142-220 at n = 1 through the ragged entry point."""
+    D = 128
+    cap = window if window else P + 1
+    stride = KH * D
+    q = data(H * D, 0.7)
+    gates = data(H, 0.7)
+    kbits = O.float_to_half(data(cap * stride, 0.6))
+    vbits = O.float_to_half(data(cap * stride, 0.8))
+    kbits[(P % cap) * stride:(P % cap + 1) * stride] = O.float_to_half(data(stride, 0.5))
+    vbits[(P % cap) * stride:(P % cap + 1) * stride] = O.float_to_half(data(stride, 0.9))
+    dk, dv = L.DeviceBuffer.of(kbits), L.DeviceBuffer.of(vbits)
+    tk, tv = pointer_table([dk.addr]), pointer_table([dv.addr])
+    caps = L.DeviceBuffer.of(np.array([cap], np.uint32))
+    pos = np.array([P], np.uint32)
+    items = (L.AttentionItem * 64)()
+    count = L.check(L.lib().lfm3_attention_plan(L.ptr(pos), 1, window, items, 64))
+    ditems = L.DeviceBuffer(count * C_ITEM)
+    L.hip_check(L.hip().hipMemcpy(ditems.addr, L.C.addressof(items), count * C_ITEM, L.H2D))
+    ws_bytes = L.lib().lfm3_attention_workspace_bytes(count, 1, H, KH, D)
+    ws = L.DeviceBuffer(ws_bytes)
+    dq, dg = L.DeviceBuffer.of(q), L.DeviceBuffer.of(gates)
+    dout = L.DeviceBuffer(H * D * 4)
+    L.check(L.lib().lfm3_decode_attention_ragged(dq.addr, H * D, dg.addr, H, tk.addr, tv.addr,
+                                                 caps.addr, ditems.addr, count, dout.addr, H * D,
+                                                 1, H, KH, D, ws.addr, ws_bytes, None))
+    L.synchronize()
+    out = dout.download(np.float32, H * D)
+    want = attention_fp64(q, gates, O.half_to_float(kbits), O.half_to_float(vbits), H, KH, D, P,
+                          cap, window)
+    assert np.max(np.abs(out - want)) < 2e-6
+
+
+# ------------------------------------------------------------------ argmax
+
+def test_argmax_first_index_of_ties():
+    rows, V = 8, 128000
+    x = L.normal(SEED, "argmax", rows * V).reshape(rows, V)
+    x[0, 5] = x[0, 70000] = 50.0          # tie: first index wins
+    x[1, :] = -3.0                         # all equal: index 0
+    x[2, 127999] = 99.0
+    x[3, 8191] = x[3, 8192] = 9.0          # tie across block boundary
+    x[4] = -np.abs(x[4]) - 1               # all negative
+    dx = L.DeviceBuffer.of(x)
+    ids = L.DeviceBuffer(rows * 4)
+    ws = L.DeviceBuffer(L.lib().lfm3_argmax_workspace_bytes(rows))
+    for _ in range(2):
+        L.check(L.lib().lfm3_argmax(dx.addr, rows, V, ids.addr, ws.addr, ws.nbytes, None))
+        L.synchronize()
+        got = ids.download(np.uint32, rows)
+        assert list(got) == [O.argmax(x[r]) for r in range(rows)]
+    assert got[0] == 5 and got[1] == 0 and got[2] == 127999 and got[3] == 8191
+
+
+def test_gemv_shapes_share_one_workspace():
+    """Engine pattern: consecutive GEMVs of different shapes (different row
+    group counts and K slices) reuse one workspace; each must match its own
+    fresh-workspace result bit for bit."""
+    shapes = [(768, 256, 8), (2048, 2048, 3), (256, 512, 8), (3088, 2048, 1), (64, 7680, 8),
+              (2048, 7680, 2), (512, 2048, 8)]
+    mats = {}
+    most = 256
+    for M, K, B in shapes:
+        mats[(M, K)] = (L.q8(SEED, f"ws{M}x{K}", M, K), DeviceMatrix(L.q8(SEED, f"ws{M}x{K}", M, K), M, K))
+        most = max(most, L.lib().lfm3_gemv_workspace_bytes(M, K, B))
+    shared = L.DeviceBuffer(most)
+    for rep in range(2):
+        for M, K, B in shapes:
+            src, m = mats[(M, K)]
+            x = L.normal(SEED, f"wsx{M}x{K}", B * K).reshape(B, K)
+            fresh = gemv(m, x)
+            dx = L.DeviceBuffer.of(x)
+            dy = L.DeviceBuffer(B * M * 4)
+            L.check(L.lib().lfm3_q8_gemv(m.codes.addr, m.scales.addr, M, K, dx.addr, K, dy.addr,
+                                         M, B, shared.addr, shared.nbytes, None))
+            L.synchronize()
+            assert np.array_equal(dy.download(np.float32, B * M).reshape(B, M), fresh), (M, K, B)

@@ -1,0 +1,146 @@
+"""Engine parity on the GPU: ForwardBatch rounds of ragged sessions against
+the CPU oracle stepping each session alone (reference.cpp), plus the
+reference's session-level contracts (session_test.cpp:224-283: batched rows
+equal independent serial sessions with the same greedy token; invalid
+batches are refused without mutating state)."""
+import numpy as np
+import pytest
+
+import lfm3amd as L
+import oracle as O
+from gpu_util import inject_state, within
+
+pytestmark = pytest.mark.gpu
+SEED = L.SEED
+
+
+def small_dims(**kw):
+    base = dict(hidden=256, intermediate=512, vocab=1000, context=1024, heads=8, head_dim=128,
+                kv_heads=2, window=32, pattern="CSGCCSCG")
+    base.update(kw)
+    return L.Dims(**base)
+
+
+def build(dims, seed, positions, context):
+    w = L.synth_weights(dims, seed=seed)
+    gm = L.Model(w)
+    om = O.Model(dims, w)
+    gs, os_ = [], []
+    for sid, p in enumerate(positions):
+        g = gm.session(context)
+        o = om.session(context, f16=True)
+        inject_state(g, o, dims, seed, sid, int(p))
+        gs.append(g)
+        os_.append(o)
+    return w, gm, om, gs, os_
+
+
+def margin(logits):
+    top = np.sort(logits)[-2:]
+    return float(top[1] - top[0])
+
+
+@pytest.mark.parametrize("dims_kw", [{}, dict(heads=8, kv_heads=4, head_dim=64),
+                                     dict(heads=16, kv_heads=2, head_dim=64, pattern="GSC")])
+def test_forward_batch_matches_oracle(dims_kw):
+    dims = small_dims(**dims_kw)
+    n = 8
+    positions = L.uniform_u32(SEED, "eng.pos", n, 0, 600)
+    w, gm, om, gs, os_ = build(dims, 21, positions, 1024)
+    worst = 0.0
+    for step in range(3):
+        toks = L.uniform_u32(SEED, f"eng.tok{step}", n, 0, dims.vocab - 1)
+        logits = gm.forward_batch(gs, toks)
+        for i in range(n):
+            want = os_[i].step(int(toks[i]))
+            err = float(np.max(np.abs(logits[i] - want)))
+            worst = max(worst, err)
+            assert err < 2e-3, (step, i, err)
+            if margin(want) > 4e-3:
+                assert int(np.argmax(logits[i])) == O.argmax(want)
+            assert gs[i].position == os_[i].position == positions[i] + step + 1
+            assert np.array_equal(gs[i].read_logits(), logits[i])
+    print(f"max |logit - oracle| = {worst:.3g}")
+
+
+def test_batch_rows_equal_serial_sessions():
+    """session_test.cpp:224-283: C2..C8 batches equal independent sessions.
+    Row arithmetic never depends on the other rows here, so equality is
+    exact."""
+    dims = small_dims()
+    positions = [1, 33, 257, 513, 2, 40, 300, 700]
+    w = L.synth_weights(dims, seed=22)
+    gm = L.Model(w)
+    om = O.Model(dims, w)
+    lanes, controls = [], []
+    for sid, p in enumerate(positions):
+        a, b = gm.session(1024), gm.session(1024)
+        o1, o2 = om.session(1024), om.session(1024)
+        inject_state(a, o1, dims, 22, sid, p)
+        inject_state(b, o2, dims, 22, sid, p)
+        lanes.append(a)
+        controls.append(b)
+    for width in (2, 3, 4, 8):
+        toks = L.uniform_u32(SEED, f"bs.tok{width}", width, 0, dims.vocab - 1)
+        batch = gm.forward_batch(lanes[:width], toks)
+        for i in range(width):
+            alone = gm.forward_batch([controls[i]], toks[i:i + 1])[0]
+            assert np.array_equal(batch[i], alone)
+            assert lanes[i].position == controls[i].position
+    ids = gm.forward_batch_greedy(lanes, np.arange(8, dtype=np.uint32))
+    for i in range(8):
+        assert ids[i] == int(np.argmax(lanes[i].read_logits()))
+
+
+def test_invalid_batches_are_refused_without_mutation():
+    dims = small_dims()
+    w = L.synth_weights(dims, seed=23)
+    gm = L.Model(w)
+    a, b = gm.session(16), gm.session(16)
+    toks = np.array([1, 2], np.uint32)
+    for bad in ([a, a], ):
+        with pytest.raises(L.LFM3Error) as e:
+            gm.forward_batch(bad, toks)
+        assert e.value.status == L.E_INVALID
+    with pytest.raises(L.LFM3Error):
+        gm.forward_batch([a, b], np.array([1, dims.vocab], np.uint32))
+    with pytest.raises(L.LFM3Error):
+        gm.forward_batch([a] * 9, np.zeros(9, np.uint32))
+    assert a.position == 0 and b.position == 0 and a.coherent() and b.coherent()
+    a.set_position(16)   # context exhausted
+    with pytest.raises(L.LFM3Error):
+        gm.forward_batch([a, b], toks)
+    assert b.position == 0
+    a.reset()
+    gm.forward_batch([a, b], toks)
+    assert a.position == 1 and b.position == 1
+
+
+def test_sliding_ring_wraps_across_rounds():
+    """Ten rounds past a 32-slot ring: logits keep matching the oracle."""
+    dims = small_dims(pattern="SCS")
+    positions = [29, 30, 31, 95]
+    w, gm, om, gs, os_ = build(dims, 24, positions, 1024)
+    for step in range(10):
+        toks = L.uniform_u32(SEED, f"wrap{step}", 4, 0, dims.vocab - 1)
+        logits = gm.forward_batch(gs, toks)
+        for i in range(4):
+            want = os_[i].step(int(toks[i]))
+            assert np.max(np.abs(logits[i] - want)) < 2e-3
+
+
+def test_full_reference_dims_round():
+    """LFM3-1.7B dims (24 layers, 13 conv / 5 sliding / 6 global, FFN 7680,
+    16/4 heads x 128, vocab 128000) with random-init Q8_0 weights: one
+    two-session round against the oracle, greedy ids identical."""
+    dims = L.Dims(context=4096)
+    positions = [150, 700]
+    w, gm, om, gs, os_ = build(dims, SEED, positions, 1024)
+    toks = np.array([11, 90000], np.uint32)
+    logits = gm.forward_batch(gs, toks)
+    for i in range(2):
+        want = os_[i].step(int(toks[i]))
+        err = float(np.max(np.abs(logits[i] - want)))
+        print(f"row {i}: max |logit - oracle| = {err:.3g}, top-2 margin {margin(want):.3g}")
+        assert err < 2e-3
+        assert int(np.argmax(logits[i])) == O.argmax(want)
