@@ -12,8 +12,8 @@
 // N values cost about 2N shuffles instead of N log2(lanes)), leaving each
 // lane one (head, key) score; max and sum finish over the key bits, then
 // the probabilities are broadcast back for the P.V update of every head.
-// Streams merge through LDS; multi-span rows merge spans in span order in
-// the last block of the row (ticket), so results do not depend on block
+// Streams merge through LDS; multi-span rows leave per-span partials that
+// a second launch merges in span order, so results do not depend on block
 // scheduling.
 #include <cmath>
 
@@ -44,8 +44,7 @@ __launch_bounds__(kAttnThreads) __global__
                                const std::uint32_t* __restrict__ capacity,
                                const lfm3_attention_item* __restrict__ items,
                                float* __restrict__ out, int ldo, int kv_heads,
-                               float* __restrict__ partial,
-                               unsigned* __restrict__ tickets) {
+                               float* __restrict__ partial) {
   constexpr int SUBS = 128 / D, LANES = 64 / SUBS;
   constexpr int KB = (LANES / G) < 8 ? (LANES / G) : 8;
   constexpr int N = KB * G;
@@ -57,7 +56,6 @@ __launch_bounds__(kAttnThreads) __global__
 
   __shared__ float s_acc[STREAMS][G][D];
   __shared__ float s_m[STREAMS][G], s_l[STREAMS][G];
-  __shared__ bool s_last;
 
   const lfm3_attention_item item = items[blockIdx.x];
   const int g = blockIdx.y;
@@ -193,36 +191,36 @@ __launch_bounds__(kAttnThreads) __global__
       po[2 + d] = a;
     }
   }
-  if (!split)
+}
+
+// Merges the spans of every multi-span row in span order: block = (first
+// item of a row, KV head); other items exit. A separate launch, so the
+// partials of every span are visible without a device-scope fence.
+template<int D, int G>
+__launch_bounds__(kAttnThreads) __global__
+    void CombineKernel(const float* __restrict__ gate, int ldg,
+                       const lfm3_attention_item* __restrict__ items,
+                       float* __restrict__ out, int ldo, int kv_heads,
+                       const float* __restrict__ partial) {
+  const lfm3_attention_item item = items[blockIdx.x];
+  if (item.parts < 2 || item.first_item != blockIdx.x)
     return;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned* ticket = tickets + std::size_t(row) * kv_heads + g;
-    const unsigned prev = atomicAdd(ticket, 1u);
-    s_last = prev == item.parts - 1;
-    if (s_last)
-      *ticket = 0;
-  }
-  __syncthreads();
-  if (!s_last)
-    return;
-  __threadfence();
+  const int g = blockIdx.y, row = int(item.row);
   for (int e = threadIdx.x; e < G * D; e += kAttnThreads) {
     const int h = e / D, d = e % D;
     float top = -INFINITY;
     for (std::uint32_t s = 0; s < item.parts; ++s) {
       const float* po = partial +
           ((std::size_t(item.first_item) + s) * kv_heads + g) * G * (D + 2) + h * (D + 2);
-      top = fmaxf(top, __builtin_nontemporal_load(po));
+      top = fmaxf(top, po[0]);
     }
     float l = 0.0f, a = 0.0f;
     for (std::uint32_t s = 0; s < item.parts; ++s) {
       const float* po = partial +
           ((std::size_t(item.first_item) + s) * kv_heads + g) * G * (D + 2) + h * (D + 2);
-      const float w = expf(__builtin_nontemporal_load(po) - top);
-      l = fmaf(__builtin_nontemporal_load(po + 1), w, l);
-      a = fmaf(__builtin_nontemporal_load(po + 2 + d), w, a);
+      const float w = expf(po[0] - top);
+      l = fmaf(po[1], w, l);
+      a = fmaf(po[2 + d], w, a);
     }
     const int head = g * G + h;
     out[std::size_t(row) * ldo + head * D + d] =
@@ -230,35 +228,36 @@ __launch_bounds__(kAttnThreads) __global__
   }
 }
 
+template<int D, int G>
+void LaunchGroup(dim3 grid, hipStream_t s, const float* q, int ldq,
+                 const float* gate, int ldg, const Half* const* ck,
+                 const Half* const* cv, const std::uint32_t* cap,
+                 const lfm3_attention_item* items, float* out, int ldo, int kv,
+                 float* partial) {
+  DecodeAttentionKernel<D, G><<<grid, kAttnThreads, 0, s>>>(
+      q, ldq, gate, ldg, ck, cv, cap, items, out, ldo, kv, partial);
+  CombineKernel<D, G><<<grid, kAttnThreads, 0, s>>>(gate, ldg, items, out, ldo,
+                                                     kv, partial);
+}
+
 template<int D>
 int LaunchDim(int group, dim3 grid, hipStream_t s, const float* q, int ldq,
               const float* gate, int ldg, const Half* const* ck,
               const Half* const* cv, const std::uint32_t* cap,
               const lfm3_attention_item* items, float* out, int ldo, int kv,
-              float* partial, unsigned* tickets) {
+              float* partial) {
   switch (group) {
     case 2:
-      DecodeAttentionKernel<D, 2><<<grid, kAttnThreads, 0, s>>>(
-          q, ldq, gate, ldg, ck, cv, cap, items, out, ldo, kv, partial, tickets);
+      LaunchGroup<D, 2>(grid, s, q, ldq, gate, ldg, ck, cv, cap, items, out, ldo, kv, partial);
       break;
     case 4:
-      DecodeAttentionKernel<D, 4><<<grid, kAttnThreads, 0, s>>>(
-          q, ldq, gate, ldg, ck, cv, cap, items, out, ldo, kv, partial, tickets);
+      LaunchGroup<D, 4>(grid, s, q, ldq, gate, ldg, ck, cv, cap, items, out, ldo, kv, partial);
       break;
     default:
-      DecodeAttentionKernel<D, 8><<<grid, kAttnThreads, 0, s>>>(
-          q, ldq, gate, ldg, ck, cv, cap, items, out, ldo, kv, partial, tickets);
+      LaunchGroup<D, 8>(grid, s, q, ldq, gate, ldg, ck, cv, cap, items, out, ldo, kv, partial);
       break;
   }
   return HipStatus(hipGetLastError(), "LFM3 decode attention launch");
-}
-
-// Ticket words at the start of every attention workspace, one per
-// (row, KV head); fixed so calls with different row counts or head counts
-// can share a workspace.
-constexpr std::uint32_t kTickets = 4096;
-std::size_t TicketBytes(std::uint32_t, std::uint32_t) {
-  return std::size_t(kTickets) * 4;
 }
 
 }  // namespace
@@ -300,9 +299,9 @@ std::size_t lfm3_attention_workspace_bytes(std::uint32_t items,
                                            std::uint32_t heads,
                                            std::uint32_t kv_heads,
                                            std::uint32_t dim) {
+  (void)rows;
   (void)kv_heads;
-  return TicketBytes(rows, kv_heads) +
-         std::size_t(items) * heads * (dim + 2) * sizeof(float);
+  return std::size_t(items) * heads * (dim + 2) * sizeof(float);
 }
 
 int lfm3_decode_attention_ragged(
@@ -320,14 +319,10 @@ int lfm3_decode_attention_ragged(
     return Fail(LFM3_E_INVALID, "unsupported LFM3 attention shape");
   if (!n_items)
     return LFM3_OK;
-  if (std::size_t(rows) * kv_heads > kTickets)
-    return Fail(LFM3_E_INVALID, "LFM3 attention has too many (row, head) pairs");
   if (!workspace || workspace_bytes < lfm3_attention_workspace_bytes(
                                           n_items, rows, heads, kv_heads, dim))
     return Fail(LFM3_E_INVALID, "LFM3 attention workspace too small");
-  auto* tickets = static_cast<unsigned*>(workspace);
-  auto* partial = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                           TicketBytes(rows, kv_heads));
+  auto* partial = static_cast<float*>(workspace);
   const dim3 grid(n_items, kv_heads);
   const auto s = static_cast<hipStream_t>(stream);
   const auto* ck = reinterpret_cast<const Half* const*>(cache_k);
@@ -335,10 +330,9 @@ int lfm3_decode_attention_ragged(
   if (dim == 128)
     return LaunchDim<128>(int(group), grid, s, q, int(ldq), gate, int(ldg), ck,
                           cv, capacity, items, out, int(ldo), int(kv_heads),
-                          partial, tickets);
+                          partial);
   return LaunchDim<64>(int(group), grid, s, q, int(ldq), gate, int(ldg), ck, cv,
-                       capacity, items, out, int(ldo), int(kv_heads), partial,
-                       tickets);
+                       capacity, items, out, int(ldo), int(kv_heads), partial);
 }
 
 }  // extern "C"

@@ -21,12 +21,14 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 // 16-byte load per lane of a wave: lane L = 16 g + n holds row n, bytes
 // [0, 8) = elements 8g..8g+7 of the chunk's first block and bytes [8, 16)
 // = elements 8g..8g+7 of its second block, which is the B operand of two
-// v_mfma_f32_16x16x32_f16 (one per Q8_0 block). Its 32 fp16 scales follow
-// the same tile order as [row][block].
+// v_mfma_f32_16x16x32_f16 (one per Q8_0 block). Codes are stored biased,
+// u = q + 128 (q ^ 0x80), so they decode with one byte permute and one
+// packed half add. The tile's 32 fp16 scales follow as [row][block].
 constexpr int kTileRows = 16;
 constexpr int kChunk = 64;
 constexpr int kTileCodeBytes = kTileRows * kChunk;     // 1024
 constexpr int kTileScales = kTileRows * 2;             // 32 halves
+constexpr std::uint8_t kCodeBias = 0x80;
 
 inline std::uint32_t RowTiles(std::uint32_t rows) {
   return (rows + kTileRows - 1) / kTileRows;
@@ -47,33 +49,24 @@ __device__ __forceinline__ Half FloatToHalfBits(float x) {
   return __builtin_bit_cast(Half, static_cast<_Float16>(x));
 }
 
-// Four Q8_0 codes (one dword) -> four exact fp16 values. v_perm_b32 places
-// each code byte (biased by 128) under an 0x64 high byte, which reads as
-// 1024 + q + 128; subtracting 1152 leaves q exactly.
-__device__ __forceinline__ void CodesToHalves(unsigned codes, h2& lo, h2& hi) {
-  codes ^= 0x80808080u;
-  const unsigned p0 = __builtin_amdgcn_perm(codes, 0x64646464u, 0x01050004u);
-  const unsigned p1 = __builtin_amdgcn_perm(codes, 0x64646464u, 0x03070206u);
+// Four biased codes (one dword) -> four exact fp16 values as two packed
+// dwords. v_perm_b32 places each code byte u under an 0x64 high byte,
+// which reads as 1024 + u = 1152 + q; the packed add of -1152 leaves q.
+__device__ __forceinline__ void CodesToHalves(unsigned codes, unsigned& lo,
+                                              unsigned& hi) {
   const h2 bias = {static_cast<_Float16>(-1152.0f),
                    static_cast<_Float16>(-1152.0f)};
-  lo = __builtin_bit_cast(h2, p0) + bias;
-  hi = __builtin_bit_cast(h2, p1) + bias;
+  const unsigned p0 = __builtin_amdgcn_perm(codes, 0x64646464u, 0x01050004u);
+  const unsigned p1 = __builtin_amdgcn_perm(codes, 0x64646464u, 0x03070206u);
+  lo = __builtin_bit_cast(unsigned, __builtin_bit_cast(h2, p0) + bias);
+  hi = __builtin_bit_cast(unsigned, __builtin_bit_cast(h2, p1) + bias);
 }
-// Eight codes (two dwords) -> one MFMA operand of eight fp16 values.
+// Eight biased codes (two dwords) -> one MFMA operand of eight fp16 values.
 __device__ __forceinline__ h8 EightCodes(unsigned a, unsigned b) {
-  h2 v0, v1, v2, v3;
-  CodesToHalves(a, v0, v1);
-  CodesToHalves(b, v2, v3);
-  h8 out;
-  out[0] = v0[0];
-  out[1] = v0[1];
-  out[2] = v1[0];
-  out[3] = v1[1];
-  out[4] = v2[0];
-  out[5] = v2[1];
-  out[6] = v3[0];
-  out[7] = v3[1];
-  return out;
+  unsigned w[4];
+  CodesToHalves(a, w[0], w[1]);
+  CodesToHalves(b, w[2], w[3]);
+  return __builtin_bit_cast(h8, w);
 }
 
 __device__ __forceinline__ float WaveSum(float v) {

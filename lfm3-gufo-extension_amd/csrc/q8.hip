@@ -1,17 +1,9 @@
 // Q8_0 weights on gfx950: tile repack, the skinny decode GEMV on MFMA, and
 // the embedding gather.
 //
-// GEMV design (B <= 8 FP32 rows). Each wave owns a K range of the matrix
-// and turns its slice of x into a pair of fp16 MFMA operands: per token a
-// power-of-two scale 2^e puts the range's maximum in [2^14, 2^15), hi =
-// fp16(x 2^e) and lo = fp16((x 2^e - hi) 2^11), so hi + lo 2^-11 carries
-// about 22 bits of every element and each code x hi product is exact in
-// FP32. The 16 A rows of v_mfma_f32_16x16x32_f16 are the 8 tokens' hi and
-// lo parts; its B operand is 16 weight rows of one Q8_0 block decoded
-// exactly to fp16, so one MFMA is the per-block dot of 16 rows and the
-// block scale applies as acc = fma(d, c, acc), as in the reference's
-// block-wise sums (hip/ops.hip:671-856: sums += scale * block_dot). The
-// weights stream once from HBM with one 16-byte load per lane per tile.
+// The GEMV (B <= 8 FP32 rows) runs on MFMA: a block stages its K slice of x
+// once as fp16 hi/lo operands in LDS and its waves stream 16-row weight
+// tiles against it (see Q8Gemv).
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -57,7 +49,7 @@ __global__ void PackKernel(const std::uint8_t* __restrict__ src,
     const bool live = row < rows && b < blocks;
     const std::uint8_t* block = src + (std::size_t(row) * blocks + b) * 34;
     for (int j = 0; j < 8; ++j)
-      bytes[blk * 8 + j] = live ? block[2 + 8 * g + j] : 0;
+      bytes[blk * 8 + j] = live ? std::uint8_t(block[2 + 8 * g + j] ^ kCodeBias) : kCodeBias;
     if (live)
       d[blk] = Half(block[0] | (block[1] << 8));
   }
@@ -70,267 +62,298 @@ __global__ void PackKernel(const std::uint8_t* __restrict__ src,
   }
 }
 
-// Launch shape of one GEMV: R row tiles per block, S K-slices across
-// blocks (merged in slice order by the last block of each row group),
-// W waves per block each taking up to CPW 64-column chunks of the slice.
+// Launch plan of one GEMV: RT row tiles per block (RT / 2 gate/up pairs
+// with SwiGLU), W waves per block, each wave owning the chunks c = w mod W
+// of every K slice of W * SPW chunks. Each block covers the whole of K, so
+// no output needs a merge across blocks: on gfx950 a merge through memory
+// costs a device-scope fence, which writes back and invalidates the XCD's
+// L2.
 struct GemvPlan {
-  int row_tiles, nchunks, groups, R, S, W, CPW;
+  int row_tiles, nchunks, groups, RT, W, SPW;
 };
 
 GemvPlan PlanGemv(std::uint32_t rows, std::uint32_t cols, bool swiglu) {
   GemvPlan p{};
-  p.row_tiles = int(RowTiles(rows)) * (swiglu ? 2 : 1);
+  const int unit = swiglu ? 2 : 1;
+  p.row_tiles = int(RowTiles(rows)) * unit;
   p.nchunks = int(Chunks(cols));
-  p.R = swiglu ? 2 : (p.row_tiles >= 4096 ? 2 : 1);
-  p.groups = (p.row_tiles + p.R - 1) / p.R;
-  p.S = 1;
-  // Enough blocks for the 256 CUs; each slice keeps at least 2 chunks.
-  while (p.groups * p.S < 256 && p.S < 8 && p.nchunks / (p.S * 2) >= 2)
-    p.S *= 2;
-  for (;;) {
-    const int cps = (p.nchunks + p.S - 1) / p.S;
-    p.CPW = 1;
-    while (p.CPW < 4 && (cps + p.CPW - 1) / p.CPW > 8)
-      p.CPW *= 2;
-    p.W = (cps + p.CPW - 1) / p.CPW;
-    if (p.W <= 16)
-      break;
-    p.S *= 2;  // long rows: more slices rather than wider blocks
-  }
+  p.SPW = 4;
+  p.W = p.nchunks <= 4 ? 1 : p.nchunks <= 8 ? 2 : p.nchunks <= 16 ? 4 : 8;
+  if (p.nchunks > 32)
+    p.SPW = 5;  // slices of 40 chunks (80 KB of LDS operands), prefetched
+  // Two 64 KB blocks fit a CU: about 512 blocks fill the device once. A
+  // multi-slice block keeps two slices of weights in registers: one tile.
+  const int units = p.row_tiles / unit;
+  int per = units > 2048 ? 4 : units > 1024 ? 2 : 1;
+  if (p.SPW == 5)
+    per = 1;
+  p.RT = per * unit;
+  p.groups = (p.row_tiles + p.RT - 1) / p.RT;
   return p;
 }
 
-constexpr int kMaxWaves = 16;
-// Ticket words at the start of every GEMV workspace (one per row group).
-constexpr int kTicketGroups = 16384;
-
-template<int CPW, int R, bool kSwiGLU>
-__launch_bounds__(1024) __global__
+// y[b][r] = sum_k W[r][k] x[b][k] for b < B <= 8. A block stages a K slice
+// of x at a time in LDS as the MFMA A operand: per token a power of two
+// 2^e puts the slice maximum in [2^14, 2^15), hi = fp16(x 2^e) and
+// lo = fp16((x 2^e - hi) 2^11); A rows 0-7 are the tokens' hi parts and
+// rows 8-15 their lo parts, so hi + lo 2^-11 keeps about 22 bits of each
+// value and every code x half product is exact in FP32. The B operand is
+// 16 weight rows of one Q8_0 block decoded exactly to fp16, so one MFMA
+// gives 16 rows' block dots and the block scale applies as
+// acc = fma(d, dot, acc) in K order (hip/ops.hip:671-856: sums += scale *
+// block_dot). Weight loads of the next slice are issued before the current
+// slice is staged. Waves sum in wave order, so results do not depend on
+// scheduling.
+template<int W, int SPW, int RT, bool kSwiGLU>
+__launch_bounds__(W * 64) __global__
     void Q8Gemv(const std::uint8_t* __restrict__ codes,
                 const Half* __restrict__ scales, int row_tiles, int nchunks,
                 int K, const float* __restrict__ x, int ldx, int B,
-                float* __restrict__ y, int ldy, int rows_out,
-                float* __restrict__ partial, unsigned* __restrict__ tickets) {
-  __shared__ float red[kMaxWaves * R * 128];
-  __shared__ float fin[R * 128];
-  __shared__ bool s_last;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int waves = blockDim.x >> 6;
-  const int i = lane & 15, g = lane >> 4, t = i & 7, part = i >> 3;
-  const int group = blockIdx.x, slice = blockIdx.y, slices = gridDim.y;
-  const int slice_begin = slice * nchunks / slices;
-  const int slice_end = (slice + 1) * nchunks / slices;
-  const int c0 = slice_begin + wave * CPW;
+                float* __restrict__ y, int ldy, int rows_out) {
+  constexpr int T = W * 64, SLICE = W * SPW;
+  // SPW 4 plans cover K in one slice; SPW 5 plans loop over slices and
+  // prefetch the next slice's weights.
+  constexpr bool kMulti = SPW > 4;
+  __shared__ uint4 s_a[SLICE * 2 * 64];
+  __shared__ float s_max[W][8];
+  __shared__ int s_exp[8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int group = blockIdx.x;
+  const int nslices = (nchunks + SLICE - 1) / SLICE;
 
-  // x of this wave's chunks, token t: elements 8g..8g+7 of block 2c (A
-  // operand of the chunk's first MFMA) and of block 2c + 1 (second MFMA).
-  // The first pass finds the range maximum; the second re-reads the same
-  // lines from L1 and converts, so no FP32 copy stays live.
-  const auto load8 = [&](int c, int blk, float (&v)[8]) {
-    const int chunk = c0 + c;
-    const int k = chunk * kChunk + blk * 32 + 8 * g;
-    float4 lo4 = make_float4(0, 0, 0, 0), hi4 = lo4;
-    if (chunk < slice_end && t < B && k < K) {
-      const float4* src = reinterpret_cast<const float4*>(x + std::size_t(t) * ldx + k);
-      lo4 = src[0];
-      hi4 = src[1];
-    }
-    v[0] = lo4.x; v[1] = lo4.y; v[2] = lo4.z; v[3] = lo4.w;
-    v[4] = hi4.x; v[5] = hi4.y; v[6] = hi4.z; v[7] = hi4.w;
-  };
-  float maximum = 0.0f;
+  // Weight tiles and scales of one slice: chunk wave + W j of the slice.
+  uint4 q[RT][SPW], qn[RT][kMulti ? SPW : 1];
+  unsigned sc[RT][SPW], scn[RT][kMulti ? SPW : 1];
+  const auto fetch = [&](int slice, auto& qq, auto& ss) {
 #pragma unroll
-  for (int c = 0; c < CPW; ++c)
+    for (int r = 0; r < RT; ++r) {
+      const int tile = group * RT + r;
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      float v[8];
-      load8(c, blk, v);
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        maximum = fmaxf(maximum, fabsf(v[j]));
-    }
-  // Lanes of one token: same t, any part and group.
-  maximum = fmaxf(maximum, __shfl_xor(maximum, 8, 64));
-  maximum = fmaxf(maximum, __shfl_xor(maximum, 16, 64));
-  maximum = fmaxf(maximum, __shfl_xor(maximum, 32, 64));
-  const int e = maximum > 0.0f ? 14 - ilogbf(maximum) : 0;
-  h8 a[CPW][2];
-#pragma unroll
-  for (int c = 0; c < CPW; ++c)
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      float v[8];
-      load8(c, blk, v);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float s = ldexpf(v[j], e);
-        const _Float16 hi = static_cast<_Float16>(s);
-        a[c][blk][j] = part ? static_cast<_Float16>((s - float(hi)) * 2048.0f) : hi;
-      }
-    }
-  // Exponent of each output token (lane t holds token t).
-  int et[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k)
-    et[k] = __builtin_amdgcn_readlane(e, k);
-
-  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f4 acc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    acc[r] = zero;
-    const int tile = group * R + r;
-    if (tile >= row_tiles)
-      continue;
-    uint4 q[CPW];
-    unsigned sc[CPW];
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      const int chunk = c0 + c;
-      if (chunk < slice_end) {
-        const std::size_t off = std::size_t(tile) * nchunks + chunk;
-        q[c] = *reinterpret_cast<const uint4*>(codes + off * kTileCodeBytes + lane * 16);
-        sc[c] = *reinterpret_cast<const unsigned*>(scales + off * kTileScales + i * 2);
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      if (c0 + c < slice_end) {
-        const h8 w0 = EightCodes(q[c].x, q[c].y), w1 = EightCodes(q[c].z, q[c].w);
-        const f4 p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][0], w0, zero, 0, 0, 0);
-        const f4 p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[c][1], w1, zero, 0, 0, 0);
-        const float d0 = HalfBitsToFloat(sc[c] & 0xffffu);
-        const float d1 = HalfBitsToFloat(sc[c] >> 16);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          acc[r][v] = fmaf(d0, p0[v], acc[r][v]);
-          acc[r][v] = fmaf(d1, p1[v], acc[r][v]);
+      for (int j = 0; j < SPW; ++j) {
+        const int chunk = slice * SLICE + wave + W * j;
+        if (tile < row_tiles && chunk < nchunks) {
+          const std::size_t off = std::size_t(tile) * nchunks + chunk;
+          qq[r][j] = *reinterpret_cast<const uint4*>(codes + off * kTileCodeBytes + lane * 16);
+          ss[r][j] = *reinterpret_cast<const unsigned*>(scales + off * kTileScales + (lane & 15) * 2);
+        } else {
+          qq[r][j] = make_uint4(0, 0, 0, 0);
+          ss[r][j] = 0;
         }
       }
     }
+  };
+  fetch(0, q, sc);
+
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 total[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+    total[r] = zero;
+  const int t = tid & 7;  // staging token of this thread
+  const int part = lane >> 5, tok0 = ((lane >> 4) & 1) * 4;
+
+  for (int slice = 0; slice < nslices; ++slice) {
+    if constexpr (kMulti) {
+      if (slice + 1 < nslices)
+        fetch(slice + 1, qn, scn);
+    }
+    // Stage the slice: unit tid + j T is token t, column group cg of eight.
+    float v[SPW][8];
+    float maximum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      const int cg = (tid + j * T) >> 3;
+      const int k = (slice * SLICE + (cg >> 3)) * kChunk + (cg & 7) * 8;
+      float4 lo4 = make_float4(0, 0, 0, 0), hi4 = lo4;
+      if (t < B && k < K) {
+        const float4* src = reinterpret_cast<const float4*>(x + std::size_t(t) * ldx + k);
+        lo4 = src[0];
+        hi4 = src[1];
+      }
+      v[j][0] = lo4.x; v[j][1] = lo4.y; v[j][2] = lo4.z; v[j][3] = lo4.w;
+      v[j][4] = hi4.x; v[j][5] = hi4.y; v[j][6] = hi4.z; v[j][7] = hi4.w;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        maximum = fmaxf(maximum, fabsf(v[j][i]));
+    }
+    maximum = fmaxf(maximum, __shfl_xor(maximum, 8, 64));
+    maximum = fmaxf(maximum, __shfl_xor(maximum, 16, 64));
+    maximum = fmaxf(maximum, __shfl_xor(maximum, 32, 64));
+    if (slice)
+      __syncthreads();  // the previous slice's operands are in registers
+    if (lane < 8)
+      s_max[wave][lane] = maximum;
+    __syncthreads();
+    maximum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+      maximum = fmaxf(maximum, s_max[w][t]);
+    const int e = maximum > 0.0f ? 14 - ilogbf(maximum) : 0;
+    if (tid < 8)
+      s_exp[tid] = e;
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      const int cg = (tid + j * T) >> 3;
+      h8 hi, lo;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float s = ldexpf(v[j][i], e);
+        const _Float16 h = static_cast<_Float16>(s);
+        hi[i] = h;
+        lo[i] = static_cast<_Float16>((s - float(h)) * 2048.0f);
+      }
+      const int idx = ((cg >> 3) * 2 + ((cg >> 2) & 1)) * 64 + 16 * (cg & 3) + t;
+      s_a[idx] = __builtin_bit_cast(uint4, hi);
+      s_a[idx + 8] = __builtin_bit_cast(uint4, lo);
+    }
+    __syncthreads();
+    // This wave's chunks of the slice: one MFMA per Q8_0 block.
+    h8 a[SPW][2];
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      const int c = wave + W * j;
+      a[j][0] = __builtin_bit_cast(h8, s_a[(c * 2) * 64 + lane]);
+      a[j][1] = __builtin_bit_cast(h8, s_a[(c * 2 + 1) * 64 + lane]);
+    }
+    int ex[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      ex[i] = -(s_exp[tok0 + i] + (part ? 11 : 0));
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      if (group * RT + r >= row_tiles)
+        continue;
+      f4 acc = zero;
+#pragma unroll
+      for (int j = 0; j < SPW; ++j) {
+        if (slice * SLICE + wave + W * j >= nchunks)
+          continue;
+        const h8 w0 = EightCodes(q[r][j].x, q[r][j].y);
+        const h8 w1 = EightCodes(q[r][j].z, q[r][j].w);
+        const f4 p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j][0], w0, zero, 0, 0, 0);
+        const f4 p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j][1], w1, zero, 0, 0, 0);
+        const float d0 = HalfBitsToFloat(sc[r][j] & 0xffffu);
+        const float d1 = HalfBitsToFloat(sc[r][j] >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[i] = fmaf(d0, p0[i], acc[i]);
+          acc[i] = fmaf(d1, p1[i], acc[i]);
+        }
+      }
+      // D layout: lane L holds A rows 4 (L / 16) + i (tokens hi 0-7, then
+      // lo 0-7) of weight row L % 16; undo the slice's powers of two.
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        total[r][i] += ldexpf(acc[i], ex[i]);
+    }
+    if constexpr (kMulti) {
+      if (slice + 1 < nslices) {
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+          for (int j = 0; j < SPW; ++j) {
+            q[r][j] = qn[r][j];
+            sc[r][j] = scn[r][j];
+          }
+      }
+    }
   }
-  // D layout: lane L holds A rows 4 (L / 16) + v (tokens hi 0-7, lo 0-7)
-  // of weight row L % 16. Undo the power-of-two scales, add lo to hi.
-  const int tok0 = (g & 1) * 4, lo = g >> 1;
+
+  // hi + lo, then the waves in wave order through LDS.
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(s_a);       // [W][RT][128]
+  float* fin = red + W * RT * 128;                  // [RT][128]
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
+  for (int r = 0; r < RT; ++r) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int ex = (g & 1) ? et[4 + v] : et[v];
-      float val = ldexpf(acc[r][v], -(ex + (lo ? 11 : 0)));
+    for (int i = 0; i < 4; ++i) {
+      float val = total[r][i];
       val += __shfl_xor(val, 32, 64);
       if (lane < 32)
-        red[(wave * R + r) * 128 + (tok0 + v) * 16 + i] = val;
+        red[(wave * RT + r) * 128 + (tok0 + i) * 16 + (lane & 15)] = val;
     }
   }
   __syncthreads();
-  // Outputs of the block: R tiles x 8 tokens x 16 rows, summed over the
-  // waves in wave order; a block may have fewer threads than outputs.
-  const int tid = threadIdx.x, threads = blockDim.x;
-  for (int o = tid; o < R * 128; o += threads) {
+  for (int o = tid; o < RT * 128; o += T) {
     const int r = o / 128, idx = o % 128;
     float sum = 0.0f;
-    for (int w = 0; w < waves; ++w)
-      sum += red[(w * R + r) * 128 + idx];
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+      sum += red[(w * RT + r) * 128 + idx];
     fin[o] = sum;
   }
   __syncthreads();
-  if (slices > 1) {
-    // Slices merge in slice order, so the result does not depend on which
-    // block finishes last.
-    float* mine = partial + (std::size_t(group) * slices + slice) * (R * 128);
-    for (int o = tid; o < R * 128; o += threads)
-      mine[o] = fin[o];
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned prev = atomicAdd(tickets + group, 1u);
-      s_last = prev == unsigned(slices - 1);
-      if (s_last)
-        tickets[group] = 0;
-    }
-    __syncthreads();
-    if (!s_last)
-      return;
-    __threadfence();
-    const float* all = partial + std::size_t(group) * slices * (R * 128);
-    for (int o = tid; o < R * 128; o += threads) {
-      float sum = 0.0f;
-      for (int s = 0; s < slices; ++s)
-        sum += __builtin_nontemporal_load(all + s * (R * 128) + o);
-      fin[o] = sum;
-    }
-    __syncthreads();
-  }
   if constexpr (kSwiGLU) {
-    // Tile 2j is gate, tile 2j + 1 is up: the same rows j*16 + n.
-    for (int o = tid; o < 128; o += threads) {
-      const int tok = o / 16, n = o % 16, row = group * kTileRows + n;
-      const float gv = fin[o], uv = fin[128 + o];
+    // Tile 2j is gate, tile 2j + 1 is up: the same rows j * 16 + n.
+    for (int o = tid; o < (RT / 2) * 128; o += T) {
+      const int pr = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
+      const int row = (group * (RT / 2) + pr) * kTileRows + n;
+      const float gv = fin[2 * pr * 128 + idx], uv = fin[(2 * pr + 1) * 128 + idx];
       if (tok < B && row < rows_out)
         y[std::size_t(tok) * ldy + row] = (gv * (1.0f / (1.0f + expf(-gv)))) * uv;
     }
   } else {
-    for (int o = tid; o < R * 128; o += threads) {
+    for (int o = tid; o < RT * 128; o += T) {
       const int r = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
-      const int row = (group * R + r) * kTileRows + n;
+      const int row = (group * RT + r) * kTileRows + n;
       if (tok < B && row < rows_out)
         y[std::size_t(tok) * ldy + row] = fin[o];
     }
   }
 }
 
+template<int W, int SPW, int RT, bool kSwiGLU>
+void LaunchPlan(const GemvPlan& p, const std::uint8_t* c, const Half* s, int K,
+                const float* x, int ldx, int B, float* y, int ldy, int rows_out,
+                hipStream_t stream) {
+  Q8Gemv<W, SPW, RT, kSwiGLU><<<p.groups, W * 64, 0, stream>>>(
+      c, s, p.row_tiles, p.nchunks, K, x, ldx, B, y, ldy, rows_out);
+}
+
+template<int W, int SPW, bool kSwiGLU>
+void LaunchRT(const GemvPlan& p, const std::uint8_t* c, const Half* s, int K,
+              const float* x, int ldx, int B, float* y, int ldy, int rows_out,
+              hipStream_t stream) {
+  if constexpr (SPW > 4) {  // multi-slice plans take one tile (or pair)
+    LaunchPlan<W, SPW, kSwiGLU ? 2 : 1, kSwiGLU>(p, c, s, K, x, ldx, B, y, ldy, rows_out,
+                                                stream);
+  } else if constexpr (kSwiGLU) {
+    if (p.RT == 2)
+      LaunchPlan<W, SPW, 2, true>(p, c, s, K, x, ldx, B, y, ldy, rows_out, stream);
+    else
+      LaunchPlan<W, SPW, 4, true>(p, c, s, K, x, ldx, B, y, ldy, rows_out, stream);
+  } else {
+    if (p.RT == 1)
+      LaunchPlan<W, SPW, 1, false>(p, c, s, K, x, ldx, B, y, ldy, rows_out, stream);
+    else if (p.RT == 2)
+      LaunchPlan<W, SPW, 2, false>(p, c, s, K, x, ldx, B, y, ldy, rows_out, stream);
+    else
+      LaunchPlan<W, SPW, 4, false>(p, c, s, K, x, ldx, B, y, ldy, rows_out, stream);
+  }
+}
+
 template<bool kSwiGLU>
 int LaunchGemv(const void* codes, const void* scales, std::uint32_t rows,
                std::uint32_t cols, const float* x, std::uint32_t ldx, float* y,
-               std::uint32_t ldy, std::uint32_t batch, void* workspace,
-               std::size_t workspace_bytes, hipStream_t stream) {
+               std::uint32_t ldy, std::uint32_t batch, hipStream_t stream) {
   if (!codes || !scales || !x || !y || rows == 0 || cols == 0 ||
       cols % 32 || batch == 0 || batch > 8 || ldx % 4 || ldx < cols ||
       ldy < rows || (reinterpret_cast<std::uintptr_t>(x) & 15))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 GEMV shape");
   const GemvPlan p = PlanGemv(rows, cols, kSwiGLU);
-  unsigned* tickets = nullptr;
-  float* partial = nullptr;
-  if (p.S > 1) {
-    if (p.groups > kTicketGroups)
-      return Fail(LFM3_E_INVALID, "LFM3 GEMV has too many row groups to split");
-    if (workspace_bytes < lfm3_gemv_workspace_bytes(rows, cols, batch) ||
-        !workspace)
-      return Fail(LFM3_E_INVALID, "LFM3 GEMV workspace too small");
-    // A fixed ticket region, so calls of different shapes can share one
-    // workspace: partial sums never land where another shape's tickets are.
-    tickets = static_cast<unsigned*>(workspace);
-    partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kTicketGroups * 4);
-  }
-  const dim3 grid(p.groups, p.S), block(p.W * 64);
   const auto* c = static_cast<const std::uint8_t*>(codes);
   const auto* s = static_cast<const Half*>(scales);
-  const int rows_out = int(rows);
-#define LFM3_GEMV(CPW, R)                                                     \
-  Q8Gemv<CPW, R, kSwiGLU><<<grid, block, 0, stream>>>(                        \
-      c, s, p.row_tiles, p.nchunks, int(cols), x, int(ldx), int(batch), y,   \
-      int(ldy), rows_out, partial, tickets)
-  if constexpr (kSwiGLU) {
-    switch (p.CPW) {
-      case 1: LFM3_GEMV(1, 2); break;
-      case 2: LFM3_GEMV(2, 2); break;
-      default: LFM3_GEMV(4, 2); break;
-    }
-  } else if (p.R == 1) {
-    switch (p.CPW) {
-      case 1: LFM3_GEMV(1, 1); break;
-      case 2: LFM3_GEMV(2, 1); break;
-      default: LFM3_GEMV(4, 1); break;
-    }
-  } else {
-    switch (p.CPW) {
-      case 1: LFM3_GEMV(1, 2); break;
-      case 2: LFM3_GEMV(2, 2); break;
-      default: LFM3_GEMV(4, 2); break;
-    }
-  }
-#undef LFM3_GEMV
+  const int K = int(cols), B = int(batch), lx = int(ldx), ly = int(ldy), ro = int(rows);
+  if (p.SPW == 5)
+    LaunchRT<8, 5, kSwiGLU>(p, c, s, K, x, lx, B, y, ly, ro, stream);
+  else if (p.W == 8)
+    LaunchRT<8, 4, kSwiGLU>(p, c, s, K, x, lx, B, y, ly, ro, stream);
+  else if (p.W == 4)
+    LaunchRT<4, 4, kSwiGLU>(p, c, s, K, x, lx, B, y, ly, ro, stream);
+  else if (p.W == 2)
+    LaunchRT<2, 4, kSwiGLU>(p, c, s, K, x, lx, B, y, ly, ro, stream);
+  else
+    LaunchRT<1, 4, kSwiGLU>(p, c, s, K, x, lx, B, y, ly, ro, stream);
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 GEMV launch");
 }
 
@@ -353,8 +376,7 @@ __global__ void EmbedKernel(const std::uint8_t* __restrict__ codes,
   const int chunk = k / kChunk, within = k % kChunk, blk = within / 32;
   const int e = within % 32, g = e / 8, j = e % 8;
   const std::size_t tile = std::size_t(rt) * nchunks + chunk;
-  const auto q = static_cast<std::int8_t>(
-      codes[tile * kTileCodeBytes + (g * 16 + nn) * 16 + blk * 8 + j]);
+  const int q = int(codes[tile * kTileCodeBytes + (g * 16 + nn) * 16 + blk * 8 + j]) - 128;
   const float d = HalfBitsToFloat(scales[tile * kTileScales + nn * 2 + blk]);
   out[std::size_t(row) * hidden + k] = d * float(q);
 }
@@ -403,7 +425,7 @@ int lfm3_q8_pack_host(const void* gguf, std::uint32_t rows, std::uint32_t cols,
             for (int g = 0; g < 4; ++g)
               for (int j = 0; j < 8; ++j)
                 out[(g * 16 + n) * 16 + blk * 8 + j] =
-                    live ? std::uint8_t(block->q[8 * g + j]) : 0;
+                    std::uint8_t((live ? std::uint8_t(block->q[8 * g + j]) : 0) ^ kCodeBias);
           }
         }
       }
@@ -440,24 +462,20 @@ int lfm3_q8_pack_device(const void* gguf, std::uint32_t rows, std::uint32_t cols
 
 std::size_t lfm3_gemv_workspace_bytes(std::uint32_t rows, std::uint32_t cols,
                                       std::uint32_t batch) {
+  // Every block covers the whole of K, so no launch needs partial sums.
+  (void)rows;
+  (void)cols;
   (void)batch;
-  std::size_t most = 0;
-  for (bool swiglu : {false, true}) {
-    const GemvPlan p = PlanGemv(rows, cols, swiglu);
-    if (p.S == 1)
-      continue;
-    most = std::max(most, std::size_t(kTicketGroups) * 4 +
-                              std::size_t(p.groups) * p.S * p.R * 128 * 4);
-  }
-  return most;
+  return 0;
 }
 
 int lfm3_q8_gemv(const void* codes, const void* scales, std::uint32_t rows,
                  std::uint32_t cols, const float* x, std::uint32_t ldx,
                  float* y, std::uint32_t ldy, std::uint32_t batch,
                  void* workspace, std::size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
   return LaunchGemv<false>(codes, scales, rows, cols, x, ldx, y, ldy, batch,
-                           workspace, workspace_bytes,
                            static_cast<hipStream_t>(stream));
 }
 
@@ -466,8 +484,9 @@ int lfm3_q8_gemv_swiglu(const void* codes, const void* scales,
                         std::uint32_t ldx, float* y, std::uint32_t ldy,
                         std::uint32_t batch, void* workspace,
                         std::size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
   return LaunchGemv<true>(codes, scales, rows, cols, x, ldx, y, ldy, batch,
-                          workspace, workspace_bytes,
                           static_cast<hipStream_t>(stream));
 }
 

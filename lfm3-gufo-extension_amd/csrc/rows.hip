@@ -45,7 +45,8 @@ __device__ float BlockSum(float v, float* scratch) {
 
 // reference.cpp:20-28 / hip/ops.hip:905-970 semantics: x += post(branch),
 // then z = x / sqrt(mean(x^2) + eps) * w, each product rounded as the
-// reference's x * scale * weight.
+// reference's x * scale * weight. Every load is issued before the first
+// reduction, so the row costs one memory round trip.
 __launch_bounds__(kNormThreads) __global__
     void ResidualNormKernel(const float* __restrict__ branch,
                             const float* __restrict__ post,
@@ -56,36 +57,33 @@ __launch_bounds__(kNormThreads) __global__
   const int row = blockIdx.x, tid = threadIdx.x;
   const int items = (H + kNormThreads - 1) / kNormThreads;
   float* xr = x + std::size_t(row) * H;
-  float v[kNormItems];
+  float v[kNormItems], b[kNormItems], pw[kNormItems], nw[kNormItems];
 #pragma unroll
   for (int i = 0; i < kNormItems; ++i) {
     const int k = tid + kNormThreads * i;
-    v[i] = i < items && k < H ? xr[k] : 0.0f;
+    const bool live = i < items && k < H;
+    v[i] = live ? xr[k] : 0.0f;
+    b[i] = live && branch ? branch[std::size_t(row) * H + k] : 0.0f;
+    pw[i] = live && post ? post[k] : 0.0f;
+    nw[i] = live && weight ? weight[k] : 0.0f;
   }
   if (branch) {
-    float b[kNormItems], squares = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kNormItems; ++i) {
-      const int k = tid + kNormThreads * i;
-      b[i] = i < items && k < H ? branch[std::size_t(row) * H + k] : 0.0f;
-      squares = fmaf(b[i], b[i], squares);
-    }
     if (post) {
+      float squares = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kNormItems; ++i)
+        squares = fmaf(b[i], b[i], squares);
       const float scale = 1.0f / sqrtf(BlockSum(squares, scratch) / float(H) + eps);
 #pragma unroll
-      for (int i = 0; i < kNormItems; ++i) {
-        const int k = tid + kNormThreads * i;
-        if (i < items && k < H)
-          b[i] = (b[i] * scale) * post[k];
-      }
+      for (int i = 0; i < kNormItems; ++i)
+        b[i] = (b[i] * scale) * pw[i];
     }
 #pragma unroll
     for (int i = 0; i < kNormItems; ++i) {
       const int k = tid + kNormThreads * i;
-      if (i < items && k < H) {
-        v[i] = v[i] + b[i];
+      v[i] = v[i] + b[i];
+      if (i < items && k < H)
         xr[k] = v[i];
-      }
     }
   }
   if (!weight)
@@ -99,7 +97,7 @@ __launch_bounds__(kNormThreads) __global__
   for (int i = 0; i < kNormItems; ++i) {
     const int k = tid + kNormThreads * i;
     if (i < items && k < H)
-      z[std::size_t(row) * H + k] = (v[i] * scale) * weight[k];
+      z[std::size_t(row) * H + k] = (v[i] * scale) * nw[i];
   }
 }
 
@@ -181,12 +179,11 @@ __launch_bounds__(D / 2) __global__
   cv[slot + pair + P] = FloatToHalfBits(vh[pair + P]);
 }
 
-// Greedy argmax: blocks reduce column ranges to a 64-bit key (ordered
-// value bits above the complemented index, so the largest key is the
-// largest value at its first index) merged with atomicMax; the last block
-// of a row writes the id and clears the key and its ticket for the next
-// call.
-constexpr int kArgmaxThreads = 256, kArgmaxPerBlock = 8192;
+// Greedy argmax: one block per row scans the row with a 64-bit key per
+// element (ordered value bits above the complemented index, so the largest
+// key is the largest value at its first index, as std::max_element) and
+// reduces it over the block; no cross-block merge.
+constexpr int kArgmaxThreads = 1024;
 
 __device__ __forceinline__ unsigned long long ArgKey(float value, unsigned index) {
   unsigned bits = __float_as_uint(value);
@@ -196,17 +193,24 @@ __device__ __forceinline__ unsigned long long ArgKey(float value, unsigned index
 
 __launch_bounds__(kArgmaxThreads) __global__
     void ArgmaxKernel(const float* __restrict__ logits, int cols,
-                      unsigned long long* __restrict__ keys,
-                      unsigned* __restrict__ tickets,
                       std::uint32_t* __restrict__ ids) {
   __shared__ unsigned long long best[kArgmaxThreads / 64];
-  __shared__ bool s_last;
-  const int row = blockIdx.y, tid = threadIdx.x;
-  const int begin = blockIdx.x * kArgmaxPerBlock;
-  const int end = min(begin + kArgmaxPerBlock, cols);
+  const int row = blockIdx.x, tid = threadIdx.x;
   const float* lr = logits + std::size_t(row) * cols;
   unsigned long long key = 0;
-  for (int c = begin + tid; c < end; c += kArgmaxThreads) {
+  int c = tid * 4;
+  for (; c + 3 < cols; c += kArgmaxThreads * 4) {
+    const float4 v = *reinterpret_cast<const float4*>(lr + c);
+    unsigned long long k = ArgKey(v.x, unsigned(c));
+    key = k > key ? k : key;
+    k = ArgKey(v.y, unsigned(c + 1));
+    key = k > key ? k : key;
+    k = ArgKey(v.z, unsigned(c + 2));
+    key = k > key ? k : key;
+    k = ArgKey(v.w, unsigned(c + 3));
+    key = k > key ? k : key;
+  }
+  for (; c < cols; ++c) {  // the ragged tail (cols % 4)
     const unsigned long long k = ArgKey(lr[c], unsigned(c));
     key = k > key ? k : key;
   }
@@ -221,18 +225,8 @@ __launch_bounds__(kArgmaxThreads) __global__
   if (tid == 0) {
     for (int w = 1; w < kArgmaxThreads / 64; ++w)
       key = best[w] > key ? best[w] : key;
-    atomicMax(keys + row, key);
-    __threadfence();
-    const unsigned prev = atomicAdd(tickets + row, 1u);
-    s_last = prev == gridDim.x - 1;
+    ids[row] = 0xffffffffu - unsigned(key & 0xffffffffu);
   }
-  __syncthreads();
-  if (!s_last || tid != 0)
-    return;
-  __threadfence();
-  const unsigned long long final_key = atomicExch(keys + row, 0ull);
-  ids[row] = 0xffffffffu - unsigned(final_key & 0xffffffffu);
-  tickets[row] = 0;
 }
 
 __global__ void ScatterRowsKernel(const float* __restrict__ src, std::size_t ld,
@@ -322,20 +316,20 @@ int lfm3_decode_heads_ragged(float* q, float* k, const float* v,
 }
 
 std::size_t lfm3_argmax_workspace_bytes(std::uint32_t rows) {
-  return std::size_t(rows) * (sizeof(unsigned long long) + sizeof(unsigned));
+  (void)rows;  // one block per row: no workspace
+  return 0;
 }
 
 int lfm3_argmax(const float* logits, std::uint32_t rows, std::uint32_t cols,
                 std::uint32_t* ids, void* workspace, std::size_t workspace_bytes,
                 void* stream) {
-  if (!logits || !ids || !rows || !cols || !workspace ||
-      workspace_bytes < lfm3_argmax_workspace_bytes(rows))
+  (void)workspace;
+  (void)workspace_bytes;
+  if (!logits || !ids || !rows || !cols || cols % 4 ||
+      (reinterpret_cast<std::uintptr_t>(logits) & 15))
     return Fail(LFM3_E_INVALID, "invalid LFM3 argmax");
-  auto* keys = static_cast<unsigned long long*>(workspace);
-  auto* tickets = reinterpret_cast<unsigned*>(keys + rows);
-  const dim3 grid((cols + kArgmaxPerBlock - 1) / kArgmaxPerBlock, rows);
-  ArgmaxKernel<<<grid, kArgmaxThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      logits, int(cols), keys, tickets, ids);
+  ArgmaxKernel<<<rows, kArgmaxThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      logits, int(cols), ids);
   return HipStatus(hipGetLastError(), "LFM3 argmax launch");
 }
 

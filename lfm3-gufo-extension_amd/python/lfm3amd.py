@@ -355,6 +355,20 @@ def hip():
         h.hipGetErrorString.argtypes = [i32]
         h.hipGetDeviceCount.argtypes = [C.POINTER(i32)]
         h.hipStreamSynchronize.argtypes = [vp]
+        h.hipStreamCreate.argtypes = [C.POINTER(vp)]
+        h.hipStreamDestroy.argtypes = [vp]
+        h.hipEventCreate.argtypes = [C.POINTER(vp)]
+        h.hipEventDestroy.argtypes = [vp]
+        h.hipEventRecord.argtypes = [vp, vp]
+        h.hipEventSynchronize.argtypes = [vp]
+        h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), vp, vp]
+        h.hipMemcpyAsync.argtypes = [vp, vp, sz, i32, vp]
+        h.hipStreamBeginCapture.argtypes = [vp, i32]
+        h.hipStreamEndCapture.argtypes = [vp, C.POINTER(vp)]
+        h.hipGraphInstantiate.argtypes = [C.POINTER(vp), vp, vp, C.c_char_p, sz]
+        h.hipGraphLaunch.argtypes = [vp, vp]
+        h.hipGraphExecDestroy.argtypes = [vp]
+        h.hipGraphDestroy.argtypes = [vp]
         _hip = h
     return _hip
 
@@ -430,3 +444,110 @@ def gpu_count() -> int:
     except OSError:
         return 0
     return n.value
+
+
+class Stream:
+    """A default-priority HIP stream."""
+
+    def __init__(self):
+        p = vp()
+        hip_check(hip().hipStreamCreate(C.byref(p)))
+        self.handle = p.value
+
+    def synchronize(self):
+        hip_check(hip().hipStreamSynchronize(self.handle))
+
+    def close(self):
+        if self.handle:
+            hip().hipStreamDestroy(self.handle)
+            self.handle = None
+
+
+class Event:
+    """hipEvent recorded on a given stream (the stream the kernels run on)."""
+
+    def __init__(self):
+        p = vp()
+        hip_check(hip().hipEventCreate(C.byref(p)))
+        self.handle = p.value
+
+    def record(self, stream=None):
+        hip_check(hip().hipEventRecord(self.handle, stream))
+
+    def synchronize(self):
+        hip_check(hip().hipEventSynchronize(self.handle))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        hip_check(hip().hipEventElapsedTime(C.byref(ms), self.handle, end.handle))
+        return ms.value
+
+    def close(self):
+        if self.handle:
+            hip().hipEventDestroy(self.handle)
+            self.handle = None
+
+
+class Graph:
+    """A HIP graph captured from the launches `record()` makes on `stream`
+    (for timing back-to-back launches without host launch overhead)."""
+
+    def __init__(self, stream: Stream, record):
+        h = hip()
+        hip_check(h.hipStreamBeginCapture(stream.handle, 0))
+        try:
+            record()
+        finally:
+            graph = vp()
+            hip_check(h.hipStreamEndCapture(stream.handle, C.byref(graph)))
+        self.graph = graph.value
+        exec_ = vp()
+        hip_check(h.hipGraphInstantiate(C.byref(exec_), self.graph, None, None, 0))
+        self.exec = exec_.value
+        self.stream = stream
+
+    def launch(self):
+        hip_check(hip().hipGraphLaunch(self.exec, self.stream.handle))
+
+    def close(self):
+        if self.exec:
+            hip().hipGraphExecDestroy(self.exec)
+            hip().hipGraphDestroy(self.graph)
+            self.exec = None
+
+
+# ------------------------------------------------------- synthetic sessions
+
+def synth_conv_state(seed: int, sid: int, layer: int, dims: Dims) -> np.ndarray:
+    """Convolution history [hidden][width - 1] of session sid, N(0, 1)."""
+    return normal(seed, f"s{sid}.l{layer}.conv", dims.hidden * (dims.conv_width - 1))
+
+
+def synth_kv_state(seed: int, sid: int, layer: int, tag: str, rows: int, dims: Dims) -> np.ndarray:
+    """The first `rows` slots of a K ("k") or V ("v") ring, F16 N(0, 1) bits."""
+    return half_normal(seed, f"s{sid}.l{layer}.{tag}", rows * dims.kv_heads * dims.head_dim)
+
+
+def live_slots(position: int, capacity: int) -> int:
+    """Ring slots holding positions before `position` (slot = t % capacity)."""
+    return min(position, capacity)
+
+
+def inject_synth_state(session: Session, dims: Dims, seed: int, sid: int, position: int):
+    """Prefilled state of a session at `position`: every conv history and the
+    ring slots of positions [0, position) are synthesized; later slots stay
+    zero and are written before any round reads them."""
+    for l in range(dims.n_layers):
+        if dims.layer_type(l) == LAYER_CONV:
+            addr, nbytes = session.state(STATE_CONV, l)
+            h = synth_conv_state(seed, sid, l, dims)
+            assert nbytes == h.nbytes
+            upload_to(addr, h)
+        else:
+            rows = live_slots(position, session.capacity(l))
+            for kind, tag in ((STATE_KEY, "k"), (STATE_VALUE, "v")):
+                addr, nbytes = session.state(kind, l)
+                bits = synth_kv_state(seed, sid, l, tag, rows, dims)
+                assert bits.nbytes <= nbytes
+                upload_to(addr, bits)
+    session.set_position(position)
