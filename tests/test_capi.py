@@ -52,11 +52,12 @@ def test_synthetic_inputs_are_deterministic():
 def unpack_tiles(codes, scales, rows, cols, tile_offset=0, tile_stride=1, tiles=None):
     """Inverse of the documented tile layout: lane 16 g + n of tile
     (r / 16, chunk) holds row n, bytes [0,8) block 2c elements 8g.., [8,16)
-    block 2c + 1 elements 8g..; scales [row][block] per tile."""
+    block 2c + 1 elements 8g..; codes stored biased (q ^ 0x80); scales
+    [row][block] per tile."""
     nchunks = (cols + 63) // 64
     q = np.zeros((rows, nchunks * 64), np.int8)
     d = np.zeros((rows, nchunks * 2), np.uint16)
-    t = codes.reshape(-1, nchunks, 4, 16, 16)      # tile, chunk, g, n, byte
+    t = (codes ^ 0x80).reshape(-1, nchunks, 4, 16, 16)      # tile, chunk, g, n, byte
     s = scales.view(np.uint16).reshape(-1, nchunks, 16, 2)
     for r in range(rows):
         tile = tile_offset + (r // 16) * tile_stride
@@ -85,8 +86,8 @@ def test_host_pack_round_trip(rows, cols):
     assert np.array_equal(q, blocks[:, :, 2:].view(np.int8).reshape(rows, cols))
     assert np.array_equal(d, blocks[:, :, :2].copy().view(np.uint16).reshape(rows, cols // 32))
     assert not q_pad.any() and not d_pad.any()
-    # padding rows of the last tile are zero too
-    t = codes.reshape(tiles, nchunks, 4, 16, 16)
+    # padding rows of the last tile hold the code of zero too
+    t = (codes ^ 0x80).reshape(tiles, nchunks, 4, 16, 16)
     if rows % 16:
         assert not t[-1, :, :, rows % 16:, :].any()
 
