@@ -62,8 +62,9 @@ int lfm3_q8_pack_device(const void* gguf, uint32_t rows, uint32_t cols,
  * gpu::LaunchBatchedQuantGEMMFp32 (hip/ops.hip:1827-1915, B = 2..8), the
  * decode projections behind gpu::Dense / gpu::Project (hip/ops.hpp:44-64).
  * x: batch rows of ldx floats (ldx % 4 == 0, 16-byte aligned); y: batch
- * rows of ldy floats. The workspace (lfm3_gemv_workspace_bytes) must be
- * zeroed once when allocated; calls leave it zeroed.
+ * rows of ldy floats. Every block covers the whole of K, so no call needs
+ * a workspace (lfm3_gemv_workspace_bytes returns 0; the arguments stay for
+ * callers that pass one).
  * ------------------------------------------------------------------- */
 size_t lfm3_gemv_workspace_bytes(uint32_t rows, uint32_t cols,
                                  uint32_t batch);
@@ -96,9 +97,10 @@ int lfm3_embed(const void* codes, const void* scales, uint32_t vocab,
                uint32_t hidden, const uint32_t* tokens, uint32_t n,
                float* out, void* stream);
 /* Greedy ids: first index of each row's maximum, as std::max_element
-   (tests/session_test.cpp:32-34). ids in device memory. The workspace
-   (lfm3_argmax_workspace_bytes) must be zeroed once; calls leave it
-   zeroed. Replaces: the host sampler's temperature-0 pick. */
+   (tests/session_test.cpp:32-34). ids in device memory; cols % 4 == 0 and
+   logits 16-byte aligned. One block per row: no workspace
+   (lfm3_argmax_workspace_bytes returns 0). Replaces: the host sampler's
+   temperature-0 pick. */
 size_t lfm3_argmax_workspace_bytes(uint32_t rows);
 int lfm3_argmax(const float* logits, uint32_t rows, uint32_t cols,
                 uint32_t* ids, void* workspace, size_t workspace_bytes,
@@ -142,20 +144,29 @@ typedef struct {
   uint32_t reserved[3];
 } lfm3_attention_item;
 /* Host planning: positions[i] is row i's position (keys [first, position],
-   first = max(0, position + 1 - window) when window > 0). Writes up to
-   max_items items and returns their count, or a negative status. */
+   first = max(0, position + 1 - window) when window > 0). Every row's keys
+   split into contiguous spans of one length for the call: a multiple of 64
+   keys between 64 and 1024, about (total keys) / 128, and long enough that
+   no row has more than 256 spans (hip/ops.hip:2295-2311 splits each
+   session's keys on its own). Writes up to max_items items and returns
+   their count, or a negative status. */
 int lfm3_attention_plan(const uint32_t* positions, uint32_t rows,
                         uint32_t window, lfm3_attention_item* items,
                         uint32_t max_items);
+/* An item-list capacity that fits any plan of `rows` rows whose positions
+   are at most max_position. */
+size_t lfm3_attention_max_items(uint32_t rows, uint32_t max_position);
+/* Partial sums of multi-span rows: items x heads x (dim + 2) floats. */
 size_t lfm3_attention_workspace_bytes(uint32_t items, uint32_t rows,
                                       uint32_t heads, uint32_t kv_heads,
                                       uint32_t dim);
 /* Gated GQA of one query per row over its session's F16 ring:
    out[i][h] = (softmax(q_h . K / sqrt(dim)) V) / (1 + exp(-gate[i][h])).
-   q/gate/out rows have strides ldq/ldg/ldo floats; items and the per-row
-   tables are in device memory. The workspace must be zeroed once; calls
-   leave its counters zeroed. dim 64 or 128; heads % kv_heads == 0 with a
-   group of 2, 4 or 8.
+   q holds normed, rotated queries and the ring already holds the current
+   K/V row (lfm3_decode_heads_ragged). q/gate/out rows have strides
+   ldq/ldg/ldo floats; items and the per-row tables are in device memory.
+   dim 64 or 128; heads % kv_heads == 0 with a group of 2, 4 or 8. Two
+   launches: the spans, then their merge in span order.
    Replaces: gpu::Attention with n == 1 (hip/ops.hip:2289-2315:
    DecodeWaves + DecodeCombine) per session (engine.cpp:430-434). */
 int lfm3_decode_attention_ragged(
@@ -165,6 +176,23 @@ int lfm3_decode_attention_ragged(
     uint32_t n_items, float* out, uint32_t ldo, uint32_t rows, uint32_t heads,
     uint32_t kv_heads, uint32_t dim, void* workspace, size_t workspace_bytes,
     void* stream);
+/* lfm3_decode_heads_ragged and lfm3_decode_attention_ragged in one pass:
+   q/k/v are the raw projection rows (stride ld floats, left unchanged);
+   each block norms and rotates its row's queries and key, the block whose
+   span ends at the current position stores the row's F16 K/V to ring slot
+   positions[i] % capacity[i], and the current key is read from that
+   block's registers, never from the ring.
+   Replaces: gpu::DecodeHeads + gpu::Attention (hip/ops.hip:2289-2315,
+   2397-2407) per session (engine.cpp:424-436). */
+int lfm3_decode_heads_attention_ragged(
+    const float* q, const float* k, const float* v, uint32_t ld,
+    const float* gate, uint32_t ldg, const float* q_norm, const float* k_norm,
+    const float* frequencies, const float* factors, uint16_t* const* cache_k,
+    uint16_t* const* cache_v, const uint32_t* positions,
+    const uint32_t* capacity, const lfm3_attention_item* items,
+    uint32_t n_items, float* out, uint32_t ldo, uint32_t rows, uint32_t heads,
+    uint32_t kv_heads, uint32_t dim, float eps, void* workspace,
+    size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------
  * Engine: Model / Session (engine.hpp:17-163).

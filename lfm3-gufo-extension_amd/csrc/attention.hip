@@ -2,19 +2,27 @@
 // decode round. A work item is (row, key span); blockIdx.y is the KV head.
 // Keys come from the row's own F16 ring (slot t % capacity), sliding
 // layers reading only the last `window` positions (the item list encodes
-// the window). Q, scores, probabilities and accumulation stay FP32, as in
-// the reference decode (hip/ops.hip:1578-1691).
+// the window), as in the reference decode (hip/ops.hip:1578-1691;
+// reference.cpp:109-144).
 //
-// Block = 4 waves. A wave splits into 128 / D sub-waves whose lanes own two
-// dimensions each, so one dword load per lane reads a whole key row. A
-// sub-wave takes batches of KB keys: the KB x G partial dots are reduced by
-// a halving butterfly (each exchange halves the values a lane carries, so
-// N values cost about 2N shuffles instead of N log2(lanes)), leaving each
-// lane one (head, key) score; max and sum finish over the key bits, then
-// the probabilities are broadcast back for the P.V update of every head.
-// Streams merge through LDS; multi-span rows leave per-span partials that
-// a second launch merges in span order, so results do not depend on block
-// scheduling.
+// Block = 4 waves; wave w takes the 16-key groups w, w + 4, ... of its span.
+// Scores S = Q K^T run on MFMA (v_mfma_f32_16x16x32_f16): the A operand
+// holds each query head as an fp16 hi row and an fp16 lo row (hi + lo 2^-11
+// keeps about 22 bits of the FP32 query; every half x half product is
+// exact in FP32), the B operand is 16 keys' F16 rows read with one 16-byte
+// load per lane per 32 dimensions. The softmax runs in (head, key) lanes
+// with FP32 online maxima and sums; P V runs on the VALU with lanes owning
+// two dimensions and the probabilities broadcast through LDS. Waves merge
+// through LDS; rows with several spans leave per-span (max, sum, acc)
+// partials that a second launch merges in span order, so results do not
+// depend on block scheduling and no device-scope fence is needed.
+//
+// With the heads fused in (lfm3_decode_heads_attention_ragged), every block
+// also applies the per-head Q/K RMSNorm and paired RoPE of its row
+// (hip/ops.hip:1072-1134) in its prologue; the block whose span holds the
+// current position stores that row's K/V to its ring slot, and every block
+// reads the current key from LDS, never from the ring being written.
+#include <algorithm>
 #include <cmath>
 
 #include "common.hpp"
@@ -22,241 +30,416 @@
 namespace lfm3amd {
 namespace {
 
-constexpr int kSpan = 256;       // keys per work item
-constexpr int kAttnThreads = 256;
+constexpr int kAttnThreads = 256, kAttnWaves = 4, kGroupKeys = 16;
+constexpr std::uint32_t kTargetItems = 128, kMinSpan = 64, kMaxSpan = 1024;
+constexpr std::uint32_t kMaxParts = 256;
 
-template<int LANES>
-__device__ __forceinline__ float SubShfl(float v, int src_in_sub) {
-  if constexpr (LANES == 64) {
-    return __shfl(v, src_in_sub, 64);
-  } else {
-    const int base = threadIdx.x & 63 & ~(LANES - 1);
-    return __shfl(v, base + src_in_sub, 64);
-  }
+// Orders this wave's LDS writes before its later LDS reads by other lanes.
+// The hardware keeps a wave's LDS operations in order; the fence stops the
+// compiler from moving a store past a load that no single lane aliases
+// (lanes here read rows other lanes wrote).
+__device__ __forceinline__ void WaveSync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
 }
 
-template<int D, int G>
-__launch_bounds__(kAttnThreads) __global__
-    void DecodeAttentionKernel(const float* __restrict__ q, int ldq,
-                               const float* __restrict__ gate, int ldg,
-                               const Half* const* __restrict__ cache_k,
-                               const Half* const* __restrict__ cache_v,
-                               const std::uint32_t* __restrict__ capacity,
-                               const lfm3_attention_item* __restrict__ items,
-                               float* __restrict__ out, int ldo, int kv_heads,
-                               float* __restrict__ partial) {
-  constexpr int SUBS = 128 / D, LANES = 64 / SUBS;
-  constexpr int KB = (LANES / G) < 8 ? (LANES / G) : 8;
-  constexpr int N = KB * G;
-  constexpr int LOG_LANES = LANES == 64 ? 6 : 5;
-  constexpr int LOG_N = N == 64 ? 6 : N == 32 ? 5 : N == 16 ? 4 : N == 8 ? 3 : 2;
-  constexpr int SH = LOG_LANES - LOG_N;
-  constexpr int STREAMS = (kAttnThreads / 64) * SUBS;
-  constexpr int LOG_KB = KB == 8 ? 3 : KB == 4 ? 2 : 1;
+__device__ __forceinline__ float GroupMax16(float v) {
+  v = fmaxf(v, __shfl_xor(v, 8, 64));
+  v = fmaxf(v, __shfl_xor(v, 4, 64));
+  v = fmaxf(v, __shfl_xor(v, 2, 64));
+  return fmaxf(v, __shfl_xor(v, 1, 64));
+}
+__device__ __forceinline__ float GroupSum16(float v) {
+  v += __shfl_xor(v, 8, 64);
+  v += __shfl_xor(v, 4, 64);
+  v += __shfl_xor(v, 2, 64);
+  return v + __shfl_xor(v, 1, 64);
+}
 
-  __shared__ float s_acc[STREAMS][G][D];
-  __shared__ float s_m[STREAMS][G], s_l[STREAMS][G];
+template<int D, int G, bool kFused>
+__launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
+    const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, int ld, const float* __restrict__ gate,
+    int ldg, const float* __restrict__ q_norm,
+    const float* __restrict__ k_norm, const float* __restrict__ frequencies,
+    const float* __restrict__ factors, Half* const* __restrict__ cache_k,
+    Half* const* __restrict__ cache_v,
+    const std::uint32_t* __restrict__ positions,
+    const std::uint32_t* __restrict__ capacity,
+    const lfm3_attention_item* __restrict__ items, float* __restrict__ out,
+    int ldo, int kv_heads, float eps, float* __restrict__ partial) {
+  static_assert(D == 64 || D == 128, "head dimension 64 or 128");
+  static_assert(2 * G <= 16, "hi and lo rows of the group fit one MFMA tile");
+  constexpr int S = D / 32;                // MFMA steps per key row
+  constexpr int HALVES = 128 / D;          // P V key split across half-waves
+  constexpr int KPL = kGroupKeys / HALVES; // keys per lane in P V
+  constexpr int PAIRS = (16 * G + 63) / 64;
+  __shared__ float s_q[G][D];
+  __shared__ __attribute__((aligned(16))) Half s_kv[2][D];
+  __shared__ float s_tile[kAttnWaves][16][17];
+  __shared__ float s_p[kAttnWaves][kGroupKeys][G];
+  __shared__ float s_alpha[kAttnWaves][G];
+  __shared__ float s_acc[kAttnWaves][G][D];
+  __shared__ float s_m[kAttnWaves][G], s_l[kAttnWaves][G];
 
   const lfm3_attention_item item = items[blockIdx.x];
-  const int g = blockIdx.y;
-  const int row = int(item.row);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub_lane = lane & (LANES - 1), sub = lane / LANES;
-  const int stream = wave * SUBS + sub;
-  const int d0 = 2 * sub_lane;
+  const int g = blockIdx.y, row = int(item.row);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int stride = kv_heads * D;
   const std::uint32_t cap = capacity[row];
-  const Half* ck = cache_k[row] + g * D + d0;
-  const Half* cv = cache_v[row] + g * D + d0;
-  const float scale = 1.0f / sqrtf(float(D));
+  const int kb = int(item.key_begin), ke = int(item.key_end);
+  const int pos = kFused ? int(positions[row]) : -1;
+  Half* ck = cache_k[row];
+  Half* cv = cache_v[row];
 
-  float qv[G][2];
+  // Prologue: queries of the group (normed and rotated when fused).
+  if constexpr (kFused) {
+#pragma clang fp contract(off)
+    constexpr int P = D / 2, SLOTS = kAttnThreads / P;
+    const int slot = tid / P, pair = tid % P;
+    const float fp = frequencies[pair];
+    for (int h0 = 0; h0 <= G; h0 += SLOTS) {
+      const int h = h0 + slot;
+      if (h <= G) {  // h == G is the key head
+        const float* src = h < G ? q + std::size_t(row) * ld + (g * G + h) * D
+                                 : k + std::size_t(row) * ld + g * D;
+        const float* w = h < G ? q_norm : k_norm;
+        const float x0 = src[pair], x1 = src[pair + P];
+        float squares = x0 * x0 + x1 * x1;
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const float2 v2 = *reinterpret_cast<const float2*>(
-        q + std::size_t(row) * ldq + (g * G + h) * D + d0);
-    qv[h][0] = v2.x;
-    qv[h][1] = v2.y;
+        for (int m = P / 2; m; m >>= 1)
+          squares += __shfl_xor(squares, m, 64);
+        const float inv = 1.0f / sqrtf(squares / float(D) + eps);
+        const float a = (x0 * inv) * w[pair], b = (x1 * inv) * w[pair + P];
+        float angle = float(pos) * fp;
+        if (factors)
+          angle /= factors[pair];
+        float sn, cs;
+        sincosf(angle, &sn, &cs);
+        const float r0 = a * cs - b * sn, r1 = b * cs + a * sn;
+        if (h < G) {
+          s_q[h][pair] = r0;
+          s_q[h][pair + P] = r1;
+        } else {
+          s_kv[0][pair] = FloatToHalfBits(r0);
+          s_kv[0][pair + P] = FloatToHalfBits(r1);
+        }
+      }
+    }
+    for (int d = tid; d < D; d += kAttnThreads)
+      s_kv[1][d] = FloatToHalfBits(v[std::size_t(row) * ld + g * D + d]);
+    __syncthreads();
+    if (ke == pos + 1 && tid < D) {  // this span holds the current position
+      const std::size_t at = std::size_t(std::uint32_t(pos) % cap) * stride + g * D + tid;
+      ck[at] = s_kv[0][tid];
+      cv[at] = s_kv[1][tid];
+    }
+  } else {
+    for (int e = tid; e < G * D; e += kAttnThreads)
+      s_q[e / D][e % D] = q[std::size_t(row) * ld + (g * G + e / D) * D + e % D];
+    __syncthreads();
   }
-  const int idx = sub_lane >> SH, my_head = idx / KB;
-  float m_own = -INFINITY, l_own = 0.0f;
+
+  // A operand: row m < G is head m's hi part, G <= m < 2G head m - G's lo.
+  h8 a[S];
+  {
+    const int m = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int dim = 32 * s + 8 * kg + i;
+        _Float16 val = 0;
+        if (m < G) {
+          val = static_cast<_Float16>(s_q[m][dim]);
+        } else if (m < 2 * G) {
+          const float x = s_q[m - G][dim];
+          val = static_cast<_Float16>((x - float(static_cast<_Float16>(x))) * 2048.0f);
+        }
+        a[s][i] = val;
+      }
+  }
+
+  const float root = sqrtf(float(D));
+  float m_own[PAIRS], l_own[PAIRS];
+#pragma unroll
+  for (int r = 0; r < PAIRS; ++r) {
+    m_own[r] = -INFINITY;
+    l_own[r] = 0.0f;
+  }
   float acc[G][2];
 #pragma unroll
   for (int h = 0; h < G; ++h)
     acc[h][0] = acc[h][1] = 0.0f;
+  const int half = lane / (64 / HALVES);
+  const int d0 = 2 * (lane % (64 / HALVES));
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int kb = int(item.key_begin), ke = int(item.key_end);
-  for (int base = kb + stream * KB; base < ke; base += STREAMS * KB) {
-    float k0[KB], k1[KB], v0[KB], v1[KB];
+  const int ngroups = (ke - kb + kGroupKeys - 1) / kGroupKeys;
+  for (int j = wave; j < ngroups; j += kAttnWaves) {
+    const int base = kb + kGroupKeys * j;
+    // K rows as the B operand: lane L reads key L % 16, dimensions
+    // 32 s + 8 (L / 16) .. + 7.
+    const int n = lane & 15, kg = lane >> 4;
+    const int t = base + n;
+    const bool valid = t < ke;
+    const Half* krow = ck + std::size_t(std::uint32_t(valid ? t : kb) % cap) * stride + g * D + 8 * kg;
+    uint4 kr[S];
 #pragma unroll
-    for (int i = 0; i < KB; ++i) {
-      const int t = min(base + i, ke - 1);
-      const std::size_t off = std::size_t(std::uint32_t(t) % cap) * stride;
-      const unsigned kw = *reinterpret_cast<const unsigned*>(ck + off);
-      const unsigned vw = *reinterpret_cast<const unsigned*>(cv + off);
-      k0[i] = HalfBitsToFloat(kw & 0xffffu);
-      k1[i] = HalfBitsToFloat(kw >> 16);
-      v0[i] = HalfBitsToFloat(vw & 0xffffu);
-      v1[i] = HalfBitsToFloat(vw >> 16);
+    for (int s = 0; s < S; ++s)
+      kr[s] = *reinterpret_cast<const uint4*>(krow + 32 * s);
+    // V words of this lane's keys and two dimensions.
+    unsigned vr[KPL];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const int tv = base + half * KPL + i;
+      const int safe = tv < ke ? tv : kb;
+      vr[i] = *reinterpret_cast<const unsigned*>(
+          cv + std::size_t(std::uint32_t(safe) % cap) * stride + g * D + d0);
     }
-    float vals[N];
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int s = 0; s < S; ++s) {
+      if (kFused && t == pos)
+        kr[s] = *reinterpret_cast<const uint4*>(&s_kv[0][32 * s + 8 * kg]);
+      if (!valid)
+        kr[s] = make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
-      for (int i = 0; i < KB; ++i)
-        vals[h * KB + i] = fmaf(qv[h][1], k1[i], qv[h][0] * k0[i]);
-    // Halving butterfly: after step s a lane carries N >> (s + 1) values.
+    for (int i = 0; i < KPL; ++i) {
+      const int tv = base + half * KPL + i;
+      if (kFused && tv == pos)
+        vr[i] = *reinterpret_cast<const unsigned*>(&s_kv[1][d0]);
+      if (tv >= ke)
+        vr[i] = 0;
+    }
+    f4 sacc = zero;
 #pragma unroll
-    for (int s = 0; s < LOG_N; ++s) {
-      const int mask = LANES >> (s + 1);
-      const int half = N >> (s + 1);
-      const bool upper = (sub_lane & mask) != 0;
+    for (int s = 0; s < S; ++s)
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], __builtin_bit_cast(h8, kr[s]), sacc, 0, 0, 0);
+    // D layout: lane L holds rows 4 (L / 16) + i of key L % 16.
 #pragma unroll
-      for (int j = 0; j < half; ++j) {
-        const float keep = upper ? vals[j + half] : vals[j];
-        const float send = upper ? vals[j] : vals[j + half];
-        vals[j] = keep + __shfl_xor(send, mask, 64);
+    for (int i = 0; i < 4; ++i)
+      s_tile[wave][4 * (lane >> 4) + i][lane & 15] = sacc[i];
+    WaveSync();
+    // Online softmax: lane owns (head, key) pairs idx = lane + 64 r.
+#pragma unroll
+    for (int r = 0; r < PAIRS; ++r) {
+      const int idx = lane + 64 * r, h = idx >> 4, nn = idx & 15;
+      if (h < G) {
+        float sc = (s_tile[wave][h][nn] + s_tile[wave][G + h][nn] * (1.0f / 2048.0f)) / root;
+        if (base + nn >= ke)
+          sc = -INFINITY;
+        const float m_new = fmaxf(m_own[r], GroupMax16(sc));
+        const float shift = m_new == -INFINITY ? 0.0f : m_new;
+        const float p = expf(sc - shift);
+        const float alpha = expf(m_own[r] - shift);
+        l_own[r] = l_own[r] * alpha + GroupSum16(p);
+        m_own[r] = m_new;
+        s_p[wave][nn][h] = p;
+        if (nn == 0)
+          s_alpha[wave][h] = alpha;
       }
     }
-    float dot = vals[0];
-#pragma unroll
-    for (int mask = (1 << SH) >> 1; mask; mask >>= 1)
-      dot += __shfl_xor(dot, mask, 64);
-    const int key = base + (idx % KB);
-    const float score = key < ke ? dot * scale : -INFINITY;
-    float top = score;
-#pragma unroll
-    for (int b = 0; b < LOG_KB; ++b)
-      top = fmaxf(top, __shfl_xor(top, (1 << SH) << b, 64));
-    const float m_new = fmaxf(m_own, top);
-    const float shift = m_new == -INFINITY ? 0.0f : m_new;
-    const float p = expf(score - shift);
-    const float alpha = expf(m_own - shift);
-    float psum = p;
-#pragma unroll
-    for (int b = 0; b < LOG_KB; ++b)
-      psum += __shfl_xor(psum, (1 << SH) << b, 64);
-    l_own = l_own * alpha + psum;
-    m_own = m_new;
+    WaveSync();
+    // P V: lane owns dimensions d0, d0 + 1 of every head of the group.
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const float a_h = SubShfl<LANES>(alpha, (h * KB) << SH);
-      float x0 = acc[h][0] * a_h, x1 = acc[h][1] * a_h;
-#pragma unroll
-      for (int i = 0; i < KB; ++i) {
-        const float p_hi = SubShfl<LANES>(p, (h * KB + i) << SH);
-        x0 = fmaf(p_hi, v0[i], x0);
-        x1 = fmaf(p_hi, v1[i], x1);
-      }
-      acc[h][0] = x0;
-      acc[h][1] = x1;
+      const float al = s_alpha[wave][h];
+      acc[h][0] *= al;
+      acc[h][1] *= al;
     }
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const float v0 = HalfBitsToFloat(vr[i] & 0xffffu);
+      const float v1 = HalfBitsToFloat(vr[i] >> 16);
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float p = s_p[wave][half * KPL + i][h];
+        acc[h][0] = fmaf(p, v0, acc[h][0]);
+        acc[h][1] = fmaf(p, v1, acc[h][1]);
+      }
+    }
+    WaveSync();  // the next group rewrites s_tile, s_p and s_alpha
   }
-  // Merge the block's streams.
+
+  // Merge the waves (and the key halves of D = 64) in a fixed order.
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    s_acc[stream][h][d0] = acc[h][0];
-    s_acc[stream][h][d0 + 1] = acc[h][1];
+    if constexpr (HALVES == 2) {
+      acc[h][0] += __shfl_xor(acc[h][0], 32, 64);
+      acc[h][1] += __shfl_xor(acc[h][1], 32, 64);
+    }
+    if (half == 0) {
+      s_acc[wave][h][d0] = acc[h][0];
+      s_acc[wave][h][d0 + 1] = acc[h][1];
+    }
   }
-  if ((sub_lane & ((1 << (SH + LOG_KB)) - 1)) == 0) {
-    s_m[stream][my_head] = m_own;
-    s_l[stream][my_head] = l_own;
+#pragma unroll
+  for (int r = 0; r < PAIRS; ++r) {
+    const int idx = lane + 64 * r, h = idx >> 4;
+    if (h < G && (idx & 15) == 0) {
+      s_m[wave][h] = m_own[r];
+      s_l[wave][h] = l_own[r];
+    }
   }
   __syncthreads();
   const bool split = item.parts > 1;
   float* part_out = partial + (std::size_t(blockIdx.x) * kv_heads + g) * G * (D + 2);
-  for (int e = threadIdx.x; e < G * D; e += kAttnThreads) {
+  for (int e = tid; e < G * D; e += kAttnThreads) {
     const int h = e / D, d = e % D;
     float top = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < STREAMS; ++s)
-      top = fmaxf(top, s_m[s][h]);
-    float l = 0.0f, a = 0.0f;
+    for (int w = 0; w < kAttnWaves; ++w)
+      top = fmaxf(top, s_m[w][h]);
+    float l = 0.0f, av = 0.0f;
 #pragma unroll
-    for (int s = 0; s < STREAMS; ++s) {
-      const float w = s_m[s][h] == -INFINITY ? 0.0f : expf(s_m[s][h] - top);
-      l = fmaf(s_l[s][h], w, l);
-      a = fmaf(s_acc[s][h][d], w, a);
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float wt = s_m[w][h] == -INFINITY ? 0.0f : expf(s_m[w][h] - top);
+      l = fmaf(s_l[w][h], wt, l);
+      av = fmaf(s_acc[w][h][d], wt, av);
     }
     const int head = g * G + h;
     if (!split) {
       out[std::size_t(row) * ldo + head * D + d] =
-          (a / l) / (1.0f + expf(-gate[std::size_t(row) * ldg + head]));
+          (av / l) / (1.0f + expf(-gate[std::size_t(row) * ldg + head]));
     } else {
       float* po = part_out + h * (D + 2);
       if (d == 0) {
         po[0] = top;
         po[1] = l;
       }
-      po[2 + d] = a;
+      po[2 + d] = av;
     }
   }
 }
 
 // Merges the spans of every multi-span row in span order: block = (first
-// item of a row, KV head); other items exit. A separate launch, so the
-// partials of every span are visible without a device-scope fence.
+// item of a row, KV head); other items exit. Span maxima, weights and
+// denominators are staged in LDS, then every output element sums its
+// spans with independent loads.
 template<int D, int G>
 __launch_bounds__(kAttnThreads) __global__
     void CombineKernel(const float* __restrict__ gate, int ldg,
                        const lfm3_attention_item* __restrict__ items,
                        float* __restrict__ out, int ldo, int kv_heads,
                        const float* __restrict__ partial) {
+  __shared__ float s_w[kMaxParts][G];
+  __shared__ float s_lv[kMaxParts][G];
+  __shared__ float s_top[G], s_den[G];
   const lfm3_attention_item item = items[blockIdx.x];
   if (item.parts < 2 || item.first_item != blockIdx.x)
     return;
-  const int g = blockIdx.y, row = int(item.row);
-  for (int e = threadIdx.x; e < G * D; e += kAttnThreads) {
-    const int h = e / D, d = e % D;
+  const int g = blockIdx.y, row = int(item.row), parts = int(item.parts);
+  const int tid = threadIdx.x;
+  const std::size_t span_stride = std::size_t(kv_heads) * G * (D + 2);
+  const float* base = partial + (std::size_t(item.first_item) * kv_heads + g) * G * (D + 2);
+  for (int e = tid; e < parts * G; e += kAttnThreads) {
+    const int s = e / G, h = e % G;
+    const float* po = base + s * span_stride + h * (D + 2);
+    s_w[s][h] = po[0];
+    s_lv[s][h] = po[1];
+  }
+  __syncthreads();
+  if (tid < G) {
     float top = -INFINITY;
-    for (std::uint32_t s = 0; s < item.parts; ++s) {
-      const float* po = partial +
-          ((std::size_t(item.first_item) + s) * kv_heads + g) * G * (D + 2) + h * (D + 2);
-      top = fmaxf(top, po[0]);
-    }
-    float l = 0.0f, a = 0.0f;
-    for (std::uint32_t s = 0; s < item.parts; ++s) {
-      const float* po = partial +
-          ((std::size_t(item.first_item) + s) * kv_heads + g) * G * (D + 2) + h * (D + 2);
-      const float w = expf(po[0] - top);
-      l = fmaf(po[1], w, l);
-      a = fmaf(po[2 + d], w, a);
-    }
+    for (int s = 0; s < parts; ++s)
+      top = fmaxf(top, s_w[s][tid]);
+    s_top[tid] = top;
+  }
+  __syncthreads();
+  for (int e = tid; e < parts * G; e += kAttnThreads) {
+    const int s = e / G, h = e % G;
+    s_w[s][h] = expf(s_w[s][h] - s_top[h]);
+  }
+  __syncthreads();
+  if (tid < G) {
+    float den = 0.0f;
+    for (int s = 0; s < parts; ++s)
+      den = fmaf(s_lv[s][tid], s_w[s][tid], den);
+    s_den[tid] = den;
+  }
+  __syncthreads();
+  for (int e = tid; e < G * D; e += kAttnThreads) {
+    const int h = e / D, d = e % D;
+    const float* po = base + h * (D + 2) + 2 + d;
+    float av = 0.0f;
+#pragma unroll 8
+    for (int s = 0; s < parts; ++s)
+      av = fmaf(po[s * span_stride], s_w[s][h], av);
     const int head = g * G + h;
     out[std::size_t(row) * ldo + head * D + d] =
-        (a / l) / (1.0f + expf(-gate[std::size_t(row) * ldg + head]));
+        (av / s_den[h]) / (1.0f + expf(-gate[std::size_t(row) * ldg + head]));
   }
 }
 
+struct AttentionArgs {
+  const float *q = nullptr, *k = nullptr, *v = nullptr;
+  int ld = 0;
+  const float* gate = nullptr;
+  int ldg = 0;
+  const float *q_norm = nullptr, *k_norm = nullptr, *frequencies = nullptr,
+              *factors = nullptr;
+  Half* const* ck = nullptr;
+  Half* const* cv = nullptr;
+  const std::uint32_t *positions = nullptr, *capacity = nullptr;
+  const lfm3_attention_item* items = nullptr;
+  float* out = nullptr;
+  int ldo = 0, kv = 0;
+  float eps = 0.0f;
+  float* partial = nullptr;
+};
+
 template<int D, int G>
-void LaunchGroup(dim3 grid, hipStream_t s, const float* q, int ldq,
-                 const float* gate, int ldg, const Half* const* ck,
-                 const Half* const* cv, const std::uint32_t* cap,
-                 const lfm3_attention_item* items, float* out, int ldo, int kv,
-                 float* partial) {
-  DecodeAttentionKernel<D, G><<<grid, kAttnThreads, 0, s>>>(
-      q, ldq, gate, ldg, ck, cv, cap, items, out, ldo, kv, partial);
-  CombineKernel<D, G><<<grid, kAttnThreads, 0, s>>>(gate, ldg, items, out, ldo,
-                                                     kv, partial);
+void LaunchGroup(const AttentionArgs& a, dim3 grid, hipStream_t s, bool fused) {
+  if (fused)
+    DecodeAttentionKernel<D, G, true><<<grid, kAttnThreads, 0, s>>>(
+        a.q, a.k, a.v, a.ld, a.gate, a.ldg, a.q_norm, a.k_norm, a.frequencies,
+        a.factors, a.ck, a.cv, a.positions, a.capacity, a.items, a.out, a.ldo,
+        a.kv, a.eps, a.partial);
+  else
+    DecodeAttentionKernel<D, G, false><<<grid, kAttnThreads, 0, s>>>(
+        a.q, a.k, a.v, a.ld, a.gate, a.ldg, a.q_norm, a.k_norm, a.frequencies,
+        a.factors, a.ck, a.cv, a.positions, a.capacity, a.items, a.out, a.ldo,
+        a.kv, a.eps, a.partial);
+  CombineKernel<D, G><<<grid, kAttnThreads, 0, s>>>(a.gate, a.ldg, a.items,
+                                                     a.out, a.ldo, a.kv,
+                                                     a.partial);
 }
 
 template<int D>
-int LaunchDim(int group, dim3 grid, hipStream_t s, const float* q, int ldq,
-              const float* gate, int ldg, const Half* const* ck,
-              const Half* const* cv, const std::uint32_t* cap,
-              const lfm3_attention_item* items, float* out, int ldo, int kv,
-              float* partial) {
+void LaunchDim(int group, const AttentionArgs& a, dim3 grid, hipStream_t s, bool fused) {
   switch (group) {
-    case 2:
-      LaunchGroup<D, 2>(grid, s, q, ldq, gate, ldg, ck, cv, cap, items, out, ldo, kv, partial);
-      break;
-    case 4:
-      LaunchGroup<D, 4>(grid, s, q, ldq, gate, ldg, ck, cv, cap, items, out, ldo, kv, partial);
-      break;
-    default:
-      LaunchGroup<D, 8>(grid, s, q, ldq, gate, ldg, ck, cv, cap, items, out, ldo, kv, partial);
-      break;
+    case 2: LaunchGroup<D, 2>(a, grid, s, fused); break;
+    case 4: LaunchGroup<D, 4>(a, grid, s, fused); break;
+    default: LaunchGroup<D, 8>(a, grid, s, fused); break;
   }
+}
+
+int Launch(const AttentionArgs& a, std::uint32_t n_items, std::uint32_t rows,
+           std::uint32_t heads, std::uint32_t kv_heads, std::uint32_t dim,
+           void* workspace, std::size_t workspace_bytes, void* stream,
+           bool fused) {
+  const std::uint32_t group = kv_heads ? heads / kv_heads : 0;
+  if (!a.q || !a.gate || !a.ck || !a.cv || !a.capacity || !a.items || !a.out ||
+      !rows || !kv_heads || heads % kv_heads ||
+      (group != 2 && group != 4 && group != 8) || (dim != 64 && dim != 128) ||
+      (fused && (!a.k || !a.v || !a.q_norm || !a.k_norm || !a.frequencies ||
+                 !a.positions)))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 attention shape");
+  if (!n_items)
+    return LFM3_OK;
+  if (!workspace || workspace_bytes < lfm3_attention_workspace_bytes(
+                                          n_items, rows, heads, kv_heads, dim))
+    return Fail(LFM3_E_INVALID, "LFM3 attention workspace too small");
+  AttentionArgs args = a;
+  args.kv = int(kv_heads);
+  args.partial = static_cast<float*>(workspace);
+  const dim3 grid(n_items, kv_heads);
+  const auto s = static_cast<hipStream_t>(stream);
+  if (dim == 128)
+    LaunchDim<128>(int(group), args, grid, s, fused);
+  else
+    LaunchDim<64>(int(group), args, grid, s, fused);
   return HipStatus(hipGetLastError(), "LFM3 decode attention launch");
 }
 
@@ -272,19 +455,35 @@ int lfm3_attention_plan(const std::uint32_t* positions, std::uint32_t rows,
                         std::uint32_t max_items) {
   if (!positions || !items)
     return Fail(LFM3_E_INVALID, "invalid LFM3 attention plan");
+  // Span length: about kTargetItems items over the round, multiples of 64
+  // keys between kMinSpan and kMaxSpan, and at most kMaxParts per row.
+  std::uint64_t total = 0;
+  std::uint32_t longest = 0;
+  for (std::uint32_t r = 0; r < rows; ++r) {
+    const std::uint32_t p = positions[r];
+    const std::uint32_t first = window && p + 1 > window ? p + 1 - window : 0;
+    total += p + 1 - first;
+    longest = std::max(longest, p + 1 - first);
+  }
+  std::uint64_t span = (total + kTargetItems - 1) / kTargetItems;
+  span = std::max<std::uint64_t>(span, (longest + kMaxParts - 1) / kMaxParts);
+  span = (span + 63) / 64 * 64;
+  span = std::min<std::uint64_t>(std::max<std::uint64_t>(span, kMinSpan), kMaxSpan);
+  if ((longest + span - 1) / span > kMaxParts)
+    return Fail(LFM3_E_INVALID, "LFM3 attention row is too long");
   std::uint32_t count = 0;
   for (std::uint32_t r = 0; r < rows; ++r) {
     const std::uint32_t p = positions[r];
     const std::uint32_t first = window && p + 1 > window ? p + 1 - window : 0;
     const std::uint32_t keys = p + 1 - first;
-    const std::uint32_t parts = (keys + kSpan - 1) / kSpan;
+    const std::uint32_t parts = std::uint32_t((keys + span - 1) / span);
     if (count + parts > max_items)
       return Fail(LFM3_E_INVALID, "LFM3 attention plan exceeds its item list");
     for (std::uint32_t s = 0; s < parts; ++s) {
       lfm3_attention_item& it = items[count + s];
       it.row = r;
-      it.key_begin = first + s * kSpan;
-      it.key_end = std::min(first + (s + 1) * kSpan, p + 1);
+      it.key_begin = first + std::uint32_t(s * span);
+      it.key_end = std::uint32_t(std::min<std::uint64_t>(first + (s + 1) * span, p + 1));
       it.first_item = count;
       it.parts = parts;
       it.reserved[0] = it.reserved[1] = it.reserved[2] = 0;
@@ -292,6 +491,15 @@ int lfm3_attention_plan(const std::uint32_t* positions, std::uint32_t rows,
     count += parts;
   }
   return int(count);
+}
+
+std::size_t lfm3_attention_max_items(std::uint32_t rows,
+                                     std::uint32_t max_position) {
+  // A span is at least max(kMinSpan, total keys / kTargetItems) keys long
+  // unless capped at kMaxSpan; rounding up costs at most one item per row.
+  const std::uint64_t keys = std::uint64_t(max_position) + 1;
+  return std::size_t(kTargetItems) + rows +
+         std::size_t(rows) * std::size_t((keys + kMaxSpan - 1) / kMaxSpan);
 }
 
 std::size_t lfm3_attention_workspace_bytes(std::uint32_t items,
@@ -311,28 +519,53 @@ int lfm3_decode_attention_ragged(
     std::uint32_t n_items, float* out, std::uint32_t ldo, std::uint32_t rows,
     std::uint32_t heads, std::uint32_t kv_heads, std::uint32_t dim,
     void* workspace, std::size_t workspace_bytes, void* stream) {
-  const std::uint32_t group = kv_heads ? heads / kv_heads : 0;
-  if (!q || !gate || !cache_k || !cache_v || !capacity || !items || !out ||
-      !rows || !kv_heads || heads % kv_heads ||
-      (group != 2 && group != 4 && group != 8) || (dim != 64 && dim != 128) ||
-      ldq % 2)
-    return Fail(LFM3_E_INVALID, "unsupported LFM3 attention shape");
-  if (!n_items)
-    return LFM3_OK;
-  if (!workspace || workspace_bytes < lfm3_attention_workspace_bytes(
-                                          n_items, rows, heads, kv_heads, dim))
-    return Fail(LFM3_E_INVALID, "LFM3 attention workspace too small");
-  auto* partial = static_cast<float*>(workspace);
-  const dim3 grid(n_items, kv_heads);
-  const auto s = static_cast<hipStream_t>(stream);
-  const auto* ck = reinterpret_cast<const Half* const*>(cache_k);
-  const auto* cv = reinterpret_cast<const Half* const*>(cache_v);
-  if (dim == 128)
-    return LaunchDim<128>(int(group), grid, s, q, int(ldq), gate, int(ldg), ck,
-                          cv, capacity, items, out, int(ldo), int(kv_heads),
-                          partial);
-  return LaunchDim<64>(int(group), grid, s, q, int(ldq), gate, int(ldg), ck, cv,
-                       capacity, items, out, int(ldo), int(kv_heads), partial);
+  AttentionArgs a;
+  a.q = q;
+  a.ld = int(ldq);
+  a.gate = gate;
+  a.ldg = int(ldg);
+  // The unfused kernel only reads the rings.
+  a.ck = const_cast<Half* const*>(reinterpret_cast<const Half* const*>(cache_k));
+  a.cv = const_cast<Half* const*>(reinterpret_cast<const Half* const*>(cache_v));
+  a.capacity = capacity;
+  a.items = items;
+  a.out = out;
+  a.ldo = int(ldo);
+  return Launch(a, n_items, rows, heads, kv_heads, dim, workspace,
+                workspace_bytes, stream, false);
+}
+
+int lfm3_decode_heads_attention_ragged(
+    const float* q, const float* k, const float* v, std::uint32_t ld,
+    const float* gate, std::uint32_t ldg, const float* q_norm,
+    const float* k_norm, const float* frequencies, const float* factors,
+    std::uint16_t* const* cache_k, std::uint16_t* const* cache_v,
+    const std::uint32_t* positions, const std::uint32_t* capacity,
+    const lfm3_attention_item* items, std::uint32_t n_items, float* out,
+    std::uint32_t ldo, std::uint32_t rows, std::uint32_t heads,
+    std::uint32_t kv_heads, std::uint32_t dim, float eps, void* workspace,
+    std::size_t workspace_bytes, void* stream) {
+  AttentionArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.ld = int(ld);
+  a.gate = gate;
+  a.ldg = int(ldg);
+  a.q_norm = q_norm;
+  a.k_norm = k_norm;
+  a.frequencies = frequencies;
+  a.factors = factors;
+  a.ck = reinterpret_cast<Half* const*>(cache_k);
+  a.cv = reinterpret_cast<Half* const*>(cache_v);
+  a.positions = positions;
+  a.capacity = capacity;
+  a.items = items;
+  a.out = out;
+  a.ldo = int(ldo);
+  a.eps = eps;
+  return Launch(a, n_items, rows, heads, kv_heads, dim, workspace,
+                workspace_bytes, stream, true);
 }
 
 }  // extern "C"

@@ -259,9 +259,7 @@ void EnsureRoundBuffers(lfm3_model& m, std::uint32_t max_context) {
   const auto& c = m.config;
   if (max_context <= m.max_context)
     return;
-  // Attention work items: at most ceil(context / 256) spans per row.
-  const std::size_t per_row = (max_context + 255) / 256 + 1;
-  m.items_capacity = per_row * kMaxBatch;
+  m.items_capacity = lfm3_attention_max_items(kMaxBatch, max_context);
   const std::size_t L = c.n_layers;
   m.table_bytes = Align(sizeof(RoundTable)) +
                   Align(L * kMaxBatch * sizeof(void*)) * 3 +   // conv / k / v
@@ -634,18 +632,15 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
       const auto* kp = reinterpret_cast<std::uint16_t* const*>(dev + k_off) + il * kMaxBatch;
       const auto* vp = reinterpret_cast<std::uint16_t* const*>(dev + v_off) + il * kMaxBatch;
       const auto* cp = reinterpret_cast<const std::uint32_t*>(dev + cap_off) + il * kMaxBatch;
-      CheckStatus(lfm3_decode_heads_ragged(
-          proj + l.q_off, proj + l.k_off, proj + l.v_off, pld,
-          l.q_norm.as<float>(), l.k_norm.as<float>(),
-          swa ? m.freq_sliding.as<float>() : m.freq_global.as<float>(),
-          swa ? nullptr : m.factors.as<float>(), kp, vp, d_rt->positions, cp, n,
-          c.heads, l.kv, D, c.eps, s));
       const auto* items = reinterpret_cast<const lfm3_attention_item*>(
           dev + (swa ? items_swa_off : items_full_off));
-      CheckStatus(lfm3_decode_attention_ragged(
-          proj + l.q_off, pld, proj + l.g_off, pld, kp, vp, cp, items,
-          std::uint32_t(swa ? n_swa : n_full), a, c.heads * D, n, c.heads, l.kv,
-          D, m.attn_ws.p, m.attn_ws_bytes, s));
+      CheckStatus(lfm3_decode_heads_attention_ragged(
+          proj + l.q_off, proj + l.k_off, proj + l.v_off, pld, proj + l.g_off,
+          pld, l.q_norm.as<float>(), l.k_norm.as<float>(),
+          swa ? m.freq_sliding.as<float>() : m.freq_global.as<float>(),
+          swa ? nullptr : m.factors.as<float>(), kp, vp, d_rt->positions, cp,
+          items, std::uint32_t(swa ? n_swa : n_full), a, c.heads * D, n,
+          c.heads, l.kv, D, c.eps, m.attn_ws.p, m.attn_ws_bytes, s));
       gemv(l.attn_out, a, c.heads * D, out, H);
     }
     CheckStatus(lfm3_residual_norm(out, l.post_norm.as<float>(), x,

@@ -62,9 +62,13 @@ _SIGS = {
     "lfm3_decode_heads_ragged": (i32, [vp, vp, vp, u32, vp, vp, vp, vp, vp, vp, vp, vp,
                                        u32, u32, u32, u32, f32, vp]),
     "lfm3_attention_plan": (i32, [vp, u32, u32, vp, u32]),
+    "lfm3_attention_max_items": (sz, [u32, u32]),
     "lfm3_attention_workspace_bytes": (sz, [u32, u32, u32, u32, u32]),
     "lfm3_decode_attention_ragged": (i32, [vp, u32, vp, u32, vp, vp, vp, vp, u32, vp, u32,
                                            u32, u32, u32, u32, vp, sz, vp]),
+    "lfm3_decode_heads_attention_ragged": (i32, [vp, vp, vp, u32, vp, u32, vp, vp, vp, vp, vp,
+                                                 vp, vp, vp, vp, u32, vp, u32, u32, u32, u32,
+                                                 u32, f32, vp, sz, vp]),
     "lfm3_model_load": (i32, [C.POINTER(Config), C.POINTER(Tensor), sz, C.POINTER(vp)]),
     "lfm3_model_destroy": (None, [vp]),
     "lfm3_model_stream": (vp, [vp]),

@@ -119,6 +119,14 @@ def test_attention_plan_covers_each_row_exactly(window):
     positions = L.uniform_u32(L.SEED, "ctx", 8, 1, 4096) - 1
     positions = np.concatenate([positions, [0, 255, 256, 257, 511, 512]]).astype(np.uint32)
     items = plan(positions, window)
+    # one span length per call: a multiple of 64 in [64, 1024], about a
+    # 128th of the keys
+    keys = [int(p) + 1 - (max(0, int(p) + 1 - window) if window else 0) for p in positions]
+    span = max(it.key_end - it.key_begin for it in items)
+    assert span % 64 == 0 and 64 <= span <= 1024
+    per_item = -(-sum(keys) // 128)
+    assert span == min(1024, max(64, (per_item + 63) // 64 * 64))
+    assert len(items) <= L.lib().lfm3_attention_max_items(len(positions), int(max(positions)))
     by_row = {}
     for idx, it in enumerate(items):
         by_row.setdefault(it.row, []).append((idx, it))
@@ -130,10 +138,10 @@ def test_attention_plan_covers_each_row_exactly(window):
         assert spans[0][0] == first and spans[-1][1] == p + 1
         for (b0, e0), (b1, e1) in zip(spans, spans[1:]):
             assert e0 == b1
-        assert all(0 < e - b <= 256 for b, e in spans)
+        assert all(0 < e - b <= span for b, e in spans)
+        assert all(e - b == span for b, e in spans[:-1])
         assert all(it.parts == len(lst) and it.first_item == lst[0][0] for _, it in lst)
-        if window:
-            assert len(lst) == 1
+        assert len(lst) <= 256
 
 
 def test_attention_plan_refuses_overflow():

@@ -171,9 +171,12 @@ def ragged_case(heads, kv, D, window, ctx_hi=4096, n=8, tag="a", global_cap=4096
 
 @pytest.mark.parametrize("heads,kv,D", [(32, 8, 64), (16, 4, 128), (16, 8, 128), (16, 2, 128)])
 @pytest.mark.parametrize("window", [0, 256])
-def test_heads_and_attention_ragged(heads, kv, D, window):
+@pytest.mark.parametrize("fused", [False, True])
+def test_heads_and_attention_ragged(heads, kv, D, window, fused):
     """Config-2 shape: 8 sessions, contexts U[1, 4096], Q/K RMSNorm, paired
-    RoPE at theta 1e6, F16 ring store, gated GQA; sliding (256) and global."""
+    RoPE at theta 1e6, F16 ring store, gated GQA; sliding (256) and global.
+    Unfused: the heads launch, then attention over the ring. Fused: one
+    entry norms, rotates and stores inside the attention launch."""
     n = 8
     ctx, positions, cap, stride, order = ragged_case(heads, kv, D, window)
     theta = 1e6
@@ -199,10 +202,11 @@ def test_heads_and_attention_ragged(heads, kv, D, window):
     dfreq, dfac = L.DeviceBuffer.of(freq), L.DeviceBuffer.of(factors)
     dq = L.DeviceBuffer.of(qkv)
     dqn, dkn = L.DeviceBuffer.of(qn), L.DeviceBuffer.of(kn)
-    L.check(L.lib().lfm3_decode_heads_ragged(
-        dq.addr + 4 * q_off, dq.addr + 4 * k_off, dq.addr + 4 * v_off, ld, dqn.addr, dkn.addr,
-        dfreq.addr, 0 if window else dfac.addr, tk.addr, tv.addr, dpos.addr, caps.addr, n,
-        heads, kv, D, 1e-5, None))
+    if not fused:
+        L.check(L.lib().lfm3_decode_heads_ragged(
+            dq.addr + 4 * q_off, dq.addr + 4 * k_off, dq.addr + 4 * v_off, ld, dqn.addr,
+            dkn.addr, dfreq.addr, 0 if window else dfac.addr, tk.addr, tv.addr, dpos.addr,
+            caps.addr, n, heads, kv, D, 1e-5, None))
     cap_items = 4096
     items = (L.AttentionItem * cap_items)()
     count = L.check(L.lib().lfm3_attention_plan(L.ptr(pos_rows), n, window, items, cap_items))
@@ -211,10 +215,19 @@ def test_heads_and_attention_ragged(heads, kv, D, window):
     ws_bytes = L.lib().lfm3_attention_workspace_bytes(count, n, heads, kv, D)
     ws = L.DeviceBuffer(ws_bytes)
     dout = L.DeviceBuffer(n * heads * D * 4)
-    for repeat in range(2):  # the second call reuses the workspace tickets
-        L.check(L.lib().lfm3_decode_attention_ragged(
-            dq.addr + 4 * q_off, ld, dq.addr + 4 * g_off, ld, tk.addr, tv.addr, caps.addr,
-            ditems.addr, count, dout.addr, heads * D, n, heads, kv, D, ws.addr, ws_bytes, None))
+    for repeat in range(2):  # the second call reuses the workspace
+        if fused:
+            L.check(L.lib().lfm3_decode_heads_attention_ragged(
+                dq.addr + 4 * q_off, dq.addr + 4 * k_off, dq.addr + 4 * v_off, ld,
+                dq.addr + 4 * g_off, ld, dqn.addr, dkn.addr, dfreq.addr,
+                0 if window else dfac.addr, tk.addr, tv.addr, dpos.addr, caps.addr,
+                ditems.addr, count, dout.addr, heads * D, n, heads, kv, D, 1e-5, ws.addr,
+                ws_bytes, None))
+        else:
+            L.check(L.lib().lfm3_decode_attention_ragged(
+                dq.addr + 4 * q_off, ld, dq.addr + 4 * g_off, ld, tk.addr, tv.addr, caps.addr,
+                ditems.addr, count, dout.addr, heads * D, n, heads, kv, D, ws.addr, ws_bytes,
+                None))
         L.synchronize()
         out = dout.download(np.float32, n * heads * D).reshape(n, heads * D)
         if repeat == 0:
@@ -242,9 +255,11 @@ def test_heads_and_attention_ragged(heads, kv, D, window):
         assert np.array_equal(gv[slot], O.float_to_half(qkv[r, v_off:g_off]))
         ulps = np.abs(gk[slot].astype(np.int32) - O.float_to_half(kr).astype(np.int32))
         assert ulps.max() <= 1 and (ulps > 0).mean() < 0.02
-        # rotated q/k written back in place, as the reference's heads kernel does
         gq = dq.download(np.float32, n * ld).reshape(n, ld)
-        np.testing.assert_allclose(gq[r, q_off:k_off], qr, rtol=1e-4, atol=2e-5)
+        if fused:  # the projection rows are left as they were
+            assert np.array_equal(gq[r], qkv[r])
+        else:  # rotated q/k written back in place, as the reference's heads kernel does
+            np.testing.assert_allclose(gq[r, q_off:k_off], qr, rtol=1e-4, atol=2e-5)
 
 
 C_ITEM = L.C.sizeof(L.AttentionItem)
@@ -268,8 +283,9 @@ def test_attention_reference_decode_vectors(P, H, KH, window):
     tk, tv = pointer_table([dk.addr]), pointer_table([dv.addr])
     caps = L.DeviceBuffer.of(np.array([cap], np.uint32))
     pos = np.array([P], np.uint32)
-    items = (L.AttentionItem * 64)()
-    count = L.check(L.lib().lfm3_attention_plan(L.ptr(pos), 1, window, items, 64))
+    cap_items = L.lib().lfm3_attention_max_items(1, int(pos[0]))
+    items = (L.AttentionItem * cap_items)()
+    count = L.check(L.lib().lfm3_attention_plan(L.ptr(pos), 1, window, items, cap_items))
     ditems = L.DeviceBuffer(count * C_ITEM)
     L.hip_check(L.hip().hipMemcpy(ditems.addr, L.C.addressof(items), count * C_ITEM, L.H2D))
     ws_bytes = L.lib().lfm3_attention_workspace_bytes(count, 1, H, KH, D)
