@@ -72,6 +72,40 @@ int lfm3_q8_gemv(const void* codes, const void* scales, uint32_t rows,
                  uint32_t cols, const float* x, uint32_t ldx, float* y,
                  uint32_t ldy, uint32_t batch, void* workspace,
                  size_t workspace_bytes, void* stream);
+/* The same products split over K into `parts` contiguous ranges, one grid
+   row of blocks each: part p writes its partial sums to y + p * batch *
+   ldy (rows of ldy floats), and the consumer adds the parts in part order
+   (lfm3_residual_norm_parts). No merge happens inside the launch, so
+   narrow matrices fill the device without a device-scope fence.
+   lfm3_q8_gemv_parts gives the number of parts (at most 8) this library
+   picks for a shape (1 when one range fills the device).
+   Replaces: the split-K tail of gpu::LaunchSplit (hip/ops.hip:2039-2069),
+   which merges partial sums in the last block of each tile. */
+uint32_t lfm3_q8_gemv_parts(uint32_t rows, uint32_t cols);
+int lfm3_q8_gemv_partials(const void* codes, const void* scales, uint32_t rows,
+                          uint32_t cols, const float* x, uint32_t ldx, float* y,
+                          uint32_t ldy, uint32_t batch, uint32_t parts,
+                          void* stream);
+/* GEMV operand images. A producer that holds whole FP32 rows of x can
+   hand them to the next GEMV already staged as its MFMA A operand: per
+   token an exponent e (x = (hi + lo 2^-11) 2^-e, e puts the row maximum
+   in [2^14, 2^15)), hi = fp16(x 2^e), lo = fp16((x 2^e - hi) 2^11), laid
+   out per 64-column chunk c and Q8_0 block b as 64 16-byte lane words at
+   ((c * 2 + b) * 64 + L), lane L = 16 g + m holding elements 8g..8g+7 of
+   the block for A row m (m < 8: token m's hi part, m >= 8: token m - 8's
+   lo part). exps holds 8 ints. The GEMV then reads its operands from L2
+   with no per-block staging; for cols <= 2048 the result is bit-identical
+   to lfm3_q8_gemv on the same rows. No counterpart in the reference (its
+   decode GEMVs read FP32 rows, hip/ops.hip:671-856). */
+size_t lfm3_operand_image_bytes(uint32_t cols);
+int lfm3_q8_gemv_image(const void* codes, const void* scales, uint32_t rows,
+                       uint32_t cols, const void* image, const int* exps,
+                       uint32_t batch, float* y, uint32_t ldy, uint32_t parts,
+                       void* stream);
+int lfm3_q8_gemv_swiglu_image(const void* codes, const void* scales,
+                              uint32_t rows, uint32_t cols, const void* image,
+                              const int* exps, uint32_t batch, float* y,
+                              uint32_t ldy, void* stream);
 /* FFN gate/up with the SwiGLU epilogue over a stride-2 interleaved pair
    (rows = rows of each of gate and up): y[b][r] = silu(g) * u.
    Replaces: gpu::ProjectSwiGLU (hip/ops.hip:2187-2204) and the decode half
@@ -91,6 +125,21 @@ int lfm3_q8_gemv_swiglu(const void* codes, const void* scales, uint32_t rows,
 int lfm3_residual_norm(const float* branch, const float* post_norm, float* x,
                        const float* norm, float* z, uint32_t rows,
                        uint32_t hidden, float eps, void* stream);
+/* The same with the branch given as `parts` (at most 8) partial sums
+   part_stride floats apart (lfm3_q8_gemv_partials output), added in part
+   order. hidden <= 4096. */
+int lfm3_residual_norm_parts(const float* branch, uint32_t parts,
+                             size_t part_stride, const float* post_norm,
+                             float* x, const float* norm, float* z,
+                             uint32_t rows, uint32_t hidden, float eps,
+                             void* stream);
+/* lfm3_residual_norm_parts whose normed rows also go out as an operand
+   image (z may be null). rows <= 8, hidden % 32 == 0. */
+int lfm3_residual_norm_image(const float* branch, uint32_t parts,
+                             size_t part_stride, const float* post_norm,
+                             float* x, const float* norm, float* z, void* image,
+                             int* exps, uint32_t rows, uint32_t hidden,
+                             float eps, void* stream);
 /* out[i] = d * q of row tokens[i] (tokens in device memory).
    Replaces: gpu::Embed (hip/ops.hip:2007-2011). */
 int lfm3_embed(const void* codes, const void* scales, uint32_t vocab,
@@ -118,6 +167,14 @@ int lfm3_conv_step_ragged(const float* p, uint32_t ldp, const float* taps,
                           float* const* history, float* y, uint32_t ldy,
                           uint32_t rows, uint32_t hidden, uint32_t width,
                           void* stream);
+/* lfm3_conv_step_ragged with one block per row, writing the output rows
+   as the out projection's operand image (y may be null). Outputs and
+   history stay bit-identical. rows <= 8, hidden % 32 == 0. */
+int lfm3_conv_step_ragged_image(const float* p, uint32_t ldp,
+                                const float* taps, float* const* history,
+                                float* y, uint32_t ldy, void* image, int* exps,
+                                uint32_t rows, uint32_t hidden, uint32_t width,
+                                void* stream);
 /* Per-head Q/K RMSNorm, paired RoPE at positions[i] and the F16 K/V store
    to ring slot positions[i] % capacity[i] of cache_k[i] / cache_v[i]
    ([capacity][kv_heads][dim] F16). q/k/v rows have stride ld floats.

@@ -156,6 +156,7 @@ struct lfm3_model {
   // Round scratch, shared by the model's rounds (calls are serialized, as
   // the Gufo scheduler serializes sessions: engine.cpp:101-113).
   Buffer x, z, proj, a, hidden, out, logits, gemv_ws, argmax_ws, ids;
+  Buffer image, exps;  // GEMV operand image of the current hidden-wide input
   std::size_t proj_ld = 0, gemv_ws_bytes = 0;
   // Per-round device tables: RoundTable, per-layer pointer rows, items.
   Buffer table;
@@ -390,7 +391,10 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     m->proj = Buffer(B * m->proj_ld * 4);
     m->a = Buffer(B * std::max<std::size_t>(H, std::size_t(c.heads) * D) * 4);
     m->hidden = Buffer(B * F * 4);
-    m->out = Buffer(B * H * 4);
+    std::size_t out_parts = lfm3_q8_gemv_parts(H, F);
+    out_parts = std::max<std::size_t>(out_parts, lfm3_q8_gemv_parts(H, H));
+    out_parts = std::max<std::size_t>(out_parts, lfm3_q8_gemv_parts(H, c.heads * D));
+    m->out = Buffer(out_parts * B * H * 4);
     m->logits = Buffer(B * std::size_t(c.vocab) * 4);
     std::size_t ws = lfm3_gemv_workspace_bytes(c.vocab, H, B);
     for (const auto& l : m->layers) {
@@ -407,6 +411,8 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     m->gemv_ws_bytes = std::max<std::size_t>(ws, 256);
     m->gemv_ws = Buffer(m->gemv_ws_bytes);
     m->argmax_ws = Buffer(lfm3_argmax_workspace_bytes(B));
+    m->image = Buffer(lfm3_operand_image_bytes(H));
+    m->exps = Buffer(kMaxBatch * sizeof(int));
     m->ids = Buffer(B * 4);
     Check(hipDeviceSynchronize(), "model upload");
     *out = m.release();
@@ -607,28 +613,50 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
   float* hid = m.hidden.as<float>();
   float* out = m.out.as<float>();
   const std::uint32_t pld = std::uint32_t(m.proj_ld);
-  const auto gemv = [&](const Matrix& w, const float* in, std::uint32_t ldx,
-                        float* y, std::uint32_t ldy) {
-    CheckStatus(lfm3_q8_gemv(w.codes.p, w.scales.p, w.rows, w.cols, in, ldx, y,
-                             ldy, n, m.gemv_ws.p, m.gemv_ws_bytes, s));
+
+  // Narrow matrices (hidden rows) split K into parts whose partial sums the
+  // following residual norm adds in part order.
+  const auto partials = [&](const Matrix& w, const float* in,
+                            std::uint32_t ldx) -> std::uint32_t {
+    const std::uint32_t parts = lfm3_q8_gemv_parts(w.rows, w.cols);
+    CheckStatus(lfm3_q8_gemv_partials(w.codes.p, w.scales.p, w.rows, w.cols, in,
+                                      ldx, out, H, n, parts, s));
+    return parts;
+  };
+  std::uint32_t mixer_parts = 1;
+
+  // Normed rows go out as operand images; the convolution and attention
+  // outputs and the FFN hidden state are staged by their GEMVs.
+  void* image = m.image.p;
+  int* exps = m.exps.as<int>();
+  const auto gemv_image = [&](const Matrix& w, float* y, std::uint32_t ldy) {
+    CheckStatus(lfm3_q8_gemv_image(w.codes.p, w.scales.p, w.rows, w.cols, image,
+                                   exps, n, y, ldy, 1, s));
+  };
+  const auto norm_image = [&](std::uint32_t parts, const float* post,
+                              const float* weight, float* zrow) {
+    CheckStatus(lfm3_residual_norm_image(parts ? out : nullptr, parts ? parts : 1,
+                                         std::size_t(n) * H, post, x, weight, zrow,
+                                         image, exps, n, H, c.eps, s));
   };
 
   CheckStatus(lfm3_embed(m.embedding.codes.p, m.embedding.scales.p, c.vocab, H,
                          d_rt->tokens, n, x, s));
-  CheckStatus(lfm3_residual_norm(nullptr, nullptr, x, m.layers[0].norm.as<float>(),
-                                 z, n, H, c.eps, s));
+  norm_image(0, nullptr, m.layers[0].norm.as<float>(), nullptr);
   for (std::uint32_t il = 0; il < L; ++il) {
     const Layer& l = m.layers[il];
     if (l.type == LFM3_LAYER_CONV) {
-      gemv(l.in_proj, z, H, proj, pld);
+      gemv_image(l.in_proj, proj, pld);
+      // The convolution step spreads over (channel block, row) blocks; its
+      // FP32 output is staged by the out projection.
       CheckStatus(lfm3_conv_step_ragged(
           proj, pld, l.conv.as<float>(),
           reinterpret_cast<float* const*>(dev + conv_off) + il * kMaxBatch, a, H,
           n, H, c.conv_width, s));
-      gemv(l.out_proj, a, H, out, H);
+      mixer_parts = partials(l.out_proj, a, H);
     } else {
       const bool swa = l.type == LFM3_LAYER_SLIDING;
-      gemv(l.qkvg, z, H, proj, pld);
+      gemv_image(l.qkvg, proj, pld);
       const auto* kp = reinterpret_cast<std::uint16_t* const*>(dev + k_off) + il * kMaxBatch;
       const auto* vp = reinterpret_cast<std::uint16_t* const*>(dev + v_off) + il * kMaxBatch;
       const auto* cp = reinterpret_cast<const std::uint32_t*>(dev + cap_off) + il * kMaxBatch;
@@ -641,22 +669,22 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
           swa ? nullptr : m.factors.as<float>(), kp, vp, d_rt->positions, cp,
           items, std::uint32_t(swa ? n_swa : n_full), a, c.heads * D, n,
           c.heads, l.kv, D, c.eps, m.attn_ws.p, m.attn_ws_bytes, s));
-      gemv(l.attn_out, a, c.heads * D, out, H);
+      mixer_parts = partials(l.attn_out, a, c.heads * D);
     }
-    CheckStatus(lfm3_residual_norm(out, l.post_norm.as<float>(), x,
-                                   l.ffn_norm.as<float>(), z, n, H, c.eps, s));
-    CheckStatus(lfm3_q8_gemv_swiglu(l.ffn.codes.p, l.ffn.scales.p, F, H, z, H,
-                                    hid, F, n, m.gemv_ws.p, m.gemv_ws_bytes, s));
-    gemv(l.down, hid, F, out, H);
-    const float* next = il + 1 < L ? m.layers[il + 1].norm.as<float>()
-                                   : m.output_norm.as<float>();
-    CheckStatus(lfm3_residual_norm(out, l.post_ffn_norm.as<float>(), x, next, z,
-                                   n, H, c.eps, s));
+    norm_image(mixer_parts, l.post_norm.as<float>(), l.ffn_norm.as<float>(), nullptr);
+    CheckStatus(lfm3_q8_gemv_swiglu_image(l.ffn.codes.p, l.ffn.scales.p, F, H,
+                                          image, exps, n, hid, F, s));
+    const std::uint32_t ffn_parts = partials(l.down, hid, F);
+    const bool last = il + 1 == L;
+    // The last norm's FP32 rows are the frontier rows (engine.cpp:505-511).
+    norm_image(ffn_parts, l.post_ffn_norm.as<float>(),
+               last ? m.output_norm.as<float>() : m.layers[il + 1].norm.as<float>(),
+               last ? z : nullptr);
   }
-  // z holds the final-normed rows (engine.cpp:505): LM head, then each
-  // session's logits and frontier rows.
+  // LM head over the final-normed rows, then each session's logits and
+  // frontier rows.
   const Matrix& head = m.head();
-  gemv(head, z, H, m.logits.as<float>(), c.vocab);
+  gemv_image(head, m.logits.as<float>(), c.vocab);
   CheckStatus(LaunchScatterRows(m.logits.as<float>(), c.vocab, d_rt->logits, n,
                                 c.vocab, s));
   CheckStatus(LaunchScatterRows(z, H, d_rt->frontier, n, H, s));

@@ -69,17 +69,33 @@ __global__ void PackKernel(const std::uint8_t* __restrict__ src,
 // costs a device-scope fence, which writes back and invalidates the XCD's
 // L2.
 struct GemvPlan {
-  int row_tiles, nchunks, groups, RT, W, SPW;
+  int row_tiles, nchunks, groups, RT, W, SPW, parts;
 };
 
-GemvPlan PlanGemv(std::uint32_t rows, std::uint32_t cols, bool swiglu) {
+// Number of K parts a partial-sum launch of this shape takes: enough that
+// each part fits one LDS slice (32 chunks) and that about 512 blocks fill
+// the device, keeping at least 8 chunks a part.
+constexpr int kMaxGemvParts = 8;
+int GemvParts(std::uint32_t rows, std::uint32_t cols) {
+  const int tiles = int(RowTiles(rows)), nchunks = int(Chunks(cols));
+  int parts = std::min((nchunks + 31) / 32, kMaxGemvParts);
+  while (parts * 2 <= kMaxGemvParts && tiles * parts * 2 <= 512 &&
+         nchunks / (parts * 2) >= 8)
+    parts *= 2;
+  return parts;
+}
+
+GemvPlan PlanGemv(std::uint32_t rows, std::uint32_t cols, bool swiglu,
+                  int parts = 1) {
   GemvPlan p{};
   const int unit = swiglu ? 2 : 1;
+  p.parts = parts;
   p.row_tiles = int(RowTiles(rows)) * unit;
   p.nchunks = int(Chunks(cols));
+  const int nloc = (p.nchunks + parts - 1) / parts;
   p.SPW = 4;
-  p.W = p.nchunks <= 4 ? 1 : p.nchunks <= 8 ? 2 : p.nchunks <= 16 ? 4 : 8;
-  if (p.nchunks > 32)
+  p.W = nloc <= 4 ? 1 : nloc <= 8 ? 2 : nloc <= 16 ? 4 : 8;
+  if (nloc > 32)
     p.SPW = 5;  // slices of 40 chunks (80 KB of LDS operands), prefetched
   // Two 64 KB blocks fit a CU: about 512 blocks fill the device once. A
   // multi-slice block keeps two slices of weights in registers: one tile.
@@ -90,6 +106,58 @@ GemvPlan PlanGemv(std::uint32_t rows, std::uint32_t cols, bool swiglu) {
   p.RT = per * unit;
   p.groups = (p.row_tiles + p.RT - 1) / p.RT;
   return p;
+}
+
+// Kernel tail shared by the GEMVs: total[r] holds this lane's un-scaled
+// sums for A rows 4 (L / 16) + i (tokens hi 0-7 then lo 0-7) of tile r's
+// weight row L % 16. hi and lo add, then the W waves' partial sums add in
+// wave order through LDS (red: W * RT * 128 + RT * 128 floats), and the
+// block writes its rows (SwiGLU: tile 2j is gate, 2j + 1 up, rows j * 16
+// + n).
+template<int W, int RT, bool kSwiGLU>
+__device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int group,
+                                             int B, float* __restrict__ y, int ldy,
+                                             int rows_out) {
+  constexpr int T = W * 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tok0 = ((lane >> 4) & 1) * 4;
+  float* fin = red + W * RT * 128;
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float val = total[r][i];
+      val += __shfl_xor(val, 32, 64);
+      if (lane < 32)
+        red[(wave * RT + r) * 128 + (tok0 + i) * 16 + (lane & 15)] = val;
+    }
+  }
+  __syncthreads();
+  for (int o = tid; o < RT * 128; o += T) {
+    const int r = o / 128, idx = o % 128;
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+      sum += red[(w * RT + r) * 128 + idx];
+    fin[o] = sum;
+  }
+  __syncthreads();
+  if constexpr (kSwiGLU) {
+    for (int o = tid; o < (RT / 2) * 128; o += T) {
+      const int pr = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
+      const int row = (group * (RT / 2) + pr) * kTileRows + n;
+      const float gv = fin[2 * pr * 128 + idx], uv = fin[(2 * pr + 1) * 128 + idx];
+      if (tok < B && row < rows_out)
+        y[std::size_t(tok) * ldy + row] = (gv * (1.0f / (1.0f + expf(-gv)))) * uv;
+    }
+  } else {
+    for (int o = tid; o < RT * 128; o += T) {
+      const int r = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
+      const int row = (group * RT + r) * kTileRows + n;
+      if (tok < B && row < rows_out)
+        y[std::size_t(tok) * ldy + row] = fin[o];
+    }
+  }
 }
 
 // y[b][r] = sum_k W[r][k] x[b][k] for b < B <= 8. A block stages a K slice
@@ -105,21 +173,27 @@ GemvPlan PlanGemv(std::uint32_t rows, std::uint32_t cols, bool swiglu) {
 // slice is staged. Waves sum in wave order, so results do not depend on
 // scheduling.
 template<int W, int SPW, int RT, bool kSwiGLU>
-__launch_bounds__(W * 64) __global__
-    void Q8Gemv(const std::uint8_t* __restrict__ codes,
-                const Half* __restrict__ scales, int row_tiles, int nchunks,
-                int K, const float* __restrict__ x, int ldx, int B,
-                float* __restrict__ y, int ldy, int rows_out) {
+__launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(RT >= 4 ? 2 : 4)))
+__global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
+                       const Half* __restrict__ scales, int row_tiles,
+                       int nchunks, int K, const float* __restrict__ x, int ldx,
+                       int B, float* __restrict__ y, int ldy, int rows_out,
+                       std::size_t part_stride) {
   constexpr int T = W * 64, SLICE = W * SPW;
-  // SPW 4 plans cover K in one slice; SPW 5 plans loop over slices and
-  // prefetch the next slice's weights.
+  // SPW 4 plans cover a block's K range in one slice; SPW 5 plans loop over
+  // slices and prefetch the next slice's weights.
   constexpr bool kMulti = SPW > 4;
   __shared__ uint4 s_a[SLICE * 2 * 64];
   __shared__ float s_max[W][8];
   __shared__ int s_exp[8];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int group = blockIdx.x;
-  const int nslices = (nchunks + SLICE - 1) / SLICE;
+  // K part of this block (blockIdx.y of gridDim.y); part p writes its sums
+  // to y + p * part_stride.
+  const int c_begin = int(blockIdx.y) * nchunks / int(gridDim.y);
+  const int nloc = (int(blockIdx.y) + 1) * nchunks / int(gridDim.y) - c_begin;
+  y += std::size_t(blockIdx.y) * part_stride;
+  const int nslices = (nloc + SLICE - 1) / SLICE;
 
   // Weight tiles and scales of one slice: chunk wave + W j of the slice.
   uint4 q[RT][SPW], qn[RT][kMulti ? SPW : 1];
@@ -131,8 +205,8 @@ __launch_bounds__(W * 64) __global__
 #pragma unroll
       for (int j = 0; j < SPW; ++j) {
         const int chunk = slice * SLICE + wave + W * j;
-        if (tile < row_tiles && chunk < nchunks) {
-          const std::size_t off = std::size_t(tile) * nchunks + chunk;
+        if (tile < row_tiles && chunk < nloc) {
+          const std::size_t off = std::size_t(tile) * nchunks + c_begin + chunk;
           qq[r][j] = *reinterpret_cast<const uint4*>(codes + off * kTileCodeBytes + lane * 16);
           ss[r][j] = *reinterpret_cast<const unsigned*>(scales + off * kTileScales + (lane & 15) * 2);
         } else {
@@ -163,9 +237,10 @@ __launch_bounds__(W * 64) __global__
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
       const int cg = (tid + j * T) >> 3;
-      const int k = (slice * SLICE + (cg >> 3)) * kChunk + (cg & 7) * 8;
+      const int local = slice * SLICE + (cg >> 3);
+      const int k = (c_begin + local) * kChunk + (cg & 7) * 8;
       float4 lo4 = make_float4(0, 0, 0, 0), hi4 = lo4;
-      if (t < B && k < K) {
+      if (t < B && local < nloc && k < K) {
         const float4* src = reinterpret_cast<const float4*>(x + std::size_t(t) * ldx + k);
         lo4 = src[0];
         hi4 = src[1];
@@ -207,45 +282,47 @@ __launch_bounds__(W * 64) __global__
       s_a[idx + 8] = __builtin_bit_cast(uint4, lo);
     }
     __syncthreads();
-    // This wave's chunks of the slice: one MFMA per Q8_0 block.
-    h8 a[SPW][2];
-#pragma unroll
-    for (int j = 0; j < SPW; ++j) {
-      const int c = wave + W * j;
-      a[j][0] = __builtin_bit_cast(h8, s_a[(c * 2) * 64 + lane]);
-      a[j][1] = __builtin_bit_cast(h8, s_a[(c * 2 + 1) * 64 + lane]);
-    }
+    // This wave's chunks of the slice: one MFMA per Q8_0 block. Chunk
+    // outer, tile inner, so one chunk's A operands are live at a time.
     int ex[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       ex[i] = -(s_exp[tok0 + i] + (part ? 11 : 0));
+    f4 acc[RT];
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      if (group * RT + r >= row_tiles)
+    for (int r = 0; r < RT; ++r)
+      acc[r] = zero;
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      const int c = wave + W * j;
+      if (slice * SLICE + c >= nloc)
         continue;
-      f4 acc = zero;
+      const h8 a0 = __builtin_bit_cast(h8, s_a[(c * 2) * 64 + lane]);
+      const h8 a1 = __builtin_bit_cast(h8, s_a[(c * 2 + 1) * 64 + lane]);
 #pragma unroll
-      for (int j = 0; j < SPW; ++j) {
-        if (slice * SLICE + wave + W * j >= nchunks)
+      for (int r = 0; r < RT; ++r) {
+        if (group * RT + r >= row_tiles)
           continue;
         const h8 w0 = EightCodes(q[r][j].x, q[r][j].y);
         const h8 w1 = EightCodes(q[r][j].z, q[r][j].w);
-        const f4 p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j][0], w0, zero, 0, 0, 0);
-        const f4 p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j][1], w1, zero, 0, 0, 0);
+        const f4 p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, w0, zero, 0, 0, 0);
+        const f4 p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, w1, zero, 0, 0, 0);
         const float d0 = HalfBitsToFloat(sc[r][j] & 0xffffu);
         const float d1 = HalfBitsToFloat(sc[r][j] >> 16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          acc[i] = fmaf(d0, p0[i], acc[i]);
-          acc[i] = fmaf(d1, p1[i], acc[i]);
+          acc[r][i] = fmaf(d0, p0[i], acc[r][i]);
+          acc[r][i] = fmaf(d1, p1[i], acc[r][i]);
         }
       }
-      // D layout: lane L holds A rows 4 (L / 16) + i (tokens hi 0-7, then
-      // lo 0-7) of weight row L % 16; undo the slice's powers of two.
+    }
+    // D layout: lane L holds A rows 4 (L / 16) + i (tokens hi 0-7, then lo
+    // 0-7) of weight row L % 16; undo the slice's powers of two.
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        total[r][i] += ldexpf(acc[i], ex[i]);
-    }
+        total[r][i] += ldexpf(acc[r][i], ex[i]);
     if constexpr (kMulti) {
       if (slice + 1 < nslices) {
 #pragma unroll
@@ -259,55 +336,102 @@ __launch_bounds__(W * 64) __global__
     }
   }
 
-  // hi + lo, then the waves in wave order through LDS.
+  // hi + lo, then the waves in wave order through LDS (the operand image
+  // is free once every wave has its operands).
   __syncthreads();
-  float* red = reinterpret_cast<float*>(s_a);       // [W][RT][128]
-  float* fin = red + W * RT * 128;                  // [RT][128]
+  GemvEpilogue<W, RT, kSwiGLU>(total, reinterpret_cast<float*>(s_a), group, B,
+                               y, ldy, rows_out);
+}
+
+template<int W, int RT, bool kSwiGLU>
+__launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(RT >= 4 ? 2 : 4)))
+__global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
+                            const Half* __restrict__ scales, int row_tiles,
+                            int nchunks, const uint4* __restrict__ image,
+                            const int* __restrict__ exps, int B,
+                            float* __restrict__ y, int ldy, int rows_out,
+                            std::size_t part_stride) {
+  constexpr int SPW = 4, ROUND = W * SPW;  // chunks per wave per round
+  __shared__ float red[W * RT * 128 + RT * 128];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int group = blockIdx.x;
+  const int c_begin = int(blockIdx.y) * nchunks / int(gridDim.y);
+  const int nloc = (int(blockIdx.y) + 1) * nchunks / int(gridDim.y) - c_begin;
+  y += std::size_t(blockIdx.y) * part_stride;
+  const bool a_live = (lane & 7) < B;
+  const int part = lane >> 5, tok0 = ((lane >> 4) & 1) * 4;
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 acc[RT];
 #pragma unroll
-  for (int r = 0; r < RT; ++r) {
+  for (int r = 0; r < RT; ++r)
+    acc[r] = zero;
+  for (int base = 0; base < nloc; base += ROUND) {
+    uint4 q[RT][SPW];
+    unsigned sc[RT][SPW];
+    uint4 a[SPW][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float val = total[r][i];
-      val += __shfl_xor(val, 32, 64);
-      if (lane < 32)
-        red[(wave * RT + r) * 128 + (tok0 + i) * 16 + (lane & 15)] = val;
+    for (int j = 0; j < SPW; ++j) {
+      const int chunk = base + wave + W * j;
+      const bool live = chunk < nloc;
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        const int tile = group * RT + r;
+        if (live && tile < row_tiles) {
+          const std::size_t off = std::size_t(tile) * nchunks + c_begin + chunk;
+          q[r][j] = *reinterpret_cast<const uint4*>(codes + off * kTileCodeBytes + lane * 16);
+          sc[r][j] = *reinterpret_cast<const unsigned*>(scales + off * kTileScales + (lane & 15) * 2);
+        } else {
+          q[r][j] = make_uint4(0, 0, 0, 0);
+          sc[r][j] = 0;
+        }
+      }
+      const std::size_t at = std::size_t(c_begin + chunk) * 2 * 64 + lane;
+      a[j][0] = live && a_live ? image[at] : make_uint4(0, 0, 0, 0);
+      a[j][1] = live && a_live ? image[at + 64] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      if (base + wave + W * j >= nloc)
+        continue;
+      const h8 a0 = __builtin_bit_cast(h8, a[j][0]), a1 = __builtin_bit_cast(h8, a[j][1]);
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        if (group * RT + r >= row_tiles)
+          continue;
+        const h8 w0 = EightCodes(q[r][j].x, q[r][j].y);
+        const h8 w1 = EightCodes(q[r][j].z, q[r][j].w);
+        const f4 p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, w0, zero, 0, 0, 0);
+        const f4 p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, w1, zero, 0, 0, 0);
+        const float d0 = HalfBitsToFloat(sc[r][j] & 0xffffu);
+        const float d1 = HalfBitsToFloat(sc[r][j] >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[r][i] = fmaf(d0, p0[i], acc[r][i]);
+          acc[r][i] = fmaf(d1, p1[i], acc[r][i]);
+        }
+      }
     }
   }
-  __syncthreads();
-  for (int o = tid; o < RT * 128; o += T) {
-    const int r = o / 128, idx = o % 128;
-    float sum = 0.0f;
+  // D layout: lane L holds A rows 4 (L / 16) + i of weight row L % 16.
+  f4 total[RT];
 #pragma unroll
-    for (int w = 0; w < W; ++w)
-      sum += red[(w * RT + r) * 128 + idx];
-    fin[o] = sum;
+  for (int i = 0; i < 4; ++i) {
+    const int t = tok0 + i;
+    const int ex = -((t < B ? exps[t] : 0) + (part ? 11 : 0));
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+      total[r][i] = ldexpf(acc[r][i], ex);
   }
-  __syncthreads();
-  if constexpr (kSwiGLU) {
-    // Tile 2j is gate, tile 2j + 1 is up: the same rows j * 16 + n.
-    for (int o = tid; o < (RT / 2) * 128; o += T) {
-      const int pr = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
-      const int row = (group * (RT / 2) + pr) * kTileRows + n;
-      const float gv = fin[2 * pr * 128 + idx], uv = fin[(2 * pr + 1) * 128 + idx];
-      if (tok < B && row < rows_out)
-        y[std::size_t(tok) * ldy + row] = (gv * (1.0f / (1.0f + expf(-gv)))) * uv;
-    }
-  } else {
-    for (int o = tid; o < RT * 128; o += T) {
-      const int r = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
-      const int row = (group * RT + r) * kTileRows + n;
-      if (tok < B && row < rows_out)
-        y[std::size_t(tok) * ldy + row] = fin[o];
-    }
-  }
+  GemvEpilogue<W, RT, kSwiGLU>(total, red, group, B, y, ldy, rows_out);
 }
 
 template<int W, int SPW, int RT, bool kSwiGLU>
 void LaunchPlan(const GemvPlan& p, const std::uint8_t* c, const Half* s, int K,
                 const float* x, int ldx, int B, float* y, int ldy, int rows_out,
                 hipStream_t stream) {
-  Q8Gemv<W, SPW, RT, kSwiGLU><<<p.groups, W * 64, 0, stream>>>(
-      c, s, p.row_tiles, p.nchunks, K, x, ldx, B, y, ldy, rows_out);
+  Q8Gemv<W, SPW, RT, kSwiGLU><<<dim3(p.groups, p.parts), W * 64, 0, stream>>>(
+      c, s, p.row_tiles, p.nchunks, K, x, ldx, B, y, ldy, rows_out,
+      std::size_t(ldy) * B);
 }
 
 template<int W, int SPW, bool kSwiGLU>
@@ -335,12 +459,14 @@ void LaunchRT(const GemvPlan& p, const std::uint8_t* c, const Half* s, int K,
 template<bool kSwiGLU>
 int LaunchGemv(const void* codes, const void* scales, std::uint32_t rows,
                std::uint32_t cols, const float* x, std::uint32_t ldx, float* y,
-               std::uint32_t ldy, std::uint32_t batch, hipStream_t stream) {
+               std::uint32_t ldy, std::uint32_t batch, hipStream_t stream,
+               int parts = 1) {
   if (!codes || !scales || !x || !y || rows == 0 || cols == 0 ||
       cols % 32 || batch == 0 || batch > 8 || ldx % 4 || ldx < cols ||
-      ldy < rows || (reinterpret_cast<std::uintptr_t>(x) & 15))
+      ldy < rows || (reinterpret_cast<std::uintptr_t>(x) & 15) || parts < 1 ||
+      parts > int(Chunks(cols)))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 GEMV shape");
-  const GemvPlan p = PlanGemv(rows, cols, kSwiGLU);
+  const GemvPlan p = PlanGemv(rows, cols, kSwiGLU, parts);
   const auto* c = static_cast<const std::uint8_t*>(codes);
   const auto* s = static_cast<const Half*>(scales);
   const int K = int(cols), B = int(batch), lx = int(ldx), ly = int(ldy), ro = int(rows);
@@ -355,6 +481,59 @@ int LaunchGemv(const void* codes, const void* scales, std::uint32_t rows,
   else
     LaunchRT<1, 4, kSwiGLU>(p, c, s, K, x, lx, B, y, ly, ro, stream);
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 GEMV launch");
+}
+
+template<int W, int RT, bool kSwiGLU>
+void LaunchImagePlan(const GemvPlan& p, const std::uint8_t* c, const Half* s,
+                     const uint4* image, const int* exps, int B, float* y,
+                     int ldy, int rows_out, hipStream_t stream) {
+  Q8GemvImage<W, RT, kSwiGLU><<<dim3(p.groups, p.parts), W * 64, 0, stream>>>(
+      c, s, p.row_tiles, p.nchunks, image, exps, B, y, ldy, rows_out,
+      std::size_t(ldy) * B);
+}
+
+template<int W, bool kSwiGLU>
+void LaunchImageRT(const GemvPlan& p, const std::uint8_t* c, const Half* s,
+                   const uint4* image, const int* exps, int B, float* y, int ldy,
+                   int rows_out, hipStream_t stream) {
+  if constexpr (kSwiGLU) {
+    LaunchImagePlan<W, 2, true>(p, c, s, image, exps, B, y, ldy, rows_out, stream);
+  } else {
+    if (p.RT == 1)
+      LaunchImagePlan<W, 1, false>(p, c, s, image, exps, B, y, ldy, rows_out, stream);
+    else
+      LaunchImagePlan<W, 2, false>(p, c, s, image, exps, B, y, ldy, rows_out, stream);
+  }
+}
+
+template<bool kSwiGLU>
+int LaunchGemvImage(const void* codes, const void* scales, std::uint32_t rows,
+                    std::uint32_t cols, const void* image, const int* exps,
+                    std::uint32_t batch, float* y, std::uint32_t ldy,
+                    std::uint32_t parts, hipStream_t stream) {
+  if (!codes || !scales || !image || !exps || !y || rows == 0 || cols == 0 ||
+      cols % 32 || batch == 0 || batch > 8 || ldy < rows || parts < 1 ||
+      parts > Chunks(cols) || (kSwiGLU && parts != 1) ||
+      (reinterpret_cast<std::uintptr_t>(image) & 15))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 operand-image GEMV");
+  GemvPlan p = PlanGemv(rows, cols, kSwiGLU, int(parts));
+  // Rounds of W * 4 chunks need no LDS: keep two tiles (one SwiGLU pair)
+  // at most, so two blocks of eight waves fit a CU.
+  p.RT = kSwiGLU ? 2 : std::min(p.RT, 2);
+  p.groups = (p.row_tiles + p.RT - 1) / p.RT;
+  const auto* c = static_cast<const std::uint8_t*>(codes);
+  const auto* s = static_cast<const Half*>(scales);
+  const auto* im = static_cast<const uint4*>(image);
+  const int B = int(batch), ly = int(ldy), ro = int(rows);
+  if (p.W == 8)
+    LaunchImageRT<8, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream);
+  else if (p.W == 4)
+    LaunchImageRT<4, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream);
+  else if (p.W == 2)
+    LaunchImageRT<2, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream);
+  else
+    LaunchImageRT<1, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream);
+  return HipStatus(hipGetLastError(), "LFM3 Q8_0 operand-image GEMV launch");
 }
 
 // Embedding rows from the tiled table: element k of row r sits in tile
@@ -477,6 +656,43 @@ int lfm3_q8_gemv(const void* codes, const void* scales, std::uint32_t rows,
   (void)workspace_bytes;
   return LaunchGemv<false>(codes, scales, rows, cols, x, ldx, y, ldy, batch,
                            static_cast<hipStream_t>(stream));
+}
+
+std::uint32_t lfm3_q8_gemv_parts(std::uint32_t rows, std::uint32_t cols) {
+  if (!rows || !cols)
+    return 1;
+  return std::uint32_t(GemvParts(rows, cols));
+}
+
+int lfm3_q8_gemv_partials(const void* codes, const void* scales,
+                          std::uint32_t rows, std::uint32_t cols,
+                          const float* x, std::uint32_t ldx, float* y,
+                          std::uint32_t ldy, std::uint32_t batch,
+                          std::uint32_t parts, void* stream) {
+  return LaunchGemv<false>(codes, scales, rows, cols, x, ldx, y, ldy, batch,
+                           static_cast<hipStream_t>(stream), int(parts));
+}
+
+std::size_t lfm3_operand_image_bytes(std::uint32_t cols) {
+  return std::size_t(Chunks(cols)) * 2 * 64 * 16;
+}
+
+int lfm3_q8_gemv_image(const void* codes, const void* scales,
+                       std::uint32_t rows, std::uint32_t cols,
+                       const void* image, const int* exps,
+                       std::uint32_t batch, float* y, std::uint32_t ldy,
+                       std::uint32_t parts, void* stream) {
+  return LaunchGemvImage<false>(codes, scales, rows, cols, image, exps, batch,
+                                y, ldy, parts, static_cast<hipStream_t>(stream));
+}
+
+int lfm3_q8_gemv_swiglu_image(const void* codes, const void* scales,
+                              std::uint32_t rows, std::uint32_t cols,
+                              const void* image, const int* exps,
+                              std::uint32_t batch, float* y, std::uint32_t ldy,
+                              void* stream) {
+  return LaunchGemvImage<true>(codes, scales, rows, cols, image, exps, batch,
+                               y, ldy, 1, static_cast<hipStream_t>(stream));
 }
 
 int lfm3_q8_gemv_swiglu(const void* codes, const void* scales,

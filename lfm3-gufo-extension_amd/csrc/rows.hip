@@ -26,10 +26,10 @@ int HipStatus(hipError_t e, const char* what) {
 
 namespace {
 
-constexpr int kNormThreads = 256, kNormItems = 16;
+constexpr int kNormThreads = 1024, kNormItems = 4, kNormParts = 8;
 
-// Block sum of one value per thread: wave butterflies then the four wave
-// sums in wave order.
+// Block sum of one value per thread: wave butterflies then the wave sums
+// in wave order.
 __device__ float BlockSum(float v, float* scratch) {
   v = WaveSum(v);
   const int wave = threadIdx.x >> 6;
@@ -43,46 +43,100 @@ __device__ float BlockSum(float v, float* scratch) {
   return total;
 }
 
+// Writes one token's row (H floats in LDS) into a GEMV operand image (see
+// lfm3_q8_gemv_image): exponent e puts the row maximum in [2^14, 2^15),
+// hi = fp16(x 2^e), lo = fp16((x 2^e - hi) 2^11); columns past H (the tail
+// of the last 64-column chunk) are written as zeros.
+__device__ void WriteOperandRow(const float* __restrict__ s_row, int H, int t,
+                                float maximum, uint4* __restrict__ image,
+                                int* __restrict__ exps) {
+  const int e = maximum > 0.0f ? 14 - ilogbf(maximum) : 0;
+  if (threadIdx.x == 0)
+    exps[t] = e;
+  const int groups = (H + kChunk - 1) / kChunk * 8;
+  for (int cg = threadIdx.x; cg < groups; cg += blockDim.x) {
+    h8 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int k = cg * 8 + i;
+      const float sv = k < H ? ldexpf(s_row[k], e) : 0.0f;
+      const _Float16 h = static_cast<_Float16>(sv);
+      hi[i] = h;
+      lo[i] = static_cast<_Float16>((sv - float(h)) * 2048.0f);
+    }
+    const int idx = ((cg >> 3) * 2 + ((cg >> 2) & 1)) * 64 + 16 * (cg & 3) + t;
+    image[idx] = __builtin_bit_cast(uint4, hi);
+    image[idx + 8] = __builtin_bit_cast(uint4, lo);
+  }
+}
+
+__device__ float BlockMax(float v, float* scratch) {
+  v = WaveMax(v);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0)
+    scratch[wave] = v;
+  __syncthreads();
+  float m = 0.0f;
+  for (int w = 0; w < int(blockDim.x >> 6); ++w)
+    m = fmaxf(m, scratch[w]);
+  return m;
+}
+
 // reference.cpp:20-28 / hip/ops.hip:905-970 semantics: x += post(branch),
 // then z = x / sqrt(mean(x^2) + eps) * w, each product rounded as the
-// reference's x * scale * weight. Every load is issued before the first
-// reduction, so the row costs one memory round trip.
+// reference's x * scale * weight. The branch may arrive as `parts` K-part
+// partial sums of a GEMV (lfm3_q8_gemv_partials), part_stride floats
+// apart, added in part order. Every load, of every part, is issued before
+// the first reduction, so the row costs one memory round trip.
+// With an operand image, the normed row also goes out as the next GEMV's
+// MFMA A operand (z may then be null).
 __launch_bounds__(kNormThreads) __global__
-    void ResidualNormKernel(const float* __restrict__ branch,
+    void ResidualNormKernel(const float* __restrict__ branch, int parts,
+                            std::size_t part_stride,
                             const float* __restrict__ post,
                             float* __restrict__ x,
                             const float* __restrict__ weight,
-                            float* __restrict__ z, int H, float eps) {
+                            float* __restrict__ z, int H, float eps,
+                            uint4* __restrict__ image, int* __restrict__ exps) {
   __shared__ float scratch[kNormThreads / 64];
+  __shared__ float s_row[kNormThreads * kNormItems];
   const int row = blockIdx.x, tid = threadIdx.x;
-  const int items = (H + kNormThreads - 1) / kNormThreads;
   float* xr = x + std::size_t(row) * H;
-  float v[kNormItems], b[kNormItems], pw[kNormItems], nw[kNormItems];
+  float v[kNormItems], b[kNormParts][kNormItems], pw[kNormItems], nw[kNormItems];
 #pragma unroll
   for (int i = 0; i < kNormItems; ++i) {
     const int k = tid + kNormThreads * i;
-    const bool live = i < items && k < H;
+    const bool live = k < H;
     v[i] = live ? xr[k] : 0.0f;
-    b[i] = live && branch ? branch[std::size_t(row) * H + k] : 0.0f;
     pw[i] = live && post ? post[k] : 0.0f;
     nw[i] = live && weight ? weight[k] : 0.0f;
+#pragma unroll
+    for (int p = 0; p < kNormParts; ++p)
+      b[p][i] = live && branch && p < parts
+                    ? branch[p * part_stride + std::size_t(row) * H + k]
+                    : 0.0f;
   }
   if (branch) {
-    if (post) {
-      float squares = 0.0f;
+    float squares = 0.0f;
 #pragma unroll
-      for (int i = 0; i < kNormItems; ++i)
-        squares = fmaf(b[i], b[i], squares);
+    for (int i = 0; i < kNormItems; ++i) {
+#pragma unroll
+      for (int p = 1; p < kNormParts; ++p)
+        b[0][i] += b[p][i];
+      squares = fmaf(b[0][i], b[0][i], squares);
+    }
+    if (post) {
       const float scale = 1.0f / sqrtf(BlockSum(squares, scratch) / float(H) + eps);
 #pragma unroll
       for (int i = 0; i < kNormItems; ++i)
-        b[i] = (b[i] * scale) * pw[i];
+        b[0][i] = (b[0][i] * scale) * pw[i];
     }
 #pragma unroll
     for (int i = 0; i < kNormItems; ++i) {
       const int k = tid + kNormThreads * i;
-      v[i] = v[i] + b[i];
-      if (i < items && k < H)
+      v[i] = v[i] + b[0][i];
+      if (k < H)
         xr[k] = v[i];
     }
   }
@@ -93,12 +147,22 @@ __launch_bounds__(kNormThreads) __global__
   for (int i = 0; i < kNormItems; ++i)
     squares = fmaf(v[i], v[i], squares);
   const float scale = 1.0f / sqrtf(BlockSum(squares, scratch) / float(H) + eps);
+  float maximum = 0.0f;
 #pragma unroll
   for (int i = 0; i < kNormItems; ++i) {
     const int k = tid + kNormThreads * i;
-    if (i < items && k < H)
-      z[std::size_t(row) * H + k] = (v[i] * scale) * nw[i];
+    const float zv = (v[i] * scale) * nw[i];
+    if (k < H) {
+      if (z)
+        z[std::size_t(row) * H + k] = zv;
+      s_row[k] = zv;
+      maximum = fmaxf(maximum, fabsf(zv));
+    }
   }
+  if (!image)
+    return;
+  maximum = BlockMax(maximum, scratch);  // its barriers publish s_row
+  WriteOperandRow(s_row, H, row, maximum, image, exps);
 }
 
 // reference.cpp:85-101: one owner per (row, channel); the window sum keeps
@@ -124,6 +188,42 @@ __global__ void ConvStepKernel(const float* __restrict__ p, int ldp,
     own[t - 1] = own[t];
   own[L - 2] = bx;
   y[std::size_t(row) * ldy + ch] = sum * pr[H + ch];
+}
+
+// ConvStepKernel with one block per row, writing the output row as the
+// out projection's operand image (y, when given, also gets the FP32 row).
+// Same expressions and order, so outputs and history stay bit-identical.
+__launch_bounds__(kNormThreads) __global__
+    void ConvRowImageKernel(const float* __restrict__ p, int ldp,
+                            const float* __restrict__ taps,
+                            float* const* __restrict__ history,
+                            float* __restrict__ y, int ldy, int H, int L,
+                            uint4* __restrict__ image, int* __restrict__ exps) {
+#pragma clang fp contract(off)
+  __shared__ float scratch[kNormThreads / 64];
+  __shared__ float s_row[kNormThreads * kNormItems];
+  const int row = blockIdx.x;
+  const float* pr = p + std::size_t(row) * ldp;
+  float maximum = 0.0f;
+  for (int ch = threadIdx.x; ch < H; ch += kNormThreads) {
+    float* own = history[row] + std::size_t(ch) * (L - 1);
+    const float bx = pr[ch] * pr[2 * H + ch];
+    const float* w = taps + std::size_t(ch) * L;
+    float sum = 0.0f;
+    for (int t = 0; t < L - 1; ++t)
+      sum += w[t] * own[t];
+    sum += w[L - 1] * bx;
+    for (int t = 1; t < L - 1; ++t)
+      own[t - 1] = own[t];
+    own[L - 2] = bx;
+    const float out = sum * pr[H + ch];
+    if (y)
+      y[std::size_t(row) * ldy + ch] = out;
+    s_row[ch] = out;
+    maximum = fmaxf(maximum, fabsf(out));
+  }
+  maximum = BlockMax(maximum, scratch);
+  WriteOperandRow(s_row, H, row, maximum, image, exps);
 }
 
 // Per-head RMSNorm + paired RoPE + F16 store. A block is one row and the
@@ -263,15 +363,59 @@ extern "C" {
 
 const char* lfm3_last_error(void) { return g_error.c_str(); }
 
+int lfm3_residual_norm_parts(const float* branch, std::uint32_t parts,
+                             std::size_t part_stride, const float* post_norm,
+                             float* x, const float* norm, float* z,
+                             std::uint32_t rows, std::uint32_t hidden,
+                             float eps, void* stream) {
+  if (!x || !rows || !hidden || hidden > kNormThreads * kNormItems ||
+      (norm && !z) || !parts || parts > kNormParts ||
+      (parts > 1 && part_stride < std::size_t(rows) * hidden))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 residual norm shape");
+  ResidualNormKernel<<<rows, kNormThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      branch, int(parts), part_stride, branch ? post_norm : nullptr, x, norm, z,
+      int(hidden), eps, nullptr, nullptr);
+  return HipStatus(hipGetLastError(), "LFM3 residual norm launch");
+}
+
+int lfm3_residual_norm_image(const float* branch, std::uint32_t parts,
+                             std::size_t part_stride, const float* post_norm,
+                             float* x, const float* norm, float* z, void* image,
+                             int* exps, std::uint32_t rows,
+                             std::uint32_t hidden, float eps, void* stream) {
+  if (!x || !norm || !image || !exps || !rows || rows > 8 || !hidden ||
+      hidden % 32 || hidden > kNormThreads * kNormItems || !parts ||
+      parts > kNormParts || (parts > 1 && part_stride < std::size_t(rows) * hidden) ||
+      (reinterpret_cast<std::uintptr_t>(image) & 15))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 residual norm image shape");
+  ResidualNormKernel<<<rows, kNormThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      branch, int(parts), part_stride, branch ? post_norm : nullptr, x, norm, z,
+      int(hidden), eps, static_cast<uint4*>(image), exps);
+  return HipStatus(hipGetLastError(), "LFM3 residual norm launch");
+}
+
+int lfm3_conv_step_ragged_image(const float* p, std::uint32_t ldp,
+                                const float* taps, float* const* history,
+                                float* y, std::uint32_t ldy, void* image,
+                                int* exps, std::uint32_t rows,
+                                std::uint32_t hidden, std::uint32_t width,
+                                void* stream) {
+  if (!p || !taps || !history || !image || !exps || !rows || rows > 8 ||
+      !hidden || hidden % 32 || hidden > kNormThreads * kNormItems ||
+      width < 2 || width > 32 || ldp < 3 * hidden || (y && ldy < hidden) ||
+      (reinterpret_cast<std::uintptr_t>(image) & 15))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 convolution image shape");
+  ConvRowImageKernel<<<rows, kNormThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      p, int(ldp), taps, history, y, int(ldy), int(hidden), int(width),
+      static_cast<uint4*>(image), exps);
+  return HipStatus(hipGetLastError(), "LFM3 convolution launch");
+}
+
 int lfm3_residual_norm(const float* branch, const float* post_norm, float* x,
                        const float* norm, float* z, std::uint32_t rows,
                        std::uint32_t hidden, float eps, void* stream) {
-  if (!x || !rows || !hidden || hidden > kNormThreads * kNormItems ||
-      (norm && !z))
-    return Fail(LFM3_E_INVALID, "unsupported LFM3 residual norm shape");
-  ResidualNormKernel<<<rows, kNormThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      branch, branch ? post_norm : nullptr, x, norm, z, int(hidden), eps);
-  return HipStatus(hipGetLastError(), "LFM3 residual norm launch");
+  return lfm3_residual_norm_parts(branch, 1, 0, post_norm, x, norm, z, rows,
+                                  hidden, eps, stream);
 }
 
 int lfm3_conv_step_ragged(const float* p, std::uint32_t ldp, const float* taps,

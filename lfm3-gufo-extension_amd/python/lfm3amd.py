@@ -53,6 +53,14 @@ _SIGS = {
     "lfm3_q8_pack_device": (i32, [vp, u32, u32, vp, vp, u32, u32, vp]),
     "lfm3_gemv_workspace_bytes": (sz, [u32, u32, u32]),
     "lfm3_q8_gemv": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, u32, vp, sz, vp]),
+    "lfm3_q8_gemv_parts": (u32, [u32, u32]),
+    "lfm3_q8_gemv_partials": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, u32, u32, vp]),
+    "lfm3_residual_norm_parts": (i32, [vp, u32, sz, vp, vp, vp, vp, u32, u32, f32, vp]),
+    "lfm3_operand_image_bytes": (sz, [u32]),
+    "lfm3_q8_gemv_image": (i32, [vp, vp, u32, u32, vp, vp, u32, vp, u32, u32, vp]),
+    "lfm3_q8_gemv_swiglu_image": (i32, [vp, vp, u32, u32, vp, vp, u32, vp, u32, vp]),
+    "lfm3_residual_norm_image": (i32, [vp, u32, sz, vp, vp, vp, vp, vp, vp, u32, u32, f32, vp]),
+    "lfm3_conv_step_ragged_image": (i32, [vp, u32, vp, vp, vp, u32, vp, vp, u32, u32, u32, vp]),
     "lfm3_q8_gemv_swiglu": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, u32, vp, sz, vp]),
     "lfm3_residual_norm": (i32, [vp, vp, vp, vp, vp, u32, u32, f32, vp]),
     "lfm3_embed": (i32, [vp, vp, u32, u32, vp, u32, vp, vp]),

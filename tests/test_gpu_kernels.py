@@ -346,3 +346,122 @@ def test_gemv_shapes_share_one_workspace():
                                          M, B, shared.addr, shared.nbytes, None))
             L.synchronize()
             assert np.array_equal(dy.download(np.float32, B * M).reshape(B, M), fresh), (M, K, B)
+
+
+# ------------------------------------------------- partials, operand images
+
+def decode_image(image: np.ndarray, exps: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """Inverse of the operand-image layout: (hi + lo 2^-11) 2^-e per token."""
+    nch = (cols + 63) // 64
+    lanes = image.view(np.float16).reshape(nch, 2, 4, 16, 8).astype(np.float64)  # c, b, g, m, i
+    out = np.zeros((rows, nch * 64))
+    for t in range(rows):
+        hi, lo = lanes[:, :, :, t, :], lanes[:, :, :, 8 + t, :]
+        val = (hi + lo / 2048.0) * 2.0 ** (-int(exps[t]))
+        out[t] = val.reshape(nch * 64)  # c, b, g, i -> 64 c + 32 b + 8 g + i
+    return out[:, :cols]
+
+
+@pytest.mark.parametrize("B", [1, 3, 8])
+def test_norm_image_feeds_gemv_bit_exactly(B):
+    """lfm3_residual_norm_image on K-part partial branches: x and z follow the
+    oracle's residual + RMSNorm, the image decodes to z, and the image GEMV
+    (plain, partials, SwiGLU) equals the FP32 GEMV of the same z bit for bit."""
+    H, M, F, parts = 2048, 3088, 512, 4
+    x = L.normal(SEED, f"ni.x{B}", B * H, 0, 3).reshape(B, H)
+    br = L.normal(SEED, f"ni.b{B}", parts * B * H, 0, 1).reshape(parts, B, H)
+    post = L.normal(SEED, "ni.post", H, 1, 0.02)
+    wn = L.normal(SEED, "ni.w", H, 1, 0.02)
+    dx, dbr = L.DeviceBuffer.of(x), L.DeviceBuffer.of(br)
+    dpost, dwn = L.DeviceBuffer.of(post), L.DeviceBuffer.of(wn)
+    dz = L.DeviceBuffer(B * H * 4)
+    img = L.DeviceBuffer(L.lib().lfm3_operand_image_bytes(H))
+    L.hip_check(L.hip().hipMemset(img.addr, 0x7f, img.nbytes))  # poison: every word is rewritten
+    ex = L.DeviceBuffer(32)
+    L.check(L.lib().lfm3_residual_norm_image(dbr.addr, parts, B * H, dpost.addr, dx.addr, dwn.addr,
+                                             dz.addr, img.addr, ex.addr, B, H, 1e-5, None))
+    L.synchronize()
+    gx = dx.download(np.float32, B * H).reshape(B, H)
+    gz = dz.download(np.float32, B * H).reshape(B, H)
+    branch = br[0] + br[1] + br[2] + br[3]  # part order
+    for r in range(B):
+        wx = x[r] + O.norm(branch[r], post, 1e-5)
+        np.testing.assert_allclose(gx[r], wx, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(gz[r], O.norm(wx, wn, 1e-5), rtol=1e-5, atol=1e-6)
+    image = img.download(np.uint8, img.nbytes)
+    exps = ex.download(np.int32, 8)
+    dec = decode_image(image, exps, B, H)
+    assert np.all(np.abs(dec - gz) <= np.abs(gz).max(axis=1, keepdims=True) * 2.0 ** -22)
+    # plain and K-part image GEMVs against the FP32 GEMV of z
+    w = L.q8(SEED, "ni.W", M, H)
+    m = DeviceMatrix(w, M, H)
+    want = gemv(m, gz)
+    dy = L.DeviceBuffer(B * M * 4)
+    L.check(L.lib().lfm3_q8_gemv_image(m.codes.addr, m.scales.addr, M, H, img.addr, ex.addr, B,
+                                       dy.addr, M, 1, None))
+    L.synchronize()
+    assert np.array_equal(dy.download(np.float32, B * M).reshape(B, M), want)
+    k_parts = 4
+    dp = L.DeviceBuffer(k_parts * B * M * 4)
+    L.check(L.lib().lfm3_q8_gemv_image(m.codes.addr, m.scales.addr, M, H, img.addr, ex.addr, B,
+                                       dp.addr, M, k_parts, None))
+    L.synchronize()
+    got = dp.download(np.float32, k_parts * B * M).reshape(k_parts, B, M).sum(axis=0, dtype=np.float64)
+    ok, err = within(got, O.mat(O.q8_tensor(w, M, H), gz))
+    assert ok, err
+    # SwiGLU pair
+    g, u = L.q8(SEED, "ni.g", F, H), L.q8(SEED, "ni.u", F, H)
+    ms = DeviceMatrix(g, F, H, interleave_with=u)
+    want = gemv(ms, gz, swiglu=True)
+    dh = L.DeviceBuffer(B * F * 4)
+    L.check(L.lib().lfm3_q8_gemv_swiglu_image(ms.codes.addr, ms.scales.addr, F, H, img.addr,
+                                              ex.addr, B, dh.addr, F, None))
+    L.synchronize()
+    assert np.array_equal(dh.download(np.float32, B * F).reshape(B, F), want)
+
+
+@pytest.mark.parametrize("M,K,B", [(2048, 7680, 8), (2048, 2048, 5), (64, 96, 2)])
+def test_gemv_partials_sum_to_the_product(M, K, B):
+    parts = L.lib().lfm3_q8_gemv_parts(M, K)
+    assert 1 <= parts <= 8
+    w = L.q8(SEED, f"gp.{M}x{K}", M, K)
+    m = DeviceMatrix(w, M, K)
+    x = L.normal(SEED, f"gp.x{M}x{K}", B * K).reshape(B, K)
+    dx = L.DeviceBuffer.of(x)
+    want = O.mat(O.q8_tensor(w, M, K), x)
+    for p in sorted({1, parts, min(3, (K + 63) // 64)}):
+        dy = L.DeviceBuffer(p * B * M * 4)
+        L.check(L.lib().lfm3_q8_gemv_partials(m.codes.addr, m.scales.addr, M, K, dx.addr, K,
+                                              dy.addr, M, B, p, None))
+        L.synchronize()
+        got = dy.download(np.float32, p * B * M).reshape(p, B, M)
+        acc = got[0].copy()
+        for q in range(1, p):
+            acc = acc + got[q]
+        ok, err = within(acc, want)
+        assert ok, (p, err)
+
+
+def test_conv_row_image_bit_exact():
+    """Row-per-block convolution writing the out projection's operand image:
+    outputs and histories equal the oracle's bit for bit."""
+    H, Lw, n = 2048, 7, 8
+    p = L.normal(SEED, "cri.p", n * 3 * H).reshape(n, 3 * H)
+    taps = L.normal(SEED, "cri.taps", H * Lw, 0, 0.1)
+    hist = [L.normal(SEED, f"cri.h{i}", H * (Lw - 1)) for i in range(n)]
+    dh = [L.DeviceBuffer.of(h) for h in hist]
+    table = pointer_table([b.addr for b in dh])
+    dp, dt = L.DeviceBuffer.of(p), L.DeviceBuffer.of(taps)
+    dy = L.DeviceBuffer(n * H * 4)
+    img = L.DeviceBuffer(L.lib().lfm3_operand_image_bytes(H))
+    ex = L.DeviceBuffer(32)
+    L.check(L.lib().lfm3_conv_step_ragged_image(dp.addr, 3 * H, dt.addr, table.addr, dy.addr, H,
+                                                img.addr, ex.addr, n, H, Lw, None))
+    L.synchronize()
+    y = dy.download(np.float32, n * H).reshape(n, H)
+    for r in range(n):
+        want_y, want_h = O.conv_step(p[r], taps, hist[r], H, Lw)
+        assert np.array_equal(y[r], want_y)
+        assert np.array_equal(dh[r].download(np.float32, H * (Lw - 1)), want_h)
+    dec = decode_image(img.download(np.uint8, img.nbytes), ex.download(np.int32, 8), n, H)
+    assert np.all(np.abs(dec - y) <= np.abs(y).max(axis=1, keepdims=True) * 2.0 ** -22)
