@@ -116,6 +116,41 @@ int lfm3_q8_gemv_swiglu(const void* codes, const void* scales, uint32_t rows,
                         size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------
+ * Prompt projections (n >= 16 rows of one session) on MFMA.
+ * ------------------------------------------------------------------- */
+/* FP16 row-scaled activations (hip/q8_prefill.hpp:27-74): per row
+   e = 14 - ilogb(max |x|) (0 for a zero row), out = fp16(x 2^e), scale =
+   2^-e. out rows have lda halves (lda % 64 == 0, lda >= cols; the tail is
+   zeroed). With row_max (FP32 bits of each row's maximum, e.g. from
+   lfm3_q8_gemm_swiglu) the row scan is skipped.
+   Replaces: HalfRows / HalfRowsFromMax (q8_prefill.hpp:30-74). */
+int lfm3_half_rows(const float* x, uint32_t ldx, const unsigned* row_max,
+                   uint16_t* out, uint32_t lda, float* scale, uint32_t rows,
+                   uint32_t cols, void* stream);
+/* Y[t][r] = scale[t] * sum over Q8_0 blocks of d * (exact code x fp16 dot
+   in FP32), one FP32 fma per block; tokens rows of activations a (lda
+   halves each, chunk tails zero) with their scales. K splits into `parts`
+   (1..8) ranges written to y + p * tokens * ldy; the consumer adds the
+   parts in part order. lfm3_q8_gemm_parts gives this library's choice.
+   Replaces: gpu::Project / gpu::Dense for prompt rows (LaunchSplit,
+   hip/ops.hip:2019-2119; RegQ8Gemm, q8_prefill.hpp:415-645). */
+uint32_t lfm3_q8_gemm_parts(uint32_t rows, uint32_t cols, uint32_t tokens,
+                            int swiglu);
+int lfm3_q8_gemm(const void* codes, const void* scales, uint32_t rows,
+                 uint32_t cols, const uint16_t* a, uint32_t lda,
+                 const float* a_scale, uint32_t tokens, float* y, uint32_t ldy,
+                 uint32_t parts, void* stream);
+/* Gate/up over a stride-2 interleaved pair with the SwiGLU epilogue
+   (q8_prefill.hpp:622-635): y = silu(g) * u, and atomicMax of each token
+   row's max |y| (FP32 bits) into row_max (NULL: skipped), which must hold
+   zeros before the call. Replaces: gpu::ProjectFfn's first half for prompt
+   rows (hip/ops.hip:2205-2222). */
+int lfm3_q8_gemm_swiglu(const void* codes, const void* scales, uint32_t rows,
+                        uint32_t cols, const uint16_t* a, uint32_t lda,
+                        const float* a_scale, uint32_t tokens, float* y,
+                        uint32_t ldy, unsigned* row_max, void* stream);
+
+/* ---------------------------------------------------------------------
  * Row operations.
  * ------------------------------------------------------------------- */
 /* x[i] += post_norm(branch[i]) (branch/post may be NULL), then

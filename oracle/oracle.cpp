@@ -293,6 +293,22 @@ void orc_attention_step(float* q, float* k, const float* v, const float* gate,
   AttentionRead(q, gate, ck, cv, heads, kv_heads, D, position, capacity,
                 sliding ? window : 0, out);
 }
+void orc_half_rows(const float* x, size_t rows, size_t cols, float* inputs,
+                   int* exps) {
+  for (size_t r = 0; r < rows; ++r) {
+    const float* row = x + r * cols;
+    float maximum = 0;
+    for (size_t k = 0; k < cols; ++k)
+      maximum = std::max(maximum, std::fabs(row[k]));
+    const int e = maximum > 0 ? 14 - std::ilogb(maximum) : 0;
+    if (exps)
+      exps[r] = e;
+    for (size_t k = 0; k < cols; ++k)
+      inputs[r * cols + k] =
+          std::ldexp(HalfToFloat(FloatToHalf(std::ldexp(row[k], e))), -e);
+  }
+}
+
 void orc_swiglu(float* gate, const float* up, size_t n) {
   for (size_t i = 0; i < n; ++i)
     gate[i] = (gate[i] / (1 + std::exp(-gate[i]))) * up[i];

@@ -113,6 +113,12 @@ void orc_attention_read(const float* q, const float* gate,
                         uint32_t heads, uint32_t kv_heads, uint32_t dim,
                         uint32_t position, uint32_t capacity, uint32_t window,
                         float* out);
+/* Prompt-path activations (hip/q8_prefill.hpp:27-51, as tests/ops_test.cpp
+   :55-68 restates them): per row e = 14 - ilogb(max |x|) (0 for a zero
+   row); inputs[k] = ldexp(float(binary16(ldexp(x[k], e))), -e). Writes the
+   effective inputs and, when exps is not NULL, e per row. */
+void orc_half_rows(const float* x, size_t rows, size_t cols, float* inputs,
+                   int* exps);
 /* reference.cpp:151-160 SwiGLU: (g / (1 + exp(-g))) * u. */
 void orc_swiglu(float* gate, const float* up, size_t n);
 /* First index of the maximum (std::max_element). */

@@ -44,6 +44,7 @@ _SIGS = {
     "orc_attention_step": (None, [vp, vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32,
                                   u32, u32, f32, i32, f32, i32, vp]),
     "orc_attention_read": (None, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp]),
+    "orc_half_rows": (None, [vp, sz, sz, vp, vp]),
     "orc_swiglu": (None, [vp, vp, sz]),
     "orc_argmax": (u32, [vp, sz]),
     "orc_model_create": (vp, [C.POINTER(Config), C.POINTER(Tensor), sz]),
@@ -175,6 +176,16 @@ def attention_step(q, k, v, gate, q_norm, k_norm, factors, cache_k, cache_v, hea
                              _p(cache_k), _p(cache_v), heads, kv_heads, dim, position, capacity,
                              window, theta, int(sliding), eps, int(f16), _p(out))
     return out, q, k
+
+
+def half_rows(x: np.ndarray):
+    """Prompt activations: (effective inputs, exponent per row)."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, cols = x.shape
+    inputs = np.empty_like(x)
+    exps = np.empty(rows, np.int32)
+    lib().orc_half_rows(_p(x), rows, cols, _p(inputs), _p(exps))
+    return inputs, exps
 
 
 def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:

@@ -1,0 +1,108 @@
+"""Prompt-pass kernels on the GPU against the oracle: FP16 row-scaled
+activations (bit-exact), the Q8_0 x FP16 MFMA GEMM against FP64 over the
+same rounded inputs (the reference's 1e-4 gate, ops_test.cpp:55-89, and the
+1e-3 / 1e-4 gate), the SwiGLU epilogue and its row maxima."""
+import numpy as np
+import pytest
+
+import lfm3amd as L
+import oracle as O
+from gpu_util import DeviceMatrix, within
+from test_oracle import data, formula_q8
+
+pytestmark = pytest.mark.gpu
+SEED = L.SEED
+
+
+def half_rows_gpu(x, lda=None, row_max=None):
+    n, K = x.shape
+    lda = lda or (K + 63) // 64 * 64
+    dx = L.DeviceBuffer.of(np.ascontiguousarray(x, np.float32))
+    da = L.DeviceBuffer(n * lda * 2)
+    ds = L.DeviceBuffer(n * 4)
+    dm = None if row_max is None else L.DeviceBuffer.of(row_max)
+    L.check(L.lib().lfm3_half_rows(dx.addr, K, 0 if dm is None else dm.addr, da.addr, lda, ds.addr,
+                                   n, K, None))
+    L.synchronize()
+    return da, ds, lda
+
+
+@pytest.mark.parametrize("n,K", [(16, 2048), (37, 96), (512, 7680)])
+def test_half_rows_bit_exact(n, K):
+    x = (L.normal(SEED, f"hr.{n}.{K}", n * K) * np.float32(3.0)).reshape(n, K)
+    x[0] = 0
+    da, ds, lda = half_rows_gpu(x)
+    inputs, exps = O.half_rows(x)
+    a = da.download(np.uint16, n * lda).reshape(n, lda)
+    scale = ds.download(np.float32, n)
+    assert np.array_equal(scale, np.ldexp(np.float32(1), -exps).astype(np.float32))
+    want = O.float_to_half(np.ldexp(x, exps[:, None]).astype(np.float32))
+    assert np.array_equal(a[:, :K], want)
+    assert not a[:, K:].any()
+    # effective inputs match the oracle's
+    got = np.ldexp(O.half_to_float(a[:, :K]), -exps[:, None])
+    assert np.array_equal(got.astype(np.float32), inputs)
+
+
+def gemm(m: DeviceMatrix, x, parts=None, swiglu=False):
+    n, K = x.shape
+    da, ds, lda = half_rows_gpu(x)
+    M = m.rows
+    parts = parts or L.lib().lfm3_q8_gemm_parts(M, K, n, int(swiglu))
+    if swiglu:
+        dy = L.DeviceBuffer(n * M * 4)
+        rm = L.DeviceBuffer(n * 4)
+        L.check(L.lib().lfm3_q8_gemm_swiglu(m.codes.addr, m.scales.addr, M, K, da.addr, lda, ds.addr,
+                                            n, dy.addr, M, rm.addr, None))
+        L.synchronize()
+        return dy.download(np.float32, n * M).reshape(n, M), rm.download(np.uint32, n)
+    dy = L.DeviceBuffer(parts * n * M * 4)
+    L.check(L.lib().lfm3_q8_gemm(m.codes.addr, m.scales.addr, M, K, da.addr, lda, ds.addr, n,
+                                 dy.addr, M, parts, None))
+    L.synchronize()
+    y = dy.download(np.float32, parts * n * M).reshape(parts, n, M)
+    out = y[0].copy()
+    for p in range(1, parts):
+        out = out + y[p]
+    return out
+
+
+@pytest.mark.parametrize("n", [16, 29, 512])
+def test_gemm_reference_projection_vectors(n):
+    """ops_test.cpp:46-89: M = 37, K = 2048 formula weights, prompt rows as
+    FP16 row-scaled inputs, FP64 expectation, gate 1e-4."""
+    M, K = 37, 2048
+    w = formula_q8(M, K)
+    x = data(n * K, 0.07).reshape(n, K)
+    y = gemm(DeviceMatrix(w, M, K), x)
+    inputs, _ = O.half_rows(x)
+    want = inputs.astype(np.float64) @ L.q8_dequant(w, M, K).T
+    assert np.max(np.abs(y - want)) < 1e-4
+
+
+@pytest.mark.parametrize("M,K,n,parts", [(2048, 2048, 512, None), (3088, 2048, 512, 1),
+                                         (6144, 2048, 130, None), (2048, 7680, 512, None),
+                                         (2048, 7680, 64, 3), (48, 96, 17, 2)])
+def test_gemm_model_shapes(M, K, n, parts):
+    w = L.q8(SEED, f"pg.{M}.{K}", M, K)
+    x = L.normal(SEED, f"pg.x.{M}.{K}.{n}", n * K).reshape(n, K)
+    y = gemm(DeviceMatrix(w, M, K), x, parts)
+    inputs, _ = O.half_rows(x)
+    want = inputs.astype(np.float64) @ L.q8_dequant(w, M, K).T
+    ok, err = within(y, want)
+    assert ok, err
+
+
+@pytest.mark.parametrize("F,K,n", [(7680, 2048, 512), (192, 128, 20)])
+def test_gemm_swiglu_and_row_max(F, K, n):
+    g = L.q8(SEED, f"ps.g{F}", F, K)
+    u = L.q8(SEED, f"ps.u{F}", F, K)
+    x = L.normal(SEED, f"ps.x{F}", n * K).reshape(n, K)
+    y, rm = gemm(DeviceMatrix(g, F, K, interleave_with=u), x, swiglu=True)
+    inputs, _ = O.half_rows(x)
+    gv = inputs.astype(np.float64) @ L.q8_dequant(g, F, K).T
+    uv = inputs.astype(np.float64) @ L.q8_dequant(u, F, K).T
+    want = gv / (1 + np.exp(-gv)) * uv
+    ok, err = within(y, want)
+    assert ok, err
+    assert np.array_equal(rm.view(np.float32), np.abs(y).max(axis=1))

@@ -308,3 +308,27 @@ def test_f16_switch_stores_binary16_rows():
             assert np.array_equal(row, row.astype(np.float16).astype(np.float32))
             assert np.any(row != 0)
     model.close()
+
+
+def test_half_rows_matches_binary16_and_exponent_rule():
+    """Prompt activations (q8_prefill.hpp:27-51): the row maximum lands in
+    [2^14, 2^15) after scaling, each element is numpy's binary16 rounding of
+    the scaled value, a zero row keeps exponent 0, and tiny and large rows
+    keep 11 significant bits relative to the maximum."""
+    rng = np.random.default_rng(5)
+    x = rng.normal(0, 1, (6, 300)).astype(np.float32)
+    x[1] *= 1e-6
+    x[2] *= 3e4
+    x[3] = 0
+    x[4, 7] = -65504.0 * 4
+    inputs, exps = O.half_rows(x)
+    for r in range(6):
+        m = np.abs(x[r]).max()
+        if m == 0:
+            assert exps[r] == 0 and not inputs[r].any()
+            continue
+        scaled = np.ldexp(m, exps[r])
+        assert 2.0 ** 14 <= scaled < 2.0 ** 15
+        want = np.ldexp(np.ldexp(x[r], exps[r]).astype(np.float16).astype(np.float32), -exps[r])
+        assert np.array_equal(inputs[r], want)
+        assert np.max(np.abs(inputs[r] - x[r])) <= m * 2.0 ** -11
