@@ -11,9 +11,10 @@
 // code x half products summed in FP32 (A operand = 16 tokens' activations,
 // B operand = 16 weight rows decoded exactly from the tiled layout), and
 // the block scale applies as acc = fma(d, dot, acc) (q8_prefill.hpp:
-// 538-560). A block of 4 waves owns 64 RT weight rows (16 RT per wave,
-// held in registers and prefetched a chunk ahead) and 16 TT tokens, whose
-// activations are double-buffered through LDS. Narrow outputs split K
+// 538-560). A block of 4 waves owns 64 RT weight rows (16 RT per wave) and
+// 16 TT tokens. Each chunk's activations, weight tiles and scales arrive
+// by direct-to-LDS loads into a two-stage pipeline, so registers hold only
+// the accumulators and the chunk being multiplied. Narrow outputs split K
 // across blockIdx.z into parts written separately; their consumer adds the
 // parts in part order, so no launch merges blocks through memory.
 #include <algorithm>
@@ -24,8 +25,15 @@
 namespace lfm3amd {
 namespace {
 
-constexpr int kGemmThreads = 256, kGemmWaves = 4;
-constexpr int kRowPad = 8;  // halves of padding per LDS activation row
+// Block shape: kGemmWR x kGemmWT waves; each wave owns kGemmRT weight
+// tiles (16 rows each) and 16 kGemmTT tokens, so a block covers 256 weight
+// rows and 128 tokens: 128 FLOP per staged byte (2 M N / (M + 2 N) for 1-
+// byte codes and 2-byte activations), about one block per CU for the
+// 512-token pass.
+constexpr int kGemmRT = 4, kGemmTT = 4, kGemmWR = 4, kGemmWT = 2, kGemmStages = 3;
+constexpr int kGemmWaves = kGemmWR * kGemmWT, kGemmThreads = 64 * kGemmWaves;
+constexpr int kGemmTiles = kGemmWR * kGemmRT;  // weight tiles a block
+constexpr int kGemmTokens = kGemmWT * kGemmTT * 16;
 
 __device__ __forceinline__ int RowExponent(float maximum) {
   return maximum > 0.0f ? 14 - ilogbf(maximum) : 0;
@@ -61,79 +69,174 @@ __launch_bounds__(256) __global__
         k < K ? FloatToHalfBits(ldexpf(src[k], e)) : Half(0);
 }
 
-template<int RT, int TT, bool kSwiGLU>
-__launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1)))
+// Direct-to-LDS buffer loads (buffer_load_dword{,x4} ... lds): lane L's
+// bytes land at the wave-uniform LDS base + L * size. Reads outside the
+// resource's byte range return zero.
+typedef __attribute__((address_space(3))) void LdsVoid;
+using BufferResource = __amdgpu_buffer_rsrc_t;
+constexpr int kBufferWord3 = 0x00020000;  // 32-bit data format, raw access
+__device__ __forceinline__ BufferResource MakeBuffer(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), kBufferWord3);
+}
+__device__ __forceinline__ void BufferToLds16(BufferResource res, unsigned lane_offset,
+                                              unsigned scalar_offset, void* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(res, (LdsVoid*)lds_base, 16, lane_offset,
+                                           scalar_offset, 0, 0);
+}
+__device__ __forceinline__ void BufferToLds4(BufferResource res, unsigned lane_offset,
+                                             unsigned scalar_offset, void* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(res, (LdsVoid*)lds_base, 4, lane_offset,
+                                           scalar_offset, 0, 0);
+}
+
+// s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt
+// 11:8). Issued through the builtin so the compiler's own wait insertion
+// sees them.
+constexpr int WaitVm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kWaitLgkm0 = 15 | (3 << 14) | (7 << 4);
+
+__device__ __forceinline__ void BlockBarrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// One pipeline stage: the block's activation rows for one 64-column chunk
+// (kGemmTokens rows x 8 16-byte slots; slot j of row t holds segment
+// j ^ (t & 7), so the A reads of 8 consecutive rows hit distinct banks),
+// the block's weight tiles for the chunk (1 KB each, lane order), and their
+// scales (256 B per group of 4 tiles, row n's 4 tiles at 16 n).
+struct GemmStage {
+  static constexpr int kW = kGemmTokens * 128;
+  static constexpr int kS = kW + kGemmTiles * kTileCodeBytes;
+  static constexpr int kBytes = kS + kGemmTiles * kTileScales * 2;
+};
+
+// Block b of a launch -> work item, XCD-major: blocks are dispatched to
+// the 8 XCDs round robin (b % 8), so XCD x gets the consecutive items
+// [first(x), first(x) + count(x)); items sharing weight rows are adjacent,
+// so their tiles come from HBM once per XCD and then from its L2.
+__device__ __forceinline__ int XcdMajorItem(int b, int blocks) {
+  const int q = blocks / 8, rem = blocks % 8, x = b % 8, i = b / 8;
+  return (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + i;
+}
+
+// Pins 16 accumulators at this point: the FMAs producing them run before
+// it and the values stay in their registers.
+#define LFM3_PIN4(a) "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3])
+
+template<bool kSwiGLU>
+__launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)))
 __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
                              const Half* __restrict__ scales, int row_tiles,
                              int nchunks, const Half* __restrict__ a, int lda,
                              const float* __restrict__ a_scale, int n,
                              float* __restrict__ y, int ldy, int rows_out,
+                             int row_blocks, int token_blocks, int parts,
                              std::size_t part_stride,
                              unsigned* __restrict__ row_max) {
-  constexpr int TOK = 16 * TT;                 // tokens per block
-  constexpr int ROW_HALVES = kChunk + kRowPad; // LDS row stride (halves)
-  constexpr int UNITS = TOK * 8 / kGemmThreads; // 16-byte A pieces per thread
-  __shared__ __attribute__((aligned(16))) Half s_a[2][TOK * ROW_HALVES];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tile0 = (blockIdx.x * kGemmWaves + wave) * RT;
-  const int tok0 = blockIdx.y * TOK;
-  const int c_begin = int(blockIdx.z) * nchunks / int(gridDim.z);
-  const int c_end = (int(blockIdx.z) + 1) * nchunks / int(gridDim.z);
-  y += std::size_t(blockIdx.z) * part_stride;
+  constexpr int RT = kGemmRT, TT = kGemmTT;
+  using Stage = GemmStage;
+  constexpr int A_LOADS = kGemmTokens * 8 / kGemmThreads;  // 16-byte loads a lane
+  constexpr int W_LOADS = kGemmTiles / kGemmWaves;         // tiles a wave loads
+  static_assert(A_LOADS * kGemmThreads == kGemmTokens * 8, "A loads cover the rows");
+  static_assert(W_LOADS * kGemmWaves == kGemmTiles, "W loads cover the tiles");
+  static_assert(RT == 4 && kGemmWR <= kGemmWaves, "scale groups of four tiles");
+  // One array per stage (not one indexed by stage) lets the compiler see
+  // that a stage's reads never alias the other stages' loads in flight.
+  __shared__ __attribute__((aligned(16))) std::uint8_t s_st0[Stage::kBytes];
+  __shared__ __attribute__((aligned(16))) std::uint8_t s_st1[Stage::kBytes];
+  __shared__ __attribute__((aligned(16))) std::uint8_t s_st2[Stage::kBytes];
+  static_assert(kGemmStages == 3, "three stage arrays");
 
-  uint4 q[RT], qn[RT];
-  unsigned sc[RT], scn[RT];
-  const auto fetch_w = [&](int c, uint4 (&qq)[RT], unsigned (&ss)[RT]) {
+  const int item = XcdMajorItem(blockIdx.x, gridDim.x);
+  const int tb = item % token_blocks, rb = (item / token_blocks) % row_blocks;
+  const int part = item / (token_blocks * row_blocks);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = wave % kGemmWR, wt = wave / kGemmWR;
+  const int btile0 = rb * kGemmTiles;              // the block's first tile
+  const int tile0 = btile0 + wr * RT;              // this wave's first tile
+  const int tok0 = tb * kGemmTokens;               // the block's first token
+  const int c_begin = part * nchunks / parts, c_end = (part + 1) * nchunks / parts;
+  y += std::size_t(part) * part_stride;
+
+  // Sources as buffer resources (scalar registers), a scalar offset per
+  // chunk and tile, and a 32-bit byte offset per lane: no 64-bit lane
+  // addresses live across the loop. Rows past the last token and tiles
+  // past the last tile read the last valid one; their results are
+  // discarded. The host keeps every operand under 2 GiB.
+  const BufferResource a_res = MakeBuffer(a + std::size_t(tok0) * lda,
+                                          unsigned(n - tok0) * unsigned(lda) * 2u);
+  const BufferResource w_res = MakeBuffer(codes, unsigned(row_tiles) * unsigned(nchunks) *
+                                                     unsigned(kTileCodeBytes));
+  const BufferResource s_res = MakeBuffer(scales, unsigned(row_tiles) * unsigned(nchunks) *
+                                                      unsigned(kTileScales * 2));
+  unsigned a_off[A_LOADS];
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      const int tile = tile0 + r;
-      if (tile < row_tiles) {
-        const std::size_t off = std::size_t(tile) * nchunks + c;
-        qq[r] = *reinterpret_cast<const uint4*>(codes + off * kTileCodeBytes + lane * 16);
-        ss[r] = *reinterpret_cast<const unsigned*>(scales + off * kTileScales + (lane & 15) * 2);
-      } else {
-        qq[r] = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
-        ss[r] = 0;
-      }
-    }
+  for (int j = 0; j < A_LOADS; ++j) {
+    const int t = (wave * A_LOADS + j) * 8 + (lane >> 3);
+    const int seg = (lane & 7) ^ (t & 7);
+    a_off[j] = (unsigned(min(t, n - 1 - tok0)) * unsigned(lda) + unsigned(seg * 8)) * 2u;
+  }
+  unsigned w_tile[W_LOADS];  // byte offset of each loaded tile's chunk 0 (uniform)
+#pragma unroll
+  for (int j = 0; j < W_LOADS; ++j)
+    w_tile[j] = unsigned(min(btile0 + wave * W_LOADS + j, row_tiles - 1)) *
+                unsigned(nchunks * kTileCodeBytes);
+  const unsigned w_off = unsigned(lane) * 16u;
+  // Scales: wave g < kGemmWR loads group g; lane L brings tile 4 g + L % 4's
+  // dword L / 4 (row L / 4's two block scales).
+  const bool loads_scales = wave < kGemmWR;
+  const unsigned s_off =
+      unsigned(min(btile0 + wave * 4 + (lane & 3), row_tiles - 1)) *
+          unsigned(nchunks * kTileScales * 2) +
+      unsigned((lane >> 2) * 4);
+  const auto issue = [&](int c, std::uint8_t* stage) {
+#pragma unroll
+    for (int j = 0; j < A_LOADS; ++j)
+      BufferToLds16(a_res, a_off[j], unsigned(c * kChunk * 2),
+                    stage + (wave * A_LOADS + j) * 1024);
+#pragma unroll
+    for (int j = 0; j < W_LOADS; ++j)
+      BufferToLds16(w_res, w_off, w_tile[j] + unsigned(c * kTileCodeBytes),
+                    stage + Stage::kW + (wave * W_LOADS + j) * kTileCodeBytes);
+    if (loads_scales)
+      BufferToLds4(s_res, s_off, unsigned(c * kTileScales * 2),
+                   stage + Stage::kS + wave * 4 * kTileScales * 2);
   };
-  uint4 ar[UNITS];
-  const auto fetch_a = [&](int c) {
-#pragma unroll
-    for (int u = 0; u < UNITS; ++u) {
-      const int idx = tid + u * kGemmThreads, t = idx >> 3, seg = idx & 7;
-      const int token = tok0 + t;
-      ar[u] = token < n ? *reinterpret_cast<const uint4*>(a + std::size_t(token) * lda + c * kChunk + seg * 8)
-                        : make_uint4(0, 0, 0, 0);
-    }
-  };
-  const auto commit_a = [&](int stage) {
-#pragma unroll
-    for (int u = 0; u < UNITS; ++u) {
-      const int idx = tid + u * kGemmThreads, t = idx >> 3, seg = idx & 7;
-      *reinterpret_cast<uint4*>(&s_a[stage][t * ROW_HALVES + seg * 8]) = ar[u];
-    }
+  // Waits until at most one chunk's loads of this wave remain in flight.
+  const auto wait_all_but_one_chunk = [&]() {
+    if (loads_scales)
+      __builtin_amdgcn_s_waitcnt(WaitVm(A_LOADS + W_LOADS + 1));
+    else
+      __builtin_amdgcn_s_waitcnt(WaitVm(A_LOADS + W_LOADS));
   };
 
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-  f4 acc[RT][TT];
+  // Scalars, not f4: updating one lane of a 4-register tuple at a time
+  // makes the register allocator copy whole tuples.
+  float acc[RT][TT][4];
 #pragma unroll
   for (int r = 0; r < RT; ++r)
 #pragma unroll
     for (int t = 0; t < TT; ++t)
-      acc[r][t] = zero;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        acc[r][t][i] = 0.0f;
 
-  fetch_w(c_begin, q, sc);
-  fetch_a(c_begin);
-  commit_a(0);
-  __syncthreads();
-  for (int c = c_begin; c < c_end; ++c) {
-    const int stage = (c - c_begin) & 1;
-    const bool more = c + 1 < c_end;
-    if (more) {
-      fetch_w(c + 1, qn, scn);
-      fetch_a(c + 1);
-    }
+  // A read of lane L: row wt 16 TT + 16 t + L % 16, segment 4 blk + L / 16,
+  // stored in slot segment ^ (L & 7).
+  const int a_row = wt * TT * 16 + (lane & 15);
+  const auto compute = [&](const std::uint8_t* stage) {
+    uint4 q[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+      q[r] = *reinterpret_cast<const uint4*>(stage + Stage::kW +
+                                             (wr * RT + r) * kTileCodeBytes + lane * 16);
+    const uint4 sc4 = *reinterpret_cast<const uint4*>(
+        stage + Stage::kS + wr * RT * kTileScales * 2 + (lane & 15) * 16);
+    const unsigned sc[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
       h8 w[RT];
@@ -141,42 +244,105 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
         w[r] = blk ? EightCodes(q[r].z, q[r].w) : EightCodes(q[r].x, q[r].y);
-        d[r] = HalfBitsToFloat(blk ? sc[r] >> 16 : sc[r] & 0xffffu);
+        // An opaque conversion keeps the scale FMAs as in-place v_fmac_f32
+        // (a v_fma_mix_f32 reading the half would write a fresh register).
+        asm("v_cvt_f32_f16 %0, %1" : "=v"(d[r]) : "v"(blk ? sc[r] >> 16 : sc[r]));
       }
+      const int slot = (blk * 4 + (lane >> 4)) ^ (lane & 7);
+      const auto a_frag = [&](int t) {
+        return *reinterpret_cast<const h8*>(stage + (t * 16 + a_row) * 128 + slot * 16);
+      };
+      // Software pipeline over token groups: the MFMAs of group t issue
+      // beside the scale FMAs of group t - 1; a scheduling barrier per
+      // group and the register pins keep the compiler from hoisting every
+      // MFMA of the chunk (which would hold 4 RT TT result registers).
+      h8 av = a_frag(0);
+      f4 prev[RT];
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
-        // A operand: lane L holds token 16 t + L % 16, elements 8 (L / 16)..
-        const h8 av = *reinterpret_cast<const h8*>(
-            &s_a[stage][(t * 16 + (lane & 15)) * ROW_HALVES + blk * 32 + 8 * (lane >> 4)]);
+        const h8 next = a_frag(t + 1 < TT ? t + 1 : t);
+        f4 cur[RT];
 #pragma unroll
-        for (int r = 0; r < RT; ++r) {
-          const f4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, w[r], zero, 0, 0, 0);
+        for (int r = 0; r < RT; ++r)
+          cur[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, w[r], zero, 0, 0, 0);
+        if (t > 0) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            acc[r][t][i] = fmaf(d[r], p[i], acc[r][t][i]);
+          for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              acc[r][t - 1][i] = fmaf(d[r], prev[r][i], acc[r][t - 1][i]);
+          asm volatile("" : LFM3_PIN4(acc[0][t - 1]), LFM3_PIN4(acc[1][t - 1]),
+                       LFM3_PIN4(acc[2][t - 1]), LFM3_PIN4(acc[3][t - 1]));
         }
-      }
-    }
-    if (more) {
-      commit_a(stage ^ 1);
 #pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        q[r] = qn[r];
-        sc[r] = scn[r];
+        for (int r = 0; r < RT; ++r)
+          prev[r] = cur[r];
+        av = next;
+        // Issue order: the A read for t + 1, then each MFMA of t followed
+        // by 4 FMAs of t - 1, so the matrix pipe runs while the VALU works.
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (t > 0) {
+#pragma unroll
+          for (int r = 0; r < RT; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[r][TT - 1][i] = fmaf(d[r], prev[r][i], acc[r][TT - 1][i]);
+      asm volatile("" : LFM3_PIN4(acc[0][TT - 1]), LFM3_PIN4(acc[1][TT - 1]),
+                   LFM3_PIN4(acc[2][TT - 1]), LFM3_PIN4(acc[3][TT - 1]));
     }
-    __syncthreads();
+  };
+
+  // Three-stage pipeline, unrolled so each stage is a fixed array. Step c:
+  // wait until chunk c's loads are done (chunk c + 1's may remain in
+  // flight), barrier (chunk c visible to every wave, and every wave done
+  // with chunk c - 1), issue chunk c + 2 into chunk c - 1's stage, then
+  // multiply chunk c. Loads get two chunks' compute to arrive.
+  issue(c_begin, s_st0);
+  if (c_begin + 1 < c_end)
+    issue(c_begin + 1, s_st1);
+  const auto step = [&](int c, std::uint8_t* stage, std::uint8_t* refill) {
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 1 < c_end)
+      wait_all_but_one_chunk();
+    else
+      __builtin_amdgcn_s_waitcnt(WaitVm(0));
+    BlockBarrier();
+    if (c + 2 < c_end)
+      issue(c + 2, refill);
+    compute(stage);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Whole rounds of three chunks, then the ones left (no exits from inside
+  // a round).
+  int c = c_begin;
+  for (; c + 3 <= c_end; c += 3) {
+    step(c, s_st0, s_st2);
+    step(c + 1, s_st1, s_st0);
+    step(c + 2, s_st2, s_st1);
   }
+  if (c < c_end)
+    step(c, s_st0, s_st2);
+  if (c + 1 < c_end)
+    step(c + 1, s_st1, s_st0);
 
   // D layout: lane L holds tokens 16 t + 4 (L / 16) + i of weight row L % 16.
   const int sub = lane & 15, quad = lane >> 4;
+  const int wtok0 = tok0 + wt * TT * 16;
   if constexpr (kSwiGLU) {
     // Tiles (2 j, 2 j + 1) are a (gate, up) pair for output rows j * 16 + n.
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int token = tok0 + t * 16 + 4 * quad + i;
+        const int token = wtok0 + t * 16 + 4 * quad + i;
         const float s = token < n ? a_scale[token] : 0.0f;
         float m = 0.0f;
 #pragma unroll
@@ -203,7 +369,7 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
     for (int t = 0; t < TT; ++t) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int token = tok0 + t * 16 + 4 * quad + i;
+        const int token = wtok0 + t * 16 + 4 * quad + i;
         if (token >= n)
           continue;
         const float s = a_scale[token];
@@ -218,14 +384,36 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   }
 }
 
-// K parts for a prompt GEMM: enough blocks for the 256 CUs (two resident
-// each), keeping at least 4 chunks a part, at most 8 parts.
+// K parts for a prompt GEMM: double while the blocks still fit one round
+// on the 256 CUs (one block each, with a quarter over), keeping at least 4
+// chunks a part, at most 8 parts. Each part costs its consumer one more
+// FP32 output pass.
 int PromptParts(int row_blocks, int token_blocks, int nchunks) {
   int parts = 1;
-  while (parts < 8 && row_blocks * token_blocks * parts < 256 &&
+  while (parts < 8 && row_blocks * token_blocks * parts * 2 <= 320 &&
          nchunks / (parts * 2) >= 4)
     parts *= 2;
   return parts;
+}
+
+// The kernel addresses codes, scales and activations with 32-bit buffer
+// offsets.
+bool GemmOperandsFit(std::uint64_t row_tiles, std::uint64_t nchunks, std::uint64_t tokens,
+                     std::uint64_t lda) {
+  return row_tiles * nchunks * kTileCodeBytes < (1ull << 31) && tokens * lda * 2 < (1ull << 31);
+}
+
+template<bool kSwiGLU>
+void LaunchGemm(const void* codes, const void* scales, int row_tiles, int nchunks,
+                const std::uint16_t* a, std::uint32_t lda, const float* a_scale,
+                std::uint32_t tokens, float* y, std::uint32_t ldy, std::uint32_t rows,
+                int parts, std::size_t part_stride, unsigned* row_max, hipStream_t stream) {
+  const int row_blocks = (row_tiles + kGemmTiles - 1) / kGemmTiles;
+  const int token_blocks = (int(tokens) + kGemmTokens - 1) / kGemmTokens;
+  Q8GemmKernel<kSwiGLU><<<row_blocks * token_blocks * parts, kGemmThreads, 0, stream>>>(
+      static_cast<const std::uint8_t*>(codes), static_cast<const Half*>(scales), row_tiles,
+      nchunks, reinterpret_cast<const Half*>(a), int(lda), a_scale, int(tokens), y, int(ldy),
+      int(rows), row_blocks, token_blocks, parts, part_stride, row_max);
 }
 
 }  // namespace
@@ -250,8 +438,8 @@ std::uint32_t lfm3_q8_gemm_parts(std::uint32_t rows, std::uint32_t cols,
                                  std::uint32_t tokens, int swiglu) {
   if (!rows || !cols || !tokens || swiglu)
     return 1;
-  const int row_blocks = (int(RowTiles(rows)) + 15) / 16;
-  const int token_blocks = (int(tokens) + 127) / 128;
+  const int row_blocks = (int(RowTiles(rows)) + kGemmTiles - 1) / kGemmTiles;
+  const int token_blocks = (int(tokens) + kGemmTokens - 1) / kGemmTokens;
   return std::uint32_t(PromptParts(row_blocks, token_blocks, int(Chunks(cols))));
 }
 
@@ -262,14 +450,12 @@ int lfm3_q8_gemm(const void* codes, const void* scales, std::uint32_t rows,
   if (!codes || !scales || !a || !a_scale || !y || !rows || !cols ||
       cols % 32 || !tokens || lda % 64 || lda < Chunks(cols) * kChunk ||
       ldy < rows || !parts || parts > 8 || parts > Chunks(cols) ||
-      (reinterpret_cast<std::uintptr_t>(a) & 15))
+      (reinterpret_cast<std::uintptr_t>(a) & 15) ||
+      !GemmOperandsFit(RowTiles(rows), Chunks(cols), tokens, lda))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 prompt GEMM shape");
-  const int row_tiles = int(RowTiles(rows)), nchunks = int(Chunks(cols));
-  const dim3 grid((row_tiles + 15) / 16, (tokens + 127) / 128, parts);
-  Q8GemmKernel<4, 8, false><<<grid, kGemmThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const std::uint8_t*>(codes), static_cast<const Half*>(scales),
-      row_tiles, nchunks, reinterpret_cast<const Half*>(a), int(lda), a_scale,
-      int(tokens), y, int(ldy), int(rows), std::size_t(ldy) * tokens, nullptr);
+  LaunchGemm<false>(codes, scales, int(RowTiles(rows)), int(Chunks(cols)), a, lda, a_scale,
+                    tokens, y, ldy, rows, int(parts), std::size_t(ldy) * tokens, nullptr,
+                    static_cast<hipStream_t>(stream));
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 prompt GEMM launch");
 }
 
@@ -280,14 +466,12 @@ int lfm3_q8_gemm_swiglu(const void* codes, const void* scales,
                         std::uint32_t ldy, unsigned* row_max, void* stream) {
   if (!codes || !scales || !a || !a_scale || !y || !rows || !cols ||
       cols % 32 || !tokens || lda % 64 || lda < Chunks(cols) * kChunk ||
-      ldy < rows || (reinterpret_cast<std::uintptr_t>(a) & 15))
+      ldy < rows || (reinterpret_cast<std::uintptr_t>(a) & 15) ||
+      !GemmOperandsFit(2 * RowTiles(rows), Chunks(cols), tokens, lda))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 prompt SwiGLU shape");
-  const int row_tiles = 2 * int(RowTiles(rows)), nchunks = int(Chunks(cols));
-  const dim3 grid((row_tiles + 15) / 16, (tokens + 127) / 128, 1);
-  Q8GemmKernel<4, 8, true><<<grid, kGemmThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const std::uint8_t*>(codes), static_cast<const Half*>(scales),
-      row_tiles, nchunks, reinterpret_cast<const Half*>(a), int(lda), a_scale,
-      int(tokens), y, int(ldy), int(rows), 0, row_max);
+  LaunchGemm<true>(codes, scales, int(2 * RowTiles(rows)), int(Chunks(cols)), a, lda,
+                   a_scale, tokens, y, ldy, rows, 1, 0, row_max,
+                   static_cast<hipStream_t>(stream));
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 prompt SwiGLU launch");
 }
 
