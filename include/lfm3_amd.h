@@ -287,6 +287,71 @@ int lfm3_decode_heads_attention_ragged(
     size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------
+ * Prompt chunk rows: n consecutive rows of one session (or, for the
+ * convolution, packed segments of several sessions).
+ * ------------------------------------------------------------------- */
+/* Gated short convolution over packed ragged prompt segments: segment s is
+   rows [begin[s], begin[s] + rows[s]) of p ([B | C | x], stride ldp) and of
+   y, and continues history[s] ([hidden][width - 1] FP32, oldest first).
+   Each output keeps lfm3_conv_step_ragged's expressions and order, so a
+   segment of n rows gives bit-identical outputs to n decode steps. With
+   update_history the history becomes the segment's last width - 1 B x
+   products. begin/rows/history are host arrays; segments <= 8.
+   Replaces: gpu::ShortConv with n > 1 (hip/ops.hip:2250-2264:
+   ConvolutionWindow + ConvolutionHistory) per prompt (engine.cpp:386-393). */
+int lfm3_conv_prompt(const float* p, uint32_t ldp, const float* taps,
+                     float* const* history, const uint32_t* begin,
+                     const uint32_t* rows, uint32_t segments, float* y,
+                     uint32_t ldy, uint32_t hidden, uint32_t width,
+                     int update_history, void* stream);
+/* Per-head Q/K RMSNorm and paired RoPE of `rows` chunk rows at positions
+   position + r (q/k/v rows of stride ld floats, rotated in place), and the
+   F16 K/V of row r stored to row r of k16/v16 (kv_heads * dim halves a
+   row: a staging chunk, or the cache rows themselves for a full-attention
+   ring that does not wrap). Replaces: gpu::PromptHeads
+   (hip/ops.hip:2407-2417; engine.cpp:441-450). */
+int lfm3_prompt_heads(float* q, float* k, const float* v, uint32_t ld,
+                      const float* q_norm, const float* k_norm,
+                      const float* frequencies, const float* factors,
+                      uint16_t* k16, uint16_t* v16, uint32_t rows,
+                      uint32_t heads, uint32_t kv_heads, uint32_t dim,
+                      uint32_t position, float eps, void* stream);
+/* Chunk rows 0..rows-1 at positions position + r into the F16 ring: row r
+   goes to slot (position + r) % capacity; only the last min(rows, capacity)
+   rows are copied (their slots are distinct). stride = kv_heads * dim.
+   Replaces: gpu::StoreKV (hip/ops.hip:1737-1749, 2392-2396;
+   engine.cpp:467-470). */
+int lfm3_store_kv(const uint16_t* k16, const uint16_t* v16, uint16_t* cache_k,
+                  uint16_t* cache_v, uint32_t rows, uint32_t stride,
+                  uint32_t position, uint32_t capacity, void* stream);
+/* Workspace of lfm3_prompt_attention: key spans of long global histories
+   (at least 2048 keys each, at most 8) keep partial sums, rows x heads x
+   (dim + 2) floats a span; 0 when the keys fit one span or window > 0. */
+size_t lfm3_prompt_attention_workspace_bytes(uint32_t rows, uint32_t heads,
+                                             uint32_t dim, uint32_t position,
+                                             uint32_t window);
+/* Causal gated GQA of `rows` query rows at positions position + r:
+   out[r][h] = (softmax(q . K / sqrt(dim)) V) / (1 + exp(-gate[r][h])) over
+   keys [first, position + r], first = max(0, position + r + 1 - window)
+   when window > 0. Keys at or after position are rows of k/v (the chunk,
+   row 0 at position), earlier keys come from cache_k/cache_v slot
+   t % capacity ([capacity][kv_heads][dim] F16; unused when position is 0).
+   q holds normed, rotated queries; q/gate/out rows have strides
+   ldq/ldg/ldo floats (multiples of 4, 16-byte aligned rows). F16 Q (with
+   the base-2 softmax scale), K, V and probabilities on the matrix cores,
+   FP32 scores, sums and outputs. dim 64 or 128; group 2, 4 or 8.
+   Replaces: gpu::Attention with n > 1 (hip/ops.hip:2316-2332: WmmaAttn +
+   PromptCombine; engine.cpp:451-466). */
+int lfm3_prompt_attention(const float* q, uint32_t ldq, const uint16_t* k,
+                          const uint16_t* v, const float* gate, uint32_t ldg,
+                          const uint16_t* cache_k, const uint16_t* cache_v,
+                          float* out, uint32_t ldo, uint32_t rows,
+                          uint32_t heads, uint32_t kv_heads, uint32_t dim,
+                          uint32_t position, uint32_t capacity,
+                          uint32_t window, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------
  * Engine: Model / Session (engine.hpp:17-163).
  * ------------------------------------------------------------------- */
 enum { LFM3_LAYER_CONV = 0, LFM3_LAYER_FULL = 1, LFM3_LAYER_SLIDING = 2 };

@@ -1,0 +1,451 @@
+// Causal prompt attention on gfx950 MFMA: n query rows at positions
+// position .. position + n - 1 over the F16 K/V of the chunk (keys at or
+// after position) and of the ring (earlier keys), with an optional sliding
+// window (hip/ops.hip:1355-1561 WmmaAttn, 1692-1709 PromptCombine,
+// 2275-2280 PromptSplits, 2289-2333 Attention for n > 1).
+//
+// Numerics follow the reference's prompt path: Q is scaled by
+// log2(e) / sqrt(D) in FP32 and rounded to F16; scores are FP32 sums of F16
+// products in base-2 units; per 64-key tile the running maximum rescales the
+// running sum and output; probabilities are rounded to F16 once and the sum
+// adds the rounded values, so the weights applied to V are exactly
+// normalized; out = (acc / sum) / (1 + e^-gate).
+//
+// A block of 8 waves owns one KV head's group of G query heads and 128
+// (query row, head) columns (128 / G rows x G heads); each wave owns 16
+// columns. K and V tiles of 64 keys are staged through LDS (double
+// buffered, the next tile prefetched into registers) and shared by the 8
+// waves. Each wave computes S^T = K Q^T (v_mfma_f32_16x16x32_f16: A = 16
+// keys x 32 dims, B = Q^T) and O^T += V^T P^T (A = 16 dims x 32 keys of the
+// transposed V tile, B = P^T). The K operand rows are permuted so that in
+// the S^T accumulator lane L holds exactly the 8 keys that the P^T operand
+// needs in lane L (keys 8 (L / 16) + j of a 32-key group): probabilities
+// never cross lanes. A column's softmax state is per lane; its row maximum
+// and final sum combine the 4 lanes of the column (L % 16) with two
+// exchanges. Long global histories split keys across blockIdx.y into spans
+// of at least 2048 keys (at most 8); each split stores its maximum, sum and
+// unnormalized output, merged by CombineSpansKernel.
+#include <cmath>
+
+#include "common.hpp"
+
+namespace lfm3amd {
+namespace {
+
+constexpr int kPAWaves = 8, kPAThreads = 64 * kPAWaves;
+constexpr int kPACols = 16 * kPAWaves;  // (row, head) columns a block
+constexpr int kPAKeys = 64;             // keys a tile
+constexpr int kMinPromptSpan = 2048, kMaxPromptSplits = 8;
+
+// hip/ops.hip:2275-2280: spans of at least 2048 keys, at most 8 of them.
+int PromptSplits(int keys, int& span) {
+  span = std::max(kMinPromptSpan, (keys + kMaxPromptSplits - 1) / kMaxPromptSplits);
+  return (keys + span - 1) / span;
+}
+
+// Slot of a key row's 16-byte segment: XOR swizzle chosen so that the 16
+// keys one S^T operand read touches (keys 8 (r / 4) + (r % 4), r < 16, plus
+// a constant) land in distinct banks.
+template<int D>
+__device__ __forceinline__ int KeySwizzle(int key) {
+  if constexpr (D == 128)
+    return (key & 3) | (((key >> 3) & 3) << 2);
+  else
+    return ((key >> 1) & 1) | (((key >> 3) & 3) << 1);
+}
+
+// Rows at or after position come from the chunk, earlier rows from the
+// ring (hip/ops.hip:1193-1199).
+__device__ __forceinline__ const Half* KeyRow(const Half* chunk, const Half* ring, int t,
+                                              int position, int capacity, int stride) {
+  return t >= position ? chunk + std::size_t(t - position) * stride
+                       : ring + std::size_t(t % capacity) * stride;
+}
+
+__device__ __forceinline__ unsigned PackHalves(float a, float b) {
+  return unsigned(FloatToHalfBits(a)) | (unsigned(FloatToHalfBits(b)) << 16);
+}
+
+template<int D, int G>
+__launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
+    const float* __restrict__ q, int ldq, const Half* __restrict__ k,
+    const Half* __restrict__ v, const float* __restrict__ gate, int ldg,
+    const Half* __restrict__ ck, const Half* __restrict__ cv, float* __restrict__ out,
+    int ldo, float* __restrict__ partial, int n, int heads, int kv_heads, int position,
+    int capacity, int window, int span) {
+  static_assert(D == 64 || D == 128, "head dimension");
+  static_assert(kPACols % G == 0 && G >= 2 && G <= 8, "query group");
+  constexpr int kRows = kPACols / G;       // query rows a block
+  constexpr int kSegs = D / 8;             // 16-byte segments a key row
+  constexpr int kSteps = D / 32;           // MFMA K steps over dimensions
+  constexpr int kDimBlocks = D / 16;       // O^T accumulators
+  constexpr int kVPitch = kPAKeys + 8;     // halves a transposed V row
+  constexpr int kKLoads = kPAKeys * kSegs / kPAThreads;     // K segments a thread
+  constexpr int kVPairs = kPAKeys / 2 * kSegs;               // (key pair, segment) jobs
+  static_assert(kKLoads * kPAThreads == kPAKeys * kSegs, "K staging");
+  __shared__ __attribute__((aligned(16))) Half sK[2][kPAKeys * D];
+  __shared__ __attribute__((aligned(16))) Half sV[2][D * kVPitch];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int g = blockIdx.z, split = blockIdx.y, q0 = blockIdx.x * kRows;
+  const int c = wave * 16 + col;
+  const int row = q0 + c / G, head = g * G + c % G;
+  const bool live = row < n;
+  const int stride = kv_heads * D;
+  k += g * D;
+  v += g * D;
+  ck += g * D;
+  cv += g * D;
+
+  // Q^T operand: lane L holds dims 32 s + 8 (L / 16) + j of its column,
+  // scaled in FP32 and rounded to F16.
+  const float scale = rsqrtf(float(D)) * 1.44269504088896341f;
+  h8 qf[kSteps];
+  {
+    const float* qr = q + std::size_t(live ? row : 0) * ldq + head * D;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const float4 a = live ? *reinterpret_cast<const float4*>(qr + 32 * s + 8 * grp)
+                            : make_float4(0, 0, 0, 0);
+      const float4 b = live ? *reinterpret_cast<const float4*>(qr + 32 * s + 8 * grp + 4)
+                            : make_float4(0, 0, 0, 0);
+      const unsigned w[4] = {PackHalves(a.x * scale, a.y * scale),
+                             PackHalves(a.z * scale, a.w * scale),
+                             PackHalves(b.x * scale, b.y * scale),
+                             PackHalves(b.z * scale, b.w * scale)};
+      qf[s] = __builtin_bit_cast(h8, w);
+    }
+  }
+
+  // Key ranges: the column's own, the block's, and the wave's (open = keys
+  // every column of the wave sees, where tiles skip the mask).
+  const int span_first = split * span, span_last = span_first + span - 1;
+  const auto first_key = [&](int query) {
+    return max(window > 0 ? query + 1 - window : 0, span_first);
+  };
+  const int lo = first_key(position + row), hi = min(position + row, span_last);
+  const int block_last_row = min(q0 + kRows, n) - 1;
+  const int block_first = first_key(position + q0);
+  const int block_last = min(position + block_last_row, span_last);
+  const int w_row0 = q0 + wave * 16 / G;
+  const int w_row1 = min(q0 + (wave * 16 + 15) / G, n - 1);
+  const bool wave_live = w_row0 < n;
+  const int wave_first = first_key(position + w_row0);
+  const int wave_last = min(position + w_row1, span_last);
+  const int open_first = first_key(position + w_row1);
+  const int open_last = min(position + w_row0, span_last);
+
+  // Staging: K segment u of thread tid is (key, seg) = j / kSegs, j % kSegs
+  // with j = tid + kPAThreads u; V job j = tid covers keys 2 (j % 32) and
+  // 2 (j % 32) + 1 of segment j / 32. Keys past the block's last are zero,
+  // so masked probabilities (zero) meet finite V.
+  uint4 kr[kKLoads], vr[2];
+  const auto load = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < kKLoads; ++u) {
+      const int j = tid + kPAThreads * u, t = base + j / kSegs;
+      kr[u] = t <= block_last
+                  ? *reinterpret_cast<const uint4*>(
+                        KeyRow(k, ck, t, position, capacity, stride) + (j % kSegs) * 8)
+                  : make_uint4(0, 0, 0, 0);
+    }
+    if (tid < kVPairs) {
+      const int seg = tid / 32, t = base + 2 * (tid % 32);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        vr[i] = t + i <= block_last
+                    ? *reinterpret_cast<const uint4*>(
+                          KeyRow(v, cv, t + i, position, capacity, stride) + seg * 8)
+                    : make_uint4(0, 0, 0, 0);
+    }
+  };
+  const auto store = [&](int st) {
+#pragma unroll
+    for (int u = 0; u < kKLoads; ++u) {
+      const int j = tid + kPAThreads * u, key = j / kSegs, seg = j % kSegs;
+      *reinterpret_cast<uint4*>(&sK[st][key * D + (seg ^ KeySwizzle<D>(key)) * 8]) = kr[u];
+    }
+    if (tid < kVPairs) {
+      const int seg = tid / 32, key = 2 * (tid % 32);
+      const unsigned a[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
+      const unsigned b[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        // (key, key + 1) halves of dimension seg * 8 + d.
+        const unsigned word = __builtin_amdgcn_perm(b[d / 2], a[d / 2],
+                                                    (d & 1) ? 0x07060302u : 0x05040100u);
+        *reinterpret_cast<unsigned*>(&sV[st][(seg * 8 + d) * kVPitch + key]) = word;
+      }
+    }
+  };
+
+  f4 acc[kDimBlocks];
+#pragma unroll
+  for (int m = 0; m < kDimBlocks; ++m)
+    acc[m] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float maximum = -INFINITY, sum = 0.0f;
+
+  const auto compute = [&](int st, int base) {
+    const Half* tk = sK[st];
+    const Half* tv = sV[st];
+    // S^T block kb: A row r <-> key 32 (kb / 2) + 8 (r / 4) + 4 (kb % 2) + r % 4.
+    f4 s[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int key = 32 * (kb >> 1) + 8 * (col >> 2) + 4 * (kb & 1) + (col & 3);
+      const int swz = KeySwizzle<D>(key);
+      s[kb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st2 = 0; st2 < kSteps; ++st2) {
+        const int seg = 4 * st2 + grp;
+        const h8 a = *reinterpret_cast<const h8*>(&tk[key * D + (seg ^ swz) * 8]);
+        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[st2], s[kb], 0, 0, 0);
+      }
+    }
+    // Lane L's value i of block kb is key base + 32 (kb / 2) + 8 (L / 16) +
+    // 4 (kb % 2) + i of column L % 16.
+    float tile_max = -INFINITY;
+    if (base >= open_first && base + kPAKeys - 1 <= open_last) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          tile_max = fmaxf(tile_max, s[kb][i]);
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = base + 32 * (kb >> 1) + 8 * grp + 4 * (kb & 1) + i;
+          s[kb][i] = (t >= lo && t <= hi) ? s[kb][i] : -INFINITY;
+          tile_max = fmaxf(tile_max, s[kb][i]);
+        }
+    }
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, 64));
+    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, 64));
+    const float next = fmaxf(maximum, tile_max);
+    const float shift = next == -INFINITY ? 0.0f : next;
+    const float alpha = __builtin_amdgcn_exp2f(maximum - shift);
+    maximum = next;
+    // Probabilities round to F16 once; the sum adds the rounded values.
+    unsigned pw[4][2];
+    float local = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const _Float16 a = static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][2 * j] - shift));
+        const _Float16 b =
+            static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][2 * j + 1] - shift));
+        local += float(a) + float(b);
+        pw[kb][j] = unsigned(__builtin_bit_cast(Half, a)) |
+                    (unsigned(__builtin_bit_cast(Half, b)) << 16);
+      }
+    sum = sum * alpha + local;
+    // An unchanged maximum gives alpha == 1 exactly.
+    if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+      for (int m = 0; m < kDimBlocks; ++m)
+        acc[m] *= alpha;
+    }
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) {
+      // P^T operand: keys 32 c2 + 8 (L / 16) + j, j < 8, of column L % 16:
+      // values 0..3 of block 2 c2 then of block 2 c2 + 1.
+      const unsigned w[4] = {pw[2 * c2][0], pw[2 * c2][1], pw[2 * c2 + 1][0],
+                             pw[2 * c2 + 1][1]};
+      const h8 p = __builtin_bit_cast(h8, w);
+#pragma unroll
+      for (int m = 0; m < kDimBlocks; ++m) {
+        const h8 a = *reinterpret_cast<const h8*>(
+            &tv[(16 * m + col) * kVPitch + 32 * c2 + 8 * grp]);
+        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, p, acc[m], 0, 0, 0);
+      }
+    }
+  };
+
+  // Tiles: write the prefetched tile to its stage, one barrier (the tile is
+  // visible, and every wave is done with the stage written two tiles ago),
+  // prefetch the next tile, multiply.
+  if (block_first <= block_last)
+    load(block_first);
+  int it = 0;
+  for (int base = block_first; base <= block_last; base += kPAKeys, ++it) {
+    const int st = it & 1;
+    store(st);
+    __syncthreads();
+    if (base + kPAKeys <= block_last)
+      load(base + kPAKeys);
+    if (!wave_live || base > wave_last || base + kPAKeys <= wave_first)
+      continue;
+    compute(st, base);
+  }
+
+  float total = sum + __shfl_xor(sum, 16, 64);
+  total += __shfl_xor(total, 32, 64);
+  if (!live)
+    return;
+  // Lane L holds dimensions 16 m + 4 (L / 16) + i of its column.
+  if (partial) {
+    float* part = partial + ((std::size_t(split) * n + row) * heads + head) * (D + 2);
+    if (grp == 0) {
+      part[0] = maximum;
+      part[1] = total;
+    }
+    // Records are D + 2 floats: plain float stores (no 16-byte alignment).
+#pragma unroll
+    for (int m = 0; m < kDimBlocks; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        part[2 + 16 * m + 4 * grp + i] = acc[m][i];
+    return;
+  }
+  const float g_scale = 1.0f + expf(-gate[std::size_t(row) * ldg + head]);
+  float* o = out + std::size_t(row) * ldo + head * D;
+#pragma unroll
+  for (int m = 0; m < kDimBlocks; ++m) {
+    f4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      r[i] = (acc[m][i] / total) / g_scale;
+    *reinterpret_cast<f4*>(o + 16 * m + 4 * grp) = r;
+  }
+}
+
+// hip/ops.hip:1692-1709: merges key spans (base-2 maxima); one block per
+// (row, head), one thread per dimension.
+template<int D>
+__launch_bounds__(D) __global__
+    void CombineSpansKernel(const float* __restrict__ partial, const float* __restrict__ gate,
+                            int ldg, float* __restrict__ out, int ldo, int n, int heads,
+                            int splits) {
+  const int rh = blockIdx.x, d = threadIdx.x;
+  const int row = rh / heads, head = rh % heads;
+  const std::size_t rows = std::size_t(n) * heads;
+  float maximum = -INFINITY;
+  for (int s = 0; s < splits; ++s)
+    maximum = fmaxf(maximum, partial[(s * rows + rh) * (D + 2)]);
+  float sum = 0.0f, acc = 0.0f;
+  for (int s = 0; s < splits; ++s) {
+    const float* part = partial + (s * rows + rh) * (D + 2);
+    const float w = __builtin_amdgcn_exp2f(part[0] - maximum);
+    sum = fmaf(part[1], w, sum);
+    acc = fmaf(part[2 + d], w, acc);
+  }
+  out[std::size_t(row) * ldo + head * D + d] =
+      (acc / sum) / (1.0f + expf(-gate[std::size_t(row) * ldg + head]));
+}
+
+struct PromptArgs {
+  const float* q;
+  int ldq;
+  const Half* k;
+  const Half* v;
+  const float* gate;
+  int ldg;
+  const Half* ck;
+  const Half* cv;
+  float* out;
+  int ldo;
+  float* partial;
+  int n, heads, kv_heads, position, capacity, window, span, splits;
+};
+
+template<int D, int G>
+void LaunchPrompt(const PromptArgs& a, hipStream_t s) {
+  constexpr int kRows = kPACols / G;
+  const dim3 grid((a.n + kRows - 1) / kRows, a.splits, a.kv_heads);
+  PromptAttentionKernel<D, G><<<grid, kPAThreads, 0, s>>>(
+      a.q, a.ldq, a.k, a.v, a.gate, a.ldg, a.ck, a.cv, a.out, a.ldo,
+      a.splits > 1 ? a.partial : nullptr, a.n, a.heads, a.kv_heads, a.position, a.capacity,
+      a.window, a.span);
+  if (a.splits > 1)
+    CombineSpansKernel<D><<<a.n * a.heads, D, 0, s>>>(a.partial, a.gate, a.ldg, a.out, a.ldo,
+                                                       a.n, a.heads, a.splits);
+}
+
+template<int D>
+void LaunchPromptGroup(const PromptArgs& a, int group, hipStream_t s) {
+  if (group == 2)
+    LaunchPrompt<D, 2>(a, s);
+  else if (group == 4)
+    LaunchPrompt<D, 4>(a, s);
+  else
+    LaunchPrompt<D, 8>(a, s);
+}
+
+int SplitsFor(std::uint32_t position, std::uint32_t n, std::uint32_t window, int& span) {
+  if (window) {
+    span = int(position + n);
+    return 1;
+  }
+  const int splits = PromptSplits(int(position + n), span);
+  if (splits == 1)
+    span = int(position + n);
+  return splits;
+}
+
+}  // namespace
+}  // namespace lfm3amd
+
+using namespace lfm3amd;
+
+extern "C" {
+
+std::size_t lfm3_prompt_attention_workspace_bytes(std::uint32_t rows, std::uint32_t heads,
+                                                  std::uint32_t dim, std::uint32_t position,
+                                                  std::uint32_t window) {
+  int span;
+  const int splits = SplitsFor(position, rows, window, span);
+  return splits > 1 ? std::size_t(splits) * rows * heads * (dim + 2) * sizeof(float) : 0;
+}
+
+int lfm3_prompt_attention(const float* q, std::uint32_t ldq, const std::uint16_t* k,
+                          const std::uint16_t* v, const float* gate, std::uint32_t ldg,
+                          const std::uint16_t* cache_k, const std::uint16_t* cache_v,
+                          float* out, std::uint32_t ldo, std::uint32_t rows,
+                          std::uint32_t heads, std::uint32_t kv_heads, std::uint32_t dim,
+                          std::uint32_t position, std::uint32_t capacity,
+                          std::uint32_t window, void* workspace, std::size_t workspace_bytes,
+                          void* stream) {
+  const std::uint32_t group = kv_heads ? heads / kv_heads : 0;
+  if (!q || !k || !v || !gate || !out || !rows || !heads || !kv_heads || heads % kv_heads ||
+      (group != 2 && group != 4 && group != 8) || (dim != 64 && dim != 128) ||
+      ldq < heads * dim || ldo < heads * dim || ldg < heads || ldq % 4 || ldo % 4 ||
+      (position && (!cache_k || !cache_v || !capacity)) ||
+      (!window && position && capacity < position) ||
+      std::uint64_t(position) + rows > (1ull << 31))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt attention shape");
+  PromptArgs a{};
+  a.splits = SplitsFor(position, rows, window, a.span);
+  const std::size_t need =
+      a.splits > 1 ? std::size_t(a.splits) * rows * heads * (dim + 2) * sizeof(float) : 0;
+  if (need && (!workspace || workspace_bytes < need))
+    return Fail(LFM3_E_INVALID, "LFM3 prompt attention workspace too small");
+  a.q = q;
+  a.ldq = int(ldq);
+  a.k = k;
+  a.v = v;
+  a.gate = gate;
+  a.ldg = int(ldg);
+  a.ck = cache_k;
+  a.cv = cache_v;
+  a.out = out;
+  a.ldo = int(ldo);
+  a.partial = static_cast<float*>(workspace);
+  a.n = int(rows);
+  a.heads = int(heads);
+  a.kv_heads = int(kv_heads);
+  a.position = int(position);
+  a.capacity = int(capacity ? capacity : 1);
+  a.window = int(window);
+  const auto s = static_cast<hipStream_t>(stream);
+  if (dim == 128)
+    LaunchPromptGroup<128>(a, int(group), s);
+  else
+    LaunchPromptGroup<64>(a, int(group), s);
+  return HipStatus(hipGetLastError(), "LFM3 prompt attention launch");
+}
+
+}  // extern "C"

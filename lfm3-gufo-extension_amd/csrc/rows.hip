@@ -4,6 +4,8 @@
 #include <cmath>
 #include <string>
 
+#include <algorithm>
+
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -226,10 +228,38 @@ __launch_bounds__(kNormThreads) __global__
   WriteOperandRow(s_row, H, row, maximum, image, exps);
 }
 
-// Per-head RMSNorm + paired RoPE + F16 store. A block is one row and the
-// dim / 2 threads of a head own the pairs (i, i + dim / 2); blockIdx.x walks
-// the query heads, then the KV heads, which also store K and V to the
-// row's ring slot. Sub-wave reductions cover one head (dim / 2 lanes).
+// Per-head RMSNorm + paired RoPE of one head (the dim / 2 threads own the
+// pairs (i, i + dim / 2)); writes the rotated head back and returns the
+// pair. Sub-wave reductions cover one head (dim / 2 lanes).
+template<int D>
+__device__ __forceinline__ void NormRotateHead(float* __restrict__ xh,
+                                               const float* __restrict__ w,
+                                               const float* __restrict__ frequencies,
+                                               const float* __restrict__ factors,
+                                               std::uint32_t position, float eps, int pair,
+                                               float& r0, float& r1) {
+  constexpr int P = D / 2;
+  const float x0 = xh[pair], x1 = xh[pair + P];
+  float squares = fmaf(x0, x0, x1 * x1);
+#pragma unroll
+  for (int m = P / 2; m; m >>= 1)
+    squares += __shfl_xor(squares, m, P);
+  const float scale = 1.0f / sqrtf(squares / float(D) + eps);
+  const float a = (x0 * scale) * w[pair], b = (x1 * scale) * w[pair + P];
+  float angle = float(position) * frequencies[pair];
+  if (factors)
+    angle /= factors[pair];
+  float sn, cs;
+  sincosf(angle, &sn, &cs);
+  r0 = a * cs - b * sn;
+  r1 = b * cs + a * sn;
+  xh[pair] = r0;
+  xh[pair + P] = r1;
+}
+
+// Decode heads: a block is one row (with its own position and ring) and
+// blockIdx.x walks the query heads, then the KV heads, which also store K
+// and V to the row's ring slot position % capacity.
 template<int D>
 __launch_bounds__(D / 2) __global__
     void HeadsKernel(float* __restrict__ q, float* __restrict__ k,
@@ -249,23 +279,10 @@ __launch_bounds__(D / 2) __global__
   const int kvh = head - heads;
   float* xh = is_key ? k + std::size_t(row) * ld + kvh * D
                      : q + std::size_t(row) * ld + head * D;
-  const float* w = is_key ? k_norm : q_norm;
-  const float x0 = xh[pair], x1 = xh[pair + P];
-  float squares = fmaf(x0, x0, x1 * x1);
-#pragma unroll
-  for (int m = P / 2; m; m >>= 1)
-    squares += __shfl_xor(squares, m, P);
-  const float scale = 1.0f / sqrtf(squares / float(D) + eps);
-  const float a = (x0 * scale) * w[pair], b = (x1 * scale) * w[pair + P];
   const std::uint32_t position = positions[row];
-  float angle = float(position) * frequencies[pair];
-  if (factors)
-    angle /= factors[pair];
-  float sn, cs;
-  sincosf(angle, &sn, &cs);
-  const float r0 = a * cs - b * sn, r1 = b * cs + a * sn;
-  xh[pair] = r0;
-  xh[pair + P] = r1;
+  float r0, r1;
+  NormRotateHead<D>(xh, is_key ? k_norm : q_norm, frequencies, factors, position, eps, pair,
+                    r0, r1);
   if (!is_key)
     return;
   const std::size_t slot =
@@ -277,6 +294,158 @@ __launch_bounds__(D / 2) __global__
   ck[slot + pair + P] = FloatToHalfBits(r1);
   cv[slot + pair] = FloatToHalfBits(vh[pair]);
   cv[slot + pair + P] = FloatToHalfBits(vh[pair + P]);
+}
+
+// Prompt heads (hip/ops.hip:2407-2417 PromptHeads): row r of a chunk is at
+// position + r and its K/V go to row r of k16/v16 (kv_heads * D halves a
+// row), which is either a staging chunk or the cache rows themselves.
+template<int D>
+__launch_bounds__(D / 2) __global__
+    void PromptHeadsKernel(float* __restrict__ q, float* __restrict__ k,
+                           const float* __restrict__ v, int ld,
+                           const float* __restrict__ q_norm,
+                           const float* __restrict__ k_norm,
+                           const float* __restrict__ frequencies,
+                           const float* __restrict__ factors, Half* __restrict__ k16,
+                           Half* __restrict__ v16, int heads, int kv_heads,
+                           std::uint32_t position, float eps) {
+  constexpr int P = D / 2;
+  const int head = blockIdx.x, row = blockIdx.y, pair = threadIdx.x;
+  const bool is_key = head >= heads;
+  const int kvh = head - heads;
+  float* xh = is_key ? k + std::size_t(row) * ld + kvh * D
+                     : q + std::size_t(row) * ld + head * D;
+  float r0, r1;
+  NormRotateHead<D>(xh, is_key ? k_norm : q_norm, frequencies, factors,
+                    position + std::uint32_t(row), eps, pair, r0, r1);
+  if (!is_key)
+    return;
+  const std::size_t slot = (std::size_t(row) * kv_heads + kvh) * D;
+  const float* vh = v + std::size_t(row) * ld + kvh * D;
+  k16[slot + pair] = FloatToHalfBits(r0);
+  k16[slot + pair + P] = FloatToHalfBits(r1);
+  v16[slot + pair] = FloatToHalfBits(vh[pair]);
+  v16[slot + pair + P] = FloatToHalfBits(vh[pair + P]);
+}
+
+// StoreKV (hip/ops.hip:1737-1749, engine.cpp:467-470): rows 0..n-1 of a
+// chunk at position + r go to ring slot (position + r) % capacity; only the
+// last min(n, capacity) rows have distinct slots, so only they are copied.
+__global__ void StoreRingKernel(const Half* __restrict__ k16, const Half* __restrict__ v16,
+                                Half* __restrict__ ck, Half* __restrict__ cv, int n,
+                                int stride, std::uint32_t position, std::uint32_t capacity) {
+  const std::size_t i = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int kept = min(n, int(capacity)), first = n - kept;
+  if (i >= std::size_t(kept) * stride)
+    return;
+  const int r = first + int(i / stride);
+  const std::size_t e = i % stride;
+  const std::size_t src = std::size_t(r) * stride + e;
+  const std::size_t dst = std::size_t((position + std::uint32_t(r)) % capacity) * stride + e;
+  ck[dst] = k16[src];
+  cv[dst] = v16[src];
+}
+
+// Prompt convolution over packed ragged segments (hip/ops.hip:990-1044
+// ConvolutionWindow and ConvolutionHistory; engine.cpp:386-400): segment s
+// is rows [begin, begin + rows) of p and y and continues its own history
+// [H][L - 1] (oldest first). A thread slides one channel's window down
+// kConvRows rows, forming each B x product once. The window sum keeps
+// ConvStepKernel's expressions and order (reference.cpp:85-101), so n
+// prompt rows give bit-identical outputs to n decode steps; the history
+// moves in a second launch, after every window has read it.
+constexpr int kConvRows = 16;
+constexpr int kMaxConvSegments = 8;
+struct ConvSegments {
+  float* history[kMaxConvSegments];
+  int begin[kMaxConvSegments];
+  int rows[kMaxConvSegments];
+};
+
+template<int L>
+__global__ void PromptConvKernel(const float* __restrict__ p, int ldp,
+                                 const float* __restrict__ taps, ConvSegments seg,
+                                 float* __restrict__ y, int ldy, int H) {
+#pragma clang fp contract(off)
+  const int s = blockIdx.z, ch = blockIdx.x * blockDim.x + threadIdx.x;
+  const int first = blockIdx.y * kConvRows, rows = seg.rows[s];
+  if (ch >= H || first >= rows)
+    return;
+  const float* ps = p + std::size_t(seg.begin[s]) * ldp;
+  float* ys = y + std::size_t(seg.begin[s]) * ldy;
+  const float* hist = seg.history[s] + std::size_t(ch) * (L - 1);
+  float w[L], win[L];
+#pragma unroll
+  for (int t = 0; t < L; ++t)
+    w[t] = taps[std::size_t(ch) * L + t];
+  const auto bx = [&](int r) {
+    return r >= 0 ? ps[std::size_t(r) * ldp + ch] * ps[std::size_t(r) * ldp + 2 * H + ch]
+                  : hist[(L - 1) + r];
+  };
+  // win[t] holds the product of row r - (L - 1) + t.
+#pragma unroll
+  for (int t = 0; t < L - 1; ++t)
+    win[t + 1] = bx(first - (L - 1) + t);
+  const int last = min(first + kConvRows, rows);
+  for (int r = first; r < last; ++r) {
+#pragma unroll
+    for (int t = 0; t < L - 1; ++t)
+      win[t] = win[t + 1];
+    win[L - 1] = bx(r);
+    float sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < L; ++t)
+      sum += w[t] * win[t];
+    ys[std::size_t(r) * ldy + ch] = sum * ps[std::size_t(r) * ldp + H + ch];
+  }
+}
+
+// Any width: each output recomputes its window's products (same values and
+// order as PromptConvKernel).
+__global__ void PromptConvAnyKernel(const float* __restrict__ p, int ldp,
+                                    const float* __restrict__ taps, ConvSegments seg,
+                                    float* __restrict__ y, int ldy, int H, int L) {
+#pragma clang fp contract(off)
+  const int s = blockIdx.z, ch = blockIdx.x * blockDim.x + threadIdx.x;
+  const int first = blockIdx.y * kConvRows, rows = seg.rows[s];
+  if (ch >= H || first >= rows)
+    return;
+  const float* ps = p + std::size_t(seg.begin[s]) * ldp;
+  float* ys = y + std::size_t(seg.begin[s]) * ldy;
+  const float* hist = seg.history[s] + std::size_t(ch) * (L - 1);
+  const int last = min(first + kConvRows, rows);
+  for (int r = first; r < last; ++r) {
+    float sum = 0.0f;
+    for (int t = 0; t < L; ++t) {
+      const int src = r - (L - 1) + t;
+      const float b = src >= 0 ? ps[std::size_t(src) * ldp + ch] *
+                                     ps[std::size_t(src) * ldp + 2 * H + ch]
+                               : hist[(L - 1) + src];
+      sum += taps[std::size_t(ch) * L + t] * b;
+    }
+    ys[std::size_t(r) * ldy + ch] = sum * ps[std::size_t(r) * ldp + H + ch];
+  }
+}
+
+// The history after a segment: its last L - 1 B x products, reaching into
+// the old history when the segment is shorter.
+__global__ void PromptConvHistoryKernel(const float* __restrict__ p, int ldp,
+                                        ConvSegments seg, int H, int L) {
+#pragma clang fp contract(off)
+  const int s = blockIdx.y, ch = blockIdx.x * blockDim.x + threadIdx.x;
+  if (ch >= H)
+    return;
+  const int rows = seg.rows[s];
+  const float* ps = p + std::size_t(seg.begin[s]) * ldp;
+  float* hist = seg.history[s] + std::size_t(ch) * (L - 1);
+  float past[31];
+  for (int j = 0; j < L - 1; ++j) {
+    const int r = rows - (L - 1) + j;
+    past[j] = r >= 0 ? ps[std::size_t(r) * ldp + ch] * ps[std::size_t(r) * ldp + 2 * H + ch]
+                     : hist[(L - 1) + r];
+  }
+  for (int j = 0; j < L - 1; ++j)
+    hist[j] = past[j];
 }
 
 // Greedy argmax: one block per row scans the row with a 64-bit key per
@@ -457,6 +626,71 @@ int lfm3_decode_heads_ragged(float* q, float* k, const float* v,
                                         positions, capacity, int(heads),
                                         int(kv_heads), eps);
   return HipStatus(hipGetLastError(), "LFM3 decode heads launch");
+}
+
+int lfm3_prompt_heads(float* q, float* k, const float* v, std::uint32_t ld,
+                      const float* q_norm, const float* k_norm, const float* frequencies,
+                      const float* factors, std::uint16_t* k16, std::uint16_t* v16,
+                      std::uint32_t rows, std::uint32_t heads, std::uint32_t kv_heads,
+                      std::uint32_t dim, std::uint32_t position, float eps, void* stream) {
+  if (!q || !k || !v || !q_norm || !k_norm || !frequencies || !k16 || !v16 || !rows ||
+      !heads || !kv_heads || heads % kv_heads || (dim != 64 && dim != 128) ||
+      rows > 65535 || std::uint64_t(position) + rows > (1ull << 31))
+    return Fail(LFM3_E_INVALID, "LFM3 prompt heads need dimension 64 or 128");
+  const dim3 grid(heads + kv_heads, rows);
+  const auto s = static_cast<hipStream_t>(stream);
+  if (dim == 128)
+    PromptHeadsKernel<128><<<grid, 64, 0, s>>>(q, k, v, int(ld), q_norm, k_norm, frequencies,
+                                               factors, k16, v16, int(heads), int(kv_heads),
+                                               position, eps);
+  else
+    PromptHeadsKernel<64><<<grid, 32, 0, s>>>(q, k, v, int(ld), q_norm, k_norm, frequencies,
+                                              factors, k16, v16, int(heads), int(kv_heads),
+                                              position, eps);
+  return HipStatus(hipGetLastError(), "LFM3 prompt heads launch");
+}
+
+int lfm3_store_kv(const std::uint16_t* k16, const std::uint16_t* v16, std::uint16_t* cache_k,
+                  std::uint16_t* cache_v, std::uint32_t rows, std::uint32_t stride,
+                  std::uint32_t position, std::uint32_t capacity, void* stream) {
+  if (!k16 || !v16 || !cache_k || !cache_v || !rows || !stride || !capacity)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 K/V ring store");
+  const std::size_t count = std::size_t(std::min(rows, capacity)) * stride;
+  StoreRingKernel<<<(count + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      k16, v16, cache_k, cache_v, int(rows), int(stride), position, capacity);
+  return HipStatus(hipGetLastError(), "LFM3 K/V ring store launch");
+}
+
+int lfm3_conv_prompt(const float* p, std::uint32_t ldp, const float* taps,
+                     float* const* history, const std::uint32_t* begin,
+                     const std::uint32_t* rows, std::uint32_t segments, float* y,
+                     std::uint32_t ldy, std::uint32_t hidden, std::uint32_t width,
+                     int update_history, void* stream) {
+  if (!p || !taps || !history || !begin || !rows || !y || !segments ||
+      segments > kMaxConvSegments || !hidden || width < 2 || width > 32 ||
+      ldp < 3 * hidden || ldy < hidden)
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt convolution shape");
+  ConvSegments seg{};
+  std::uint32_t most = 0;
+  for (std::uint32_t i = 0; i < segments; ++i) {
+    if (!history[i] || !rows[i])
+      return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt convolution shape");
+    seg.history[i] = history[i];
+    seg.begin[i] = int(begin[i]);
+    seg.rows[i] = int(rows[i]);
+    most = std::max(most, rows[i]);
+  }
+  const auto s = static_cast<hipStream_t>(stream);
+  const dim3 grid((hidden + 127) / 128, (most + kConvRows - 1) / kConvRows, segments);
+  if (width == 7)
+    PromptConvKernel<7><<<grid, 128, 0, s>>>(p, int(ldp), taps, seg, y, int(ldy), int(hidden));
+  else
+    PromptConvAnyKernel<<<grid, 128, 0, s>>>(p, int(ldp), taps, seg, y, int(ldy), int(hidden),
+                                             int(width));
+  if (update_history)
+    PromptConvHistoryKernel<<<dim3((hidden + 127) / 128, segments), 128, 0, s>>>(
+        p, int(ldp), seg, int(hidden), int(width));
+  return HipStatus(hipGetLastError(), "LFM3 prompt convolution launch");
 }
 
 std::size_t lfm3_argmax_workspace_bytes(std::uint32_t rows) {

@@ -182,3 +182,16 @@ def test_kernel_entry_points_refuse_unsupported_shapes():
     assert lib.lfm3_decode_attention_ragged(1, 8, 1, 8, 1, 1, 1, 1, 1, 1, 8, 1, 6, 2, 128,
                                             1, 1 << 20, None) == L.E_INVALID  # group 3
     assert b"attention" in lib.lfm3_last_error()
+
+
+def test_prompt_attention_rejects_bad_shapes():
+    """Unsupported dimension or group, and a split history without its
+    workspace, are refused before any launch."""
+    lib = L.lib()
+    assert lib.lfm3_prompt_attention(1, 512, 1, 1, 1, 4, 1, 1, 1, 512, 8, 4, 2, 96, 0, 1, 0,
+                                     None, 0, None) == L.E_INVALID
+    assert lib.lfm3_prompt_attention(1, 768, 1, 1, 1, 6, 1, 1, 1, 768, 8, 6, 2, 128, 0, 1, 0,
+                                     None, 0, None) == L.E_INVALID  # group 3
+    # a split history without its workspace
+    assert lib.lfm3_prompt_attention(1, 512, 1, 1, 1, 4, 1, 1, 1, 512, 40, 4, 2, 128, 17000,
+                                     17040, 0, None, 0, None) == L.E_INVALID
