@@ -140,6 +140,13 @@ int lfm3_q8_gemm(const void* codes, const void* scales, uint32_t rows,
                  uint32_t cols, const uint16_t* a, uint32_t lda,
                  const float* a_scale, uint32_t tokens, float* y, uint32_t ldy,
                  uint32_t parts, void* stream);
+/* Adds K parts 1..parts-1 of a lfm3_q8_gemm output into part 0 in part
+   order: y[r][c] += y[p][r][c] for p = 1.. (part_stride floats apart; row
+   stride ld). For consumers that read one FP32 row (convolution, heads).
+   Replaces: the deterministic split-K merge of LaunchSplit
+   (hip/ops.hip:2019-2119). */
+int lfm3_sum_parts(float* y, size_t part_stride, uint32_t rows, uint32_t cols,
+                   uint32_t ld, uint32_t parts, void* stream);
 /* Gate/up over a stride-2 interleaved pair with the SwiGLU epilogue
    (q8_prefill.hpp:622-635): y = silu(g) * u, and atomicMax of each token
    row's max |y| (FP32 bits) into row_max (NULL: skipped), which must hold
@@ -415,6 +422,17 @@ int lfm3_session_state(lfm3_session* session, int kind, uint32_t layer,
    (Session::FinishRestore, engine.cpp:1380-1386). */
 int lfm3_session_set_position(lfm3_session* session, uint32_t position);
 
+/* Session::Forward (engine.cpp:882-938): n tokens of one session in
+   chunks of 512 rows (engine.hpp:47); logits (vocab floats, may be NULL)
+   receive the last token's logits. Refuses an empty or oversized token
+   list, out-of-range tokens and a poisoned session without touching state;
+   a device failure poisons the session. A chunk of 16 rows or more runs
+   the prompt path (FP16 row-scaled projections on the matrix cores,
+   packed convolution, prompt heads and MFMA prompt attention), with the
+   reference's trailing-row pruning (engine.cpp:304-323); shorter chunks
+   use the FP32 projections, and one token is one decode row. */
+int lfm3_session_forward(lfm3_session* session, const uint32_t* tokens,
+                         size_t n, float* logits);
 /* Session::ForwardBatch (engine.cpp:1160-1216): one token per distinct
    session (at most 8), logits copied to host rows logits[i] (vocab floats
    each). On a device failure every session of the batch is poisoned. */

@@ -26,7 +26,9 @@
 namespace lfm3amd {
 namespace {
 
-constexpr std::uint32_t kMaxBatch = 8;  // engine.hpp:48
+constexpr std::uint32_t kMaxBatch = 8;       // engine.hpp:48
+constexpr std::uint32_t kPrefillChunk = 512;  // engine.hpp:47
+constexpr std::uint32_t kPromptRows = 16;     // hip/ops.hpp:32: FP16 GEMM from here
 
 struct Error : std::runtime_error {
   int status;
@@ -137,6 +139,15 @@ struct RoundTable {
 
 std::size_t Align(std::size_t n) { return (n + 255) / 256 * 256; }
 
+// Scratch of one prompt chunk (kPrefillChunk rows), made on the first
+// prompt and shared by the model's prompts (calls are serialized).
+struct PromptBuffers {
+  Buffer tokens, x, z, a16, scale, proj, mix, hid, out, row_max, chunk_k, chunk_v, attn_ws;
+  Buffer one_table;  // one decode-attention row: ring pointers, capacity, position, items
+  std::unique_ptr<PinnedBuffer> one_staging;
+  std::size_t lda = 0, proj_ld = 0, attn_ws_bytes = 0, one_bytes = 0, one_items = 0;
+};
+
 }  // namespace
 }  // namespace lfm3amd
 
@@ -165,6 +176,7 @@ struct lfm3_model {
   Buffer attn_ws;
   std::size_t attn_ws_bytes = 0;
   std::uint32_t max_context = 0;
+  std::unique_ptr<PromptBuffers> prompt;
 
   ~lfm3_model() {
     if (stream)
@@ -699,6 +711,268 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
   }
 }
 
+PromptBuffers& EnsurePromptBuffers(lfm3_model& m) {
+  if (m.prompt)
+    return *m.prompt;
+  const auto& c = m.config;
+  const std::size_t R = kPrefillChunk, H = c.hidden, F = c.intermediate, D = c.head_dim;
+  auto b = std::make_unique<PromptBuffers>();
+  std::size_t widest = std::max<std::size_t>({H, F, std::size_t(c.heads) * D});
+  b->lda = (widest + 63) / 64 * 64;
+  std::size_t proj_rows = 3 * H, kv_max = 0;
+  for (const auto& l : m.layers)
+    if (l.type != LFM3_LAYER_CONV) {
+      proj_rows = std::max<std::size_t>(proj_rows, l.qkvg_ld);
+      kv_max = std::max<std::size_t>(kv_max, l.kv);
+    }
+  b->proj_ld = (proj_rows + 3) / 4 * 4;
+  b->tokens = Buffer(R * 4);
+  b->x = Buffer(R * H * 4);
+  b->z = Buffer(R * H * 4);
+  b->a16 = Buffer(R * b->lda * 2);
+  b->scale = Buffer(R * 4);
+  b->proj = Buffer(8 * R * b->proj_ld * 4);  // up to 8 K parts
+  b->mix = Buffer(R * std::max<std::size_t>(H, std::size_t(c.heads) * D) * 4);
+  b->hid = Buffer(R * F * 4);
+  b->out = Buffer(8 * R * H * 4);
+  b->row_max = Buffer(R * 4);
+  b->chunk_k = Buffer(R * std::max<std::size_t>(kv_max, 1) * D * 2);
+  b->chunk_v = Buffer(R * std::max<std::size_t>(kv_max, 1) * D * 2);
+  b->attn_ws_bytes = std::max<std::size_t>(
+      lfm3_prompt_attention_workspace_bytes(std::uint32_t(R), c.heads, std::uint32_t(D),
+                                            c.context, 0),
+      256);
+  b->attn_ws = Buffer(b->attn_ws_bytes);
+  b->one_items = lfm3_attention_max_items(1, c.context);
+  b->one_bytes = Align(4 * sizeof(void*)) + Align(b->one_items * sizeof(lfm3_attention_item));
+  b->one_table = Buffer(b->one_bytes);
+  b->one_staging = std::make_unique<PinnedBuffer>(b->one_bytes);
+  m.prompt = std::move(b);
+  return *m.prompt;
+}
+
+// Trailing-row pruning (engine.cpp:304-323): only the frontier row leaves
+// the last layer, so trailing layers skip rows nothing reads. Walking back,
+// a convolution needs conv_width - 1 earlier rows for its outputs and
+// history, and an attention layer needs every row for its K/V (a sliding
+// one also for its ring). Layer i reads the last live_in[i] rows and
+// updates the last live_out[i] rows of the residual stream.
+void PruneRows(const lfm3_config& c, std::uint32_t n, std::vector<std::uint32_t>& live_in,
+               std::vector<std::uint32_t>& live_out) {
+  live_in.assign(c.n_layers, n);
+  live_out.assign(c.n_layers, n);
+  std::uint32_t need = 1;
+  for (std::uint32_t i = c.n_layers; i-- > 0;) {
+    if (c.layer_type[i] == LFM3_LAYER_SLIDING)
+      break;
+    live_out[i] = std::min(n, need);
+    if (c.layer_type[i] == LFM3_LAYER_FULL)
+      break;
+    need = std::min(n, need + c.conv_width - 1);
+    live_in[i] = need;
+  }
+}
+
+// One prompt chunk of n rows of one session (engine.cpp:257-527, the
+// single-session branch; Session::Forward engine.cpp:882-938 calls it per
+// kPrefillChunk tokens). Rows from kPromptRows on enter the projections as
+// FP16 row-scaled activations on the MFMA GEMM; fewer rows use the FP32
+// GEMV (hip/ops.hpp:32). The convolution continues the session's history;
+// full-attention K/V rows are written in place into the cache (the ring
+// does not wrap), sliding ones are staged and stored to the ring after
+// attention read its history (engine.cpp:437-470).
+void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std::uint32_t n,
+               bool want_logits) {
+  const auto& c = m.config;
+  const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
+  const std::uint32_t L = c.n_layers, position = se.position;
+  const hipStream_t s = m.stream;
+  PromptBuffers& b = EnsurePromptBuffers(m);
+  std::vector<std::uint32_t> live_in, live_out;
+  PruneRows(c, n, live_in, live_out);
+
+  float* x = b.x.as<float>();
+  float* z = b.z.as<float>();
+  float* proj = b.proj.as<float>();
+  float* mix = b.mix.as<float>();
+  float* hid = b.hid.as<float>();
+  float* out = b.out.as<float>();
+  auto* a16 = b.a16.as<std::uint16_t>();
+  float* scale = b.scale.as<float>();
+  auto* row_max = b.row_max.as<unsigned>();
+  const std::uint32_t lda = std::uint32_t(b.lda), pld = std::uint32_t(b.proj_ld);
+
+  const auto halves = [&](const float* in, std::uint32_t ldx, const unsigned* rmax,
+                          std::uint32_t rows, std::uint32_t cols) {
+    CheckStatus(lfm3_half_rows(in, ldx, rmax, a16, lda, scale, rows, cols, s));
+  };
+  const auto gemv = [&](const Matrix& w, const float* in, std::uint32_t ldx, float* y,
+                        std::uint32_t ldy, std::uint32_t rows, bool swiglu) {
+    for (std::uint32_t r = 0; r < rows; r += kMaxBatch) {
+      const std::uint32_t k = std::min(kMaxBatch, rows - r);
+      if (swiglu)
+        CheckStatus(lfm3_q8_gemv_swiglu(w.codes.p, w.scales.p, F, H, in + std::size_t(r) * ldx,
+                                        ldx, y + std::size_t(r) * ldy, ldy, k, nullptr, 0, s));
+      else
+        CheckStatus(lfm3_q8_gemv(w.codes.p, w.scales.p, w.rows, w.cols,
+                                 in + std::size_t(r) * ldx, ldx, y + std::size_t(r) * ldy, ldy,
+                                 k, nullptr, 0, s));
+    }
+  };
+  // y (rows x w.rows) = rows of `in` times W^T as one FP32 output.
+  const auto project = [&](const Matrix& w, const float* in, std::uint32_t ldx,
+                           std::uint32_t rows, float* y, std::uint32_t ldy) {
+    if (rows < kPromptRows) {
+      gemv(w, in, ldx, y, ldy, rows, false);
+      return;
+    }
+    halves(in, ldx, nullptr, rows, w.cols);
+    const std::uint32_t parts = lfm3_q8_gemm_parts(w.rows, w.cols, rows, 0);
+    CheckStatus(lfm3_q8_gemm(w.codes.p, w.scales.p, w.rows, w.cols, a16, lda, scale, rows, y,
+                             ldy, parts, s));
+    CheckStatus(lfm3_sum_parts(y, std::size_t(ldy) * rows, rows, w.rows, ldy, parts, s));
+  };
+  // Hidden-wide outputs go to `out` as K parts that the next residual norm
+  // adds in part order; returns the part count. With activations already
+  // in a16 (staged), the FP16 conversion is skipped.
+  const auto dense = [&](const Matrix& w, const float* in, std::uint32_t ldx,
+                         std::uint32_t rows, bool staged) -> std::uint32_t {
+    if (rows < kPromptRows) {
+      gemv(w, in, ldx, out, H, rows, false);
+      return 1;
+    }
+    if (!staged)
+      halves(in, ldx, nullptr, rows, w.cols);
+    const std::uint32_t parts = lfm3_q8_gemm_parts(w.rows, w.cols, rows, 0);
+    CheckStatus(lfm3_q8_gemm(w.codes.p, w.scales.p, w.rows, w.cols, a16, lda, scale, rows, out,
+                             H, parts, s));
+    return parts;
+  };
+  const auto residual_norm = [&](std::uint32_t parts, const Buffer* post, const Buffer* next,
+                                 std::uint32_t rows) {
+    const std::size_t o = std::size_t(n - rows) * H;
+    CheckStatus(lfm3_residual_norm_parts(parts ? out : nullptr, parts ? parts : 1,
+                                         std::size_t(rows) * H,
+                                         post && post->p ? post->as<float>() : nullptr, x + o,
+                                         next ? next->as<float>() : nullptr, z + o, rows, H,
+                                         c.eps, s));
+  };
+
+  Check(hipMemcpyAsync(b.tokens.p, tokens, std::size_t(n) * 4, hipMemcpyHostToDevice, s),
+        "token upload");
+  CheckStatus(lfm3_embed(m.embedding.codes.p, m.embedding.scales.p, c.vocab, H,
+                         b.tokens.as<std::uint32_t>(), n, x, s));
+  residual_norm(0, nullptr, &m.layers[0].norm, live_in[0]);
+  for (std::uint32_t il = 0; il < L; ++il) {
+    const Layer& l = m.layers[il];
+    auto& state = se.states[il];
+    const std::uint32_t rows_in = live_in[il], rows_out = live_out[il];
+    const std::uint32_t o_in = n - rows_in, o = n - rows_out;
+    std::uint32_t parts;
+    if (l.type == LFM3_LAYER_CONV) {
+      project(l.in_proj, z + std::size_t(o_in) * H, H, rows_in, proj, 3 * H);
+      // Rows before the first live one are not read: outputs that would
+      // need them are not live either (engine.cpp:386-393).
+      float* hist = state.conv.as<float>();
+      const std::uint32_t begin = 0;
+      CheckStatus(lfm3_conv_prompt(proj, 3 * H, l.conv.as<float>(), &hist, &begin, &rows_in, 1,
+                                   mix, H, H, c.conv_width, 1, s));
+      parts = dense(l.out_proj, mix + std::size_t(o - o_in) * H, H, rows_out, false);
+    } else {
+      const bool swa = l.type == LFM3_LAYER_SLIDING;
+      const std::uint32_t stride = l.kv * D;
+      project(l.qkvg, z, H, n, proj, pld);
+      const float* table = swa ? m.freq_sliding.as<float>() : m.freq_global.as<float>();
+      const float* factors = swa ? nullptr : m.factors.as<float>();
+      auto* ck = state.k.as<std::uint16_t>();
+      auto* cv = state.v.as<std::uint16_t>();
+      // Full-attention rows never wrap, so the chunk is packed in place; a
+      // sliding ring is written only after attention read its history.
+      std::uint16_t* kc = swa ? b.chunk_k.as<std::uint16_t>() : ck + std::size_t(position) * stride;
+      std::uint16_t* vc = swa ? b.chunk_v.as<std::uint16_t>() : cv + std::size_t(position) * stride;
+      CheckStatus(lfm3_prompt_heads(proj + l.q_off, proj + l.k_off, proj + l.v_off, pld,
+                                    l.q_norm.as<float>(), l.k_norm.as<float>(), table, factors,
+                                    kc, vc, n, c.heads, l.kv, D, position, c.eps, s));
+      // Only the last rows_out queries are live.
+      const std::uint32_t skip = n - rows_out;
+      float* q_rows = proj + std::size_t(skip) * pld + l.q_off;
+      float* g_rows = proj + std::size_t(skip) * pld + l.g_off;
+      float* a_rows = mix + std::size_t(skip) * c.heads * D;
+      if (rows_out == 1 && !swa) {
+        // One live row reads the cache through the FP32 decode attention
+        // (hip/ops.hip:2295-2315), as the reference's n == 1 call does.
+        auto* host = static_cast<std::uint8_t*>(b.one_staging->p);
+        auto** ptrs = reinterpret_cast<void**>(host);
+        auto* nums = reinterpret_cast<std::uint32_t*>(host + 2 * sizeof(void*));
+        ptrs[0] = ck;
+        ptrs[1] = cv;
+        nums[0] = state.capacity;
+        nums[1] = position + skip;
+        auto* items = reinterpret_cast<lfm3_attention_item*>(host + Align(4 * sizeof(void*)));
+        const int count = lfm3_attention_plan(&nums[1], 1, 0, items,
+                                              std::uint32_t(b.one_items));
+        if (count < 0)
+          throw Error(LFM3_E_INVALID, lfm3_last_error());
+        auto* dev = b.one_table.as<std::uint8_t>();
+        Check(hipMemcpyAsync(dev, host, b.one_bytes, hipMemcpyHostToDevice, s), "table upload");
+        const std::size_t ws = lfm3_attention_workspace_bytes(std::uint32_t(count), 1, c.heads,
+                                                              l.kv, D);
+        if (ws > m.attn_ws_bytes)
+          throw Error(LFM3_E_INVALID, "LFM3 attention workspace too small");
+        CheckStatus(lfm3_decode_attention_ragged(
+            q_rows, pld, g_rows, pld, reinterpret_cast<const std::uint16_t* const*>(dev),
+            reinterpret_cast<const std::uint16_t* const*>(dev + sizeof(void*)),
+            reinterpret_cast<const std::uint32_t*>(dev + 2 * sizeof(void*)),
+            reinterpret_cast<const lfm3_attention_item*>(dev + Align(4 * sizeof(void*))),
+            std::uint32_t(count), a_rows, c.heads * D, 1, c.heads, l.kv, D, m.attn_ws.p,
+            m.attn_ws_bytes, s));
+        // The staging buffer is reused by the next layer's row.
+        Check(hipStreamSynchronize(s), "decode attention row");
+      } else {
+        CheckStatus(lfm3_prompt_attention(
+            q_rows, pld, kc + std::size_t(skip) * stride, vc + std::size_t(skip) * stride,
+            g_rows, pld, ck, cv, a_rows, c.heads * D, n - skip, c.heads, l.kv, D,
+            position + skip, state.capacity, swa ? c.window : 0, b.attn_ws.p,
+            b.attn_ws_bytes, s));
+      }
+      if (swa)
+        CheckStatus(lfm3_store_kv(kc, vc, ck, cv, n, stride, position, state.capacity, s));
+      parts = dense(l.attn_out, mix + std::size_t(o) * c.heads * D, c.heads * D, rows_out,
+                    false);
+    }
+    residual_norm(parts, &l.post_norm, &l.ffn_norm, rows_out);
+    // FFN over the live rows: SwiGLU (with each row's max |y| for the down
+    // projection's FP16 conversion), then down.
+    const float* zr = z + std::size_t(o) * H;
+    if (rows_out < kPromptRows) {
+      gemv(l.ffn, zr, H, hid, F, rows_out, true);
+      parts = dense(l.down, hid, F, rows_out, false);
+    } else {
+      halves(zr, H, nullptr, rows_out, H);
+      Check(hipMemsetAsync(row_max, 0, std::size_t(rows_out) * 4, s), "row max");
+      CheckStatus(lfm3_q8_gemm_swiglu(l.ffn.codes.p, l.ffn.scales.p, F, H, a16, lda, scale,
+                                      rows_out, hid, F, row_max, s));
+      halves(hid, F, row_max, rows_out, F);
+      parts = dense(l.down, hid, F, rows_out, true);
+    }
+    const bool last = il + 1 == L;
+    residual_norm(parts, &l.post_ffn_norm, last ? nullptr : &m.layers[il + 1].norm, rows_out);
+  }
+  // The frontier row: the last row normed by output_norm; logits from it.
+  CheckStatus(lfm3_residual_norm(nullptr, nullptr, x + std::size_t(n - 1) * H,
+                                 m.output_norm.as<float>(), se.frontier.as<float>(), 1, H,
+                                 c.eps, s));
+  if (want_logits) {
+    const Matrix& head = m.head();
+    CheckStatus(lfm3_q8_gemv(head.codes.p, head.scales.p, c.vocab, H, se.frontier.as<float>(),
+                             H, se.logits.as<float>(), c.vocab, 1, nullptr, 0, s));
+  }
+  Check(hipGetLastError(), "prompt launch");
+  Check(hipStreamSynchronize(s), "prompt");
+  se.position += n;
+  se.logits_ready = want_logits;
+}
+
 // engine.cpp:1178-1195.
 void ValidateBatch(lfm3_session* const* sessions, std::size_t n,
                    const std::uint32_t* tokens) {
@@ -752,6 +1026,50 @@ int BatchEntry(lfm3_session* const* sessions, std::size_t n,
 }  // namespace lfm3amd
 
 extern "C" {
+
+int lfm3_session_forward(lfm3_session* se, const std::uint32_t* tokens, std::size_t n,
+                         float* logits) {
+  try {
+    if (!se)
+      Invalid("null LFM3 session");
+    const auto& c = se->model->config;
+    if (se->poisoned)
+      throw Error(LFM3_E_STATE, "LFM3 session requires Reset after a device error");
+    if (!tokens || n == 0 || n > se->context - se->position)
+      Invalid("invalid LFM3 token/logit count or context exhausted");
+    for (std::size_t i = 0; i < n; ++i)
+      if (tokens[i] >= c.vocab)
+        Invalid("LFM3 token out of range");
+  } catch (const Error& e) {
+    return Fail(e.status, e.what());
+  }
+  lfm3_model& m = *se->model;
+  try {
+    for (std::size_t offset = 0; offset < n; offset += kPrefillChunk) {
+      const auto count = std::uint32_t(std::min<std::size_t>(kPrefillChunk, n - offset));
+      const bool last = offset + count == n;
+      if (count == 1) {
+        // One token is one decode row (engine.cpp:412-436).
+        lfm3_session* one = se;
+        RunRound(m, &one, 1, tokens + offset, false);
+        se->logits_ready = last && logits;
+      } else {
+        RunPrompt(m, *se, tokens + offset, count, last && logits);
+      }
+    }
+    if (logits)
+      Check(hipMemcpy(logits, se->logits.p, std::size_t(m.config.vocab) * 4,
+                      hipMemcpyDeviceToHost),
+            "logits copy");
+    return LFM3_OK;
+  } catch (const Error& e) {
+    se->poisoned = true;  // engine.cpp:924-926
+    return Fail(e.status, e.what());
+  } catch (const std::exception& e) {
+    se->poisoned = true;
+    return Fail(LFM3_E_HIP, e.what());
+  }
+}
 
 int lfm3_forward_batch(lfm3_session* const* sessions, std::size_t n,
                        const std::uint32_t* tokens, float* const* logits) {

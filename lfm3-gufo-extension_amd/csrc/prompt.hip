@@ -384,6 +384,21 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   }
 }
 
+// Adds K parts 1..parts-1 into part 0, in part order (the deterministic
+// merge of split-K partial outputs, hip/ops.hip:2019-2119), for consumers
+// that read one FP32 row.
+__global__ void SumPartsKernel(float* __restrict__ y, std::size_t part_stride, int cols,
+                               int ld, int parts) {
+  const int row = blockIdx.y, col = blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= cols)
+    return;
+  float* p = y + std::size_t(row) * ld + col;
+  float sum = p[0];
+  for (int k = 1; k < parts; ++k)
+    sum += p[std::size_t(k) * part_stride];
+  p[0] = sum;
+}
+
 // K parts for a prompt GEMM: double while the blocks still fit one round
 // on the 256 CUs (one block each, with a quarter over), keeping at least 4
 // chunks a part, at most 8 parts. Each part costs its consumer one more
@@ -457,6 +472,18 @@ int lfm3_q8_gemm(const void* codes, const void* scales, std::uint32_t rows,
                     tokens, y, ldy, rows, int(parts), std::size_t(ldy) * tokens, nullptr,
                     static_cast<hipStream_t>(stream));
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 prompt GEMM launch");
+}
+
+int lfm3_sum_parts(float* y, std::size_t part_stride, std::uint32_t rows,
+                   std::uint32_t cols, std::uint32_t ld, std::uint32_t parts, void* stream) {
+  if (!y || !rows || !cols || ld < cols || !parts || parts > 8 ||
+      (parts > 1 && part_stride < std::size_t(ld) * rows) || rows > 65535)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 part sum");
+  if (parts == 1)
+    return LFM3_OK;
+  SumPartsKernel<<<dim3((cols + 255) / 256, rows), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      y, part_stride, int(cols), int(ld), int(parts));
+  return HipStatus(hipGetLastError(), "LFM3 part sum launch");
 }
 
 int lfm3_q8_gemm_swiglu(const void* codes, const void* scales,

@@ -73,6 +73,7 @@ _SIGS = {
     "lfm3_conv_step_ragged": (i32, [vp, u32, vp, vp, vp, u32, u32, u32, u32, vp]),
     "lfm3_decode_heads_ragged": (i32, [vp, vp, vp, u32, vp, vp, vp, vp, vp, vp, vp, vp,
                                        u32, u32, u32, u32, f32, vp]),
+    "lfm3_sum_parts": (i32, [vp, sz, u32, u32, u32, u32, vp]),
     "lfm3_conv_prompt": (i32, [vp, u32, vp, vp, vp, vp, u32, vp, u32, u32, u32, i32, vp]),
     "lfm3_prompt_heads": (i32, [vp, vp, vp, u32, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32,
                                 u32, f32, vp]),
@@ -99,6 +100,7 @@ _SIGS = {
     "lfm3_session_ring_capacity": (u32, [vp, u32]),
     "lfm3_session_state": (i32, [vp, i32, u32, C.POINTER(vp), C.POINTER(sz)]),
     "lfm3_session_set_position": (i32, [vp, u32]),
+    "lfm3_session_forward": (i32, [vp, vp, sz, vp]),
     "lfm3_forward_batch": (i32, [vp, sz, vp, vp]),
     "lfm3_forward_batch_greedy": (i32, [vp, sz, vp, vp]),
     "lfm3_session_read_logits": (i32, [vp, vp]),
@@ -352,6 +354,14 @@ class Session:
         data, nbytes = vp(), sz()
         check(lib().lfm3_session_state(self.handle, kind, layer, C.byref(data), C.byref(nbytes)))
         return data.value, nbytes.value
+
+    def forward(self, tokens, want_logits=True):
+        """Session::Forward: the last token's logits (or None)."""
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(self.model.dims.vocab, np.float32) if want_logits else None
+        check(lib().lfm3_session_forward(self.handle, ptr(toks), len(toks),
+                                         ptr(out) if want_logits else None))
+        return out
 
     def read_logits(self) -> np.ndarray:
         out = np.empty(self.model.dims.vocab, np.float32)
