@@ -19,7 +19,16 @@ Printed as one JSON line:
              the 256 MB MALL;
   round      the whole round's algorithmic HBM bytes and fraction of peak;
   cpu_baseline  the CPU oracle (a scalar FP32 restatement of reference.cpp)
-             running the same round on the host: one thread per session.
+             running the same round on the host: one thread per session;
+  prefill    the metric's prefill half: one 512-token prompt pass
+             (Session::Forward) at depth 24576 of a synthesized session, its
+             algorithmic FLOPs (projections 2 n W plus attention 4 D h keys,
+             over what runs after the reference's trailing-row pruning) and
+             fraction of the 2.5 PFLOP/s dense FP16 MFMA peak, with the MFMA
+             roofline of its dominant kernel (the gate/up SwiGLU GEMM,
+             15360 x 2048 Q8_0 on 512 FP16 rows);
+  mixed_round  one scheduler round at depth: 7 decode sessions at contexts
+             uniform in [16384, 32768] plus the 512-token pass.
 """
 from __future__ import annotations
 
@@ -39,8 +48,11 @@ import numpy as np  # noqa: E402
 import lfm3amd as L  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense FP16 MFMA, MI355X
 SESSIONS = 8
 CTX_LO, CTX_HI = 128, 8192
+PASS_ROWS, PASS_DEPTH = 512, 24576
+MIXED_DECODE, MIXED_LO, MIXED_HI = 7, 16384, 32768
 
 
 def log(msg: str):
@@ -125,6 +137,135 @@ def gemv_roofline(batch: int, copies: int, passes: int):
     return {"batch": batch, "bytes": nbytes, "us": us}
 
 
+def projection_weights(d: L.Dims) -> int:
+    """Weight elements of every projection a token's row goes through (the
+    vocabulary head excluded)."""
+    H, F, D = d.hidden, d.intermediate, d.head_dim
+    total = 0
+    for i in range(d.n_layers):
+        total += 3 * F * H
+        if d.layer_type(i) == L.LAYER_CONV:
+            total += 3 * H * H + H * H
+        else:
+            total += (d.heads * D + 2 * d.kv_heads * D + d.heads) * H + H * d.heads * D
+    return total
+
+
+def pass_flops(d: L.Dims, n: int, depth: int, pruned: bool) -> int:
+    """Algorithmic FLOPs of an n-row prompt pass at `depth`: 2 n W for the
+    projections and 4 D h keys for QK^T and PV per query row. With the
+    reference's trailing-row pruning (engine.cpp:304-323) a last global
+    layer runs its attention output, attention and FFN on the frontier row
+    only."""
+    H, F, D = d.hidden, d.intermediate, d.head_dim
+    flops = 2 * n * projection_weights(d)
+    for i in range(d.n_layers):
+        t = d.layer_type(i)
+        if t == L.LAYER_CONV:
+            continue
+        keys = [depth + r + 1 if t == L.LAYER_FULL else min(depth + r + 1, d.window)
+                for r in range(n)]
+        flops += 4 * D * d.heads * sum(keys)
+    if pruned and d.layer_type(d.n_layers - 1) == L.LAYER_FULL:
+        last_keys = sum(depth + r + 1 for r in range(n - 1))
+        flops -= 2 * (n - 1) * (H * d.heads * D + 3 * F * H) + 4 * D * d.heads * last_keys
+    return flops
+
+
+def gemm_roofline(copies: int, passes: int):
+    """The prompt pass's dominant kernel: the gate/up SwiGLU GEMM (7680 gate
+    + 7680 up rows x 2048, Q8_0) on 512 FP16 rows with its row maxima for the
+    down projection, as the pass runs it, over `copies` rotated
+    weight buffers, replayed from a HIP graph and timed with HIP events on
+    the stream it runs on."""
+    import ctypes as C
+    F, H, n = 7680, 2048, PASS_ROWS
+    cb, sb = C.c_size_t(), C.c_size_t()
+    L.lib().lfm3_q8_tiled_bytes(2 * F, H, C.byref(cb), C.byref(sb))
+    codes = np.zeros(cb.value, np.uint8)
+    scales = np.zeros(sb.value, np.uint8)
+    g = L.q8(L.SEED, "gemm.gate", F, H)
+    u = L.q8(L.SEED, "gemm.up", F, H)
+    L.check(L.lib().lfm3_q8_pack_host(L.ptr(g), F, H, L.ptr(codes), L.ptr(scales), 0, 2))
+    L.check(L.lib().lfm3_q8_pack_host(L.ptr(u), F, H, L.ptr(codes), L.ptr(scales), 1, 2))
+    mats = [(L.DeviceBuffer.of(codes), L.DeviceBuffer.of(scales)) for _ in range(copies)]
+    x = L.DeviceBuffer.of(L.normal(L.SEED, "gemm.x", n * H))
+    a16 = L.DeviceBuffer(n * H * 2)
+    scale = L.DeviceBuffer(n * 4)
+    L.check(L.lib().lfm3_half_rows(x.addr, H, None, 0, a16.addr, H, scale.addr, n, H, None))
+    y = L.DeviceBuffer(n * F * 4)
+    row_max = L.DeviceBuffer(L.lib().lfm3_q8_gemm_swiglu_max_blocks(F) * n * 4)
+    stream = L.Stream()
+
+    def one_pass():
+        for c, s in mats:
+            L.check(L.lib().lfm3_q8_gemm_swiglu(c.addr, s.addr, F, H, a16.addr, H, scale.addr, n,
+                                                y.addr, F, row_max.addr, stream.handle))
+
+    graph = L.Graph(stream, one_pass)
+    graph.launch()
+    stream.synchronize()
+    a, b = L.Event(), L.Event()
+    a.record(stream.handle)
+    for _ in range(passes):
+        graph.launch()
+    b.record(stream.handle)
+    b.synchronize()
+    us = a.elapsed_ms(b) * 1000.0 / (passes * copies)
+    graph.close()
+    a.close()
+    b.close()
+    stream.close()
+    flops = 2 * n * 2 * F * H
+    return {"flops": flops, "us": us, "tflops": flops / (us * 1e-6) / 1e12}
+
+
+def prefill_and_mixed(model, dims, seed, reps: int, warmup: int):
+    """The 512-token pass at depth 24576 alone, then the mixed round (7
+    decode sessions at contexts in [16384, 32768] plus the pass). Each
+    repetition rewinds the prompt session to the depth, so every pass does
+    the same work."""
+    prompt = model.session(PASS_DEPTH + PASS_ROWS)
+    L.inject_synth_state(prompt, dims, seed, 100, PASS_DEPTH)
+    tokens = L.uniform_u32(seed, "bench.pass.tokens", PASS_ROWS, 0, dims.vocab - 1)
+
+    def one_pass():
+        prompt.set_position(PASS_DEPTH)
+        prompt.forward(tokens)
+
+    for _ in range(warmup):
+        one_pass()
+    L.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        one_pass()
+    L.synchronize()
+    pass_ms = (time.perf_counter() - t0) * 1000.0 / reps
+
+    ctx = L.uniform_u32(seed, "bench.mixed.ctx", MIXED_DECODE, MIXED_LO, MIXED_HI)
+    decode = []
+    for sid, c in enumerate(ctx):
+        s = model.session(int(c) + warmup + reps + 8)
+        L.inject_synth_state(s, dims, seed, 200 + sid, int(c) - 1)
+        decode.append(s)
+    toks = L.uniform_u32(seed, "bench.mixed.tokens", MIXED_DECODE, 0, dims.vocab - 1)
+
+    def one_round(toks):
+        toks = model.forward_batch_greedy(decode, toks)
+        one_pass()
+        return toks
+
+    for _ in range(warmup):
+        toks = one_round(toks)
+    L.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        toks = one_round(toks)
+    L.synchronize()
+    mixed_ms = (time.perf_counter() - t0) * 1000.0 / reps
+    return pass_ms, mixed_ms, [int(c) for c in ctx]
+
+
 def cpu_baseline(dims, weights, ctx, tokens, seed):
     """One decode round of the eight sessions on the CPU oracle, one thread
     per session, from the same synthesized state as the GPU sessions.
@@ -178,6 +319,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--gemv-copies", type=int, default=32)
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the 512-token pass and the mixed round")
+    ap.add_argument("--prefill-reps", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (the decode "
@@ -192,7 +336,7 @@ def main():
         sys.exit(1)
 
     seed = L.SEED
-    dims = L.Dims(context=CTX_HI + 1024)
+    dims = L.Dims(context=MIXED_HI + 1024)
     t0 = time.perf_counter()
     weights = L.synth_weights(dims, seed=seed)
     log(f"synthesized weights in {time.perf_counter() - t0:.1f} s")
@@ -242,7 +386,7 @@ def main():
             f"{g['bytes'] / (g['us'] * 1e-6) / 1e9:.0f} GB/s")
 
     result = {
-        "metric": "decode tok/s @8 sessions (HBM GB/s % peak)",
+        "metric": "decode tok/s @8 sessions (HBM GB/s % peak); 512-tok prefill pass ms (MFMA %)",
         "value": round(value, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -283,6 +427,42 @@ def main():
                         "GBps": round(g["bytes"] / (g["us"] * 1e-6) / 1e9, 1)}
                        for g in sweep],
     }
+    if not args.no_prefill:
+        log("512-token prompt pass at depth 24576 and the mixed round ...")
+        pass_ms, mixed_ms, mixed_ctx = prefill_and_mixed(model, dims, seed, args.prefill_reps, 2)
+        flops = pass_flops(dims, PASS_ROWS, PASS_DEPTH, pruned=True)
+        flops_full = pass_flops(dims, PASS_ROWS, PASS_DEPTH, pruned=False)
+        tflops = flops / (pass_ms * 1e-3) / 1e12
+        gemm = gemm_roofline(8, 4)
+        log(f"pass {pass_ms:.2f} ms, {tflops:.0f} TFLOP/s; mixed round {mixed_ms:.2f} ms; "
+            f"swiglu GEMM {gemm['us']:.1f} us, {gemm['tflops']:.0f} TFLOP/s")
+        result["prefill"] = {
+            "workload": (f"one {PASS_ROWS}-token prompt pass (Session::Forward) at depth "
+                         f"{PASS_DEPTH} of a synthesized session, same model"),
+            "ms": round(pass_ms, 3),
+            "flops": int(flops),
+            "flops_without_pruning": int(flops_full),
+            "tflops": round(tflops, 1),
+            "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+            "reps": args.prefill_reps,
+            "roofline": {
+                "bound": "mfma",
+                "kernel": "Q8_0 x FP16 SwiGLU GEMM, 15360 x 2048 on 512 rows",
+                "achieved": round(gemm["tflops"], 1),
+                "peak": MFMA_PEAK_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": round(gemm["tflops"] / MFMA_PEAK_TFLOPS, 4),
+                "traffic": None,
+                "flops_per_launch": gemm["flops"],
+                "us_per_launch": round(gemm["us"], 2),
+            },
+        }
+        result["mixed_round"] = {
+            "workload": (f"{MIXED_DECODE} decode sessions at contexts in [{MIXED_LO}, {MIXED_HI}] "
+                         f"plus the {PASS_ROWS}-token pass"),
+            "ms": round(mixed_ms, 3),
+            "decode_contexts": mixed_ctx,
+        }
     if not args.no_cpu:
         log("CPU oracle round (one thread per session) ...")
         cpu, ids, margins = cpu_baseline(dims, weights, ctx, tokens0, seed)

@@ -121,12 +121,13 @@ int lfm3_q8_gemv_swiglu(const void* codes, const void* scales, uint32_t rows,
 /* FP16 row-scaled activations (hip/q8_prefill.hpp:27-74): per row
    e = 14 - ilogb(max |x|) (0 for a zero row), out = fp16(x 2^e), scale =
    2^-e. out rows have lda halves (lda % 64 == 0, lda >= cols; the tail is
-   zeroed). With row_max (FP32 bits of each row's maximum, e.g. from
-   lfm3_q8_gemm_swiglu) the row scan is skipped.
-   Replaces: HalfRows / HalfRowsFromMax (q8_prefill.hpp:30-74). */
+   zeroed). With row_max (max_blocks partial maxima of each row as FP32
+   bits, row_max[b * rows + row], e.g. from lfm3_q8_gemm_swiglu) the row
+   scan is skipped. Replaces: HalfRows / HalfRowsFromMax
+   (q8_prefill.hpp:30-74). */
 int lfm3_half_rows(const float* x, uint32_t ldx, const unsigned* row_max,
-                   uint16_t* out, uint32_t lda, float* scale, uint32_t rows,
-                   uint32_t cols, void* stream);
+                   uint32_t max_blocks, uint16_t* out, uint32_t lda,
+                   float* scale, uint32_t rows, uint32_t cols, void* stream);
 /* Y[t][r] = scale[t] * sum over Q8_0 blocks of d * (exact code x fp16 dot
    in FP32), one FP32 fma per block; tokens rows of activations a (lda
    halves each, chunk tails zero) with their scales. K splits into `parts`
@@ -148,10 +149,14 @@ int lfm3_q8_gemm(const void* codes, const void* scales, uint32_t rows,
 int lfm3_sum_parts(float* y, size_t part_stride, uint32_t rows, uint32_t cols,
                    uint32_t ld, uint32_t parts, void* stream);
 /* Gate/up over a stride-2 interleaved pair with the SwiGLU epilogue
-   (q8_prefill.hpp:622-635): y = silu(g) * u, and atomicMax of each token
-   row's max |y| (FP32 bits) into row_max (NULL: skipped), which must hold
-   zeros before the call. Replaces: gpu::ProjectFfn's first half for prompt
-   rows (hip/ops.hip:2205-2222). */
+   (q8_prefill.hpp:622-635): y = silu(g) * u, and each token row's max |y|
+   (FP32 bits) over each block of output rows stored to row_max[b * tokens
+   + t], b < lfm3_q8_gemm_swiglu_max_blocks(rows) (NULL: skipped; plain
+   stores, no zeroing needed): the partial maxima lfm3_half_rows reduces.
+   The reference forms the same row maxima with atomicMax.
+   Replaces: gpu::ProjectFfn's first half for prompt rows
+   (hip/ops.hip:2205-2222). */
+uint32_t lfm3_q8_gemm_swiglu_max_blocks(uint32_t rows);
 int lfm3_q8_gemm_swiglu(const void* codes, const void* scales, uint32_t rows,
                         uint32_t cols, const uint16_t* a, uint32_t lda,
                         const float* a_scale, uint32_t tokens, float* y,
@@ -182,6 +187,16 @@ int lfm3_residual_norm_image(const float* branch, uint32_t parts,
                              float* x, const float* norm, float* z, void* image,
                              int* exps, uint32_t rows, uint32_t hidden,
                              float eps, void* stream);
+/* lfm3_residual_norm_parts whose normed rows also go out as the prompt
+   GEMM's FP16 row-scaled activations (lfm3_half_rows of z: a16 rows of lda
+   halves, scale per row); z may be NULL. Replaces: the FP16 split branch of
+   ResidualNormKernel (hip/ops.hip:946-969). */
+int lfm3_residual_norm_half(const float* branch, uint32_t parts,
+                            size_t part_stride, const float* post_norm,
+                            float* x, const float* norm, float* z,
+                            uint16_t* a16, uint32_t lda, float* scale,
+                            uint32_t rows, uint32_t hidden, float eps,
+                            void* stream);
 /* out[i] = d * q of row tokens[i] (tokens in device memory).
    Replaces: gpu::Embed (hip/ops.hip:2007-2011). */
 int lfm3_embed(const void* codes, const void* scales, uint32_t vocab,

@@ -69,6 +69,16 @@ __device__ __forceinline__ h8 EightCodes(unsigned a, unsigned b) {
   return __builtin_bit_cast(h8, w);
 }
 
+// Prompt activations (hip/q8_prefill.hpp:27-51): a row with maximum
+// magnitude m is scaled by 2^e, e = 14 - ilogb(m) (0 for a zero row), which
+// puts m in [2^14, 2^15), rounded to fp16, and carries the scale 2^-e.
+__device__ __forceinline__ int RowExponent(float maximum) {
+  return maximum > 0.0f ? 14 - ilogbf(maximum) : 0;
+}
+__device__ __forceinline__ Half ScaledHalf(float x, int e) {
+  return FloatToHalfBits(ldexpf(x, e));
+}
+
 __device__ __forceinline__ float WaveSum(float v) {
 #pragma unroll
   for (int m = 32; m; m >>= 1)

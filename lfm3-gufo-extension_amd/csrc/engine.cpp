@@ -735,7 +735,7 @@ PromptBuffers& EnsurePromptBuffers(lfm3_model& m) {
   b->mix = Buffer(R * std::max<std::size_t>(H, std::size_t(c.heads) * D) * 4);
   b->hid = Buffer(R * F * 4);
   b->out = Buffer(8 * R * H * 4);
-  b->row_max = Buffer(R * 4);
+  b->row_max = Buffer(std::size_t(lfm3_q8_gemm_swiglu_max_blocks(c.intermediate)) * R * 4);
   b->chunk_k = Buffer(R * std::max<std::size_t>(kv_max, 1) * D * 2);
   b->chunk_v = Buffer(R * std::max<std::size_t>(kv_max, 1) * D * 2);
   b->attn_ws_bytes = std::max<std::size_t>(
@@ -802,9 +802,16 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
   auto* row_max = b.row_max.as<unsigned>();
   const std::uint32_t lda = std::uint32_t(b.lda), pld = std::uint32_t(b.proj_ld);
 
+  // a16 / scale hold FP16 row-scaled GEMM inputs. The residual norms write
+  // them at the absolute chunk row (row r at a16 + r lda), so a pruned
+  // consumer reads its last rows at the same offset; other GEMM inputs (the
+  // convolution and attention outputs, the FFN hidden rows) are converted
+  // into rows 0.. by `halves`.
+  const std::uint32_t max_blocks = lfm3_q8_gemm_swiglu_max_blocks(F);
   const auto halves = [&](const float* in, std::uint32_t ldx, const unsigned* rmax,
                           std::uint32_t rows, std::uint32_t cols) {
-    CheckStatus(lfm3_half_rows(in, ldx, rmax, a16, lda, scale, rows, cols, s));
+    CheckStatus(lfm3_half_rows(in, ldx, rmax, rmax ? max_blocks : 0, a16, lda, scale, rows,
+                               cols, s));
   };
   const auto gemv = [&](const Matrix& w, const float* in, std::uint32_t ldx, float* y,
                         std::uint32_t ldy, std::uint32_t rows, bool swiglu) {
@@ -819,50 +826,60 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
                                  k, nullptr, 0, s));
     }
   };
-  // y (rows x w.rows) = rows of `in` times W^T as one FP32 output.
-  const auto project = [&](const Matrix& w, const float* in, std::uint32_t ldx,
-                           std::uint32_t rows, float* y, std::uint32_t ldy) {
+  const auto gemm = [&](const Matrix& w, std::uint32_t a_row, std::uint32_t rows, float* y,
+                        std::uint32_t ldy) -> std::uint32_t {
+    const std::uint32_t parts = lfm3_q8_gemm_parts(w.rows, w.cols, rows, 0);
+    CheckStatus(lfm3_q8_gemm(w.codes.p, w.scales.p, w.rows, w.cols,
+                             a16 + std::size_t(a_row) * lda, lda, scale + a_row, rows, y, ldy,
+                             parts, s));
+    return parts;
+  };
+  // A mixer's input projection over the last `rows` rows (FP32 rows of z
+  // below kPromptRows, else the FP16 rows the residual norm left in a16),
+  // as one FP32 output.
+  const auto project = [&](const Matrix& w, std::uint32_t rows, float* y, std::uint32_t ldy) {
+    const std::uint32_t first = n - rows;
     if (rows < kPromptRows) {
-      gemv(w, in, ldx, y, ldy, rows, false);
+      gemv(w, z + std::size_t(first) * H, H, y, ldy, rows, false);
       return;
     }
-    halves(in, ldx, nullptr, rows, w.cols);
-    const std::uint32_t parts = lfm3_q8_gemm_parts(w.rows, w.cols, rows, 0);
-    CheckStatus(lfm3_q8_gemm(w.codes.p, w.scales.p, w.rows, w.cols, a16, lda, scale, rows, y,
-                             ldy, parts, s));
+    const std::uint32_t parts = gemm(w, first, rows, y, ldy);
     CheckStatus(lfm3_sum_parts(y, std::size_t(ldy) * rows, rows, w.rows, ldy, parts, s));
   };
-  // Hidden-wide outputs go to `out` as K parts that the next residual norm
-  // adds in part order; returns the part count. With activations already
-  // in a16 (staged), the FP16 conversion is skipped.
+  // Hidden-wide outputs of FP32 rows `in` go to `out` as K parts that the
+  // next residual norm adds in part order; returns the part count.
   const auto dense = [&](const Matrix& w, const float* in, std::uint32_t ldx,
-                         std::uint32_t rows, bool staged) -> std::uint32_t {
+                         std::uint32_t rows, const unsigned* rmax) -> std::uint32_t {
     if (rows < kPromptRows) {
       gemv(w, in, ldx, out, H, rows, false);
       return 1;
     }
-    if (!staged)
-      halves(in, ldx, nullptr, rows, w.cols);
-    const std::uint32_t parts = lfm3_q8_gemm_parts(w.rows, w.cols, rows, 0);
-    CheckStatus(lfm3_q8_gemm(w.codes.p, w.scales.p, w.rows, w.cols, a16, lda, scale, rows, out,
-                             H, parts, s));
-    return parts;
+    halves(in, ldx, rmax, rows, w.cols);
+    return gemm(w, 0, rows, out, H);
   };
+  // x += post(branch) over the last `rows` rows, then the next norm: FP16
+  // rows into a16 when its consumer runs on the matrix cores (consumer
+  // rows >= kPromptRows), else FP32 rows into z.
   const auto residual_norm = [&](std::uint32_t parts, const Buffer* post, const Buffer* next,
-                                 std::uint32_t rows) {
-    const std::size_t o = std::size_t(n - rows) * H;
-    CheckStatus(lfm3_residual_norm_parts(parts ? out : nullptr, parts ? parts : 1,
-                                         std::size_t(rows) * H,
-                                         post && post->p ? post->as<float>() : nullptr, x + o,
-                                         next ? next->as<float>() : nullptr, z + o, rows, H,
-                                         c.eps, s));
+                                 std::uint32_t rows, std::uint32_t consumer_rows) {
+    const std::size_t o = n - rows;
+    const float* branch = parts ? out : nullptr;
+    const float* pn = post && post->p ? post->as<float>() : nullptr;
+    if (next && consumer_rows >= kPromptRows)
+      CheckStatus(lfm3_residual_norm_half(branch, parts ? parts : 1, std::size_t(rows) * H, pn,
+                                          x + o * H, next->as<float>(), nullptr, a16 + o * lda,
+                                          lda, scale + o, rows, H, c.eps, s));
+    else
+      CheckStatus(lfm3_residual_norm_parts(branch, parts ? parts : 1, std::size_t(rows) * H, pn,
+                                           x + o * H, next ? next->as<float>() : nullptr,
+                                           z + o * H, rows, H, c.eps, s));
   };
 
   Check(hipMemcpyAsync(b.tokens.p, tokens, std::size_t(n) * 4, hipMemcpyHostToDevice, s),
         "token upload");
   CheckStatus(lfm3_embed(m.embedding.codes.p, m.embedding.scales.p, c.vocab, H,
                          b.tokens.as<std::uint32_t>(), n, x, s));
-  residual_norm(0, nullptr, &m.layers[0].norm, live_in[0]);
+  residual_norm(0, nullptr, &m.layers[0].norm, live_in[0], live_in[0]);
   for (std::uint32_t il = 0; il < L; ++il) {
     const Layer& l = m.layers[il];
     auto& state = se.states[il];
@@ -870,18 +887,18 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
     const std::uint32_t o_in = n - rows_in, o = n - rows_out;
     std::uint32_t parts;
     if (l.type == LFM3_LAYER_CONV) {
-      project(l.in_proj, z + std::size_t(o_in) * H, H, rows_in, proj, 3 * H);
+      project(l.in_proj, rows_in, proj, 3 * H);
       // Rows before the first live one are not read: outputs that would
       // need them are not live either (engine.cpp:386-393).
       float* hist = state.conv.as<float>();
       const std::uint32_t begin = 0;
       CheckStatus(lfm3_conv_prompt(proj, 3 * H, l.conv.as<float>(), &hist, &begin, &rows_in, 1,
                                    mix, H, H, c.conv_width, 1, s));
-      parts = dense(l.out_proj, mix + std::size_t(o - o_in) * H, H, rows_out, false);
+      parts = dense(l.out_proj, mix + std::size_t(o - o_in) * H, H, rows_out, nullptr);
     } else {
       const bool swa = l.type == LFM3_LAYER_SLIDING;
       const std::uint32_t stride = l.kv * D;
-      project(l.qkvg, z, H, n, proj, pld);
+      project(l.qkvg, n, proj, pld);
       const float* table = swa ? m.freq_sliding.as<float>() : m.freq_global.as<float>();
       const float* factors = swa ? nullptr : m.factors.as<float>();
       auto* ck = state.k.as<std::uint16_t>();
@@ -938,25 +955,23 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
       if (swa)
         CheckStatus(lfm3_store_kv(kc, vc, ck, cv, n, stride, position, state.capacity, s));
       parts = dense(l.attn_out, mix + std::size_t(o) * c.heads * D, c.heads * D, rows_out,
-                    false);
+                    nullptr);
     }
-    residual_norm(parts, &l.post_norm, &l.ffn_norm, rows_out);
-    // FFN over the live rows: SwiGLU (with each row's max |y| for the down
-    // projection's FP16 conversion), then down.
-    const float* zr = z + std::size_t(o) * H;
+    residual_norm(parts, &l.post_norm, &l.ffn_norm, rows_out, rows_out);
+    // FFN over the live rows: SwiGLU (with each row's max |y| per block of
+    // output rows for the down projection's FP16 conversion), then down.
     if (rows_out < kPromptRows) {
-      gemv(l.ffn, zr, H, hid, F, rows_out, true);
-      parts = dense(l.down, hid, F, rows_out, false);
+      gemv(l.ffn, z + std::size_t(o) * H, H, hid, F, rows_out, true);
+      parts = dense(l.down, hid, F, rows_out, nullptr);
     } else {
-      halves(zr, H, nullptr, rows_out, H);
-      Check(hipMemsetAsync(row_max, 0, std::size_t(rows_out) * 4, s), "row max");
-      CheckStatus(lfm3_q8_gemm_swiglu(l.ffn.codes.p, l.ffn.scales.p, F, H, a16, lda, scale,
-                                      rows_out, hid, F, row_max, s));
-      halves(hid, F, row_max, rows_out, F);
-      parts = dense(l.down, hid, F, rows_out, true);
+      CheckStatus(lfm3_q8_gemm_swiglu(l.ffn.codes.p, l.ffn.scales.p, F, H,
+                                      a16 + std::size_t(o) * lda, lda, scale + o, rows_out, hid,
+                                      F, row_max, s));
+      parts = dense(l.down, hid, F, rows_out, row_max);
     }
     const bool last = il + 1 == L;
-    residual_norm(parts, &l.post_ffn_norm, last ? nullptr : &m.layers[il + 1].norm, rows_out);
+    residual_norm(parts, &l.post_ffn_norm, last ? nullptr : &m.layers[il + 1].norm, rows_out,
+                  last ? 0 : live_in[il + 1]);
   }
   // The frontier row: the last row normed by output_norm; logits from it.
   CheckStatus(lfm3_residual_norm(nullptr, nullptr, x + std::size_t(n - 1) * H,

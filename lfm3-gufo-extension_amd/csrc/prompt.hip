@@ -35,14 +35,11 @@ constexpr int kGemmWaves = kGemmWR * kGemmWT, kGemmThreads = 64 * kGemmWaves;
 constexpr int kGemmTiles = kGemmWR * kGemmRT;  // weight tiles a block
 constexpr int kGemmTokens = kGemmWT * kGemmTT * 16;
 
-__device__ __forceinline__ int RowExponent(float maximum) {
-  return maximum > 0.0f ? 14 - ilogbf(maximum) : 0;
-}
-
-// One block per row: row maximum, then fp16(x 2^e) and the scale 2^-e.
+// One block per row: row maximum (scanned, or the maximum of max_blocks
+// partial maxima), then fp16(x 2^e) and the scale 2^-e.
 __launch_bounds__(256) __global__
     void HalfRowsKernel(const float* __restrict__ x, int ldx,
-                        const unsigned* __restrict__ row_max,
+                        const unsigned* __restrict__ row_max, int max_blocks,
                         Half* __restrict__ out, int lda,
                         float* __restrict__ scale, int K) {
   __shared__ float s_max[4];
@@ -50,7 +47,10 @@ __launch_bounds__(256) __global__
   const float* src = x + std::size_t(row) * ldx;
   float maximum;
   if (row_max) {
-    maximum = __uint_as_float(row_max[row]);
+    // Partial maxima of the row, one per producing row block.
+    maximum = 0.0f;
+    for (int b = 0; b < max_blocks; ++b)
+      maximum = fmaxf(maximum, __uint_as_float(row_max[std::size_t(b) * gridDim.x + row]));
   } else {
     maximum = 0.0f;
     for (int k = tid; k < K; k += 256)
@@ -66,7 +66,7 @@ __launch_bounds__(256) __global__
     scale[row] = ldexpf(1.0f, -e);
   for (int k = tid; k < lda; k += 256)
     out[std::size_t(row) * lda + k] =
-        k < K ? FloatToHalfBits(ldexpf(src[k], e)) : Half(0);
+        k < K ? ScaledHalf(src[k], e) : Half(0);
 }
 
 // Direct-to-LDS buffer loads (buffer_load_dword{,x4} ... lds): lane L's
@@ -337,6 +337,12 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   const int sub = lane & 15, quad = lane >> 4;
   const int wtok0 = tok0 + wt * TT * 16;
   if constexpr (kSwiGLU) {
+    // Each token's max |y| over the block's rows (LDS), stored once per
+    // (row block, token) for the down projection's FP16 conversion.
+    __shared__ unsigned s_max[kGemmTokens];
+    for (int i = tid; i < kGemmTokens; i += kGemmThreads)
+      s_max[i] = 0;
+    __syncthreads();
     // Tiles (2 j, 2 j + 1) are a (gate, up) pair for output rows j * 16 + n.
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
@@ -355,15 +361,19 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
             m = fmaxf(m, fabsf(value));
           }
         }
-        // Row maxima for the down projection's fp16 conversion.
         m = fmaxf(m, __shfl_xor(m, 8, 64));
         m = fmaxf(m, __shfl_xor(m, 4, 64));
         m = fmaxf(m, __shfl_xor(m, 2, 64));
         m = fmaxf(m, __shfl_xor(m, 1, 64));
-        if (row_max && sub == 0 && token < n)
-          atomicMax(row_max + token, __float_as_uint(m));
+        if (sub == 0)
+          atomicMax(&s_max[wt * TT * 16 + t * 16 + 4 * quad + i], __float_as_uint(m));
       }
     }
+    __syncthreads();
+    if (row_max)
+      for (int i = tid; i < kGemmTokens; i += kGemmThreads)
+        if (tok0 + i < n)
+          row_max[std::size_t(rb) * n + tok0 + i] = s_max[i];
   } else {
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
@@ -439,14 +449,18 @@ using namespace lfm3amd;
 extern "C" {
 
 int lfm3_half_rows(const float* x, std::uint32_t ldx, const unsigned* row_max,
-                   std::uint16_t* out, std::uint32_t lda, float* scale,
-                   std::uint32_t rows, std::uint32_t cols, void* stream) {
+                   std::uint32_t max_blocks, std::uint16_t* out, std::uint32_t lda,
+                   float* scale, std::uint32_t rows, std::uint32_t cols, void* stream) {
   if (!x || !out || !scale || !rows || !cols || ldx < cols || lda < cols ||
-      lda % 64)
+      lda % 64 || (row_max && !max_blocks))
     return Fail(LFM3_E_INVALID, "invalid LFM3 fp16 row conversion");
   HalfRowsKernel<<<rows, 256, 0, static_cast<hipStream_t>(stream)>>>(
-      x, int(ldx), row_max, out, int(lda), scale, int(cols));
+      x, int(ldx), row_max, int(max_blocks), out, int(lda), scale, int(cols));
   return HipStatus(hipGetLastError(), "LFM3 fp16 row conversion launch");
+}
+
+std::uint32_t lfm3_q8_gemm_swiglu_max_blocks(std::uint32_t rows) {
+  return (2 * RowTiles(rows) + kGemmTiles - 1) / kGemmTiles;
 }
 
 std::uint32_t lfm3_q8_gemm_parts(std::uint32_t rows, std::uint32_t cols,

@@ -100,7 +100,8 @@ __launch_bounds__(kNormThreads) __global__
                             float* __restrict__ x,
                             const float* __restrict__ weight,
                             float* __restrict__ z, int H, float eps,
-                            uint4* __restrict__ image, int* __restrict__ exps) {
+                            uint4* __restrict__ image, int* __restrict__ exps,
+                            Half* __restrict__ a16, int lda, float* __restrict__ a_scale) {
   __shared__ float scratch[kNormThreads / 64];
   __shared__ float s_row[kNormThreads * kNormItems];
   const int row = blockIdx.x, tid = threadIdx.x;
@@ -161,10 +162,19 @@ __launch_bounds__(kNormThreads) __global__
       maximum = fmaxf(maximum, fabsf(zv));
     }
   }
-  if (!image)
+  if (!image && !a16)
     return;
   maximum = BlockMax(maximum, scratch);  // its barriers publish s_row
-  WriteOperandRow(s_row, H, row, maximum, image, exps);
+  if (image)
+    WriteOperandRow(s_row, H, row, maximum, image, exps);
+  if (a16) {
+    // The prompt GEMM's FP16 row (HalfRowsKernel's expressions), zero tail.
+    const int e = RowExponent(maximum);
+    if (tid == 0)
+      a_scale[row] = ldexpf(1.0f, -e);
+    for (int k = tid; k < lda; k += kNormThreads)
+      a16[std::size_t(row) * lda + k] = k < H ? ScaledHalf(s_row[k], e) : Half(0);
+  }
 }
 
 // reference.cpp:85-101: one owner per (row, channel); the window sum keeps
@@ -543,7 +553,7 @@ int lfm3_residual_norm_parts(const float* branch, std::uint32_t parts,
     return Fail(LFM3_E_INVALID, "unsupported LFM3 residual norm shape");
   ResidualNormKernel<<<rows, kNormThreads, 0, static_cast<hipStream_t>(stream)>>>(
       branch, int(parts), part_stride, branch ? post_norm : nullptr, x, norm, z,
-      int(hidden), eps, nullptr, nullptr);
+      int(hidden), eps, nullptr, nullptr, nullptr, 0, nullptr);
   return HipStatus(hipGetLastError(), "LFM3 residual norm launch");
 }
 
@@ -559,7 +569,22 @@ int lfm3_residual_norm_image(const float* branch, std::uint32_t parts,
     return Fail(LFM3_E_INVALID, "unsupported LFM3 residual norm image shape");
   ResidualNormKernel<<<rows, kNormThreads, 0, static_cast<hipStream_t>(stream)>>>(
       branch, int(parts), part_stride, branch ? post_norm : nullptr, x, norm, z,
-      int(hidden), eps, static_cast<uint4*>(image), exps);
+      int(hidden), eps, static_cast<uint4*>(image), exps, nullptr, 0, nullptr);
+  return HipStatus(hipGetLastError(), "LFM3 residual norm launch");
+}
+
+int lfm3_residual_norm_half(const float* branch, std::uint32_t parts,
+                            std::size_t part_stride, const float* post_norm, float* x,
+                            const float* norm, float* z, std::uint16_t* a16,
+                            std::uint32_t lda, float* scale, std::uint32_t rows,
+                            std::uint32_t hidden, float eps, void* stream) {
+  if (!x || !norm || !a16 || !scale || !rows || !hidden ||
+      hidden > kNormThreads * kNormItems || lda < hidden || lda % 64 || !parts ||
+      parts > kNormParts || (parts > 1 && part_stride < std::size_t(rows) * hidden))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 residual norm shape");
+  ResidualNormKernel<<<rows, kNormThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      branch, int(parts), part_stride, branch ? post_norm : nullptr, x, norm, z,
+      int(hidden), eps, nullptr, nullptr, a16, int(lda), scale);
   return HipStatus(hipGetLastError(), "LFM3 residual norm launch");
 }
 

@@ -61,7 +61,10 @@ _SIGS = {
     "lfm3_q8_gemv_swiglu_image": (i32, [vp, vp, u32, u32, vp, vp, u32, vp, u32, vp]),
     "lfm3_residual_norm_image": (i32, [vp, u32, sz, vp, vp, vp, vp, vp, vp, u32, u32, f32, vp]),
     "lfm3_conv_step_ragged_image": (i32, [vp, u32, vp, vp, vp, u32, vp, vp, u32, u32, u32, vp]),
-    "lfm3_half_rows": (i32, [vp, u32, vp, vp, u32, vp, u32, u32, vp]),
+    "lfm3_half_rows": (i32, [vp, u32, vp, u32, vp, u32, vp, u32, u32, vp]),
+    "lfm3_q8_gemm_swiglu_max_blocks": (u32, [u32]),
+    "lfm3_residual_norm_half": (i32, [vp, u32, sz, vp, vp, vp, vp, vp, u32, vp, u32, u32, f32,
+                                      vp]),
     "lfm3_q8_gemm_parts": (u32, [u32, u32, u32, i32]),
     "lfm3_q8_gemm": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, vp, u32, u32, vp]),
     "lfm3_q8_gemm_swiglu": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, vp, u32, vp, vp]),

@@ -14,15 +14,15 @@ pytestmark = pytest.mark.gpu
 SEED = L.SEED
 
 
-def half_rows_gpu(x, lda=None, row_max=None):
+def half_rows_gpu(x, lda=None, row_max=None, max_blocks=0):
     n, K = x.shape
     lda = lda or (K + 63) // 64 * 64
     dx = L.DeviceBuffer.of(np.ascontiguousarray(x, np.float32))
     da = L.DeviceBuffer(n * lda * 2)
     ds = L.DeviceBuffer(n * 4)
     dm = None if row_max is None else L.DeviceBuffer.of(row_max)
-    L.check(L.lib().lfm3_half_rows(dx.addr, K, 0 if dm is None else dm.addr, da.addr, lda, ds.addr,
-                                   n, K, None))
+    L.check(L.lib().lfm3_half_rows(dx.addr, K, 0 if dm is None else dm.addr, max_blocks, da.addr,
+                                   lda, ds.addr, n, K, None))
     L.synchronize()
     return da, ds, lda
 
@@ -51,11 +51,13 @@ def gemm(m: DeviceMatrix, x, parts=None, swiglu=False):
     parts = parts or L.lib().lfm3_q8_gemm_parts(M, K, n, int(swiglu))
     if swiglu:
         dy = L.DeviceBuffer(n * M * 4)
-        rm = L.DeviceBuffer(n * 4)
+        blocks = L.lib().lfm3_q8_gemm_swiglu_max_blocks(M)
+        rm = L.DeviceBuffer(blocks * n * 4)
         L.check(L.lib().lfm3_q8_gemm_swiglu(m.codes.addr, m.scales.addr, M, K, da.addr, lda, ds.addr,
                                             n, dy.addr, M, rm.addr, None))
         L.synchronize()
-        return dy.download(np.float32, n * M).reshape(n, M), rm.download(np.uint32, n)
+        return (dy.download(np.float32, n * M).reshape(n, M),
+                rm.download(np.uint32, blocks * n).reshape(blocks, n))
     dy = L.DeviceBuffer(parts * n * M * 4)
     L.check(L.lib().lfm3_q8_gemm(m.codes.addr, m.scales.addr, M, K, da.addr, lda, ds.addr, n,
                                  dy.addr, M, parts, None))
@@ -105,4 +107,15 @@ def test_gemm_swiglu_and_row_max(F, K, n):
     want = gv / (1 + np.exp(-gv)) * uv
     ok, err = within(y, want)
     assert ok, err
-    assert np.array_equal(rm.view(np.float32), np.abs(y).max(axis=1))
+    # partial maxima per block of 128 output rows (16 interleaved gate/up
+    # tiles); their maximum is the row's
+    parts = rm.view(np.float32)
+    assert parts.shape[0] == -(-F // 128)
+    for b in range(parts.shape[0]):
+        assert np.array_equal(parts[b], np.abs(y[:, 128 * b:128 * (b + 1)]).max(axis=1))
+    assert np.array_equal(parts.max(axis=0), np.abs(y).max(axis=1))
+    # and they stand in for the row scan of the down projection's FP16 rows
+    da, ds, lda = half_rows_gpu(y)
+    db, dt, _ = half_rows_gpu(y, row_max=rm.reshape(-1), max_blocks=parts.shape[0])
+    assert np.array_equal(da.download(np.uint16, n * lda), db.download(np.uint16, n * lda))
+    assert np.array_equal(ds.download(np.float32, n), dt.download(np.float32, n))
