@@ -172,6 +172,7 @@ struct lfm3_model {
   // Per-round device tables: RoundTable, per-layer pointer rows, items.
   Buffer table;
   std::unique_ptr<PinnedBuffer> staging;
+  std::unique_ptr<PinnedBuffer> logits_host;  // one logits row, pinned
   std::size_t table_bytes = 0, items_capacity = 0;
   Buffer attn_ws;
   std::size_t attn_ws_bytes = 0;
@@ -711,6 +712,18 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
   }
 }
 
+// Device logits row -> caller's host row through the model's pinned
+// staging row (a DMA copy, then a host memcpy), on the model stream.
+void CopyLogits(lfm3_model& m, float* host, const void* device) {
+  const std::size_t bytes = std::size_t(m.config.vocab) * 4;
+  if (!m.logits_host)
+    m.logits_host = std::make_unique<PinnedBuffer>(bytes);
+  Check(hipMemcpyAsync(m.logits_host->p, device, bytes, hipMemcpyDeviceToHost, m.stream),
+        "logits copy");
+  Check(hipStreamSynchronize(m.stream), "logits copy");
+  std::memcpy(host, m.logits_host->p, bytes);
+}
+
 PromptBuffers& EnsurePromptBuffers(lfm3_model& m) {
   if (m.prompt)
     return *m.prompt;
@@ -1018,11 +1031,9 @@ int BatchEntry(lfm3_session* const* sessions, std::size_t n,
   lfm3_model& m = *sessions[0]->model;
   try {
     RunRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr);
-    const std::size_t V = m.config.vocab;
     if (logits)
       for (std::size_t i = 0; i < n; ++i)
-        Check(hipMemcpy(logits[i], sessions[i]->logits.p, V * 4, hipMemcpyDeviceToHost),
-              "logits copy");
+        CopyLogits(m, logits[i], sessions[i]->logits.p);
     if (ids)
       Check(hipMemcpy(ids, m.ids.p, n * 4, hipMemcpyDeviceToHost), "ids copy");
     return LFM3_OK;
@@ -1073,9 +1084,7 @@ int lfm3_session_forward(lfm3_session* se, const std::uint32_t* tokens, std::siz
       }
     }
     if (logits)
-      Check(hipMemcpy(logits, se->logits.p, std::size_t(m.config.vocab) * 4,
-                      hipMemcpyDeviceToHost),
-            "logits copy");
+      CopyLogits(m, logits, se->logits.p);
     return LFM3_OK;
   } catch (const Error& e) {
     se->poisoned = true;  // engine.cpp:924-926

@@ -36,8 +36,30 @@ constexpr int kGemmTiles = kGemmWR * kGemmRT;  // weight tiles a block
 constexpr int kGemmTokens = kGemmWT * kGemmTT * 16;
 
 // One block per row: row maximum (scanned, or the maximum of max_blocks
-// partial maxima), then fp16(x 2^e) and the scale 2^-e.
-__launch_bounds__(256) __global__
+// partial maxima), then fp16(x 2^e) and the scale 2^-e. The vector form
+// (cols % 4 == 0, cols <= 8192, 16-byte aligned rows) holds the row in
+// registers as float4 (one read) and stores four halves at a time.
+constexpr int kHalfThreads = 256, kHalfVec = 8;  // float4 a thread: 8192 columns
+constexpr int kHalfSplit = 4;  // blocks a row with known maxima: 2048 columns each
+
+__device__ __forceinline__ float RowMaximum(const unsigned* __restrict__ row_max,
+                                            int max_blocks, int rows, int row) {
+  float maximum = 0.0f;
+  for (int b = 0; b < max_blocks; ++b)
+    maximum = fmaxf(maximum, __uint_as_float(row_max[std::size_t(b) * rows + row]));
+  return maximum;
+}
+
+__device__ __forceinline__ float BlockMaximum256(float v, float* s_max) {
+  v = WaveMax(v);
+  if ((threadIdx.x & 63) == 0)
+    s_max[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+}
+
+template<bool kVec>
+__launch_bounds__(kHalfThreads) __global__
     void HalfRowsKernel(const float* __restrict__ x, int ldx,
                         const unsigned* __restrict__ row_max, int max_blocks,
                         Half* __restrict__ out, int lda,
@@ -45,28 +67,61 @@ __launch_bounds__(256) __global__
   __shared__ float s_max[4];
   const int row = blockIdx.x, tid = threadIdx.x;
   const float* src = x + std::size_t(row) * ldx;
-  float maximum;
-  if (row_max) {
-    // Partial maxima of the row, one per producing row block.
-    maximum = 0.0f;
-    for (int b = 0; b < max_blocks; ++b)
-      maximum = fmaxf(maximum, __uint_as_float(row_max[std::size_t(b) * gridDim.x + row]));
+  Half* dst = out + std::size_t(row) * lda;
+  if constexpr (kVec) {
+    // With known maxima a row spreads over blocks of 2048 columns
+    // (blockIdx.y); a scanned row is one block.
+    const int per = gridDim.y == 1 ? K / 4 : kHalfThreads * kHalfVec / kHalfSplit;
+    const int v0 = blockIdx.y * per;
+    const int nv = min(K / 4, v0 + per);
+    const float4* src4 = reinterpret_cast<const float4*>(src);
+    float4 v[kHalfVec];
+#pragma unroll
+    for (int j = 0; j < kHalfVec; ++j) {
+      const int i = v0 + tid + kHalfThreads * j;
+      v[j] = i < nv ? src4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float maximum;
+    if (row_max) {
+      maximum = RowMaximum(row_max, max_blocks, gridDim.x, row);
+    } else {
+      maximum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kHalfVec; ++j)
+        maximum = fmaxf(maximum, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)),
+                                       fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+      maximum = BlockMaximum256(maximum, s_max);
+    }
+    const int e = RowExponent(maximum);
+    if (tid == 0 && blockIdx.y == 0)
+      scale[row] = ldexpf(1.0f, -e);
+    uint2* dst2 = reinterpret_cast<uint2*>(dst);
+#pragma unroll
+    for (int j = 0; j < kHalfVec; ++j) {
+      const int i = v0 + tid + kHalfThreads * j;
+      if (i < nv)
+        dst2[i] = make_uint2(unsigned(ScaledHalf(v[j].x, e)) | (unsigned(ScaledHalf(v[j].y, e)) << 16),
+                             unsigned(ScaledHalf(v[j].z, e)) | (unsigned(ScaledHalf(v[j].w, e)) << 16));
+    }
+    if (blockIdx.y + 1 == gridDim.y)
+      for (int i = K / 4 + tid; i < lda / 4; i += kHalfThreads)
+        dst2[i] = make_uint2(0u, 0u);
   } else {
-    maximum = 0.0f;
-    for (int k = tid; k < K; k += 256)
-      maximum = fmaxf(maximum, fabsf(src[k]));
-    maximum = WaveMax(maximum);
-    if ((tid & 63) == 0)
-      s_max[tid >> 6] = maximum;
-    __syncthreads();
-    maximum = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+    float maximum;
+    if (row_max) {
+      maximum = RowMaximum(row_max, max_blocks, gridDim.x, row);
+    } else {
+      maximum = 0.0f;
+      for (int k = tid; k < K; k += kHalfThreads)
+        maximum = fmaxf(maximum, fabsf(src[k]));
+      maximum = BlockMaximum256(maximum, s_max);
+    }
+    const int e = RowExponent(maximum);
+    if (tid == 0)
+      scale[row] = ldexpf(1.0f, -e);
+    for (int k = tid; k < lda; k += kHalfThreads)
+      dst[k] = k < K ? ScaledHalf(src[k], e) : Half(0);
   }
-  const int e = RowExponent(maximum);
-  if (tid == 0)
-    scale[row] = ldexpf(1.0f, -e);
-  for (int k = tid; k < lda; k += 256)
-    out[std::size_t(row) * lda + k] =
-        k < K ? ScaledHalf(src[k], e) : Half(0);
 }
 
 // Direct-to-LDS buffer loads (buffer_load_dword{,x4} ... lds): lane L's
@@ -454,8 +509,22 @@ int lfm3_half_rows(const float* x, std::uint32_t ldx, const unsigned* row_max,
   if (!x || !out || !scale || !rows || !cols || ldx < cols || lda < cols ||
       lda % 64 || (row_max && !max_blocks))
     return Fail(LFM3_E_INVALID, "invalid LFM3 fp16 row conversion");
-  HalfRowsKernel<<<rows, 256, 0, static_cast<hipStream_t>(stream)>>>(
-      x, int(ldx), row_max, int(max_blocks), out, int(lda), scale, int(cols));
+  const bool vec = cols % 4 == 0 && ldx % 4 == 0 && cols <= 4 * kHalfThreads * kHalfVec &&
+                   (reinterpret_cast<std::uintptr_t>(x) & 15) == 0 &&
+                   (reinterpret_cast<std::uintptr_t>(out) & 7) == 0;
+  const auto s = static_cast<hipStream_t>(stream);
+  if (vec) {
+    // Known maxima: a row's columns spread over blocks of 2048.
+    const unsigned split =
+        row_max ? (cols + 4 * kHalfThreads * kHalfVec / kHalfSplit - 1) /
+                      (4 * kHalfThreads * kHalfVec / kHalfSplit)
+                : 1;
+    HalfRowsKernel<true><<<dim3(rows, split), kHalfThreads, 0, s>>>(
+        x, int(ldx), row_max, int(max_blocks), out, int(lda), scale, int(cols));
+  }
+  else
+    HalfRowsKernel<false><<<rows, kHalfThreads, 0, s>>>(x, int(ldx), row_max, int(max_blocks),
+                                                        out, int(lda), scale, int(cols));
   return HipStatus(hipGetLastError(), "LFM3 fp16 row conversion launch");
 }
 

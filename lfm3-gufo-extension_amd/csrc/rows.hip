@@ -384,29 +384,46 @@ __global__ void PromptConvKernel(const float* __restrict__ p, int ldp,
   const float* ps = p + std::size_t(seg.begin[s]) * ldp;
   float* ys = y + std::size_t(seg.begin[s]) * ldy;
   const float* hist = seg.history[s] + std::size_t(ch) * (L - 1);
-  float w[L], win[L];
+  // Every load of the thread's rows is issued before any arithmetic: the
+  // L - 1 products before the first row (from p, or the history before the
+  // segment) and B, C, x of each of its rows.
+  float w[L], pre[L - 1], bv[kConvRows], cv[kConvRows], xv[kConvRows];
 #pragma unroll
   for (int t = 0; t < L; ++t)
     w[t] = taps[std::size_t(ch) * L + t];
-  const auto bx = [&](int r) {
-    return r >= 0 ? ps[std::size_t(r) * ldp + ch] * ps[std::size_t(r) * ldp + 2 * H + ch]
-                  : hist[(L - 1) + r];
-  };
+#pragma unroll
+  for (int t = 0; t < L - 1; ++t) {
+    const int r = first - (L - 1) + t;
+    pre[t] = r >= 0 ? ps[std::size_t(r) * ldp + ch] * ps[std::size_t(r) * ldp + 2 * H + ch]
+                    : hist[(L - 1) + r];
+  }
+#pragma unroll
+  for (int i = 0; i < kConvRows; ++i) {
+    const int r = first + i;
+    const bool live = r < rows;
+    const float* pr = ps + std::size_t(live ? r : first) * ldp;
+    bv[i] = pr[ch];
+    cv[i] = pr[H + ch];
+    xv[i] = pr[2 * H + ch];
+  }
   // win[t] holds the product of row r - (L - 1) + t.
+  float win[L];
 #pragma unroll
   for (int t = 0; t < L - 1; ++t)
-    win[t + 1] = bx(first - (L - 1) + t);
-  const int last = min(first + kConvRows, rows);
-  for (int r = first; r < last; ++r) {
+    win[t + 1] = pre[t];
+#pragma unroll
+  for (int i = 0; i < kConvRows; ++i) {
+    const int r = first + i;
 #pragma unroll
     for (int t = 0; t < L - 1; ++t)
       win[t] = win[t + 1];
-    win[L - 1] = bx(r);
+    win[L - 1] = bv[i] * xv[i];
     float sum = 0.0f;
 #pragma unroll
     for (int t = 0; t < L; ++t)
       sum += w[t] * win[t];
-    ys[std::size_t(r) * ldy + ch] = sum * ps[std::size_t(r) * ldp + H + ch];
+    if (r < rows)
+      ys[std::size_t(r) * ldy + ch] = sum * cv[i];
   }
 }
 
