@@ -54,6 +54,14 @@ CTX_LO, CTX_HI = 128, 8192
 PASS_ROWS, PASS_DEPTH = 512, 24576
 MIXED_DECODE, MIXED_LO, MIXED_HI = 7, 16384, 32768
 
+# HBM bytes per launch of the two roofline kernels at the shapes timed here,
+# counted by `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` over
+# `bench.py --roofline-only` and scaled by what each counter reads for a
+# plain 256 MiB device-to-device copy in the same program (FETCH_SIZE x 2.0,
+# WRITE_SIZE x 1.0). Re-measure after a change to either kernel.
+GEMV_TRAFFIC = {"read": 18_468_416, "write": 262_144}
+GEMM_TRAFFIC = {"read": 52_804_129, "write": 15_851_520}
+
 
 def log(msg: str):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -217,7 +225,34 @@ def gemm_roofline(copies: int, passes: int):
     b.close()
     stream.close()
     flops = 2 * n * 2 * F * H
-    return {"flops": flops, "us": us, "tflops": flops / (us * 1e-6) / 1e12}
+    nbytes = (q8_bytes(2 * F, H) + n * H * 2 + n * 4 + n * F * 4
+              + L.lib().lfm3_q8_gemm_swiglu_max_blocks(F) * n * 4)
+    return {"flops": flops, "bytes": nbytes, "us": us, "tflops": flops / (us * 1e-6) / 1e12}
+
+
+def copy_calibration(nbytes: int, reps: int):
+    """Plain device-to-device copies of `nbytes` (the runtime's blit
+    kernel): the known-size launch that FETCH_SIZE and WRITE_SIZE are
+    scaled by when the roofline kernels' HBM traffic is counted."""
+    src, dst = L.DeviceBuffer(nbytes), L.DeviceBuffer(nbytes)
+    stream = L.Stream()
+    for _ in range(reps):
+        L.hip_check(L.hip().hipMemcpyAsync(dst.addr, src.addr, nbytes, L.D2D, stream.handle))
+    stream.synchronize()
+    stream.close()
+    src.close()
+    dst.close()
+
+
+def roofline_only():
+    """The two roofline kernels and the copy calibration, nothing else: the
+    program that rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE run."""
+    copy_bytes = 256 << 20
+    copy_calibration(copy_bytes, 4)
+    g = gemv_roofline(8, 32, 2)
+    m = gemm_roofline(8, 2)
+    print(json.dumps({"copy_bytes": copy_bytes, "gemv_bytes": g["bytes"], "gemv_us": g["us"],
+                      "gemm_flops": m["flops"], "gemm_us": m["us"]}), flush=True)
 
 
 def prefill_and_mixed(model, dims, seed, reps: int, warmup: int):
@@ -266,17 +301,19 @@ def prefill_and_mixed(model, dims, seed, reps: int, warmup: int):
     return pass_ms, mixed_ms, [int(c) for c in ctx]
 
 
-def cpu_baseline(dims, weights, ctx, tokens, seed):
-    """One decode round of the eight sessions on the CPU oracle, one thread
-    per session, from the same synthesized state as the GPU sessions.
-    Returns (result dict, per-session greedy ids, per-session top-2 margin)."""
+def cpu_baseline(dims, weights, ctx, tokens, seed, rounds: int = 7):
+    """`rounds` decode rounds of the eight sessions on the CPU oracle, one
+    thread per session, from the same synthesized state as the GPU sessions,
+    each round's greedy ids fed back as the next round's tokens (about 10 s
+    of wall time on the host). Returns (result dict, per-session greedy ids
+    of the first round, per-session top-2 margin of the first round)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     om = O.Model(dims, weights)
     sessions = []
     for sid, c in enumerate(ctx):
         position = int(c) - 1
-        s = om.session(int(c) + 256, f16=True)
+        s = om.session(int(c) + rounds + 256, f16=True)
         for l in range(dims.n_layers):
             if dims.layer_type(l) == L.LAYER_CONV:
                 s.conv(l)[:] = L.synth_conv_state(seed, sid, l, dims)
@@ -287,10 +324,15 @@ def cpu_baseline(dims, weights, ctx, tokens, seed):
                     view(l)[:n] = O.half_to_float(L.synth_kv_state(seed, sid, l, tag, rows, dims))
         s.set_position(position)
         sessions.append(s)
-    out = [None] * len(sessions)
+    first = [None] * len(sessions)
 
     def work(i):
-        out[i] = sessions[i].step(int(tokens[i]))
+        tok = int(tokens[i])
+        for r in range(rounds):
+            logits = sessions[i].step(tok)
+            tok = O.argmax(logits)
+            if r == 0:
+                first[i] = logits
 
     threads = [threading.Thread(target=work, args=(i,)) for i in range(len(sessions))]
     t0 = time.perf_counter()
@@ -299,16 +341,16 @@ def cpu_baseline(dims, weights, ctx, tokens, seed):
     for t in threads:
         t.join()
     wall = time.perf_counter() - t0
-    ids = [O.argmax(o) for o in out]
-    margins = [float(np.diff(np.sort(o)[-2:])[0]) for o in out]
+    ids = [O.argmax(o) for o in first]
+    margins = [float(np.diff(np.sort(o)[-2:])[0]) for o in first]
     for s in sessions:
         s.close()
     om.close()
-    res = {"value": round(len(sessions) / wall, 4), "unit": "tok/s", "cores": len(sessions),
-           "kind": "port",
-           "sample": (f"one decode round of {len(sessions)} sessions (one token each) through "
-                      f"the full model at the same contexts and state, one thread per session; "
-                      f"{wall:.1f} s wall")}
+    res = {"value": round(rounds * len(sessions) / wall, 4), "unit": "tok/s",
+           "cores": len(sessions), "kind": "port",
+           "sample": (f"{rounds} decode rounds of {len(sessions)} sessions (one token each, greedy "
+                      f"ids fed back) through the full model from the same contexts and state, "
+                      f"one thread per session; {wall:.1f} s wall")}
     return res, ids, margins
 
 
@@ -322,6 +364,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the 512-token pass and the mixed round")
     ap.add_argument("--prefill-reps", type=int, default=5)
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="run only the roofline kernels and a plain copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (the decode "
@@ -334,6 +378,9 @@ def main():
     if L.gpu_count() < 1:
         print("bench.py needs a GPU (hipGetDeviceCount reports none)", file=sys.stderr)
         sys.exit(1)
+    if args.roofline_only:
+        roofline_only()
+        return
 
     seed = L.SEED
     dims = L.Dims(context=MIXED_HI + 1024)
@@ -413,7 +460,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": GEMV_TRAFFIC["read"] + GEMV_TRAFFIC["write"],
+            "traffic_read_write": [GEMV_TRAFFIC["read"], GEMV_TRAFFIC["write"]],
             "bytes_per_launch": g8["bytes"],
             "us_per_launch": round(g8["us"], 3),
         },
@@ -452,7 +500,9 @@ def main():
                 "peak": MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": round(gemm["tflops"] / MFMA_PEAK_TFLOPS, 4),
-                "traffic": None,
+                "traffic": GEMM_TRAFFIC["read"] + GEMM_TRAFFIC["write"],
+                "traffic_read_write": [GEMM_TRAFFIC["read"], GEMM_TRAFFIC["write"]],
+                "algorithmic_bytes": gemm["bytes"],
                 "flops_per_launch": gemm["flops"],
                 "us_per_launch": round(gemm["us"], 2),
             },
