@@ -69,6 +69,19 @@ __device__ __forceinline__ h8 EightCodes(unsigned a, unsigned b) {
   return __builtin_bit_cast(h8, w);
 }
 
+// GEMV operand split of x0, x1 scaled by 2^e (the row or slice maximum in
+// [2^14, 2^15)): hi = fp16(x 2^e) and lo = fp16((x 2^e - hi) 2^11), both
+// truncated, two values per conversion instruction. x 2^e - hi is exact in
+// FP32, so hi + lo 2^-11 keeps about 21 bits of x.
+__device__ __forceinline__ void SplitPair(float x0, float x1, int e, unsigned& hi,
+                                          unsigned& lo) {
+  const auto hp = __builtin_amdgcn_cvt_pkrtz(ldexpf(x0, e), ldexpf(x1, e));
+  const float r0 = fmaf(float(hp[0]), -2048.0f, ldexpf(x0, e + 11));
+  const float r1 = fmaf(float(hp[1]), -2048.0f, ldexpf(x1, e + 11));
+  hi = __builtin_bit_cast(unsigned, hp);
+  lo = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+}
+
 // Prompt activations (hip/q8_prefill.hpp:27-51): a row with maximum
 // magnitude m is scaled by 2^e, e = 14 - ilogb(m) (0 for a zero row), which
 // puts m in [2^14, 2^15), rounded to fp16, and carries the scale 2^-e.
@@ -77,6 +90,30 @@ __device__ __forceinline__ int RowExponent(float maximum) {
 }
 __device__ __forceinline__ Half ScaledHalf(float x, int e) {
   return FloatToHalfBits(ldexpf(x, e));
+}
+
+// Raw buffer resources over one tensor (at most 2^31 bytes). A lane whose
+// byte offset is past the range reads zeros, so guarded loads need no
+// branch and the compiler's wait counts stay exact across them.
+using BufferResource = __amdgpu_buffer_rsrc_t;
+constexpr int kBufferWord3 = 0x00020000;  // 32-bit data format, raw access
+constexpr unsigned kOutOfRange = 0x80000000u;
+inline bool BufferFits(std::size_t bytes) { return bytes < std::size_t(kOutOfRange); }
+__device__ __forceinline__ BufferResource MakeBuffer(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), kBufferWord3);
+}
+__device__ __forceinline__ uint4 LoadB128(BufferResource res, unsigned offset) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  const u4 v = __builtin_amdgcn_raw_buffer_load_b128(res, offset, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 LoadF4(BufferResource res, unsigned offset) {
+  const uint4 v = LoadB128(res, offset);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z),
+                     __uint_as_float(v.w));
+}
+__device__ __forceinline__ unsigned LoadB32(BufferResource res, unsigned offset) {
+  return __builtin_amdgcn_raw_buffer_load_b32(res, offset, 0, 0);
 }
 
 __device__ __forceinline__ float WaveSum(float v) {

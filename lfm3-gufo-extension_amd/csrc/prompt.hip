@@ -128,11 +128,6 @@ __launch_bounds__(kHalfThreads) __global__
 // bytes land at the wave-uniform LDS base + L * size. Reads outside the
 // resource's byte range return zero.
 typedef __attribute__((address_space(3))) void LdsVoid;
-using BufferResource = __amdgpu_buffer_rsrc_t;
-constexpr int kBufferWord3 = 0x00020000;  // 32-bit data format, raw access
-__device__ __forceinline__ BufferResource MakeBuffer(const void* base, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), kBufferWord3);
-}
 __device__ __forceinline__ void BufferToLds16(BufferResource res, unsigned lane_offset,
                                               unsigned scalar_offset, void* lds_base) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(res, (LdsVoid*)lds_base, 16, lane_offset,

@@ -97,10 +97,12 @@ GemvPlan PlanGemv(std::uint32_t rows, std::uint32_t cols, bool swiglu,
   p.W = nloc <= 4 ? 1 : nloc <= 8 ? 2 : nloc <= 16 ? 4 : 8;
   if (nloc > 32)
     p.SPW = 5;  // slices of 40 chunks (80 KB of LDS operands), prefetched
-  // Two 64 KB blocks fit a CU: about 512 blocks fill the device once. A
-  // multi-slice block keeps two slices of weights in registers: one tile.
+  // Two 64 KB blocks fit a CU. Past 256 tiles a block takes two tiles: it
+  // stages x and reduces across waves once for both (at 8192 x 2048 this is
+  // about 10% faster than 512 one-tile blocks). A multi-slice block keeps
+  // two slices of weights in registers: one tile (or gate/up pair).
   const int units = p.row_tiles / unit;
-  int per = units > 2048 ? 4 : units > 1024 ? 2 : 1;
+  int per = units > 256 && !swiglu ? 2 : 1;
   if (p.SPW == 5)
     per = 1;
   p.RT = per * unit;
@@ -163,9 +165,9 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
 // y[b][r] = sum_k W[r][k] x[b][k] for b < B <= 8. A block stages a K slice
 // of x at a time in LDS as the MFMA A operand: per token a power of two
 // 2^e puts the slice maximum in [2^14, 2^15), hi = fp16(x 2^e) and
-// lo = fp16((x 2^e - hi) 2^11); A rows 0-7 are the tokens' hi parts and
-// rows 8-15 their lo parts, so hi + lo 2^-11 keeps about 22 bits of each
-// value and every code x half product is exact in FP32. The B operand is
+// lo = fp16((x 2^e - hi) 2^11), both truncated; A rows 0-7 are the tokens'
+// hi parts and rows 8-15 their lo parts, so hi + lo 2^-11 keeps about 21
+// bits of each value and every code x half product is exact in FP32. The B operand is
 // 16 weight rows of one Q8_0 block decoded exactly to fp16, so one MFMA
 // gives 16 rows' block dots and the block scale applies as
 // acc = fma(d, dot, acc) in K order (hip/ops.hip:671-856: sums += scale *
@@ -173,7 +175,7 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
 // slice is staged. Waves sum in wave order, so results do not depend on
 // scheduling.
 template<int W, int SPW, int RT, bool kSwiGLU>
-__launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(RT >= 4 ? 2 : 4)))
+__launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(RT >= 2 ? 2 : 4)))
 __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
                        const Half* __restrict__ scales, int row_tiles,
                        int nchunks, int K, const float* __restrict__ x, int ldx,
@@ -196,6 +198,12 @@ __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
   const int nslices = (nloc + SLICE - 1) / SLICE;
 
   // Weight tiles and scales of one slice: chunk wave + W j of the slice.
+  // Buffer loads: a tile or chunk past the end reads zeros, without a
+  // branch.
+  const unsigned tiles_bytes = unsigned(row_tiles) * unsigned(nchunks);
+  const BufferResource c_res = MakeBuffer(codes, tiles_bytes * kTileCodeBytes);
+  const BufferResource s_res = MakeBuffer(scales, tiles_bytes * kTileScales * 2);
+  const BufferResource x_res = MakeBuffer(x, unsigned(((B - 1) * ldx + K) * 4));
   uint4 q[RT][SPW], qn[RT][kMulti ? SPW : 1];
   unsigned sc[RT][SPW], scn[RT][kMulti ? SPW : 1];
   const auto fetch = [&](int slice, auto& qq, auto& ss) {
@@ -205,17 +213,31 @@ __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
 #pragma unroll
       for (int j = 0; j < SPW; ++j) {
         const int chunk = slice * SLICE + wave + W * j;
-        if (tile < row_tiles && chunk < nloc) {
-          const std::size_t off = std::size_t(tile) * nchunks + c_begin + chunk;
-          qq[r][j] = *reinterpret_cast<const uint4*>(codes + off * kTileCodeBytes + lane * 16);
-          ss[r][j] = *reinterpret_cast<const unsigned*>(scales + off * kTileScales + (lane & 15) * 2);
-        } else {
-          qq[r][j] = make_uint4(0, 0, 0, 0);
-          ss[r][j] = 0;
-        }
+        const bool live = tile < row_tiles && chunk < nloc;
+        const unsigned off = unsigned(tile) * unsigned(nchunks) + unsigned(c_begin + chunk);
+        qq[r][j] = LoadB128(c_res, live ? off * kTileCodeBytes + lane * 16 : kOutOfRange);
+        ss[r][j] = LoadB32(s_res, live ? off * (kTileScales * 2) + (lane & 15) * 4 : kOutOfRange);
       }
     }
   };
+  const int t = tid & 7;  // staging token of this thread
+  // x of one slice: unit tid + j T is token t, column group cg of eight.
+  float v[SPW][8];
+  const auto load_x = [&](int slice) {
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      const int cg = (tid + j * T) >> 3;
+      const int local = slice * SLICE + (cg >> 3);
+      const int k = (c_begin + local) * kChunk + (cg & 7) * 8;
+      const unsigned off = t < B && local < nloc && k < K ? unsigned(t * ldx + k) * 4 : kOutOfRange;
+      const float4 lo4 = LoadF4(x_res, off), hi4 = LoadF4(x_res, off + 16);
+      v[j][0] = lo4.x; v[j][1] = lo4.y; v[j][2] = lo4.z; v[j][3] = lo4.w;
+      v[j][4] = hi4.x; v[j][5] = hi4.y; v[j][6] = hi4.z; v[j][7] = hi4.w;
+    }
+  };
+  // Memory results return in issue order: x (from L2) goes first so the
+  // slice is staged while the weights stream in.
+  load_x(0);
   fetch(0, q, sc);
 
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -223,30 +245,17 @@ __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
 #pragma unroll
   for (int r = 0; r < RT; ++r)
     total[r] = zero;
-  const int t = tid & 7;  // staging token of this thread
   const int part = lane >> 5, tok0 = ((lane >> 4) & 1) * 4;
 
   for (int slice = 0; slice < nslices; ++slice) {
     if constexpr (kMulti) {
-      if (slice + 1 < nslices)
-        fetch(slice + 1, qn, scn);
+      if (slice > 0)
+        load_x(slice);
+      fetch(slice + 1, qn, scn);  // past the last slice: zeros, no traffic
     }
-    // Stage the slice: unit tid + j T is token t, column group cg of eight.
-    float v[SPW][8];
     float maximum = 0.0f;
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
-      const int cg = (tid + j * T) >> 3;
-      const int local = slice * SLICE + (cg >> 3);
-      const int k = (c_begin + local) * kChunk + (cg & 7) * 8;
-      float4 lo4 = make_float4(0, 0, 0, 0), hi4 = lo4;
-      if (t < B && local < nloc && k < K) {
-        const float4* src = reinterpret_cast<const float4*>(x + std::size_t(t) * ldx + k);
-        lo4 = src[0];
-        hi4 = src[1];
-      }
-      v[j][0] = lo4.x; v[j][1] = lo4.y; v[j][2] = lo4.z; v[j][3] = lo4.w;
-      v[j][4] = hi4.x; v[j][5] = hi4.y; v[j][6] = hi4.z; v[j][7] = hi4.w;
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         maximum = fmaxf(maximum, fabsf(v[j][i]));
@@ -269,17 +278,13 @@ __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
       const int cg = (tid + j * T) >> 3;
-      h8 hi, lo;
+      unsigned hw[4], lw[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float s = ldexpf(v[j][i], e);
-        const _Float16 h = static_cast<_Float16>(s);
-        hi[i] = h;
-        lo[i] = static_cast<_Float16>((s - float(h)) * 2048.0f);
-      }
+      for (int i = 0; i < 8; i += 2)
+        SplitPair(v[j][i], v[j][i + 1], e, hw[i / 2], lw[i / 2]);
       const int idx = ((cg >> 3) * 2 + ((cg >> 2) & 1)) * 64 + 16 * (cg & 3) + t;
-      s_a[idx] = __builtin_bit_cast(uint4, hi);
-      s_a[idx + 8] = __builtin_bit_cast(uint4, lo);
+      s_a[idx] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      s_a[idx + 8] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     }
     __syncthreads();
     // This wave's chunks of the slice: one MFMA per Q8_0 block. Chunk
@@ -365,6 +370,10 @@ __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
 #pragma unroll
   for (int r = 0; r < RT; ++r)
     acc[r] = zero;
+  const unsigned tiles_bytes = unsigned(row_tiles) * unsigned(nchunks);
+  const BufferResource c_res = MakeBuffer(codes, tiles_bytes * kTileCodeBytes);
+  const BufferResource s_res = MakeBuffer(scales, tiles_bytes * kTileScales * 2);
+  const BufferResource a_res = MakeBuffer(image, unsigned(nchunks) * 2 * 64 * 16);
   for (int base = 0; base < nloc; base += ROUND) {
     uint4 q[RT][SPW];
     unsigned sc[RT][SPW];
@@ -376,18 +385,14 @@ __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
         const int tile = group * RT + r;
-        if (live && tile < row_tiles) {
-          const std::size_t off = std::size_t(tile) * nchunks + c_begin + chunk;
-          q[r][j] = *reinterpret_cast<const uint4*>(codes + off * kTileCodeBytes + lane * 16);
-          sc[r][j] = *reinterpret_cast<const unsigned*>(scales + off * kTileScales + (lane & 15) * 2);
-        } else {
-          q[r][j] = make_uint4(0, 0, 0, 0);
-          sc[r][j] = 0;
-        }
+        const unsigned off = unsigned(tile) * unsigned(nchunks) + unsigned(c_begin + chunk);
+        const bool ok = live && tile < row_tiles;
+        q[r][j] = LoadB128(c_res, ok ? off * kTileCodeBytes + lane * 16 : kOutOfRange);
+        sc[r][j] = LoadB32(s_res, ok ? off * (kTileScales * 2) + (lane & 15) * 4 : kOutOfRange);
       }
-      const std::size_t at = std::size_t(c_begin + chunk) * 2 * 64 + lane;
-      a[j][0] = live && a_live ? image[at] : make_uint4(0, 0, 0, 0);
-      a[j][1] = live && a_live ? image[at + 64] : make_uint4(0, 0, 0, 0);
+      const unsigned at = (unsigned(c_begin + chunk) * 2 * 64 + lane) * 16;
+      a[j][0] = LoadB128(a_res, live && a_live ? at : kOutOfRange);
+      a[j][1] = LoadB128(a_res, live && a_live ? at + 64 * 16 : kOutOfRange);
     }
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
@@ -438,21 +443,14 @@ template<int W, int SPW, bool kSwiGLU>
 void LaunchRT(const GemvPlan& p, const std::uint8_t* c, const Half* s, int K,
               const float* x, int ldx, int B, float* y, int ldy, int rows_out,
               hipStream_t stream) {
-  if constexpr (SPW > 4) {  // multi-slice plans take one tile (or pair)
+  if constexpr (SPW > 4 || kSwiGLU) {  // one tile, or one gate/up pair
     LaunchPlan<W, SPW, kSwiGLU ? 2 : 1, kSwiGLU>(p, c, s, K, x, ldx, B, y, ldy, rows_out,
                                                 stream);
-  } else if constexpr (kSwiGLU) {
-    if (p.RT == 2)
-      LaunchPlan<W, SPW, 2, true>(p, c, s, K, x, ldx, B, y, ldy, rows_out, stream);
-    else
-      LaunchPlan<W, SPW, 4, true>(p, c, s, K, x, ldx, B, y, ldy, rows_out, stream);
   } else {
     if (p.RT == 1)
       LaunchPlan<W, SPW, 1, false>(p, c, s, K, x, ldx, B, y, ldy, rows_out, stream);
-    else if (p.RT == 2)
-      LaunchPlan<W, SPW, 2, false>(p, c, s, K, x, ldx, B, y, ldy, rows_out, stream);
     else
-      LaunchPlan<W, SPW, 4, false>(p, c, s, K, x, ldx, B, y, ldy, rows_out, stream);
+      LaunchPlan<W, SPW, 2, false>(p, c, s, K, x, ldx, B, y, ldy, rows_out, stream);
   }
 }
 
@@ -464,7 +462,10 @@ int LaunchGemv(const void* codes, const void* scales, std::uint32_t rows,
   if (!codes || !scales || !x || !y || rows == 0 || cols == 0 ||
       cols % 32 || batch == 0 || batch > 8 || ldx % 4 || ldx < cols ||
       ldy < rows || (reinterpret_cast<std::uintptr_t>(x) & 15) || parts < 1 ||
-      parts > int(Chunks(cols)))
+      parts > int(Chunks(cols)) ||
+      !BufferFits(std::size_t(RowTiles(rows) * (kSwiGLU ? 2 : 1)) * Chunks(cols) *
+                  kTileCodeBytes) ||
+      !BufferFits((std::size_t(batch - 1) * ldx + cols) * 4))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 GEMV shape");
   const GemvPlan p = PlanGemv(rows, cols, kSwiGLU, parts);
   const auto* c = static_cast<const std::uint8_t*>(codes);
@@ -514,7 +515,9 @@ int LaunchGemvImage(const void* codes, const void* scales, std::uint32_t rows,
   if (!codes || !scales || !image || !exps || !y || rows == 0 || cols == 0 ||
       cols % 32 || batch == 0 || batch > 8 || ldy < rows || parts < 1 ||
       parts > Chunks(cols) || (kSwiGLU && parts != 1) ||
-      (reinterpret_cast<std::uintptr_t>(image) & 15))
+      (reinterpret_cast<std::uintptr_t>(image) & 15) ||
+      !BufferFits(std::size_t(RowTiles(rows) * (kSwiGLU ? 2 : 1)) * Chunks(cols) *
+                  kTileCodeBytes))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 operand-image GEMV");
   GemvPlan p = PlanGemv(rows, cols, kSwiGLU, int(parts));
   // Rounds of W * 4 chunks need no LDS: keep two tiles (one SwiGLU pair)

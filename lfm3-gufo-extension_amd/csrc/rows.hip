@@ -47,8 +47,8 @@ __device__ float BlockSum(float v, float* scratch) {
 
 // Writes one token's row (H floats in LDS) into a GEMV operand image (see
 // lfm3_q8_gemv_image): exponent e puts the row maximum in [2^14, 2^15),
-// hi = fp16(x 2^e), lo = fp16((x 2^e - hi) 2^11); columns past H (the tail
-// of the last 64-column chunk) are written as zeros.
+// and SplitPair gives hi and lo, as the FP32 GEMV stages them; columns past
+// H (the tail of the last 64-column chunk) are written as zeros.
 __device__ void WriteOperandRow(const float* __restrict__ s_row, int H, int t,
                                 float maximum, uint4* __restrict__ image,
                                 int* __restrict__ exps) {
@@ -57,18 +57,16 @@ __device__ void WriteOperandRow(const float* __restrict__ s_row, int H, int t,
     exps[t] = e;
   const int groups = (H + kChunk - 1) / kChunk * 8;
   for (int cg = threadIdx.x; cg < groups; cg += blockDim.x) {
-    h8 hi, lo;
+    unsigned hi[4], lo[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 8; i += 2) {
       const int k = cg * 8 + i;
-      const float sv = k < H ? ldexpf(s_row[k], e) : 0.0f;
-      const _Float16 h = static_cast<_Float16>(sv);
-      hi[i] = h;
-      lo[i] = static_cast<_Float16>((sv - float(h)) * 2048.0f);
+      SplitPair(k < H ? s_row[k] : 0.0f, k + 1 < H ? s_row[k + 1] : 0.0f, e, hi[i / 2],
+                lo[i / 2]);
     }
     const int idx = ((cg >> 3) * 2 + ((cg >> 2) & 1)) * 64 + 16 * (cg & 3) + t;
-    image[idx] = __builtin_bit_cast(uint4, hi);
-    image[idx + 8] = __builtin_bit_cast(uint4, lo);
+    image[idx] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    image[idx + 8] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
   }
 }
 
@@ -174,6 +172,148 @@ __launch_bounds__(kNormThreads) __global__
       a_scale[row] = ldexpf(1.0f, -e);
     for (int k = tid; k < lda; k += kNormThreads)
       a16[std::size_t(row) * lda + k] = k < H ? ScaledHalf(s_row[k], e) : Half(0);
+  }
+}
+
+// Decode-round residual norm with the operand image (rows <= 8): the same
+// expressions as ResidualNormKernel on a 256-thread block per row. Thread t
+// owns column groups g = t + 256 i (columns 8g..8g+7) and holds them in
+// registers from the loads to the image write, so the block needs no row
+// staging; every load (x, norm weights, every K part) is issued before the
+// first reduction.
+constexpr int kImageNormThreads = 256;
+
+template<int N>
+__device__ __forceinline__ float SmallBlockSum(float v, float* slots) {
+  v = WaveSum(v);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0)
+    slots[wave] = v;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int w = 0; w < N; ++w)
+    total += slots[w];
+  return total;
+}
+
+template<int G>
+__launch_bounds__(kImageNormThreads) __global__
+    void NormImageKernel(const float* __restrict__ branch, int parts, std::size_t part_stride,
+                         const float* __restrict__ post, float* __restrict__ x,
+                         const float* __restrict__ weight, float* __restrict__ z, int H,
+                         float eps, uint4* __restrict__ image, int* __restrict__ exps) {
+  constexpr int kWaves = kImageNormThreads / 64;
+  __shared__ float s_red[3][kWaves];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const unsigned row_bytes = unsigned(H) * 4;
+  const BufferResource x_res = MakeBuffer(x + std::size_t(row) * H, row_bytes);
+  const BufferResource w_res = MakeBuffer(weight, row_bytes);
+  const BufferResource p_res = MakeBuffer(post ? post : weight, post ? row_bytes : 0u);
+  float v[G][8], pw[G][8], nw[G][8], b[kNormParts][G][8];
+  const auto load8 = [](BufferResource r, unsigned off, float* out) {
+    const float4 lo = LoadF4(r, off), hi = LoadF4(r, off + 16);
+    out[0] = lo.x; out[1] = lo.y; out[2] = lo.z; out[3] = lo.w;
+    out[4] = hi.x; out[5] = hi.y; out[6] = hi.z; out[7] = hi.w;
+  };
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = tid + kImageNormThreads * i;
+    const unsigned off = g * 8 < H ? unsigned(g) * 32 : kOutOfRange;
+    load8(x_res, off, v[i]);
+    load8(w_res, off, nw[i]);
+    load8(p_res, off, pw[i]);
+  }
+  if (branch) {
+#pragma unroll
+    for (int p = 0; p < kNormParts; ++p) {
+      const BufferResource b_res =
+          MakeBuffer(branch + p * part_stride + std::size_t(row) * H, p < parts ? row_bytes : 0u);
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const int g = tid + kImageNormThreads * i;
+        load8(b_res, g * 8 < H ? unsigned(g) * 32 : kOutOfRange, b[p][i]);
+      }
+    }
+    float squares = 0.0f;
+#pragma unroll
+    for (int i = 0; i < G; ++i)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+#pragma unroll
+        for (int p = 1; p < kNormParts; ++p)
+          b[0][i][k] += b[p][i][k];
+        squares = fmaf(b[0][i][k], b[0][i][k], squares);
+      }
+    if (post) {
+      const float scale =
+          1.0f / sqrtf(SmallBlockSum<kWaves>(squares, s_red[0]) / float(H) + eps);
+#pragma unroll
+      for (int i = 0; i < G; ++i)
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          b[0][i][k] = (b[0][i][k] * scale) * pw[i][k];
+    }
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int g = tid + kImageNormThreads * i;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        v[i][k] = v[i][k] + b[0][i][k];
+      if (g * 8 < H) {
+        float4* xr = reinterpret_cast<float4*>(x + std::size_t(row) * H + g * 8);
+        xr[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+        xr[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+      }
+    }
+  }
+  float squares = 0.0f;
+#pragma unroll
+  for (int i = 0; i < G; ++i)
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      squares = fmaf(v[i][k], v[i][k], squares);
+  const float scale = 1.0f / sqrtf(SmallBlockSum<kWaves>(squares, s_red[1]) / float(H) + eps);
+  float maximum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int g = tid + kImageNormThreads * i;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      v[i][k] = (v[i][k] * scale) * nw[i][k];  // zero past H
+      maximum = fmaxf(maximum, fabsf(v[i][k]));
+    }
+    if (z && g * 8 < H) {
+      float4* zr = reinterpret_cast<float4*>(z + std::size_t(row) * H + g * 8);
+      zr[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+      zr[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+    }
+  }
+  maximum = WaveMax(maximum);
+  if ((tid & 63) == 0)
+    s_red[2][tid >> 6] = maximum;
+  __syncthreads();
+  maximum = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w)
+    maximum = fmaxf(maximum, s_red[2][w]);
+  const int e = RowExponent(maximum);
+  if (tid == 0)
+    exps[row] = e;
+  // Image groups: every group of the row's 64-column chunks, zeros past H.
+  const int groups = (H + kChunk - 1) / kChunk * 8;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int cg = tid + kImageNormThreads * i;
+    if (cg >= groups)
+      continue;
+    unsigned hi[4], lo[4];
+#pragma unroll
+    for (int k = 0; k < 8; k += 2)
+      SplitPair(v[i][k], v[i][k + 1], e, hi[k / 2], lo[k / 2]);
+    const int idx = ((cg >> 3) * 2 + ((cg >> 2) & 1)) * 64 + 16 * (cg & 3) + row;
+    image[idx] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    image[idx + 8] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
   }
 }
 
@@ -584,9 +724,20 @@ int lfm3_residual_norm_image(const float* branch, std::uint32_t parts,
       parts > kNormParts || (parts > 1 && part_stride < std::size_t(rows) * hidden) ||
       (reinterpret_cast<std::uintptr_t>(image) & 15))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 residual norm image shape");
-  ResidualNormKernel<<<rows, kNormThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      branch, int(parts), part_stride, branch ? post_norm : nullptr, x, norm, z,
-      int(hidden), eps, static_cast<uint4*>(image), exps, nullptr, 0, nullptr);
+  const auto* post = branch ? post_norm : nullptr;
+  auto* im = static_cast<uint4*>(image);
+  const auto st = static_cast<hipStream_t>(stream);
+  const int groups = int(Chunks(hidden)) * 8;
+  if (groups <= kImageNormThreads)
+    NormImageKernel<1><<<rows, kImageNormThreads, 0, st>>>(
+        branch, int(parts), part_stride, post, x, norm, z, int(hidden), eps, im, exps);
+  else if (groups <= 2 * kImageNormThreads)
+    NormImageKernel<2><<<rows, kImageNormThreads, 0, st>>>(
+        branch, int(parts), part_stride, post, x, norm, z, int(hidden), eps, im, exps);
+  else
+    ResidualNormKernel<<<rows, kNormThreads, 0, st>>>(
+        branch, int(parts), part_stride, post, x, norm, z, int(hidden), eps, im, exps,
+        nullptr, 0, nullptr);
   return HipStatus(hipGetLastError(), "LFM3 residual norm launch");
 }
 

@@ -351,7 +351,9 @@ def test_gemv_shapes_share_one_workspace():
 # ------------------------------------------------- partials, operand images
 
 def decode_image(image: np.ndarray, exps: np.ndarray, rows: int, cols: int) -> np.ndarray:
-    """Inverse of the operand-image layout: (hi + lo 2^-11) 2^-e per token."""
+    """Inverse of the operand-image layout: (hi + lo 2^-11) 2^-e per token.
+    hi and lo are truncations, so the decoded row is within 2^-21 of the
+    row maximum."""
     nch = (cols + 63) // 64
     lanes = image.view(np.float16).reshape(nch, 2, 4, 16, 8).astype(np.float64)  # c, b, g, m, i
     out = np.zeros((rows, nch * 64))
@@ -391,7 +393,7 @@ def test_norm_image_feeds_gemv_bit_exactly(B):
     image = img.download(np.uint8, img.nbytes)
     exps = ex.download(np.int32, 8)
     dec = decode_image(image, exps, B, H)
-    assert np.all(np.abs(dec - gz) <= np.abs(gz).max(axis=1, keepdims=True) * 2.0 ** -22)
+    assert np.all(np.abs(dec - gz) <= np.abs(gz).max(axis=1, keepdims=True) * 2.0 ** -21)
     # plain and K-part image GEMVs against the FP32 GEMV of z
     w = L.q8(SEED, "ni.W", M, H)
     m = DeviceMatrix(w, M, H)
@@ -464,4 +466,4 @@ def test_conv_row_image_bit_exact():
         assert np.array_equal(y[r], want_y)
         assert np.array_equal(dh[r].download(np.float32, H * (Lw - 1)), want_h)
     dec = decode_image(img.download(np.uint8, img.nbytes), ex.download(np.int32, 8), n, H)
-    assert np.all(np.abs(dec - y) <= np.abs(y).max(axis=1, keepdims=True) * 2.0 ** -22)
+    assert np.all(np.abs(dec - y) <= np.abs(y).max(axis=1, keepdims=True) * 2.0 ** -21)
