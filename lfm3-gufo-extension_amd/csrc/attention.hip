@@ -11,8 +11,10 @@
 // keeps about 22 bits of the FP32 query; every half x half product is
 // exact in FP32), the B operand is 16 keys' F16 rows read with one 16-byte
 // load per lane per 32 dimensions. The softmax runs in (head, key) lanes
-// with FP32 online maxima and sums; P V runs on the VALU with lanes owning
-// two dimensions and the probabilities broadcast through LDS. Waves merge
+// with FP32 online maxima and sums; P V runs on the VALU, a lane owning
+// eight dimensions of a quarter of the group's keys (one 16-byte V load per
+// key), with the probabilities broadcast through LDS. The next group's K
+// and V loads are issued before the current group is computed. Waves merge
 // through LDS; rows with several spans leave per-span (max, sum, acc)
 // partials that a second launch merges in span order, so results do not
 // depend on block scheduling and no device-scope fence is needed.
@@ -43,17 +45,45 @@ __device__ __forceinline__ void WaveSync() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// Cross-lane moves without the LDS crossbar: DPP within 16-lane rows
+// (quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror,
+// row_ror 8) and gfx950's permlane swaps across rows. Every lane of a
+// reduced group ends with the same value (the pairs add commutatively).
+template<int kCtrl>
+__device__ __forceinline__ float Dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float GroupMax16(float v) {
-  v = fmaxf(v, __shfl_xor(v, 8, 64));
-  v = fmaxf(v, __shfl_xor(v, 4, 64));
-  v = fmaxf(v, __shfl_xor(v, 2, 64));
-  return fmaxf(v, __shfl_xor(v, 1, 64));
+  v = fmaxf(v, Dpp<0xB1>(v));
+  v = fmaxf(v, Dpp<0x4E>(v));
+  v = fmaxf(v, Dpp<0x141>(v));
+  return fmaxf(v, Dpp<0x140>(v));
 }
 __device__ __forceinline__ float GroupSum16(float v) {
-  v += __shfl_xor(v, 8, 64);
-  v += __shfl_xor(v, 4, 64);
-  v += __shfl_xor(v, 2, 64);
-  return v + __shfl_xor(v, 1, 64);
+  v += Dpp<0xB1>(v);
+  v += Dpp<0x4E>(v);
+  v += Dpp<0x141>(v);
+  return v + Dpp<0x140>(v);
+}
+// v of lane L plus v of lane L ^ 8 (within a row), L ^ 16, L ^ 32.
+__device__ __forceinline__ float SumXor8(float v) { return v + Dpp<0x128>(v); }
+// The row swaps as inline assembly: this compiler folds the sum of the two
+// results of __builtin_amdgcn_permlane{16,32}_swap(v, v) into twice the
+// first. Two wait states after the VALU writes of the operands.
+__device__ __forceinline__ float SumXor16(float v) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b = a;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float SumXor32(float v) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
+__device__ __forceinline__ int ngroups_of(int kb, int ke) {
+  return (ke - kb + kGroupKeys - 1) / kGroupKeys;
 }
 
 template<int D, int G, bool kFused>
@@ -71,20 +101,19 @@ __launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
   static_assert(D == 64 || D == 128, "head dimension 64 or 128");
   static_assert(2 * G <= 16, "hi and lo rows of the group fit one MFMA tile");
   constexpr int S = D / 32;                // MFMA steps per key row
-  constexpr int HALVES = 128 / D;          // P V key split across half-waves
-  constexpr int KPL = kGroupKeys / HALVES; // keys per lane in P V
   constexpr int PAIRS = (16 * G + 63) / 64;
   __shared__ float s_q[G][D];
   __shared__ __attribute__((aligned(16))) Half s_kv[2][D];
   __shared__ float s_tile[kAttnWaves][16][17];
   __shared__ float s_p[kAttnWaves][kGroupKeys][G];
   __shared__ float s_alpha[kAttnWaves][G];
-  __shared__ float s_acc[kAttnWaves][G][D];
+  __shared__ __attribute__((aligned(16))) float s_acc[kAttnWaves][G][D];
   __shared__ float s_m[kAttnWaves][G], s_l[kAttnWaves][G];
 
   const lfm3_attention_item item = items[blockIdx.x];
   const int g = blockIdx.y, row = int(item.row);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int stride = kv_heads * D;
   const std::uint32_t cap = capacity[row];
   const int kb = int(item.key_begin), ke = int(item.key_end);
@@ -144,19 +173,15 @@ __launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
   h8 a[S];
   {
     const int m = lane & 15, kg = lane >> 4;
+    const int head = m < G ? m : m < 2 * G ? m - G : 0;
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int dim = 32 * s + 8 * kg + i;
-        _Float16 val = 0;
-        if (m < G) {
-          val = static_cast<_Float16>(s_q[m][dim]);
-        } else if (m < 2 * G) {
-          const float x = s_q[m - G][dim];
-          val = static_cast<_Float16>((x - float(static_cast<_Float16>(x))) * 2048.0f);
-        }
-        a[s][i] = val;
+        const float x = s_q[head][32 * s + 8 * kg + i];
+        const _Float16 hi = static_cast<_Float16>(x);
+        const _Float16 lo = static_cast<_Float16>((x - float(hi)) * 2048.0f);
+        a[s][i] = m < G ? hi : m < 2 * G ? lo : _Float16(0);
       }
   }
 
@@ -167,55 +192,68 @@ __launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
     m_own[r] = -INFINITY;
     l_own[r] = 0.0f;
   }
-  float acc[G][2];
+  // P V layout: lane L owns dimensions 8 (L % DL) .. + 7 of keys
+  // L / DL + KG i (i < KPL) of each 16-key group, one 16-byte V load per key.
+  constexpr int DL = D / 8, KG = 64 / DL, KPL = 16 / KG;
+  const int dg = lane % DL, kq = lane / DL;
+  float acc[G][8];
 #pragma unroll
   for (int h = 0; h < G; ++h)
-    acc[h][0] = acc[h][1] = 0.0f;
-  const int half = lane / (64 / HALVES);
-  const int d0 = 2 * (lane % (64 / HALVES));
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      acc[h][i] = 0.0f;
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int ngroups = (ke - kb + kGroupKeys - 1) / kGroupKeys;
+  // The rings as buffers: a key past the span reads zeros, without a branch.
+  const unsigned ring_bytes = cap * unsigned(stride) * 2;
+  const BufferResource k_res = MakeBuffer(ck, ring_bytes);
+  const BufferResource v_res = MakeBuffer(cv, ring_bytes);
+  const int n = lane & 15, kg = lane >> 4;
+  // Ring slot of key base + o (o < 16): one (wave-uniform) division per
+  // group, then the wrap as a subtraction (rings of 16 slots or more).
+  const auto slot_of = [&](int base, int o) -> unsigned {
+    const unsigned sl = unsigned(base) % cap + unsigned(o);
+    return cap >= 16 ? (sl >= cap ? sl - cap : sl) : sl % cap;
+  };
+  const auto fetch = [&](int j, uint4 (&kr)[S], uint4 (&vr)[KPL]) {
+    const int base = kb + kGroupKeys * j;
+    const bool kvalid = j < ngroups_of(kb, ke) && base + n < ke;
+    const unsigned koff = kvalid ? (slot_of(base, n) * unsigned(stride) + g * D + 8 * kg) * 2
+                                 : kOutOfRange;
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2)
+      kr[s2] = LoadB128(k_res, koff + 64 * s2);
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const int o = kq + KG * i;
+      const bool vvalid = j < ngroups_of(kb, ke) && base + o < ke;
+      vr[i] = LoadB128(v_res, vvalid ? (slot_of(base, o) * unsigned(stride) + g * D + 8 * dg) * 2
+                                     : kOutOfRange);
+    }
+  };
+
+  const int ngroups = ngroups_of(kb, ke);
+  uint4 kr[S], vr[KPL], kn[S], vn[KPL];
+  fetch(wave, kr, vr);
   for (int j = wave; j < ngroups; j += kAttnWaves) {
     const int base = kb + kGroupKeys * j;
-    // K rows as the B operand: lane L reads key L % 16, dimensions
-    // 32 s + 8 (L / 16) .. + 7.
-    const int n = lane & 15, kg = lane >> 4;
-    const int t = base + n;
-    const bool valid = t < ke;
-    const Half* krow = ck + std::size_t(std::uint32_t(valid ? t : kb) % cap) * stride + g * D + 8 * kg;
-    uint4 kr[S];
+    fetch(j + kAttnWaves, kn, vn);  // past the span: zeros, no traffic
+    if constexpr (kFused) {
+      // The current key and value come from LDS, never from the ring.
+      if (base + n == pos) {
 #pragma unroll
-    for (int s = 0; s < S; ++s)
-      kr[s] = *reinterpret_cast<const uint4*>(krow + 32 * s);
-    // V words of this lane's keys and two dimensions.
-    unsigned vr[KPL];
+        for (int s2 = 0; s2 < S; ++s2)
+          kr[s2] = *reinterpret_cast<const uint4*>(&s_kv[0][32 * s2 + 8 * kg]);
+      }
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) {
-      const int tv = base + half * KPL + i;
-      const int safe = tv < ke ? tv : kb;
-      vr[i] = *reinterpret_cast<const unsigned*>(
-          cv + std::size_t(std::uint32_t(safe) % cap) * stride + g * D + d0);
-    }
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-      if (kFused && t == pos)
-        kr[s] = *reinterpret_cast<const uint4*>(&s_kv[0][32 * s + 8 * kg]);
-      if (!valid)
-        kr[s] = make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < KPL; ++i) {
-      const int tv = base + half * KPL + i;
-      if (kFused && tv == pos)
-        vr[i] = *reinterpret_cast<const unsigned*>(&s_kv[1][d0]);
-      if (tv >= ke)
-        vr[i] = 0;
+      for (int i = 0; i < KPL; ++i)
+        if (base + kq + KG * i == pos)
+          vr[i] = *reinterpret_cast<const uint4*>(&s_kv[1][8 * dg]);
     }
     f4 sacc = zero;
 #pragma unroll
-    for (int s = 0; s < S; ++s)
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], __builtin_bit_cast(h8, kr[s]), sacc, 0, 0, 0);
+    for (int s2 = 0; s2 < S; ++s2)
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s2], __builtin_bit_cast(h8, kr[s2]), sacc, 0, 0, 0);
     // D layout: lane L holds rows 4 (L / 16) + i of key L % 16.
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -241,37 +279,59 @@ __launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
       }
     }
     WaveSync();
-    // P V: lane owns dimensions d0, d0 + 1 of every head of the group.
+    // P V: lane owns dimensions 8 dg .. + 7 of every head of the group.
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       const float al = s_alpha[wave][h];
-      acc[h][0] *= al;
-      acc[h][1] *= al;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        acc[h][i] *= al;
     }
 #pragma unroll
     for (int i = 0; i < KPL; ++i) {
-      const float v0 = HalfBitsToFloat(vr[i] & 0xffffu);
-      const float v1 = HalfBitsToFloat(vr[i] >> 16);
+      const int o = kq + KG * i;
+      float vf[8];
+      const unsigned w4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        vf[2 * d] = HalfBitsToFloat(w4[d] & 0xffffu);
+        vf[2 * d + 1] = HalfBitsToFloat(w4[d] >> 16);
+      }
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        const float p = s_p[wave][half * KPL + i][h];
-        acc[h][0] = fmaf(p, v0, acc[h][0]);
-        acc[h][1] = fmaf(p, v1, acc[h][1]);
+        const float p = s_p[wave][o][h];
+#pragma unroll
+        for (int d = 0; d < 8; ++d)
+          acc[h][d] = fmaf(p, vf[d], acc[h][d]);
       }
     }
     WaveSync();  // the next group rewrites s_tile, s_p and s_alpha
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2)
+      kr[s2] = kn[s2];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i)
+      vr[i] = vn[i];
   }
 
-  // Merge the waves (and the key halves of D = 64) in a fixed order.
+  // Merge the key quarters (eighths for D = 64) across lanes, then the
+  // waves, in a fixed order.
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    if constexpr (HALVES == 2) {
-      acc[h][0] += __shfl_xor(acc[h][0], 32, 64);
-      acc[h][1] += __shfl_xor(acc[h][1], 32, 64);
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float t = acc[h][i];
+      if constexpr (DL == 8)
+        t = SumXor8(t);
+      t = SumXor32(SumXor16(t));
+      acc[h][i] = t;
     }
-    if (half == 0) {
-      s_acc[wave][h][d0] = acc[h][0];
-      s_acc[wave][h][d0 + 1] = acc[h][1];
+  if (kq == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float4* dst = reinterpret_cast<float4*>(&s_acc[wave][h][8 * dg]);
+      dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+      dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
     }
   }
 #pragma unroll
