@@ -89,14 +89,15 @@ int lfm3_q8_gemv_partials(const void* codes, const void* scales, uint32_t rows,
 /* GEMV operand images. A producer that holds whole FP32 rows of x can
    hand them to the next GEMV already staged as its MFMA A operand: per
    token an exponent e (x = (hi + lo 2^-11) 2^-e, e puts the row maximum
-   in [2^14, 2^15)), hi = fp16(x 2^e), lo = fp16((x 2^e - hi) 2^11), laid
-   out per 64-column chunk c and Q8_0 block b as 64 16-byte lane words at
-   ((c * 2 + b) * 64 + L), lane L = 16 g + m holding elements 8g..8g+7 of
-   the block for A row m (m < 8: token m's hi part, m >= 8: token m - 8's
-   lo part). exps holds 8 ints. The GEMV then reads its operands from L2
-   with no per-block staging; for cols <= 2048 the result is bit-identical
-   to lfm3_q8_gemv on the same rows. No counterpart in the reference (its
-   decode GEMVs read FP32 rows, hip/ops.hip:671-856). */
+   in [2^14, 2^15)), hi = fp16(x 2^e), lo = fp16((x 2^e - hi) 2^11), both
+   truncated, laid out per 64-column chunk c and Q8_0 block b as 64 16-byte
+   lane words at ((c * 2 + b) * 64 + L), lane L = 16 g + m holding elements
+   8g..8g+7 of the block for A row m (m < 8: token m's hi part, m >= 8:
+   token m - 8's lo part). exps holds 8 ints. The GEMV then reads its
+   operands from L2 with no per-block staging; its result equals
+   lfm3_q8_gemv on the same rows up to the order in which chunk sums add.
+   No counterpart in the reference (its decode GEMVs read FP32 rows,
+   hip/ops.hip:671-856). */
 size_t lfm3_operand_image_bytes(uint32_t cols);
 int lfm3_q8_gemv_image(const void* codes, const void* scales, uint32_t rows,
                        uint32_t cols, const void* image, const int* exps,
@@ -106,6 +107,18 @@ int lfm3_q8_gemv_swiglu_image(const void* codes, const void* scales,
                               uint32_t rows, uint32_t cols, const void* image,
                               const int* exps, uint32_t batch, float* y,
                               uint32_t ldy, void* stream);
+/* The convolution block's in projection ([3 hidden x hidden], rows B | C |
+   X in the usual tiled layout) on an operand image, with the decode
+   convolution step in its epilogue: y[b][ch] and the history of row b
+   (history[b], [hidden][width - 1]) as lfm3_conv_step_ragged leaves them
+   after the projection, bit for bit. hidden % 16 == 0, batch <= 8.
+   Replaces: gpu::Project of in_proj then gpu::ShortConv for n == 1
+   (engine.cpp:386-393, hip/ops.hip:2250-2264). */
+int lfm3_q8_gemv_conv_image(const void* codes, const void* scales,
+                            uint32_t hidden, const void* image, const int* exps,
+                            uint32_t batch, const float* taps,
+                            float* const* history, uint32_t width, float* y,
+                            uint32_t ldy, void* stream);
 /* FFN gate/up with the SwiGLU epilogue over a stride-2 interleaved pair
    (rows = rows of each of gate and up): y[b][r] = silu(g) * u.
    Replaces: gpu::ProjectSwiGLU (hip/ops.hip:2187-2204) and the decode half

@@ -659,13 +659,12 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
   for (std::uint32_t il = 0; il < L; ++il) {
     const Layer& l = m.layers[il];
     if (l.type == LFM3_LAYER_CONV) {
-      gemv_image(l.in_proj, proj, pld);
-      // The convolution step spreads over (channel block, row) blocks; its
+      // The in projection with the convolution step in its epilogue; the
       // FP32 output is staged by the out projection.
-      CheckStatus(lfm3_conv_step_ragged(
-          proj, pld, l.conv.as<float>(),
-          reinterpret_cast<float* const*>(dev + conv_off) + il * kMaxBatch, a, H,
-          n, H, c.conv_width, s));
+      CheckStatus(lfm3_q8_gemv_conv_image(
+          l.in_proj.codes.p, l.in_proj.scales.p, H, image, exps, n, l.conv.as<float>(),
+          reinterpret_cast<float* const*>(dev + conv_off) + il * kMaxBatch, c.conv_width, a,
+          H, s));
       mixer_parts = partials(l.out_proj, a, H);
     } else {
       const bool swa = l.type == LFM3_LAYER_SLIDING;

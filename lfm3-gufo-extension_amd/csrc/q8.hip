@@ -110,16 +110,15 @@ GemvPlan PlanGemv(std::uint32_t rows, std::uint32_t cols, bool swiglu,
   return p;
 }
 
-// Kernel tail shared by the GEMVs: total[r] holds this lane's un-scaled
-// sums for A rows 4 (L / 16) + i (tokens hi 0-7 then lo 0-7) of tile r's
-// weight row L % 16. hi and lo add, then the W waves' partial sums add in
-// wave order through LDS (red: W * RT * 128 + RT * 128 floats), and the
-// block writes its rows (SwiGLU: tile 2j is gate, 2j + 1 up, rows j * 16
-// + n).
-template<int W, int RT, bool kSwiGLU>
-__device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int group,
-                                             int B, float* __restrict__ y, int ldy,
-                                             int rows_out) {
+// Kernel tail shared by the GEMVs: total[r] holds this lane's sums for A
+// rows 4 (L / 16) + i (tokens hi 0-7 then lo 0-7) of tile r's weight row
+// L % 16. hi and lo add, then the W waves' partial sums add in wave order
+// through LDS (red: W * RT * 128 + RT * 128 floats): fin[r * 128 + tok * 16
+// + n] holds tile r's row n for token tok when the block's barrier returns.
+// GemvEpilogue then writes the block's rows (SwiGLU: tile 2j is gate,
+// 2j + 1 up, rows j * 16 + n).
+template<int W, int RT>
+__device__ __forceinline__ float* ReduceWaves(f4 (&total)[RT], float* red) {
   constexpr int T = W * 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tok0 = ((lane >> 4) & 1) * 4;
@@ -144,6 +143,16 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
     fin[o] = sum;
   }
   __syncthreads();
+  return fin;
+}
+
+template<int W, int RT, bool kSwiGLU>
+__device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int group,
+                                             int B, float* __restrict__ y, int ldy,
+                                             int rows_out) {
+  constexpr int T = W * 64;
+  const int tid = threadIdx.x;
+  const float* fin = ReduceWaves<W, RT>(total, red);
   if constexpr (kSwiGLU) {
     for (int o = tid; o < (RT / 2) * 128; o += T) {
       const int pr = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
@@ -348,21 +357,17 @@ __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
                                y, ldy, rows_out);
 }
 
-template<int W, int RT, bool kSwiGLU>
-__launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(RT >= 4 ? 2 : 4)))
-__global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
-                            const Half* __restrict__ scales, int row_tiles,
-                            int nchunks, const uint4* __restrict__ image,
-                            const int* __restrict__ exps, int B,
-                            float* __restrict__ y, int ldy, int rows_out,
-                            std::size_t part_stride) {
-  constexpr int SPW = 4, ROUND = W * SPW;  // chunks per wave per round
-  __shared__ float red[W * RT * 128 + RT * 128];
+// The operand-image GEMV's main loop: tile r of the block is tile_of(r);
+// returns each lane's un-scaled sums (D layout: lane L holds A rows
+// 4 (L / 16) + i of weight row L % 16) with the rows' powers of two undone.
+template<int W, int RT, int SPW, typename TileOf>
+__device__ __forceinline__ void ImageGemvCore(const std::uint8_t* __restrict__ codes,
+                                              const Half* __restrict__ scales, int row_tiles,
+                                              int nchunks, const uint4* __restrict__ image,
+                                              const int* __restrict__ exps, int B, int c_begin,
+                                              int nloc, TileOf tile_of, f4 (&total)[RT]) {
+  constexpr int ROUND = W * SPW;  // chunks per wave per round
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int group = blockIdx.x;
-  const int c_begin = int(blockIdx.y) * nchunks / int(gridDim.y);
-  const int nloc = (int(blockIdx.y) + 1) * nchunks / int(gridDim.y) - c_begin;
-  y += std::size_t(blockIdx.y) * part_stride;
   const bool a_live = (lane & 7) < B;
   const int part = lane >> 5, tok0 = ((lane >> 4) & 1) * 4;
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -384,7 +389,7 @@ __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
       const bool live = chunk < nloc;
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
-        const int tile = group * RT + r;
+        const int tile = tile_of(r);
         const unsigned off = unsigned(tile) * unsigned(nchunks) + unsigned(c_begin + chunk);
         const bool ok = live && tile < row_tiles;
         q[r][j] = LoadB128(c_res, ok ? off * kTileCodeBytes + lane * 16 : kOutOfRange);
@@ -401,7 +406,7 @@ __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
       const h8 a0 = __builtin_bit_cast(h8, a[j][0]), a1 = __builtin_bit_cast(h8, a[j][1]);
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
-        if (group * RT + r >= row_tiles)
+        if (tile_of(r) >= row_tiles)
           continue;
         const h8 w0 = EightCodes(q[r][j].x, q[r][j].y);
         const h8 w1 = EightCodes(q[r][j].z, q[r][j].w);
@@ -417,8 +422,6 @@ __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
       }
     }
   }
-  // D layout: lane L holds A rows 4 (L / 16) + i of weight row L % 16.
-  f4 total[RT];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = tok0 + i;
@@ -427,7 +430,84 @@ __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
     for (int r = 0; r < RT; ++r)
       total[r][i] = ldexpf(acc[r][i], ex);
   }
+}
+
+template<int W, int RT, bool kSwiGLU, int SPW>
+__launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(RT >= 4 ? 2 : 4)))
+__global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
+                            const Half* __restrict__ scales, int row_tiles,
+                            int nchunks, const uint4* __restrict__ image,
+                            const int* __restrict__ exps, int B,
+                            float* __restrict__ y, int ldy, int rows_out,
+                            std::size_t part_stride) {
+  __shared__ float red[W * RT * 128 + RT * 128];
+  const int group = blockIdx.x;
+  const int c_begin = int(blockIdx.y) * nchunks / int(gridDim.y);
+  const int nloc = (int(blockIdx.y) + 1) * nchunks / int(gridDim.y) - c_begin;
+  y += std::size_t(blockIdx.y) * part_stride;
+  f4 total[RT];
+  ImageGemvCore<W, RT, SPW>(codes, scales, row_tiles, nchunks, image, exps, B, c_begin, nloc,
+                            [=](int r) { return group * RT + r; }, total);
   GemvEpilogue<W, RT, kSwiGLU>(total, red, group, B, y, ldy, rows_out);
+}
+
+// The convolution block's in projection with the decode convolution step
+// (reference.cpp:85-101) in its epilogue: block g computes tiles g, g + T
+// and g + 2T (T = hidden / 16) of the [B | C | X] projection, i.e. B, C and
+// X of channels 16 g .. 16 g + 15, then applies ConvStepKernel's
+// expressions to them, in the same order: outputs and history are
+// bit-identical to the projection GEMV followed by lfm3_conv_step_ragged.
+template<int W>
+__launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void Q8GemvConvImage(const std::uint8_t* __restrict__ codes,
+                                const Half* __restrict__ scales, int third_tiles,
+                                int nchunks, const uint4* __restrict__ image,
+                                const int* __restrict__ exps, int B,
+                                const float* __restrict__ taps,
+                                float* const* __restrict__ history, int L, int H,
+                                float* __restrict__ y, int ldy) {
+  constexpr int RT = 3, T = W * 64, kMaxWidth = 32;
+  __shared__ float red[W * RT * 128 + RT * 128];
+  __shared__ float s_hist[128][kMaxWidth - 1];
+  __shared__ float s_taps[kTileRows][kMaxWidth];
+  const int group = blockIdx.x;
+  // The step's history rows and taps do not depend on the projection: they
+  // are staged before the weights stream, so the epilogue reads LDS only.
+  for (int e = threadIdx.x; e < 128 * (L - 1); e += T) {
+    const int o = e / (L - 1), t = e % (L - 1);
+    const int tok = o / 16, ch = group * kTileRows + o % 16;
+    if (tok < B && ch < H)
+      s_hist[o][t] = history[tok][std::size_t(ch) * (L - 1) + t];
+  }
+  for (int e = threadIdx.x; e < kTileRows * L; e += T) {
+    const int n = e / L, t = e % L, ch = group * kTileRows + n;
+    if (ch < H)
+      s_taps[n][t] = taps[std::size_t(ch) * L + t];
+  }
+  f4 total[RT];
+  ImageGemvCore<W, RT, W >= 16 ? 2 : 4>(codes, scales, 3 * third_tiles, nchunks, image, exps, B,
+                                         0, nchunks,
+                                         [=](int r) { return group + r * third_tiles; }, total);
+  const float* fin = ReduceWaves<W, RT>(total, red);  // its barriers publish s_hist
+  for (int o = threadIdx.x; o < 128; o += T) {
+#pragma clang fp contract(off)
+    const int tok = o / 16, n = o % 16, ch = group * kTileRows + n;
+    if (tok >= B || ch >= H)
+      continue;
+    const float b = fin[o], c = fin[128 + o], x = fin[256 + o];
+    const float* own = s_hist[o];
+    const float bx = b * x;
+    const float* w = s_taps[n];
+    float sum = 0.0f;
+    for (int t = 0; t < L - 1; ++t)
+      sum += w[t] * own[t];
+    sum += w[L - 1] * bx;
+    float* dst = history[tok] + std::size_t(ch) * (L - 1);
+    for (int t = 1; t < L - 1; ++t)
+      dst[t - 1] = own[t];
+    dst[L - 2] = bx;
+    y[std::size_t(tok) * ldy + ch] = sum * c;
+  }
 }
 
 template<int W, int SPW, int RT, bool kSwiGLU>
@@ -488,7 +568,7 @@ template<int W, int RT, bool kSwiGLU>
 void LaunchImagePlan(const GemvPlan& p, const std::uint8_t* c, const Half* s,
                      const uint4* image, const int* exps, int B, float* y,
                      int ldy, int rows_out, hipStream_t stream) {
-  Q8GemvImage<W, RT, kSwiGLU><<<dim3(p.groups, p.parts), W * 64, 0, stream>>>(
+  Q8GemvImage<W, RT, kSwiGLU, W >= 16 ? 2 : 4><<<dim3(p.groups, p.parts), W * 64, 0, stream>>>(
       c, s, p.row_tiles, p.nchunks, image, exps, B, y, ldy, rows_out,
       std::size_t(ldy) * B);
 }
@@ -687,6 +767,43 @@ int lfm3_q8_gemv_image(const void* codes, const void* scales,
                        std::uint32_t parts, void* stream) {
   return LaunchGemvImage<false>(codes, scales, rows, cols, image, exps, batch,
                                 y, ldy, parts, static_cast<hipStream_t>(stream));
+}
+
+int lfm3_q8_gemv_conv_image(const void* codes, const void* scales, std::uint32_t hidden,
+                            const void* image, const int* exps, std::uint32_t batch,
+                            const float* taps, float* const* history, std::uint32_t width,
+                            float* y, std::uint32_t ldy, void* stream) {
+  if (!codes || !scales || !image || !exps || !taps || !history || !y || !hidden ||
+      hidden % kTileRows || batch == 0 || batch > 8 || width < 2 || width > 32 ||
+      ldy < hidden || (reinterpret_cast<std::uintptr_t>(image) & 15) ||
+      !BufferFits(std::size_t(RowTiles(3 * hidden)) * Chunks(hidden) * kTileCodeBytes))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 projection + convolution shape");
+  const int third = int(hidden / kTileRows), nchunks = int(Chunks(hidden));
+  // One block per 16 channels: few blocks, so each takes 16 waves (two
+  // chunks each of a 32-chunk round) for more loads in flight per CU.
+  const int W = nchunks <= 4 ? 1 : nchunks <= 8 ? 2 : nchunks <= 16 ? 4 : nchunks <= 24 ? 8 : 16;
+  const auto* c = static_cast<const std::uint8_t*>(codes);
+  const auto* s = static_cast<const Half*>(scales);
+  const auto* im = static_cast<const uint4*>(image);
+  const auto st = static_cast<hipStream_t>(stream);
+  const dim3 grid(third);
+  const int B = int(batch), L = int(width), H = int(hidden), ly = int(ldy);
+  if (W == 16)
+    Q8GemvConvImage<16><<<grid, 1024, 0, st>>>(c, s, third, nchunks, im, exps, B, taps, history,
+                                               L, H, y, ly);
+  else if (W == 8)
+    Q8GemvConvImage<8><<<grid, 512, 0, st>>>(c, s, third, nchunks, im, exps, B, taps, history,
+                                             L, H, y, ly);
+  else if (W == 4)
+    Q8GemvConvImage<4><<<grid, 256, 0, st>>>(c, s, third, nchunks, im, exps, B, taps, history,
+                                             L, H, y, ly);
+  else if (W == 2)
+    Q8GemvConvImage<2><<<grid, 128, 0, st>>>(c, s, third, nchunks, im, exps, B, taps, history,
+                                             L, H, y, ly);
+  else
+    Q8GemvConvImage<1><<<grid, 64, 0, st>>>(c, s, third, nchunks, im, exps, B, taps, history,
+                                            L, H, y, ly);
+  return HipStatus(hipGetLastError(), "LFM3 projection + convolution launch");
 }
 
 int lfm3_q8_gemv_swiglu_image(const void* codes, const void* scales,

@@ -59,6 +59,7 @@ _SIGS = {
     "lfm3_operand_image_bytes": (sz, [u32]),
     "lfm3_q8_gemv_image": (i32, [vp, vp, u32, u32, vp, vp, u32, vp, u32, u32, vp]),
     "lfm3_q8_gemv_swiglu_image": (i32, [vp, vp, u32, u32, vp, vp, u32, vp, u32, vp]),
+    "lfm3_q8_gemv_conv_image": (i32, [vp, vp, u32, vp, vp, u32, vp, vp, u32, vp, u32, vp]),
     "lfm3_residual_norm_image": (i32, [vp, u32, sz, vp, vp, vp, vp, vp, vp, u32, u32, f32, vp]),
     "lfm3_conv_step_ragged_image": (i32, [vp, u32, vp, vp, vp, u32, vp, vp, u32, u32, u32, vp]),
     "lfm3_half_rows": (i32, [vp, u32, vp, u32, vp, u32, vp, u32, u32, vp]),

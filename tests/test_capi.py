@@ -195,3 +195,15 @@ def test_prompt_attention_rejects_bad_shapes():
     # a split history without its workspace
     assert lib.lfm3_prompt_attention(1, 512, 1, 1, 1, 4, 1, 1, 1, 512, 40, 4, 2, 128, 17000,
                                      17040, 0, None, 0, None) == L.E_INVALID
+
+
+def test_projection_conv_rejects_bad_shapes():
+    """Missing operands, a width outside [2, 32] or a hidden size that is not
+    a whole number of 16-row tiles are refused before any launch."""
+    lib = L.lib()
+    assert lib.lfm3_q8_gemv_conv_image(None, None, 2048, None, None, 1, None, None, 7, None, 2048,
+                                       None) == L.E_INVALID
+    assert lib.lfm3_q8_gemv_conv_image(1, 1, 2048, 16, 1, 1, 1, 1, 1, 1, 2048,
+                                       None) == L.E_INVALID  # width 1
+    assert lib.lfm3_q8_gemv_conv_image(1, 1, 2056, 16, 1, 1, 1, 1, 7, 1, 2056,
+                                       None) == L.E_INVALID  # 2056 % 16
