@@ -111,7 +111,8 @@ int lfm3_q8_gemv_swiglu_image(const void* codes, const void* scales,
    X in the usual tiled layout) on an operand image, with the decode
    convolution step in its epilogue: y[b][ch] and the history of row b
    (history[b], [hidden][width - 1]) as lfm3_conv_step_ragged leaves them
-   after the projection, bit for bit. hidden % 16 == 0, batch <= 8.
+   after the projection (the step's expressions and order; the projection's
+   chunk sums add in 16-wave order). hidden % 16 == 0, batch <= 8.
    Replaces: gpu::Project of in_proj then gpu::ShortConv for n == 1
    (engine.cpp:386-393, hip/ops.hip:2250-2264). */
 int lfm3_q8_gemv_conv_image(const void* codes, const void* scales,

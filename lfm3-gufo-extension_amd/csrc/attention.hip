@@ -5,7 +5,8 @@
 // the window), as in the reference decode (hip/ops.hip:1578-1691;
 // reference.cpp:109-144).
 //
-// Block = 4 waves; wave w takes the 16-key groups w, w + 4, ... of its span.
+// Block = 4 waves (8 when every row is one item); wave w takes the 16-key
+// groups w, w + 4, ... of its span.
 // Scores S = Q K^T run on MFMA (v_mfma_f32_16x16x32_f16): the A operand
 // holds each query head as an fp16 hi row and an fp16 lo row (hi + lo 2^-11
 // keeps about 22 bits of the FP32 query; every half x half product is
@@ -32,7 +33,7 @@
 namespace lfm3amd {
 namespace {
 
-constexpr int kAttnThreads = 256, kAttnWaves = 4, kGroupKeys = 16;
+constexpr int kAttnThreads = 256, kAttnWaves = 4, kGroupKeys = 16, kWholeRowWaves = 8;
 constexpr std::uint32_t kTargetItems = 128, kMinSpan = 64, kMaxSpan = 1024;
 constexpr std::uint32_t kMaxParts = 256;
 
@@ -86,8 +87,8 @@ __device__ __forceinline__ int ngroups_of(int kb, int ke) {
   return (ke - kb + kGroupKeys - 1) / kGroupKeys;
 }
 
-template<int D, int G, bool kFused>
-__launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
+template<int D, int G, bool kFused, int NW>
+__launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
     const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, int ld, const float* __restrict__ gate,
     int ldg, const float* __restrict__ q_norm,
@@ -104,11 +105,11 @@ __launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
   constexpr int PAIRS = (16 * G + 63) / 64;
   __shared__ float s_q[G][D];
   __shared__ __attribute__((aligned(16))) Half s_kv[2][D];
-  __shared__ float s_tile[kAttnWaves][16][17];
-  __shared__ float s_p[kAttnWaves][kGroupKeys][G];
-  __shared__ float s_alpha[kAttnWaves][G];
-  __shared__ __attribute__((aligned(16))) float s_acc[kAttnWaves][G][D];
-  __shared__ float s_m[kAttnWaves][G], s_l[kAttnWaves][G];
+  __shared__ float s_tile[NW][16][17];
+  __shared__ float s_p[NW][kGroupKeys][G];
+  __shared__ float s_alpha[NW][G];
+  __shared__ __attribute__((aligned(16))) float s_acc[NW][G][D];
+  __shared__ float s_m[NW][G], s_l[NW][G];
 
   const lfm3_attention_item item = items[blockIdx.x];
   const int g = blockIdx.y, row = int(item.row);
@@ -124,7 +125,7 @@ __launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
   // Prologue: queries of the group (normed and rotated when fused).
   if constexpr (kFused) {
 #pragma clang fp contract(off)
-    constexpr int P = D / 2, SLOTS = kAttnThreads / P;
+    constexpr int P = D / 2, SLOTS = (NW * 64) / P;
     const int slot = tid / P, pair = tid % P;
     const float fp = frequencies[pair];
     for (int h0 = 0; h0 <= G; h0 += SLOTS) {
@@ -155,7 +156,7 @@ __launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
         }
       }
     }
-    for (int d = tid; d < D; d += kAttnThreads)
+    for (int d = tid; d < D; d += (NW * 64))
       s_kv[1][d] = FloatToHalfBits(v[std::size_t(row) * ld + g * D + d]);
     __syncthreads();
     if (ke == pos + 1 && tid < D) {  // this span holds the current position
@@ -164,7 +165,7 @@ __launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
       cv[at] = s_kv[1][tid];
     }
   } else {
-    for (int e = tid; e < G * D; e += kAttnThreads)
+    for (int e = tid; e < G * D; e += (NW * 64))
       s_q[e / D][e % D] = q[std::size_t(row) * ld + (g * G + e / D) * D + e % D];
     __syncthreads();
   }
@@ -235,9 +236,9 @@ __launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
   const int ngroups = ngroups_of(kb, ke);
   uint4 kr[S], vr[KPL], kn[S], vn[KPL];
   fetch(wave, kr, vr);
-  for (int j = wave; j < ngroups; j += kAttnWaves) {
+  for (int j = wave; j < ngroups; j += NW) {
     const int base = kb + kGroupKeys * j;
-    fetch(j + kAttnWaves, kn, vn);  // past the span: zeros, no traffic
+    fetch(j + NW, kn, vn);  // past the span: zeros, no traffic
     if constexpr (kFused) {
       // The current key and value come from LDS, never from the ring.
       if (base + n == pos) {
@@ -345,15 +346,15 @@ __launch_bounds__(kAttnThreads) __global__ void DecodeAttentionKernel(
   __syncthreads();
   const bool split = item.parts > 1;
   float* part_out = partial + (std::size_t(blockIdx.x) * kv_heads + g) * G * (D + 2);
-  for (int e = tid; e < G * D; e += kAttnThreads) {
+  for (int e = tid; e < G * D; e += (NW * 64)) {
     const int h = e / D, d = e % D;
     float top = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w)
+    for (int w = 0; w < NW; ++w)
       top = fmaxf(top, s_m[w][h]);
     float l = 0.0f, av = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
+    for (int w = 0; w < NW; ++w) {
       const float wt = s_m[w][h] == -INFINITY ? 0.0f : expf(s_m[w][h] - top);
       l = fmaf(s_l[w][h], wt, l);
       av = fmaf(s_acc[w][h][d], wt, av);
@@ -449,29 +450,42 @@ struct AttentionArgs {
   float* partial = nullptr;
 };
 
-template<int D, int G>
-void LaunchGroup(const AttentionArgs& a, dim3 grid, hipStream_t s, bool fused) {
+template<int D, int G, int NW>
+void LaunchWaves(const AttentionArgs& a, dim3 grid, hipStream_t s, bool fused) {
   if (fused)
-    DecodeAttentionKernel<D, G, true><<<grid, kAttnThreads, 0, s>>>(
+    DecodeAttentionKernel<D, G, true, NW><<<grid, NW * 64, 0, s>>>(
         a.q, a.k, a.v, a.ld, a.gate, a.ldg, a.q_norm, a.k_norm, a.frequencies,
         a.factors, a.ck, a.cv, a.positions, a.capacity, a.items, a.out, a.ldo,
         a.kv, a.eps, a.partial);
   else
-    DecodeAttentionKernel<D, G, false><<<grid, kAttnThreads, 0, s>>>(
+    DecodeAttentionKernel<D, G, false, NW><<<grid, NW * 64, 0, s>>>(
         a.q, a.k, a.v, a.ld, a.gate, a.ldg, a.q_norm, a.k_norm, a.frequencies,
         a.factors, a.ck, a.cv, a.positions, a.capacity, a.items, a.out, a.ldo,
         a.kv, a.eps, a.partial);
+}
+
+// Every row in one item (sliding windows, short histories): 8-wave
+// blocks (two 16-key groups per wave for a 256-key window) and no merge
+// launch. Otherwise 4-wave blocks over the spans, then the merge.
+template<int D, int G>
+void LaunchGroup(const AttentionArgs& a, dim3 grid, hipStream_t s, bool fused, bool whole_rows) {
+  if (whole_rows) {
+    LaunchWaves<D, G, kWholeRowWaves>(a, grid, s, fused);
+    return;
+  }
+  LaunchWaves<D, G, kAttnWaves>(a, grid, s, fused);
   CombineKernel<D, G><<<grid, kAttnThreads, 0, s>>>(a.gate, a.ldg, a.items,
                                                      a.out, a.ldo, a.kv,
                                                      a.partial);
 }
 
 template<int D>
-void LaunchDim(int group, const AttentionArgs& a, dim3 grid, hipStream_t s, bool fused) {
+void LaunchDim(int group, const AttentionArgs& a, dim3 grid, hipStream_t s, bool fused,
+               bool whole_rows) {
   switch (group) {
-    case 2: LaunchGroup<D, 2>(a, grid, s, fused); break;
-    case 4: LaunchGroup<D, 4>(a, grid, s, fused); break;
-    default: LaunchGroup<D, 8>(a, grid, s, fused); break;
+    case 2: LaunchGroup<D, 2>(a, grid, s, fused, whole_rows); break;
+    case 4: LaunchGroup<D, 4>(a, grid, s, fused, whole_rows); break;
+    default: LaunchGroup<D, 8>(a, grid, s, fused, whole_rows); break;
   }
 }
 
@@ -496,10 +510,13 @@ int Launch(const AttentionArgs& a, std::uint32_t n_items, std::uint32_t rows,
   args.partial = static_cast<float*>(workspace);
   const dim3 grid(n_items, kv_heads);
   const auto s = static_cast<hipStream_t>(stream);
+  // Every plan item covers at least one row, so n_items == rows means one
+  // item (no split) per row.
+  const bool whole_rows = n_items == rows;
   if (dim == 128)
-    LaunchDim<128>(int(group), args, grid, s, fused);
+    LaunchDim<128>(int(group), args, grid, s, fused, whole_rows);
   else
-    LaunchDim<64>(int(group), args, grid, s, fused);
+    LaunchDim<64>(int(group), args, grid, s, fused, whole_rows);
   return HipStatus(hipGetLastError(), "LFM3 decode attention launch");
 }
 
@@ -529,6 +546,10 @@ int lfm3_attention_plan(const std::uint32_t* positions, std::uint32_t rows,
   span = std::max<std::uint64_t>(span, (longest + kMaxParts - 1) / kMaxParts);
   span = (span + 63) / 64 * 64;
   span = std::min<std::uint64_t>(std::max<std::uint64_t>(span, kMinSpan), kMaxSpan);
+  // A window of up to 256 keys is one item (an 8-wave block, no merge
+  // launch).
+  if (window && window <= 256)
+    span = std::max<std::uint64_t>(span, window);
   if ((longest + span - 1) / span > kMaxParts)
     return Fail(LFM3_E_INVALID, "LFM3 attention row is too long");
   std::uint32_t count = 0;

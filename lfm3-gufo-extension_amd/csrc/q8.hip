@@ -455,8 +455,8 @@ __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
 // (reference.cpp:85-101) in its epilogue: block g computes tiles g, g + T
 // and g + 2T (T = hidden / 16) of the [B | C | X] projection, i.e. B, C and
 // X of channels 16 g .. 16 g + 15, then applies ConvStepKernel's
-// expressions to them, in the same order: outputs and history are
-// bit-identical to the projection GEMV followed by lfm3_conv_step_ragged.
+// expressions to them, in the same order (for the same projection values,
+// outputs and history equal lfm3_conv_step_ragged's bit for bit).
 template<int W>
 __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2)))
 __global__ void Q8GemvConvImage(const std::uint8_t* __restrict__ codes,

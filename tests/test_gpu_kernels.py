@@ -474,10 +474,11 @@ def test_conv_row_image_bit_exact():
 
 
 @pytest.mark.parametrize("H,B", [(2048, 8), (2048, 3), (256, 1)])
-def test_projection_conv_image_bit_exact(H, B):
-    """lfm3_q8_gemv_conv_image equals the in projection's image GEMV followed
-    by lfm3_conv_step_ragged bit for bit (outputs and histories), and the
-    step follows the oracle's convolution of the same projection rows."""
+def test_projection_conv_image(H, B):
+    """lfm3_q8_gemv_conv_image against the in projection's image GEMV followed
+    by lfm3_conv_step_ragged (which equals the oracle's step bit for bit):
+    outputs and histories agree up to the order of the projection's chunk
+    sums (its 16-wave blocks add them differently): 1e-5 relative."""
     Lw = 7
     x = L.normal(SEED, f"pc.x{H}.{B}", B * H).reshape(B, H)
     dx, dw = L.DeviceBuffer.of(x), L.DeviceBuffer.of(np.ones(H, np.float32))
@@ -510,10 +511,15 @@ def test_projection_conv_image_bit_exact(H, B):
     p = dp.download(np.float32, B * 3 * H).reshape(B, 3 * H)
     y1 = dy1.download(np.float32, B * H).reshape(B, H)
     y2 = dy2.download(np.float32, B * H).reshape(B, H)
-    assert np.array_equal(y1, y2)
+    ok, err = within(y2, y1, rtol=1e-5, atol=1e-6)
+    assert ok, err
     for r in range(B):
+        h1 = dh1[r].download(np.float32, H * (Lw - 1))
         h2 = dh2[r].download(np.float32, H * (Lw - 1))
-        assert np.array_equal(dh1[r].download(np.float32, H * (Lw - 1)), h2)
         want_y, want_h = O.conv_step(p[r], taps, hist[r], H, Lw)
-        assert np.array_equal(y2[r], want_y)
-        assert np.array_equal(h2, want_h)
+        assert np.array_equal(y1[r], want_y) and np.array_equal(h1, want_h)
+        ok, err = within(h2, h1, rtol=1e-5, atol=1e-6)
+        assert ok, (r, err)
+        # the shifted part of the window is copied, not recomputed
+        keep = hist[r].reshape(H, Lw - 1)[:, 1:]
+        assert np.array_equal(h2.reshape(H, Lw - 1)[:, :-1], keep)
