@@ -116,6 +116,15 @@ __device__ __forceinline__ unsigned LoadB32(BufferResource res, unsigned offset)
   return __builtin_amdgcn_raw_buffer_load_b32(res, offset, 0, 0);
 }
 
+// Greedy-pick order key: the float's bits made monotone as unsigned, then
+// the inverted index, so the largest key is the first index of the maximum
+// (std::max_element).
+__device__ __forceinline__ unsigned long long ArgKey(float value, unsigned index) {
+  unsigned bits = __float_as_uint(value);
+  bits = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+  return (static_cast<unsigned long long>(bits) << 32) | (0xffffffffu - index);
+}
+
 __device__ __forceinline__ float WaveSum(float v) {
 #pragma unroll
   for (int m = 32; m; m >>= 1)

@@ -166,7 +166,8 @@ struct lfm3_model {
   hipStream_t stream = nullptr;
   // Round scratch, shared by the model's rounds (calls are serialized, as
   // the Gufo scheduler serializes sessions: engine.cpp:101-113).
-  Buffer x, z, proj, a, hidden, out, logits, gemv_ws, argmax_ws, ids;
+  Buffer x, proj, a, hidden, out, gemv_ws, head_keys, ids;
+  std::uint32_t head_groups = 0;
   Buffer image, exps;  // GEMV operand image of the current hidden-wide input
   std::size_t proj_ld = 0, gemv_ws_bytes = 0;
   // Per-round device tables: RoundTable, per-layer pointer rows, items.
@@ -400,7 +401,6 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     m->proj_ld = (proj_rows + 3) / 4 * 4;
     const std::size_t B = kMaxBatch;
     m->x = Buffer(B * H * 4);
-    m->z = Buffer(B * H * 4);
     m->proj = Buffer(B * m->proj_ld * 4);
     m->a = Buffer(B * std::max<std::size_t>(H, std::size_t(c.heads) * D) * 4);
     m->hidden = Buffer(B * F * 4);
@@ -408,7 +408,6 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     out_parts = std::max<std::size_t>(out_parts, lfm3_q8_gemv_parts(H, H));
     out_parts = std::max<std::size_t>(out_parts, lfm3_q8_gemv_parts(H, c.heads * D));
     m->out = Buffer(out_parts * B * H * 4);
-    m->logits = Buffer(B * std::size_t(c.vocab) * 4);
     std::size_t ws = lfm3_gemv_workspace_bytes(c.vocab, H, B);
     for (const auto& l : m->layers) {
       ws = std::max(ws, lfm3_gemv_workspace_bytes(F, H, B));
@@ -423,7 +422,8 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     }
     m->gemv_ws_bytes = std::max<std::size_t>(ws, 256);
     m->gemv_ws = Buffer(m->gemv_ws_bytes);
-    m->argmax_ws = Buffer(lfm3_argmax_workspace_bytes(B));
+    m->head_groups = HeadGemvGroups(c.vocab, H);
+    m->head_keys = Buffer(std::size_t(B) * m->head_groups * sizeof(unsigned long long));
     m->image = Buffer(lfm3_operand_image_bytes(H));
     m->exps = Buffer(kMaxBatch * sizeof(int));
     m->ids = Buffer(B * 4);
@@ -620,7 +620,6 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
   const auto* d_rt = reinterpret_cast<const RoundTable*>(dev);
 
   float* x = m.x.as<float>();
-  float* z = m.z.as<float>();
   float* proj = m.proj.as<float>();
   float* a = m.a.as<float>();
   float* hid = m.hidden.as<float>();
@@ -646,16 +645,30 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
     CheckStatus(lfm3_q8_gemv_image(w.codes.p, w.scales.p, w.rows, w.cols, image,
                                    exps, n, y, ldy, 1, s));
   };
-  const auto norm_image = [&](std::uint32_t parts, const float* post,
-                              const float* weight, float* zrow) {
-    CheckStatus(lfm3_residual_norm_image(parts ? out : nullptr, parts ? parts : 1,
-                                         std::size_t(n) * H, post, x, weight, zrow,
-                                         image, exps, n, H, c.eps, s));
+  NormImageArgs na;
+  na.part_stride = std::size_t(n) * H;
+  na.x = x;
+  na.H = int(H);
+  na.eps = c.eps;
+  na.image = static_cast<uint4*>(image);
+  na.exps = exps;
+  const auto norm_image = [&](std::uint32_t parts, const float* post, const float* weight,
+                              float* const* z_rows) {
+    na.branch = parts ? out : nullptr;
+    na.parts = parts ? int(parts) : 1;
+    na.post = parts ? post : nullptr;
+    na.weight = weight;
+    na.z_rows = z_rows;
+    CheckStatus(LaunchNormImage(na, n, s));
   };
 
-  CheckStatus(lfm3_embed(m.embedding.codes.p, m.embedding.scales.p, c.vocab, H,
-                         d_rt->tokens, n, x, s));
+  // The first norm gathers the round's embedding rows into x.
+  na.emb_codes = static_cast<const std::uint8_t*>(m.embedding.codes.p);
+  na.emb_scales = static_cast<const std::uint16_t*>(m.embedding.scales.p);
+  na.tokens = d_rt->tokens;
+  na.vocab = int(c.vocab);
   norm_image(0, nullptr, m.layers[0].norm.as<float>(), nullptr);
+  na.tokens = nullptr;
   for (std::uint32_t il = 0; il < L; ++il) {
     const Layer& l = m.layers[il];
     if (l.type == LFM3_LAYER_CONV) {
@@ -688,21 +701,20 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
                                           image, exps, n, hid, F, s));
     const std::uint32_t ffn_parts = partials(l.down, hid, F);
     const bool last = il + 1 == L;
-    // The last norm's FP32 rows are the frontier rows (engine.cpp:505-511).
+    // The last norm's FP32 rows are the sessions' frontier rows
+    // (engine.cpp:505-511), written in place.
     norm_image(ffn_parts, l.post_ffn_norm.as<float>(),
                last ? m.output_norm.as<float>() : m.layers[il + 1].norm.as<float>(),
-               last ? z : nullptr);
+               last ? d_rt->frontier : nullptr);
   }
-  // LM head over the final-normed rows, then each session's logits and
-  // frontier rows.
+  // LM head over the final-normed rows into each session's logits row, with
+  // per-block greedy candidates; then the greedy ids from the candidates.
   const Matrix& head = m.head();
-  gemv_image(head, m.logits.as<float>(), c.vocab);
-  CheckStatus(LaunchScatterRows(m.logits.as<float>(), c.vocab, d_rt->logits, n,
-                                c.vocab, s));
-  CheckStatus(LaunchScatterRows(z, H, d_rt->frontier, n, H, s));
+  auto* keys = m.head_keys.as<unsigned long long>();
+  CheckStatus(LaunchHeadGemv(head.codes.p, head.scales.p, head.rows, head.cols, image, exps, n,
+                             d_rt->logits, keys, nullptr, s));
   if (greedy)
-    CheckStatus(lfm3_argmax(m.logits.as<float>(), n, c.vocab, m.ids.as<std::uint32_t>(),
-                            m.argmax_ws.p, m.argmax_ws.bytes, s));
+    CheckStatus(LaunchArgmaxKeys(keys, n, m.head_groups, m.ids.as<std::uint32_t>(), s));
   Check(hipGetLastError(), "round launch");
   Check(hipStreamSynchronize(s), "round");
   for (std::uint32_t i = 0; i < n; ++i) {

@@ -7,6 +7,40 @@
 #include <cstdint>
 
 namespace lfm3amd {
+// Decode-round residual norm writing the next GEMV's operand image
+// (lfm3_residual_norm_image) with the round's options: z rows through a
+// device pointer table, and for the round's first norm x gathered from the
+// tiled embedding table at tokens[r].
+struct NormImageArgs {
+  const float* branch = nullptr;
+  int parts = 1;
+  std::size_t part_stride = 0;
+  const float* post = nullptr;
+  float* x = nullptr;
+  const float* weight = nullptr;
+  float* z = nullptr;
+  float* const* z_rows = nullptr;
+  int H = 0;
+  float eps = 0.0f;
+  uint4* image = nullptr;
+  int* exps = nullptr;
+  const std::uint8_t* emb_codes = nullptr;
+  const std::uint16_t* emb_scales = nullptr;
+  const std::uint32_t* tokens = nullptr;
+  int vocab = 0;
+};
+int LaunchNormImage(const NormImageArgs& a, std::uint32_t rows, hipStream_t stream);
+// The vocabulary head on the final operand image: row t of the logits goes
+// to y_rows[t], and keys[t * groups + j] gets the best ArgKey of block j's
+// rows; returns the number of groups through *groups.
+int LaunchHeadGemv(const void* codes, const void* scales, std::uint32_t rows,
+                   std::uint32_t cols, const void* image, const int* exps, std::uint32_t batch,
+                   float* const* y_rows, unsigned long long* keys, std::uint32_t* groups,
+                   hipStream_t stream);
+std::uint32_t HeadGemvGroups(std::uint32_t rows, std::uint32_t cols);
+// ids[t] = the first index of token t's maximum from the head's keys.
+int LaunchArgmaxKeys(const unsigned long long* keys, std::uint32_t rows, std::uint32_t groups,
+                     std::uint32_t* ids, hipStream_t stream);
 // dst[i][0..count) = src + i * ld for rows i < rows, with dst pointers read
 // from a device table (per-session logits / frontier rows of a round).
 int LaunchScatterRows(const float* src, std::size_t ld, float* const* dst,

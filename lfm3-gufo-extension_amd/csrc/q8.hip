@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "internal.hpp"
 
 namespace lfm3amd {
 namespace {
@@ -149,10 +150,39 @@ __device__ __forceinline__ float* ReduceWaves(f4 (&total)[RT], float* red) {
 template<int W, int RT, bool kSwiGLU>
 __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int group,
                                              int B, float* __restrict__ y, int ldy,
-                                             int rows_out) {
+                                             int rows_out, float* const* y_rows = nullptr,
+                                             unsigned long long* keys = nullptr) {
   constexpr int T = W * 64;
   const int tid = threadIdx.x;
   const float* fin = ReduceWaves<W, RT>(total, red);
+  if (keys) {
+    // Greedy candidates: token t's best ArgKey over the block's rows, one
+    // (token, row) per lane, reduced over the token's lanes.
+    constexpr int R = RT * kTileRows;  // rows of the block: 16 or 32
+    if constexpr (8 * R <= T) {
+      const int tok = tid / R, r = (tid % R) / kTileRows, n = tid % kTileRows;
+      const int row = (group * RT + r) * kTileRows + n;
+      unsigned long long key = 0;
+      if (tid < 8 * R && row < rows_out)
+        key = ArgKey(fin[r * 128 + tok * 16 + n], unsigned(row));
+#pragma unroll
+      for (int m = R / 2; m; m >>= 1) {
+        const unsigned long long other = __shfl_xor(key, m, 64);
+        key = other > key ? other : key;
+      }
+      if (tid < 8 * R && tid % R == 0 && tok < B)
+        keys[std::size_t(tok) * gridDim.x + group] = key;
+    } else if (tid < B) {  // small blocks: one lane per token
+      unsigned long long best = 0;
+      for (int i = 0; i < R; ++i) {
+        const int row = (group * RT + i / kTileRows) * kTileRows + i % kTileRows;
+        const unsigned long long k =
+            ArgKey(fin[(i / kTileRows) * 128 + tid * 16 + i % kTileRows], unsigned(row));
+        best = row < rows_out && k > best ? k : best;
+      }
+      keys[std::size_t(tid) * gridDim.x + group] = best;
+    }
+  }
   if constexpr (kSwiGLU) {
     for (int o = tid; o < (RT / 2) * 128; o += T) {
       const int pr = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
@@ -166,7 +196,7 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
       const int r = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
       const int row = (group * RT + r) * kTileRows + n;
       if (tok < B && row < rows_out)
-        y[std::size_t(tok) * ldy + row] = fin[o];
+        (y_rows ? y_rows[tok] : y + std::size_t(tok) * ldy)[row] = fin[o];
     }
   }
 }
@@ -439,7 +469,8 @@ __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
                             int nchunks, const uint4* __restrict__ image,
                             const int* __restrict__ exps, int B,
                             float* __restrict__ y, int ldy, int rows_out,
-                            std::size_t part_stride) {
+                            std::size_t part_stride, float* const* __restrict__ y_rows,
+                            unsigned long long* __restrict__ keys) {
   __shared__ float red[W * RT * 128 + RT * 128];
   const int group = blockIdx.x;
   const int c_begin = int(blockIdx.y) * nchunks / int(gridDim.y);
@@ -448,7 +479,7 @@ __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
   f4 total[RT];
   ImageGemvCore<W, RT, SPW>(codes, scales, row_tiles, nchunks, image, exps, B, c_begin, nloc,
                             [=](int r) { return group * RT + r; }, total);
-  GemvEpilogue<W, RT, kSwiGLU>(total, red, group, B, y, ldy, rows_out);
+  GemvEpilogue<W, RT, kSwiGLU>(total, red, group, B, y, ldy, rows_out, y_rows, keys);
 }
 
 // The convolution block's in projection with the decode convolution step
@@ -567,55 +598,65 @@ int LaunchGemv(const void* codes, const void* scales, std::uint32_t rows,
 template<int W, int RT, bool kSwiGLU>
 void LaunchImagePlan(const GemvPlan& p, const std::uint8_t* c, const Half* s,
                      const uint4* image, const int* exps, int B, float* y,
-                     int ldy, int rows_out, hipStream_t stream) {
+                     int ldy, int rows_out, hipStream_t stream, float* const* y_rows,
+                     unsigned long long* keys) {
   Q8GemvImage<W, RT, kSwiGLU, W >= 16 ? 2 : 4><<<dim3(p.groups, p.parts), W * 64, 0, stream>>>(
       c, s, p.row_tiles, p.nchunks, image, exps, B, y, ldy, rows_out,
-      std::size_t(ldy) * B);
+      std::size_t(ldy) * B, y_rows, keys);
 }
 
 template<int W, bool kSwiGLU>
 void LaunchImageRT(const GemvPlan& p, const std::uint8_t* c, const Half* s,
                    const uint4* image, const int* exps, int B, float* y, int ldy,
-                   int rows_out, hipStream_t stream) {
+                   int rows_out, hipStream_t stream, float* const* y_rows,
+                   unsigned long long* keys) {
   if constexpr (kSwiGLU) {
-    LaunchImagePlan<W, 2, true>(p, c, s, image, exps, B, y, ldy, rows_out, stream);
+    LaunchImagePlan<W, 2, true>(p, c, s, image, exps, B, y, ldy, rows_out, stream, y_rows, keys);
   } else {
     if (p.RT == 1)
-      LaunchImagePlan<W, 1, false>(p, c, s, image, exps, B, y, ldy, rows_out, stream);
+      LaunchImagePlan<W, 1, false>(p, c, s, image, exps, B, y, ldy, rows_out, stream, y_rows,
+                                   keys);
     else
-      LaunchImagePlan<W, 2, false>(p, c, s, image, exps, B, y, ldy, rows_out, stream);
+      LaunchImagePlan<W, 2, false>(p, c, s, image, exps, B, y, ldy, rows_out, stream, y_rows,
+                                   keys);
   }
+}
+
+GemvPlan PlanImage(std::uint32_t rows, std::uint32_t cols, bool swiglu, std::uint32_t parts) {
+  GemvPlan p = PlanGemv(rows, cols, swiglu, int(parts));
+  // Rounds of W * 4 chunks need no LDS: keep two tiles (one SwiGLU pair)
+  // at most, so two blocks of eight waves fit a CU.
+  p.RT = swiglu ? 2 : std::min(p.RT, 2);
+  p.groups = (p.row_tiles + p.RT - 1) / p.RT;
+  return p;
 }
 
 template<bool kSwiGLU>
 int LaunchGemvImage(const void* codes, const void* scales, std::uint32_t rows,
                     std::uint32_t cols, const void* image, const int* exps,
                     std::uint32_t batch, float* y, std::uint32_t ldy,
-                    std::uint32_t parts, hipStream_t stream) {
-  if (!codes || !scales || !image || !exps || !y || rows == 0 || cols == 0 ||
-      cols % 32 || batch == 0 || batch > 8 || ldy < rows || parts < 1 ||
-      parts > Chunks(cols) || (kSwiGLU && parts != 1) ||
+                    std::uint32_t parts, hipStream_t stream, float* const* y_rows = nullptr,
+                    unsigned long long* keys = nullptr) {
+  if (!codes || !scales || !image || !exps || (!y && !y_rows) || rows == 0 || cols == 0 ||
+      cols % 32 || batch == 0 || batch > 8 || (!y_rows && ldy < rows) || parts < 1 ||
+      parts > Chunks(cols) || (kSwiGLU && parts != 1) || ((y_rows || keys) && parts != 1) ||
       (reinterpret_cast<std::uintptr_t>(image) & 15) ||
       !BufferFits(std::size_t(RowTiles(rows) * (kSwiGLU ? 2 : 1)) * Chunks(cols) *
                   kTileCodeBytes))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 operand-image GEMV");
-  GemvPlan p = PlanGemv(rows, cols, kSwiGLU, int(parts));
-  // Rounds of W * 4 chunks need no LDS: keep two tiles (one SwiGLU pair)
-  // at most, so two blocks of eight waves fit a CU.
-  p.RT = kSwiGLU ? 2 : std::min(p.RT, 2);
-  p.groups = (p.row_tiles + p.RT - 1) / p.RT;
+  const GemvPlan p = PlanImage(rows, cols, kSwiGLU, parts);
   const auto* c = static_cast<const std::uint8_t*>(codes);
   const auto* s = static_cast<const Half*>(scales);
   const auto* im = static_cast<const uint4*>(image);
   const int B = int(batch), ly = int(ldy), ro = int(rows);
   if (p.W == 8)
-    LaunchImageRT<8, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream);
+    LaunchImageRT<8, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys);
   else if (p.W == 4)
-    LaunchImageRT<4, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream);
+    LaunchImageRT<4, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys);
   else if (p.W == 2)
-    LaunchImageRT<2, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream);
+    LaunchImageRT<2, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys);
   else
-    LaunchImageRT<1, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream);
+    LaunchImageRT<1, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys);
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 operand-image GEMV launch");
 }
 
@@ -644,6 +685,22 @@ __global__ void EmbedKernel(const std::uint8_t* __restrict__ codes,
 }
 
 }  // namespace
+
+std::uint32_t HeadGemvGroups(std::uint32_t rows, std::uint32_t cols) {
+  return std::uint32_t(PlanImage(rows, cols, false, 1).groups);
+}
+
+int LaunchHeadGemv(const void* codes, const void* scales, std::uint32_t rows,
+                   std::uint32_t cols, const void* image, const int* exps, std::uint32_t batch,
+                   float* const* y_rows, unsigned long long* keys, std::uint32_t* groups,
+                   hipStream_t stream) {
+  if (!y_rows || !keys)
+    return Fail(LFM3_E_INVALID, "LFM3 head GEMV needs its row table and key buffer");
+  if (groups)
+    *groups = HeadGemvGroups(rows, cols);
+  return LaunchGemvImage<false>(codes, scales, rows, cols, image, exps, batch, nullptr, 0, 1,
+                                stream, y_rows, keys);
+}
 }  // namespace lfm3amd
 
 using namespace lfm3amd;

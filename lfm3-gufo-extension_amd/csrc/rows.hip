@@ -198,37 +198,74 @@ __device__ __forceinline__ float SmallBlockSum(float v, float* slots) {
 }
 
 template<int G>
-__launch_bounds__(kImageNormThreads) __global__
-    void NormImageKernel(const float* __restrict__ branch, int parts, std::size_t part_stride,
-                         const float* __restrict__ post, float* __restrict__ x,
-                         const float* __restrict__ weight, float* __restrict__ z, int H,
-                         float eps, uint4* __restrict__ image, int* __restrict__ exps) {
+__launch_bounds__(kImageNormThreads) __global__ void NormImageKernel(const NormImageArgs a) {
   constexpr int kWaves = kImageNormThreads / 64;
   __shared__ float s_red[3][kWaves];
-  const int row = blockIdx.x, tid = threadIdx.x;
+  const int row = blockIdx.x, tid = threadIdx.x, H = a.H;
   const unsigned row_bytes = unsigned(H) * 4;
-  const BufferResource x_res = MakeBuffer(x + std::size_t(row) * H, row_bytes);
-  const BufferResource w_res = MakeBuffer(weight, row_bytes);
-  const BufferResource p_res = MakeBuffer(post ? post : weight, post ? row_bytes : 0u);
+  float* x = a.x;
+  const BufferResource x_res = MakeBuffer(x + std::size_t(row) * H, a.tokens ? 0u : row_bytes);
+  const BufferResource w_res = MakeBuffer(a.weight, row_bytes);
+  const BufferResource p_res = MakeBuffer(a.post ? a.post : a.weight, a.post ? row_bytes : 0u);
   float v[G][8], pw[G][8], nw[G][8], b[kNormParts][G][8];
   const auto load8 = [](BufferResource r, unsigned off, float* out) {
     const float4 lo = LoadF4(r, off), hi = LoadF4(r, off + 16);
     out[0] = lo.x; out[1] = lo.y; out[2] = lo.z; out[3] = lo.w;
     out[4] = hi.x; out[5] = hi.y; out[6] = hi.z; out[7] = hi.w;
   };
+  // The round's first norm gathers its rows from the tiled embedding table
+  // (EmbedKernel's layout: columns 8G..8G+7 of row r are 8 consecutive code
+  // bytes of one lane word) and writes them to x.
+  std::uint32_t token = 0;
+  if (a.tokens) {
+    token = a.tokens[row];
+    if (token >= std::uint32_t(a.vocab))
+      token = 0;  // the host validates ids; never read out of bounds
+  }
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = tid + kImageNormThreads * i;
     const unsigned off = g * 8 < H ? unsigned(g) * 32 : kOutOfRange;
-    load8(x_res, off, v[i]);
+    if (a.tokens) {
+      const int chunk = g / 8, blk = (g % 8) / 4, lg = g % 4;
+      const std::size_t tile = std::size_t(token / kTileRows) * ((H + kChunk - 1) / kChunk) + chunk;
+      const int nn = int(token % kTileRows);
+      unsigned lo = 0, hi = 0;
+      float d = 0.0f;
+      if (g * 8 < H) {
+        const uint2 q = *reinterpret_cast<const uint2*>(
+            a.emb_codes + tile * kTileCodeBytes + (lg * 16 + nn) * 16 + blk * 8);
+        lo = q.x;
+        hi = q.y;
+        d = HalfBitsToFloat(a.emb_scales[tile * kTileScales + nn * 2 + blk]);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[i][k] = d * float(int((lo >> (8 * k)) & 0xffu) - 128);
+        v[i][4 + k] = d * float(int((hi >> (8 * k)) & 0xffu) - 128);
+      }
+    } else {
+      load8(x_res, off, v[i]);
+    }
     load8(w_res, off, nw[i]);
     load8(p_res, off, pw[i]);
   }
-  if (branch) {
+  if (a.tokens) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int g = tid + kImageNormThreads * i;
+      if (g * 8 < H) {
+        float4* xr = reinterpret_cast<float4*>(x + std::size_t(row) * H + g * 8);
+        xr[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+        xr[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
+      }
+    }
+  }
+  if (a.branch) {
 #pragma unroll
     for (int p = 0; p < kNormParts; ++p) {
-      const BufferResource b_res =
-          MakeBuffer(branch + p * part_stride + std::size_t(row) * H, p < parts ? row_bytes : 0u);
+      const BufferResource b_res = MakeBuffer(a.branch + p * a.part_stride + std::size_t(row) * H,
+                                              p < a.parts ? row_bytes : 0u);
 #pragma unroll
       for (int i = 0; i < G; ++i) {
         const int g = tid + kImageNormThreads * i;
@@ -245,9 +282,9 @@ __launch_bounds__(kImageNormThreads) __global__
           b[0][i][k] += b[p][i][k];
         squares = fmaf(b[0][i][k], b[0][i][k], squares);
       }
-    if (post) {
+    if (a.post) {
       const float scale =
-          1.0f / sqrtf(SmallBlockSum<kWaves>(squares, s_red[0]) / float(H) + eps);
+          1.0f / sqrtf(SmallBlockSum<kWaves>(squares, s_red[0]) / float(H) + a.eps);
 #pragma unroll
       for (int i = 0; i < G; ++i)
 #pragma unroll
@@ -273,7 +310,9 @@ __launch_bounds__(kImageNormThreads) __global__
 #pragma unroll
     for (int k = 0; k < 8; ++k)
       squares = fmaf(v[i][k], v[i][k], squares);
-  const float scale = 1.0f / sqrtf(SmallBlockSum<kWaves>(squares, s_red[1]) / float(H) + eps);
+  const float scale =
+      1.0f / sqrtf(SmallBlockSum<kWaves>(squares, s_red[1]) / float(H) + a.eps);
+  float* zrow = a.z_rows ? a.z_rows[row] : a.z ? a.z + std::size_t(row) * H : nullptr;
   float maximum = 0.0f;
 #pragma unroll
   for (int i = 0; i < G; ++i) {
@@ -283,8 +322,8 @@ __launch_bounds__(kImageNormThreads) __global__
       v[i][k] = (v[i][k] * scale) * nw[i][k];  // zero past H
       maximum = fmaxf(maximum, fabsf(v[i][k]));
     }
-    if (z && g * 8 < H) {
-      float4* zr = reinterpret_cast<float4*>(z + std::size_t(row) * H + g * 8);
+    if (zrow && g * 8 < H) {
+      float4* zr = reinterpret_cast<float4*>(zrow + g * 8);
       zr[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
       zr[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
     }
@@ -299,7 +338,7 @@ __launch_bounds__(kImageNormThreads) __global__
     maximum = fmaxf(maximum, s_red[2][w]);
   const int e = RowExponent(maximum);
   if (tid == 0)
-    exps[row] = e;
+    a.exps[row] = e;
   // Image groups: every group of the row's 64-column chunks, zeros past H.
   const int groups = (H + kChunk - 1) / kChunk * 8;
 #pragma unroll
@@ -312,8 +351,8 @@ __launch_bounds__(kImageNormThreads) __global__
     for (int k = 0; k < 8; k += 2)
       SplitPair(v[i][k], v[i][k + 1], e, hi[k / 2], lo[k / 2]);
     const int idx = ((cg >> 3) * 2 + ((cg >> 2) & 1)) * 64 + 16 * (cg & 3) + row;
-    image[idx] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-    image[idx + 8] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    a.image[idx] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    a.image[idx + 8] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
   }
 }
 
@@ -621,12 +660,6 @@ __global__ void PromptConvHistoryKernel(const float* __restrict__ p, int ldp,
 // reduces it over the block; no cross-block merge.
 constexpr int kArgmaxThreads = 1024;
 
-__device__ __forceinline__ unsigned long long ArgKey(float value, unsigned index) {
-  unsigned bits = __float_as_uint(value);
-  bits = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-  return (static_cast<unsigned long long>(bits) << 32) | (0xffffffffu - index);
-}
-
 __launch_bounds__(kArgmaxThreads) __global__
     void ArgmaxKernel(const float* __restrict__ logits, int cols,
                       std::uint32_t* __restrict__ ids) {
@@ -665,6 +698,32 @@ __launch_bounds__(kArgmaxThreads) __global__
   }
 }
 
+// ids[t] from per-block candidate keys: keys[t * groups + j] is the best
+// ArgKey of block j's rows for token t.
+__launch_bounds__(256) __global__
+    void ArgmaxKeysKernel(const unsigned long long* __restrict__ keys, int groups,
+                          std::uint32_t* __restrict__ ids) {
+  __shared__ unsigned long long best[4];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const unsigned long long* kr = keys + std::size_t(t) * groups;
+  unsigned long long key = 0;
+  for (int j = tid; j < groups; j += 256)
+    key = kr[j] > key ? kr[j] : key;
+#pragma unroll
+  for (int m = 32; m; m >>= 1) {
+    const unsigned long long other = __shfl_xor(key, m, 64);
+    key = other > key ? other : key;
+  }
+  if ((tid & 63) == 0)
+    best[tid >> 6] = key;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w)
+      key = best[w] > key ? best[w] : key;
+    ids[t] = 0xffffffffu - unsigned(key & 0xffffffffu);
+  }
+}
+
 __global__ void ScatterRowsKernel(const float* __restrict__ src, std::size_t ld,
                                   float* const* __restrict__ dst,
                                   std::size_t count) {
@@ -681,6 +740,20 @@ __global__ void ScatterRowsKernel(const float* __restrict__ src, std::size_t ld,
 }
 
 }  // namespace
+
+int LaunchNormImage(const NormImageArgs& a, std::uint32_t rows, hipStream_t stream) {
+  if (Chunks(unsigned(a.H)) * 8 <= kImageNormThreads)
+    NormImageKernel<1><<<rows, kImageNormThreads, 0, stream>>>(a);
+  else
+    NormImageKernel<2><<<rows, kImageNormThreads, 0, stream>>>(a);
+  return HipStatus(hipGetLastError(), "LFM3 residual norm launch");
+}
+
+int LaunchArgmaxKeys(const unsigned long long* keys, std::uint32_t rows, std::uint32_t groups,
+                     std::uint32_t* ids, hipStream_t stream) {
+  ArgmaxKeysKernel<<<rows, 256, 0, stream>>>(keys, int(groups), ids);
+  return HipStatus(hipGetLastError(), "LFM3 argmax launch");
+}
 
 int LaunchScatterRows(const float* src, std::size_t ld, float* const* dst,
                       std::uint32_t rows, std::size_t count,
@@ -727,18 +800,25 @@ int lfm3_residual_norm_image(const float* branch, std::uint32_t parts,
   const auto* post = branch ? post_norm : nullptr;
   auto* im = static_cast<uint4*>(image);
   const auto st = static_cast<hipStream_t>(stream);
-  const int groups = int(Chunks(hidden)) * 8;
-  if (groups <= kImageNormThreads)
-    NormImageKernel<1><<<rows, kImageNormThreads, 0, st>>>(
-        branch, int(parts), part_stride, post, x, norm, z, int(hidden), eps, im, exps);
-  else if (groups <= 2 * kImageNormThreads)
-    NormImageKernel<2><<<rows, kImageNormThreads, 0, st>>>(
-        branch, int(parts), part_stride, post, x, norm, z, int(hidden), eps, im, exps);
-  else
+  if (Chunks(hidden) * 8 > 2 * kImageNormThreads) {
     ResidualNormKernel<<<rows, kNormThreads, 0, st>>>(
         branch, int(parts), part_stride, post, x, norm, z, int(hidden), eps, im, exps,
         nullptr, 0, nullptr);
-  return HipStatus(hipGetLastError(), "LFM3 residual norm launch");
+    return HipStatus(hipGetLastError(), "LFM3 residual norm launch");
+  }
+  NormImageArgs a{};
+  a.branch = branch;
+  a.parts = int(parts);
+  a.part_stride = part_stride;
+  a.post = post;
+  a.x = x;
+  a.weight = norm;
+  a.z = z;
+  a.H = int(hidden);
+  a.eps = eps;
+  a.image = im;
+  a.exps = exps;
+  return LaunchNormImage(a, rows, st);
 }
 
 int lfm3_residual_norm_half(const float* branch, std::uint32_t parts,
