@@ -134,8 +134,9 @@ int lfm3_q8_gemv_swiglu(const void* codes, const void* scales, uint32_t rows,
  * ------------------------------------------------------------------- */
 /* FP16 row-scaled activations (hip/q8_prefill.hpp:27-74): per row
    e = 14 - ilogb(max |x|) (0 for a zero row), out = fp16(x 2^e), scale =
-   2^-e. out rows have lda halves (lda % 64 == 0, lda >= cols; the tail is
-   zeroed). With row_max (max_blocks partial maxima of each row as FP32
+   2^-e. out rows have lda halves (lda % 64 == 0, lda >= cols); columns
+   [cols, cols rounded up to 64) are zeroed (the GEMM's last chunk), later
+   ones are not written. With row_max (max_blocks partial maxima of each row as FP32
    bits, row_max[b * rows + row], e.g. from lfm3_q8_gemm_swiglu) the row
    scan is skipped. Replaces: HalfRows / HalfRowsFromMax
    (q8_prefill.hpp:30-74). */

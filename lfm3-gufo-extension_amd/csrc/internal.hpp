@@ -28,6 +28,10 @@ struct NormImageArgs {
   const std::uint16_t* emb_scales = nullptr;
   const std::uint32_t* tokens = nullptr;
   int vocab = 0;
+  // The prompt GEMM's FP16 rows instead of (or beside) the image.
+  std::uint16_t* a16 = nullptr;
+  int lda = 0;
+  float* a_scale = nullptr;
 };
 int LaunchNormImage(const NormImageArgs& a, std::uint32_t rows, hipStream_t stream);
 // The vocabulary head on the final operand image: row t of the logits goes

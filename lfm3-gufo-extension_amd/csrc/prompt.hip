@@ -42,20 +42,22 @@ constexpr int kGemmTokens = kGemmWT * kGemmTT * 16;
 constexpr int kHalfThreads = 256, kHalfVec = 8;  // float4 a thread: 8192 columns
 constexpr int kHalfSplit = 4;  // blocks a row with known maxima: 2048 columns each
 
-__device__ __forceinline__ float RowMaximum(const unsigned* __restrict__ row_max,
-                                            int max_blocks, int rows, int row) {
-  float maximum = 0.0f;
-  for (int b = 0; b < max_blocks; ++b)
-    maximum = fmaxf(maximum, __uint_as_float(row_max[std::size_t(b) * rows + row]));
-  return maximum;
-}
-
 __device__ __forceinline__ float BlockMaximum256(float v, float* s_max) {
   v = WaveMax(v);
   if ((threadIdx.x & 63) == 0)
     s_max[threadIdx.x >> 6] = v;
   __syncthreads();
   return fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+}
+
+// The row's maximum from max_blocks partial maxima: one load per thread,
+// then a block maximum (a serial loop would chain max_blocks loads).
+__device__ __forceinline__ float RowMaximum(const unsigned* __restrict__ row_max,
+                                            int max_blocks, int rows, int row, float* s_max) {
+  float maximum = 0.0f;
+  for (int b = threadIdx.x; b < max_blocks; b += kHalfThreads)
+    maximum = fmaxf(maximum, __uint_as_float(row_max[std::size_t(b) * rows + row]));
+  return BlockMaximum256(maximum, s_max);
 }
 
 template<bool kVec>
@@ -83,7 +85,7 @@ __launch_bounds__(kHalfThreads) __global__
     }
     float maximum;
     if (row_max) {
-      maximum = RowMaximum(row_max, max_blocks, gridDim.x, row);
+      maximum = RowMaximum(row_max, max_blocks, gridDim.x, row, s_max);
     } else {
       maximum = 0.0f;
 #pragma unroll
@@ -103,13 +105,13 @@ __launch_bounds__(kHalfThreads) __global__
         dst2[i] = make_uint2(unsigned(ScaledHalf(v[j].x, e)) | (unsigned(ScaledHalf(v[j].y, e)) << 16),
                              unsigned(ScaledHalf(v[j].z, e)) | (unsigned(ScaledHalf(v[j].w, e)) << 16));
     }
-    if (blockIdx.y + 1 == gridDim.y)
-      for (int i = K / 4 + tid; i < lda / 4; i += kHalfThreads)
+    if (blockIdx.y + 1 == gridDim.y)  // the zero tail of the last chunk
+      for (int i = K / 4 + tid; i < (K + kChunk - 1) / kChunk * (kChunk / 4); i += kHalfThreads)
         dst2[i] = make_uint2(0u, 0u);
   } else {
     float maximum;
     if (row_max) {
-      maximum = RowMaximum(row_max, max_blocks, gridDim.x, row);
+      maximum = RowMaximum(row_max, max_blocks, gridDim.x, row, s_max);
     } else {
       maximum = 0.0f;
       for (int k = tid; k < K; k += kHalfThreads)
@@ -119,7 +121,7 @@ __launch_bounds__(kHalfThreads) __global__
     const int e = RowExponent(maximum);
     if (tid == 0)
       scale[row] = ldexpf(1.0f, -e);
-    for (int k = tid; k < lda; k += kHalfThreads)
+    for (int k = tid; k < (K + kChunk - 1) / kChunk * kChunk; k += kHalfThreads)
       dst[k] = k < K ? ScaledHalf(src[k], e) : Half(0);
   }
 }

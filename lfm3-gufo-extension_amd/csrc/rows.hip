@@ -170,7 +170,8 @@ __launch_bounds__(kNormThreads) __global__
     const int e = RowExponent(maximum);
     if (tid == 0)
       a_scale[row] = ldexpf(1.0f, -e);
-    for (int k = tid; k < lda; k += kNormThreads)
+    // The zero tail of the last 64-column chunk; later columns are not read.
+    for (int k = tid; k < (H + kChunk - 1) / kChunk * kChunk; k += kNormThreads)
       a16[std::size_t(row) * lda + k] = k < H ? ScaledHalf(s_row[k], e) : Half(0);
   }
 }
@@ -337,22 +338,41 @@ __launch_bounds__(kImageNormThreads) __global__ void NormImageKernel(const NormI
   for (int w = 0; w < kWaves; ++w)
     maximum = fmaxf(maximum, s_red[2][w]);
   const int e = RowExponent(maximum);
-  if (tid == 0)
-    a.exps[row] = e;
-  // Image groups: every group of the row's 64-column chunks, zeros past H.
+  // Every group of the row's 64-column chunks, zeros past H.
   const int groups = (H + kChunk - 1) / kChunk * 8;
+  if (a.image) {
+    if (tid == 0)
+      a.exps[row] = e;
 #pragma unroll
-  for (int i = 0; i < G; ++i) {
-    const int cg = tid + kImageNormThreads * i;
-    if (cg >= groups)
-      continue;
-    unsigned hi[4], lo[4];
+    for (int i = 0; i < G; ++i) {
+      const int cg = tid + kImageNormThreads * i;
+      if (cg >= groups)
+        continue;
+      unsigned hi[4], lo[4];
 #pragma unroll
-    for (int k = 0; k < 8; k += 2)
-      SplitPair(v[i][k], v[i][k + 1], e, hi[k / 2], lo[k / 2]);
-    const int idx = ((cg >> 3) * 2 + ((cg >> 2) & 1)) * 64 + 16 * (cg & 3) + row;
-    a.image[idx] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-    a.image[idx + 8] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+      for (int k = 0; k < 8; k += 2)
+        SplitPair(v[i][k], v[i][k + 1], e, hi[k / 2], lo[k / 2]);
+      const int idx = ((cg >> 3) * 2 + ((cg >> 2) & 1)) * 64 + 16 * (cg & 3) + row;
+      a.image[idx] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+      a.image[idx + 8] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    }
+  }
+  if (a.a16) {
+    // The prompt GEMM's FP16 row (HalfRowsKernel's expressions).
+    if (tid == 0)
+      a.a_scale[row] = ldexpf(1.0f, -e);
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int cg = tid + kImageNormThreads * i;
+      if (cg >= groups)
+        continue;
+      unsigned h[4];
+#pragma unroll
+      for (int k = 0; k < 8; k += 2)
+        h[k / 2] = unsigned(ScaledHalf(v[i][k], e)) | (unsigned(ScaledHalf(v[i][k + 1], e)) << 16);
+      *reinterpret_cast<uint4*>(a.a16 + std::size_t(row) * a.lda + cg * 8) =
+          make_uint4(h[0], h[1], h[2], h[3]);
+    }
   }
 }
 
@@ -830,6 +850,26 @@ int lfm3_residual_norm_half(const float* branch, std::uint32_t parts,
       hidden > kNormThreads * kNormItems || lda < hidden || lda % 64 || !parts ||
       parts > kNormParts || (parts > 1 && part_stride < std::size_t(rows) * hidden))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 residual norm shape");
+  const auto aligned = [](const void* p) {
+    return (reinterpret_cast<std::uintptr_t>(p) & 15) == 0;
+  };
+  if (Chunks(hidden) * 8 <= 2 * kImageNormThreads && hidden % 32 == 0 && aligned(a16) &&
+      aligned(x) && aligned(z)) {
+    NormImageArgs a{};
+    a.branch = branch;
+    a.parts = int(parts);
+    a.part_stride = part_stride;
+    a.post = branch ? post_norm : nullptr;
+    a.x = x;
+    a.weight = norm;
+    a.z = z;
+    a.H = int(hidden);
+    a.eps = eps;
+    a.a16 = a16;
+    a.lda = int(lda);
+    a.a_scale = scale;
+    return LaunchNormImage(a, rows, static_cast<hipStream_t>(stream));
+  }
   ResidualNormKernel<<<rows, kNormThreads, 0, static_cast<hipStream_t>(stream)>>>(
       branch, int(parts), part_stride, branch ? post_norm : nullptr, x, norm, z,
       int(hidden), eps, nullptr, nullptr, a16, int(lda), scale);

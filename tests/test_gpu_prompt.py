@@ -38,7 +38,7 @@ def test_half_rows_bit_exact(n, K):
     assert np.array_equal(scale, np.ldexp(np.float32(1), -exps).astype(np.float32))
     want = O.float_to_half(np.ldexp(x, exps[:, None]).astype(np.float32))
     assert np.array_equal(a[:, :K], want)
-    assert not a[:, K:].any()
+    assert not a[:, K:(K + 63) // 64 * 64].any()  # the last chunk's zero tail
     # effective inputs match the oracle's
     got = np.ldexp(O.half_to_float(a[:, :K]), -exps[:, None])
     assert np.array_equal(got.astype(np.float32), inputs)
