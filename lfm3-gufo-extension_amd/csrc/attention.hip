@@ -46,43 +46,6 @@ __device__ __forceinline__ void WaveSync() {
   __builtin_amdgcn_wave_barrier();
 }
 
-// Cross-lane moves without the LDS crossbar: DPP within 16-lane rows
-// (quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror,
-// row_ror 8) and gfx950's permlane swaps across rows. Every lane of a
-// reduced group ends with the same value (the pairs add commutatively).
-template<int kCtrl>
-__device__ __forceinline__ float Dpp(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float GroupMax16(float v) {
-  v = fmaxf(v, Dpp<0xB1>(v));
-  v = fmaxf(v, Dpp<0x4E>(v));
-  v = fmaxf(v, Dpp<0x141>(v));
-  return fmaxf(v, Dpp<0x140>(v));
-}
-__device__ __forceinline__ float GroupSum16(float v) {
-  v += Dpp<0xB1>(v);
-  v += Dpp<0x4E>(v);
-  v += Dpp<0x141>(v);
-  return v + Dpp<0x140>(v);
-}
-// v of lane L plus v of lane L ^ 8 (within a row), L ^ 16, L ^ 32.
-__device__ __forceinline__ float SumXor8(float v) { return v + Dpp<0x128>(v); }
-// The row swaps as inline assembly: this compiler folds the sum of the two
-// results of __builtin_amdgcn_permlane{16,32}_swap(v, v) into twice the
-// first. Two wait states after the VALU writes of the operands.
-__device__ __forceinline__ float SumXor16(float v) {
-  unsigned a = __builtin_bit_cast(unsigned, v), b = a;
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
-}
-__device__ __forceinline__ float SumXor32(float v) {
-  unsigned a = __builtin_bit_cast(unsigned, v), b = a;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
-}
-
 __device__ __forceinline__ int ngroups_of(int kb, int ke) {
   return (ke - kb + kGroupKeys - 1) / kGroupKeys;
 }

@@ -119,32 +119,46 @@ GemvPlan PlanGemv(std::uint32_t rows, std::uint32_t cols, bool swiglu,
 // GemvEpilogue then writes the block's rows (SwiGLU: tile 2j is gate,
 // 2j + 1 up, rows j * 16 + n).
 template<int W, int RT>
+__device__ __forceinline__ void StoreWaveSums(f4 (&total)[RT], float* red);
+template<int W, int RT>
+__device__ __forceinline__ float SumOverWaves(const float* red, int r, int idx);
+
+template<int W, int RT>
 __device__ __forceinline__ float* ReduceWaves(f4 (&total)[RT], float* red) {
   constexpr int T = W * 64;
+  float* fin = red + W * RT * 128;
+  StoreWaveSums<W, RT>(total, red);
+  for (int o = threadIdx.x; o < RT * 128; o += T)
+    fin[o] = SumOverWaves<W, RT>(red, o / 128, o % 128);
+  __syncthreads();
+  return fin;
+}
+
+// Each lane's hi + lo sums go to red[(wave * RT + r) * 128 + tok * 16 + n]
+// (lanes L and L ^ 32 hold a token's hi and lo parts); after the block
+// barrier, SumOverWaves adds one output's W wave sums in wave order.
+template<int W, int RT>
+__device__ __forceinline__ void StoreWaveSums(f4 (&total)[RT], float* red) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tok0 = ((lane >> 4) & 1) * 4;
-  float* fin = red + W * RT * 128;
 #pragma unroll
   for (int r = 0; r < RT; ++r) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float val = total[r][i];
-      val += __shfl_xor(val, 32, 64);
+      const float val = SumXor32(total[r][i]);
       if (lane < 32)
         red[(wave * RT + r) * 128 + (tok0 + i) * 16 + (lane & 15)] = val;
     }
   }
   __syncthreads();
-  for (int o = tid; o < RT * 128; o += T) {
-    const int r = o / 128, idx = o % 128;
-    float sum = 0.0f;
+}
+template<int W, int RT>
+__device__ __forceinline__ float SumOverWaves(const float* red, int r, int idx) {
+  float sum = 0.0f;
 #pragma unroll
-    for (int w = 0; w < W; ++w)
-      sum += red[(w * RT + r) * 128 + idx];
-    fin[o] = sum;
-  }
-  __syncthreads();
-  return fin;
+  for (int w = 0; w < W; ++w)
+    sum += red[(w * RT + r) * 128 + idx];
+  return sum;
 }
 
 template<int W, int RT, bool kSwiGLU>
@@ -154,7 +168,7 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
                                              unsigned long long* keys = nullptr) {
   constexpr int T = W * 64;
   const int tid = threadIdx.x;
-  const float* fin = ReduceWaves<W, RT>(total, red);
+  StoreWaveSums<W, RT>(total, red);
   if (keys) {
     // Greedy candidates: token t's best ArgKey over the block's rows, one
     // (token, row) per lane, reduced over the token's lanes.
@@ -164,7 +178,7 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
       const int row = (group * RT + r) * kTileRows + n;
       unsigned long long key = 0;
       if (tid < 8 * R && row < rows_out)
-        key = ArgKey(fin[r * 128 + tok * 16 + n], unsigned(row));
+        key = ArgKey(SumOverWaves<W, RT>(red, r, tok * 16 + n), unsigned(row));
 #pragma unroll
       for (int m = R / 2; m; m >>= 1) {
         const unsigned long long other = __shfl_xor(key, m, 64);
@@ -176,8 +190,8 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
       unsigned long long best = 0;
       for (int i = 0; i < R; ++i) {
         const int row = (group * RT + i / kTileRows) * kTileRows + i % kTileRows;
-        const unsigned long long k =
-            ArgKey(fin[(i / kTileRows) * 128 + tid * 16 + i % kTileRows], unsigned(row));
+        const unsigned long long k = ArgKey(
+            SumOverWaves<W, RT>(red, i / kTileRows, tid * 16 + i % kTileRows), unsigned(row));
         best = row < rows_out && k > best ? k : best;
       }
       keys[std::size_t(tid) * gridDim.x + group] = best;
@@ -187,7 +201,8 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
     for (int o = tid; o < (RT / 2) * 128; o += T) {
       const int pr = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
       const int row = (group * (RT / 2) + pr) * kTileRows + n;
-      const float gv = fin[2 * pr * 128 + idx], uv = fin[(2 * pr + 1) * 128 + idx];
+      const float gv = SumOverWaves<W, RT>(red, 2 * pr, idx);
+      const float uv = SumOverWaves<W, RT>(red, 2 * pr + 1, idx);
       if (tok < B && row < rows_out)
         y[std::size_t(tok) * ldy + row] = (gv * (1.0f / (1.0f + expf(-gv)))) * uv;
     }
@@ -196,7 +211,8 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
       const int r = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
       const int row = (group * RT + r) * kTileRows + n;
       if (tok < B && row < rows_out)
-        (y_rows ? y_rows[tok] : y + std::size_t(tok) * ldy)[row] = fin[o];
+        (y_rows ? y_rows[tok] : y + std::size_t(tok) * ldy)[row] =
+            SumOverWaves<W, RT>(red, r, idx);
     }
   }
 }
