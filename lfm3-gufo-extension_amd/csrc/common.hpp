@@ -175,5 +175,18 @@ __device__ __forceinline__ float SumXor32(float v) {
   return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
 }
 
+// Maxima of v over lanes L, L ^ 8 (within a row), L ^ 16 and L ^ 32.
+__device__ __forceinline__ float MaxXor8(float v) { return fmaxf(v, Dpp<0x128>(v)); }
+__device__ __forceinline__ float MaxXor16(float v) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b = a;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+__device__ __forceinline__ float MaxXor32(float v) {
+  unsigned a = __builtin_bit_cast(unsigned, v), b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
 }  // namespace lfm3amd
 #endif

@@ -217,18 +217,19 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
   }
 }
 
-// y[b][r] = sum_k W[r][k] x[b][k] for b < B <= 8. A block stages a K slice
-// of x at a time in LDS as the MFMA A operand: per token a power of two
-// 2^e puts the slice maximum in [2^14, 2^15), hi = fp16(x 2^e) and
+// y[b][r] = sum_k W[r][k] x[b][k] for b < B <= 8. Each wave stages the x
+// columns of its own chunks (chunk wave + W j of a K slice) in LDS as the
+// MFMA A operand, with no block barrier: per token a power of two 2^e puts
+// the maximum over those columns in [2^14, 2^15), hi = fp16(x 2^e) and
 // lo = fp16((x 2^e - hi) 2^11), both truncated; A rows 0-7 are the tokens'
 // hi parts and rows 8-15 their lo parts, so hi + lo 2^-11 keeps about 21
-// bits of each value and every code x half product is exact in FP32. The B operand is
-// 16 weight rows of one Q8_0 block decoded exactly to fp16, so one MFMA
-// gives 16 rows' block dots and the block scale applies as
+// bits of each value and every code x half product is exact in FP32. The
+// B operand is 16 weight rows of one Q8_0 block decoded exactly to fp16,
+// so one MFMA gives 16 rows' block dots and the block scale applies as
 // acc = fma(d, dot, acc) in K order (hip/ops.hip:671-856: sums += scale *
-// block_dot). Weight loads of the next slice are issued before the current
-// slice is staged. Waves sum in wave order, so results do not depend on
-// scheduling.
+// block_dot); 2^-e applies to each wave's sums. Weight loads of the next
+// slice are issued before the current slice is staged. Waves sum in wave
+// order, so results do not depend on scheduling.
 template<int W, int SPW, int RT, bool kSwiGLU>
 __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(RT >= 2 ? 2 : 4)))
 __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
@@ -236,14 +237,13 @@ __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
                        int nchunks, int K, const float* __restrict__ x, int ldx,
                        int B, float* __restrict__ y, int ldy, int rows_out,
                        std::size_t part_stride) {
-  constexpr int T = W * 64, SLICE = W * SPW;
+  constexpr int SLICE = W * SPW;
   // SPW 4 plans cover a block's K range in one slice; SPW 5 plans loop over
   // slices and prefetch the next slice's weights.
   constexpr bool kMulti = SPW > 4;
-  __shared__ uint4 s_a[SLICE * 2 * 64];
-  __shared__ float s_max[W][8];
-  __shared__ int s_exp[8];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ uint4 s_a[W][SPW * 2 * 64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int group = blockIdx.x;
   // K part of this block (blockIdx.y of gridDim.y); part p writes its sums
   // to y + p * part_stride.
@@ -275,15 +275,15 @@ __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
       }
     }
   };
-  const int t = tid & 7;  // staging token of this thread
-  // x of one slice: unit tid + j T is token t, column group cg of eight.
+  // Staging lane layout: token t = L % 8, eight columns 8 (L / 8) .. + 7 of
+  // each of the wave's chunks.
+  const int t = lane & 7, g8 = lane >> 3;
   float v[SPW][8];
   const auto load_x = [&](int slice) {
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
-      const int cg = (tid + j * T) >> 3;
-      const int local = slice * SLICE + (cg >> 3);
-      const int k = (c_begin + local) * kChunk + (cg & 7) * 8;
+      const int local = slice * SLICE + wave + W * j;
+      const int k = (c_begin + local) * kChunk + g8 * 8;
       const unsigned off = t < B && local < nloc && k < K ? unsigned(t * ldx + k) * 4 : kOutOfRange;
       const float4 lo4 = LoadF4(x_res, off), hi4 = LoadF4(x_res, off + 16);
       v[j][0] = lo4.x; v[j][1] = lo4.y; v[j][2] = lo4.z; v[j][3] = lo4.w;
@@ -301,6 +301,7 @@ __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
   for (int r = 0; r < RT; ++r)
     total[r] = zero;
   const int part = lane >> 5, tok0 = ((lane >> 4) & 1) * 4;
+  uint4* s_own = s_a[wave];
 
   for (int slice = 0; slice < nslices; ++slice) {
     if constexpr (kMulti) {
@@ -308,6 +309,8 @@ __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
         load_x(slice);
       fetch(slice + 1, qn, scn);  // past the last slice: zeros, no traffic
     }
+    // Token t's maximum over the wave's columns: its 8 lanes (L ^ 8, ^ 16,
+    // ^ 32) reduce, then each lane reads the exponents of its A rows.
     float maximum = 0.0f;
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
@@ -315,50 +318,46 @@ __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
       for (int i = 0; i < 8; ++i)
         maximum = fmaxf(maximum, fabsf(v[j][i]));
     }
-    maximum = fmaxf(maximum, __shfl_xor(maximum, 8, 64));
-    maximum = fmaxf(maximum, __shfl_xor(maximum, 16, 64));
-    maximum = fmaxf(maximum, __shfl_xor(maximum, 32, 64));
-    if (slice)
-      __syncthreads();  // the previous slice's operands are in registers
-    if (lane < 8)
-      s_max[wave][lane] = maximum;
-    __syncthreads();
-    maximum = 0.0f;
+    maximum = MaxXor32(MaxXor16(MaxXor8(maximum)));
+    const int e = RowExponent(maximum);
+    int ex[4];
 #pragma unroll
-    for (int w = 0; w < W; ++w)
-      maximum = fmaxf(maximum, s_max[w][t]);
-    const int e = maximum > 0.0f ? 14 - ilogbf(maximum) : 0;
-    if (tid < 8)
-      s_exp[tid] = e;
+    for (int i = 0; i < 4; ++i) {
+      const int lo_tok = __builtin_amdgcn_readlane(e, i), hi_tok = __builtin_amdgcn_readlane(e, 4 + i);
+      ex[i] = -((tok0 ? hi_tok : lo_tok) + (part ? 11 : 0));
+    }
+    // A words of chunk j, block b = g8 / 4, lane group g8 % 4: row t (hi)
+    // and row 8 + t (lo), after the previous slice's reads.
+    if (slice) {
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    }
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
-      const int cg = (tid + j * T) >> 3;
       unsigned hw[4], lw[4];
 #pragma unroll
       for (int i = 0; i < 8; i += 2)
         SplitPair(v[j][i], v[j][i + 1], e, hw[i / 2], lw[i / 2]);
-      const int idx = ((cg >> 3) * 2 + ((cg >> 2) & 1)) * 64 + 16 * (cg & 3) + t;
-      s_a[idx] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-      s_a[idx + 8] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+      const int idx = (j * 2 + (g8 >> 2)) * 64 + 16 * (g8 & 3) + t;
+      s_own[idx] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      s_own[idx + 8] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     }
-    __syncthreads();
+    // The wave reads what its own lanes wrote: LDS keeps a wave's operations
+    // in order; the fence keeps the compiler's order too.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
     // This wave's chunks of the slice: one MFMA per Q8_0 block. Chunk
     // outer, tile inner, so one chunk's A operands are live at a time.
-    int ex[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      ex[i] = -(s_exp[tok0 + i] + (part ? 11 : 0));
     f4 acc[RT];
 #pragma unroll
     for (int r = 0; r < RT; ++r)
       acc[r] = zero;
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
-      const int c = wave + W * j;
-      if (slice * SLICE + c >= nloc)
+      if (slice * SLICE + wave + W * j >= nloc)
         continue;
-      const h8 a0 = __builtin_bit_cast(h8, s_a[(c * 2) * 64 + lane]);
-      const h8 a1 = __builtin_bit_cast(h8, s_a[(c * 2 + 1) * 64 + lane]);
+      const h8 a0 = __builtin_bit_cast(h8, s_own[(j * 2) * 64 + lane]);
+      const h8 a1 = __builtin_bit_cast(h8, s_own[(j * 2 + 1) * 64 + lane]);
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
         if (group * RT + r >= row_tiles)
