@@ -74,13 +74,15 @@ struct GemvPlan {
 };
 
 // Number of K parts a partial-sum launch of this shape takes: enough that
-// each part fits one LDS slice (32 chunks) and that about 512 blocks fill
-// the device, keeping at least 8 chunks a part.
+// each part fits one LDS slice (32 chunks), then doubled while the grid
+// stays within 256 blocks and parts keep 8 chunks (at 8 rows, 2048 x 2048
+// runs fastest in 2 parts and 2048 x 7680 in 4; fewer parts are also
+// fewer partial rows for the norm to read).
 constexpr int kMaxGemvParts = 8;
 int GemvParts(std::uint32_t rows, std::uint32_t cols) {
   const int tiles = int(RowTiles(rows)), nchunks = int(Chunks(cols));
   int parts = std::min((nchunks + 31) / 32, kMaxGemvParts);
-  while (parts * 2 <= kMaxGemvParts && tiles * parts * 2 <= 512 &&
+  while (parts * 2 <= kMaxGemvParts && tiles * parts * 2 <= 256 &&
          nchunks / (parts * 2) >= 8)
     parts *= 2;
   return parts;
