@@ -125,18 +125,6 @@ __device__ __forceinline__ unsigned long long ArgKey(float value, unsigned index
   return (static_cast<unsigned long long>(bits) << 32) | (0xffffffffu - index);
 }
 
-__device__ __forceinline__ float WaveSum(float v) {
-#pragma unroll
-  for (int m = 32; m; m >>= 1)
-    v += __shfl_xor(v, m, 64);
-  return v;
-}
-__device__ __forceinline__ float WaveMax(float v) {
-#pragma unroll
-  for (int m = 32; m; m >>= 1)
-    v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
-}
 
 // Cross-lane moves without the LDS crossbar: DPP within 16-lane rows
 // (quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror, row_mirror,
@@ -187,6 +175,11 @@ __device__ __forceinline__ float MaxXor32(float v) {
   asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
   return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
+
+// Wave-wide sum and maximum through DPP and the row swaps (no LDS
+// crossbar); every lane ends with the same value.
+__device__ __forceinline__ float WaveSum(float v) { return SumXor32(SumXor16(GroupSum16(v))); }
+__device__ __forceinline__ float WaveMax(float v) { return MaxXor32(MaxXor16(GroupMax16(v))); }
 
 }  // namespace lfm3amd
 #endif

@@ -265,12 +265,20 @@ __launch_bounds__(kImageNormThreads) __global__ void NormImageKernel(const NormI
   if (a.branch) {
 #pragma unroll
     for (int p = 0; p < kNormParts; ++p) {
-      const BufferResource b_res = MakeBuffer(a.branch + p * a.part_stride + std::size_t(row) * H,
-                                              p < a.parts ? row_bytes : 0u);
+      if (p < a.parts) {  // uniform: only the parts that exist are read
+        const BufferResource b_res =
+            MakeBuffer(a.branch + p * a.part_stride + std::size_t(row) * H, row_bytes);
 #pragma unroll
-      for (int i = 0; i < G; ++i) {
-        const int g = tid + kImageNormThreads * i;
-        load8(b_res, g * 8 < H ? unsigned(g) * 32 : kOutOfRange, b[p][i]);
+        for (int i = 0; i < G; ++i) {
+          const int g = tid + kImageNormThreads * i;
+          load8(b_res, g * 8 < H ? unsigned(g) * 32 : kOutOfRange, b[p][i]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < G; ++i)
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            b[p][i][k] = 0.0f;
       }
     }
     float squares = 0.0f;
