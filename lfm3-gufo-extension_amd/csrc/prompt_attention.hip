@@ -11,13 +11,16 @@
 // adds the rounded values, so the weights applied to V are exactly
 // normalized; out = (acc / sum) / (1 + e^-gate).
 //
-// A block of 8 waves owns one KV head's group of G query heads and 128
-// (query row, head) columns (128 / G rows x G heads); each wave owns 16
-// columns. K and V tiles of 64 keys are staged through LDS (double
-// buffered, the next tile prefetched into registers) and shared by the 8
-// waves. Each wave computes S^T = K Q^T (v_mfma_f32_16x16x32_f16: A = 16
-// keys x 32 dims, B = Q^T) and O^T += V^T P^T (A = 16 dims x 32 keys of the
-// transposed V tile, B = P^T). The K operand rows are permuted so that in
+// A block of 8 waves owns one KV head's group of G query heads and 128 CT
+// (query row, head) columns (128 CT / G rows x G heads); each wave owns CT
+// tiles of 16 columns (two for long histories, so each K and V operand read
+// from LDS feeds two MFMAs). K and V tiles of 64 keys are staged through
+// LDS (double buffered, the next tile prefetched into registers) and shared
+// by the 8 waves; the row blocks of one (span, KV head) run on one XCD, so
+// its K/V tiles come from HBM once and then from that XCD's L2. Each wave
+// computes S^T = K Q^T (v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims,
+// B = Q^T) and O^T += V^T P^T (A = 16 dims x 32 keys of the transposed V
+// tile, B = P^T). The K operand rows are permuted so that in
 // the S^T accumulator lane L holds exactly the 8 keys that the P^T operand
 // needs in lane L (keys 8 (L / 16) + j of a 32-key group): probabilities
 // never cross lanes. A column's softmax state is per lane; its row maximum
@@ -33,7 +36,6 @@ namespace lfm3amd {
 namespace {
 
 constexpr int kPAWaves = 8, kPAThreads = 64 * kPAWaves;
-constexpr int kPACols = 16 * kPAWaves;  // (row, head) columns a block
 constexpr int kPAKeys = 64;             // keys a tile
 constexpr int kMinPromptSpan = 2048, kMaxPromptSplits = 8;
 
@@ -66,16 +68,26 @@ __device__ __forceinline__ unsigned PackHalves(float a, float b) {
   return unsigned(FloatToHalfBits(a)) | (unsigned(FloatToHalfBits(b)) << 16);
 }
 
-template<int D, int G>
+// Block b of a launch over (row blocks, splits, KV heads): blocks are
+// dispatched to the 8 XCDs round robin, so the row blocks of one (split,
+// KV head), which read the same K/V tiles, are placed on one XCD's L2.
+__device__ __forceinline__ void PromptBlock(int b, int row_blocks, int& rb, int& pair) {
+  const int xcd = b % 8, i = b / 8;
+  rb = i % row_blocks;
+  pair = xcd + 8 * (i / row_blocks);
+}
+
+template<int D, int G, int CT>
 __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
     const float* __restrict__ q, int ldq, const Half* __restrict__ k,
     const Half* __restrict__ v, const float* __restrict__ gate, int ldg,
     const Half* __restrict__ ck, const Half* __restrict__ cv, float* __restrict__ out,
     int ldo, float* __restrict__ partial, int n, int heads, int kv_heads, int position,
-    int capacity, int window, int span) {
+    int capacity, int window, int span, int row_blocks, int splits) {
   static_assert(D == 64 || D == 128, "head dimension");
-  static_assert(kPACols % G == 0 && G >= 2 && G <= 8, "query group");
-  constexpr int kRows = kPACols / G;       // query rows a block
+  constexpr int kCols = 16 * CT * kPAWaves;  // (row, head) columns a block
+  static_assert(kCols % G == 0 && G >= 2 && G <= 8, "query group");
+  constexpr int kRows = kCols / G;         // query rows a block
   constexpr int kSegs = D / 8;             // 16-byte segments a key row
   constexpr int kSteps = D / 32;           // MFMA K steps over dimensions
   constexpr int kDimBlocks = D / 16;       // O^T accumulators
@@ -88,48 +100,67 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
-  const int g = blockIdx.z, split = blockIdx.y, q0 = blockIdx.x * kRows;
-  const int c = wave * 16 + col;
-  const int row = q0 + c / G, head = g * G + c % G;
-  const bool live = row < n;
+  int rb, pair;
+  PromptBlock(blockIdx.x, row_blocks, rb, pair);
+  // Past the last (split, KV head) pair: the grid rounds up to whole XCD
+  // rows of row blocks.
+  if (pair >= splits * kv_heads)
+    return;
+  const int g = pair / splits, split = pair % splits, q0 = rb * kRows;
   const int stride = kv_heads * D;
   k += g * D;
   v += g * D;
   ck += g * D;
   cv += g * D;
+  // Column tile ct of this wave: columns wave 16 CT + 16 ct + L % 16.
+  int row[CT], head[CT];
+  bool live[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const int c = (wave * CT + ct) * 16 + col;
+    row[ct] = q0 + c / G;
+    head[ct] = g * G + c % G;
+    live[ct] = row[ct] < n;
+  }
 
-  // Q^T operand: lane L holds dims 32 s + 8 (L / 16) + j of its column,
+  // Q^T operands: lane L holds dims 32 s + 8 (L / 16) + j of its column,
   // scaled in FP32 and rounded to F16.
   const float scale = rsqrtf(float(D)) * 1.44269504088896341f;
-  h8 qf[kSteps];
-  {
-    const float* qr = q + std::size_t(live ? row : 0) * ldq + head * D;
+  h8 qf[CT][kSteps];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const float* qr = q + std::size_t(live[ct] ? row[ct] : 0) * ldq + head[ct] * D;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
-      const float4 a = live ? *reinterpret_cast<const float4*>(qr + 32 * s + 8 * grp)
-                            : make_float4(0, 0, 0, 0);
-      const float4 b = live ? *reinterpret_cast<const float4*>(qr + 32 * s + 8 * grp + 4)
-                            : make_float4(0, 0, 0, 0);
+      const float4 a = live[ct] ? *reinterpret_cast<const float4*>(qr + 32 * s + 8 * grp)
+                                : make_float4(0, 0, 0, 0);
+      const float4 b = live[ct] ? *reinterpret_cast<const float4*>(qr + 32 * s + 8 * grp + 4)
+                                : make_float4(0, 0, 0, 0);
       const unsigned w[4] = {PackHalves(a.x * scale, a.y * scale),
                              PackHalves(a.z * scale, a.w * scale),
                              PackHalves(b.x * scale, b.y * scale),
                              PackHalves(b.z * scale, b.w * scale)};
-      qf[s] = __builtin_bit_cast(h8, w);
+      qf[ct][s] = __builtin_bit_cast(h8, w);
     }
   }
 
-  // Key ranges: the column's own, the block's, and the wave's (open = keys
+  // Key ranges: each column's own, the block's, and the wave's (open = keys
   // every column of the wave sees, where tiles skip the mask).
   const int span_first = split * span, span_last = span_first + span - 1;
   const auto first_key = [&](int query) {
     return max(window > 0 ? query + 1 - window : 0, span_first);
   };
-  const int lo = first_key(position + row), hi = min(position + row, span_last);
+  int lo[CT], hi[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    lo[ct] = first_key(position + row[ct]);
+    hi[ct] = min(position + row[ct], span_last);
+  }
   const int block_last_row = min(q0 + kRows, n) - 1;
   const int block_first = first_key(position + q0);
   const int block_last = min(position + block_last_row, span_last);
-  const int w_row0 = q0 + wave * 16 / G;
-  const int w_row1 = min(q0 + (wave * 16 + 15) / G, n - 1);
+  const int w_row0 = q0 + wave * 16 * CT / G;
+  const int w_row1 = min(q0 + (wave * 16 * CT + 16 * CT - 1) / G, n - 1);
   const bool wave_live = w_row0 < n;
   const int wave_first = first_key(position + w_row0);
   const int wave_last = min(position + w_row1, span_last);
@@ -180,87 +211,109 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
     }
   };
 
-  f4 acc[kDimBlocks];
+  f4 acc[CT][kDimBlocks];
+  float maximum[CT], sum[CT];
 #pragma unroll
-  for (int m = 0; m < kDimBlocks; ++m)
-    acc[m] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  float maximum = -INFINITY, sum = 0.0f;
+  for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+    for (int m = 0; m < kDimBlocks; ++m)
+      acc[ct][m] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    maximum[ct] = -INFINITY;
+    sum[ct] = 0.0f;
+  }
 
   const auto compute = [&](int st, int base) {
     const Half* tk = sK[st];
     const Half* tv = sV[st];
     // S^T block kb: A row r <-> key 32 (kb / 2) + 8 (r / 4) + 4 (kb % 2) + r % 4.
-    f4 s[4];
+    // Each K operand read feeds every column tile of the wave.
+    f4 s[CT][4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const int key = 32 * (kb >> 1) + 8 * (col >> 2) + 4 * (kb & 1) + (col & 3);
       const int swz = KeySwizzle<D>(key);
-      s[kb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+        s[ct][kb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int st2 = 0; st2 < kSteps; ++st2) {
         const int seg = 4 * st2 + grp;
         const h8 a = *reinterpret_cast<const h8*>(&tk[key * D + (seg ^ swz) * 8]);
-        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[st2], s[kb], 0, 0, 0);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+          s[ct][kb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ct][st2], s[ct][kb], 0, 0, 0);
       }
     }
     // Lane L's value i of block kb is key base + 32 (kb / 2) + 8 (L / 16) +
-    // 4 (kb % 2) + i of column L % 16.
-    float tile_max = -INFINITY;
-    if (base >= open_first && base + kPAKeys - 1 <= open_last) {
+    // 4 (kb % 2) + i of its column.
+    const bool open = base >= open_first && base + kPAKeys - 1 <= open_last;
+    h8 p[CT][2];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+    for (int ct = 0; ct < CT; ++ct) {
+      float tile_max = -INFINITY;
+      if (open) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          tile_max = fmaxf(tile_max, s[kb][i]);
-    } else {
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+          for (int i = 0; i < 4; ++i)
+            tile_max = fmaxf(tile_max, s[ct][kb][i]);
+      } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = base + 32 * (kb >> 1) + 8 * grp + 4 * (kb & 1) + i;
-          s[kb][i] = (t >= lo && t <= hi) ? s[kb][i] : -INFINITY;
-          tile_max = fmaxf(tile_max, s[kb][i]);
-        }
-    }
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 16, 64));
-    tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32, 64));
-    const float next = fmaxf(maximum, tile_max);
-    const float shift = next == -INFINITY ? 0.0f : next;
-    const float alpha = __builtin_amdgcn_exp2f(maximum - shift);
-    maximum = next;
-    // Probabilities round to F16 once; the sum adds the rounded values.
-    unsigned pw[4][2];
-    float local = 0.0f;
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const _Float16 a = static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][2 * j] - shift));
-        const _Float16 b =
-            static_cast<_Float16>(__builtin_amdgcn_exp2f(s[kb][2 * j + 1] - shift));
-        local += float(a) + float(b);
-        pw[kb][j] = unsigned(__builtin_bit_cast(Half, a)) |
-                    (unsigned(__builtin_bit_cast(Half, b)) << 16);
+          for (int i = 0; i < 4; ++i) {
+            const int t = base + 32 * (kb >> 1) + 8 * grp + 4 * (kb & 1) + i;
+            s[ct][kb][i] = (t >= lo[ct] && t <= hi[ct]) ? s[ct][kb][i] : -INFINITY;
+            tile_max = fmaxf(tile_max, s[ct][kb][i]);
+          }
       }
-    sum = sum * alpha + local;
-    // An unchanged maximum gives alpha == 1 exactly.
-    if (__ballot(alpha != 1.0f)) {
+      // The column's 4 lanes (L % 16 equal): L ^ 16 and L ^ 32.
+      tile_max = MaxXor32(MaxXor16(tile_max));
+      const float next = fmaxf(maximum[ct], tile_max);
+      const float shift = next == -INFINITY ? 0.0f : next;
+      const float alpha = __builtin_amdgcn_exp2f(maximum[ct] - shift);
+      maximum[ct] = next;
+      // Probabilities round to F16 once; the sum adds the rounded values.
+      unsigned pw[4][2];
+      float local = 0.0f;
 #pragma unroll
-      for (int m = 0; m < kDimBlocks; ++m)
-        acc[m] *= alpha;
-    }
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2) {
+        for (int j = 0; j < 2; ++j) {
+          const _Float16 a =
+              static_cast<_Float16>(__builtin_amdgcn_exp2f(s[ct][kb][2 * j] - shift));
+          const _Float16 b =
+              static_cast<_Float16>(__builtin_amdgcn_exp2f(s[ct][kb][2 * j + 1] - shift));
+          local += float(a) + float(b);
+          pw[kb][j] = unsigned(__builtin_bit_cast(Half, a)) |
+                      (unsigned(__builtin_bit_cast(Half, b)) << 16);
+        }
+      sum[ct] = sum[ct] * alpha + local;
+      // An unchanged maximum gives alpha == 1 exactly.
+      if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+        for (int m = 0; m < kDimBlocks; ++m)
+          acc[ct][m] *= alpha;
+      }
       // P^T operand: keys 32 c2 + 8 (L / 16) + j, j < 8, of column L % 16:
       // values 0..3 of block 2 c2 then of block 2 c2 + 1.
-      const unsigned w[4] = {pw[2 * c2][0], pw[2 * c2][1], pw[2 * c2 + 1][0],
-                             pw[2 * c2 + 1][1]};
-      const h8 p = __builtin_bit_cast(h8, w);
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        const unsigned w[4] = {pw[2 * c2][0], pw[2 * c2][1], pw[2 * c2 + 1][0],
+                               pw[2 * c2 + 1][1]};
+        p[ct][c2] = __builtin_bit_cast(h8, w);
+      }
+    }
+    // O^T += V^T P^T: each V operand read feeds every column tile.
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) {
 #pragma unroll
       for (int m = 0; m < kDimBlocks; ++m) {
         const h8 a = *reinterpret_cast<const h8*>(
             &tv[(16 * m + col) * kVPitch + 32 * c2 + 8 * grp]);
-        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, p, acc[m], 0, 0, 0);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+          acc[ct][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, p[ct][c2], acc[ct][m], 0, 0, 0);
       }
     }
   };
@@ -282,34 +335,36 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
     compute(st, base);
   }
 
-  float total = sum + __shfl_xor(sum, 16, 64);
-  total += __shfl_xor(total, 32, 64);
-  if (!live)
-    return;
-  // Lane L holds dimensions 16 m + 4 (L / 16) + i of its column.
-  if (partial) {
-    float* part = partial + ((std::size_t(split) * n + row) * heads + head) * (D + 2);
-    if (grp == 0) {
-      part[0] = maximum;
-      part[1] = total;
-    }
-    // Records are D + 2 floats: plain float stores (no 16-byte alignment).
 #pragma unroll
-    for (int m = 0; m < kDimBlocks; ++m)
+  for (int ct = 0; ct < CT; ++ct) {
+    const float total = SumXor32(SumXor16(sum[ct]));
+    if (!live[ct])
+      continue;
+    // Lane L holds dimensions 16 m + 4 (L / 16) + i of its column.
+    if (partial) {
+      float* part = partial + ((std::size_t(split) * n + row[ct]) * heads + head[ct]) * (D + 2);
+      if (grp == 0) {
+        part[0] = maximum[ct];
+        part[1] = total;
+      }
+      // Records are D + 2 floats: plain float stores (no 16-byte alignment).
+#pragma unroll
+      for (int m = 0; m < kDimBlocks; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          part[2 + 16 * m + 4 * grp + i] = acc[ct][m][i];
+      continue;
+    }
+    const float g_scale = 1.0f + expf(-gate[std::size_t(row[ct]) * ldg + head[ct]]);
+    float* o = out + std::size_t(row[ct]) * ldo + head[ct] * D;
+#pragma unroll
+    for (int m = 0; m < kDimBlocks; ++m) {
+      f4 r;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        part[2 + 16 * m + 4 * grp + i] = acc[m][i];
-    return;
-  }
-  const float g_scale = 1.0f + expf(-gate[std::size_t(row) * ldg + head]);
-  float* o = out + std::size_t(row) * ldo + head * D;
-#pragma unroll
-  for (int m = 0; m < kDimBlocks; ++m) {
-    f4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      r[i] = (acc[m][i] / total) / g_scale;
-    *reinterpret_cast<f4*>(o + 16 * m + 4 * grp) = r;
+        r[i] = (acc[ct][m][i] / total) / g_scale;
+      *reinterpret_cast<f4*>(o + 16 * m + 4 * grp) = r;
+    }
   }
 }
 
@@ -352,14 +407,27 @@ struct PromptArgs {
   int n, heads, kv_heads, position, capacity, window, span, splits;
 };
 
-template<int D, int G>
-void LaunchPrompt(const PromptArgs& a, hipStream_t s) {
-  constexpr int kRows = kPACols / G;
-  const dim3 grid((a.n + kRows - 1) / kRows, a.splits, a.kv_heads);
-  PromptAttentionKernel<D, G><<<grid, kPAThreads, 0, s>>>(
+template<int D, int G, int CT>
+void LaunchTiles(const PromptArgs& a, hipStream_t s) {
+  constexpr int kRows = 16 * CT * kPAWaves / G;
+  const int row_blocks = (a.n + kRows - 1) / kRows;
+  // 8 XCD slots of row_blocks blocks per group of 8 (split, KV head) pairs.
+  const int pairs = a.splits * a.kv_heads;
+  const int blocks = (pairs + 7) / 8 * 8 * row_blocks;
+  PromptAttentionKernel<D, G, CT><<<blocks, kPAThreads, 0, s>>>(
       a.q, a.ldq, a.k, a.v, a.gate, a.ldg, a.ck, a.cv, a.out, a.ldo,
       a.splits > 1 ? a.partial : nullptr, a.n, a.heads, a.kv_heads, a.position, a.capacity,
-      a.window, a.span);
+      a.window, a.span, row_blocks, a.splits);
+}
+
+// Long histories: two column tiles a wave (each K / V operand read feeds two
+// MFMAs); windows and short histories: one, for more blocks.
+template<int D, int G>
+void LaunchPrompt(const PromptArgs& a, hipStream_t s) {
+  if (a.window == 0 && a.position + a.n > 4096)
+    LaunchTiles<D, G, 2>(a, s);
+  else
+    LaunchTiles<D, G, 1>(a, s);
   if (a.splits > 1)
     CombineSpansKernel<D><<<a.n * a.heads, D, 0, s>>>(a.partial, a.gate, a.ldg, a.out, a.ldo,
                                                        a.n, a.heads, a.splits);
