@@ -127,18 +127,29 @@ __launch_bounds__(kHalfThreads) __global__
 }
 
 // Direct-to-LDS buffer loads (buffer_load_dword{,x4} ... lds): lane L's
-// bytes land at the wave-uniform LDS base + L * size. Reads outside the
-// resource's byte range return zero.
+// bytes land at the wave-uniform LDS base (M0) + L * size. Reads outside
+// the resource's byte range return zero. Issued as inline assembly: the
+// compiler's wait insertion cannot tell which stage a DMA load writes, and
+// for the builtin it waited on the loads of later stages before reading an
+// earlier one (vmcnt(0) every third chunk). The pipeline waits explicitly
+// instead. One wait state separates the M0 write from the load.
 typedef __attribute__((address_space(3))) void LdsVoid;
+__device__ __forceinline__ unsigned LdsAddress(void* p) {
+  return unsigned(reinterpret_cast<std::uintptr_t>((LdsVoid*)p));
+}
 __device__ __forceinline__ void BufferToLds16(BufferResource res, unsigned lane_offset,
                                               unsigned scalar_offset, void* lds_base) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(res, (LdsVoid*)lds_base, 16, lane_offset,
-                                           scalar_offset, 0, 0);
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(lane_offset), "s"(res), "s"(scalar_offset), "{m0}"(LdsAddress(lds_base))
+               : "memory");
 }
 __device__ __forceinline__ void BufferToLds4(BufferResource res, unsigned lane_offset,
                                              unsigned scalar_offset, void* lds_base) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(res, (LdsVoid*)lds_base, 4, lane_offset,
-                                           scalar_offset, 0, 0);
+  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds"
+               :
+               : "v"(lane_offset), "s"(res), "s"(scalar_offset), "{m0}"(LdsAddress(lds_base))
+               : "memory");
 }
 
 // s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt
