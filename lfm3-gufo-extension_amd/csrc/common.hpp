@@ -115,6 +115,10 @@ __device__ __forceinline__ float4 LoadF4(BufferResource res, unsigned offset) {
 __device__ __forceinline__ unsigned LoadB32(BufferResource res, unsigned offset) {
   return __builtin_amdgcn_raw_buffer_load_b32(res, offset, 0, 0);
 }
+// A store at kOutOfRange (or any offset past the resource) is dropped.
+__device__ __forceinline__ void StoreF32(BufferResource res, unsigned offset, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), res, offset, 0, 0);
+}
 
 // Greedy-pick order key: the float's bits made monotone as unsigned, then
 // the inverted index, so the largest key is the first index of the maximum

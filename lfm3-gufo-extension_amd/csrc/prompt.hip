@@ -25,15 +25,34 @@
 namespace lfm3amd {
 namespace {
 
-// Block shape: kGemmWR x kGemmWT waves; each wave owns kGemmRT weight
-// tiles (16 rows each) and 16 kGemmTT tokens, so a block covers 256 weight
-// rows and 128 tokens: 128 FLOP per staged byte (2 M N / (M + 2 N) for 1-
-// byte codes and 2-byte activations), about one block per CU for the
-// 512-token pass.
-constexpr int kGemmRT = 4, kGemmTT = 4, kGemmWR = 4, kGemmWT = 2, kGemmStages = 3;
-constexpr int kGemmWaves = kGemmWR * kGemmWT, kGemmThreads = 64 * kGemmWaves;
-constexpr int kGemmTiles = kGemmWR * kGemmRT;  // weight tiles a block
-constexpr int kGemmTokens = kGemmWT * kGemmTT * 16;
+// Block shapes: WR x WT waves; each wave owns kGemmRT weight tiles (16
+// rows each) and 16 kGemmTT tokens. The wide shape (4 x 2 waves) covers 256
+// weight rows and 128 tokens: 128 FLOP per staged byte (2 M N / (M + 2 N)
+// for 1-byte codes and 2-byte activations), about one block per CU for the
+// 512-token pass. The narrow shape (2 x 2 waves, 128 rows x 128 tokens)
+// does a quarter of that work a block and two blocks fit a CU: projections
+// with few output rows fill the 256 CUs with fewer K parts, and each part
+// costs a full FP32 output pass.
+constexpr int kGemmRT = 4, kGemmTT = 4, kGemmStages = 3;
+
+// A block shape and its pipeline stage: the block's activation rows for
+// one 64-column chunk (kTokens rows x 8 16-byte slots; slot j of row t
+// holds segment j ^ (t & 7), so the A reads of 8 consecutive rows hit
+// distinct banks), the block's weight tiles for the chunk (1 KB each, lane
+// order), and their scales (256 B per group of 4 tiles, row n's 4 tiles at
+// 16 n).
+template<int WR, int WT>
+struct GemmShape {
+  static constexpr int kWR = WR, kWT = WT;
+  static constexpr int kWaves = WR * WT, kThreads = 64 * kWaves;
+  static constexpr int kTiles = WR * kGemmRT;  // weight tiles a block
+  static constexpr int kTokens = WT * kGemmTT * 16;
+  static constexpr int kW = kTokens * 128;
+  static constexpr int kS = kW + kTiles * kTileCodeBytes;
+  static constexpr int kBytes = kS + kTiles * kTileScales * 2;
+};
+using WideShape = GemmShape<4, 2>;
+using NarrowShape = GemmShape<2, 2>;
 
 // One block per row: row maximum (scanned, or the maximum of max_blocks
 // partial maxima), then fp16(x 2^e) and the scale 2^-e. The vector form
@@ -164,17 +183,6 @@ __device__ __forceinline__ void BlockBarrier() {
   asm volatile("" ::: "memory");
 }
 
-// One pipeline stage: the block's activation rows for one 64-column chunk
-// (kGemmTokens rows x 8 16-byte slots; slot j of row t holds segment
-// j ^ (t & 7), so the A reads of 8 consecutive rows hit distinct banks),
-// the block's weight tiles for the chunk (1 KB each, lane order), and their
-// scales (256 B per group of 4 tiles, row n's 4 tiles at 16 n).
-struct GemmStage {
-  static constexpr int kW = kGemmTokens * 128;
-  static constexpr int kS = kW + kGemmTiles * kTileCodeBytes;
-  static constexpr int kBytes = kS + kGemmTiles * kTileScales * 2;
-};
-
 // Block b of a launch -> work item, XCD-major: blocks are dispatched to
 // the 8 XCDs round robin (b % 8), so XCD x gets the consecutive items
 // [first(x), first(x) + count(x)); items sharing weight rows are adjacent,
@@ -188,8 +196,8 @@ __device__ __forceinline__ int XcdMajorItem(int b, int blocks) {
 // it and the values stay in their registers.
 #define LFM3_PIN4(a) "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3])
 
-template<bool kSwiGLU>
-__launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2)))
+template<bool kSwiGLU, class Shape>
+__launch_bounds__(Shape::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
                              const Half* __restrict__ scales, int row_tiles,
                              int nchunks, const Half* __restrict__ a, int lda,
@@ -199,12 +207,12 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
                              std::size_t part_stride,
                              unsigned* __restrict__ row_max) {
   constexpr int RT = kGemmRT, TT = kGemmTT;
-  using Stage = GemmStage;
-  constexpr int A_LOADS = kGemmTokens * 8 / kGemmThreads;  // 16-byte loads a lane
-  constexpr int W_LOADS = kGemmTiles / kGemmWaves;         // tiles a wave loads
-  static_assert(A_LOADS * kGemmThreads == kGemmTokens * 8, "A loads cover the rows");
-  static_assert(W_LOADS * kGemmWaves == kGemmTiles, "W loads cover the tiles");
-  static_assert(RT == 4 && kGemmWR <= kGemmWaves, "scale groups of four tiles");
+  using Stage = Shape;
+  constexpr int A_LOADS = Shape::kTokens * 8 / Shape::kThreads;  // 16-byte loads a lane
+  constexpr int W_LOADS = Shape::kTiles / Shape::kWaves;         // tiles a wave loads
+  static_assert(A_LOADS * Shape::kThreads == Shape::kTokens * 8, "A loads cover the rows");
+  static_assert(W_LOADS * Shape::kWaves == Shape::kTiles, "W loads cover the tiles");
+  static_assert(RT == 4 && Shape::kWR <= Shape::kWaves, "scale groups of four tiles");
   // One array per stage (not one indexed by stage) lets the compiler see
   // that a stage's reads never alias the other stages' loads in flight.
   __shared__ __attribute__((aligned(16))) std::uint8_t s_st0[Stage::kBytes];
@@ -217,10 +225,10 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   const int part = item / (token_blocks * row_blocks);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = wave % kGemmWR, wt = wave / kGemmWR;
-  const int btile0 = rb * kGemmTiles;              // the block's first tile
+  const int wr = wave % Shape::kWR, wt = wave / Shape::kWR;
+  const int btile0 = rb * Shape::kTiles;              // the block's first tile
   const int tile0 = btile0 + wr * RT;              // this wave's first tile
-  const int tok0 = tb * kGemmTokens;               // the block's first token
+  const int tok0 = tb * Shape::kTokens;               // the block's first token
   const int c_begin = part * nchunks / parts, c_end = (part + 1) * nchunks / parts;
   y += std::size_t(part) * part_stride;
 
@@ -248,9 +256,9 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
     w_tile[j] = unsigned(min(btile0 + wave * W_LOADS + j, row_tiles - 1)) *
                 unsigned(nchunks * kTileCodeBytes);
   const unsigned w_off = unsigned(lane) * 16u;
-  // Scales: wave g < kGemmWR loads group g; lane L brings tile 4 g + L % 4's
+  // Scales: wave g < Shape::kWR loads group g; lane L brings tile 4 g + L % 4's
   // dword L / 4 (row L / 4's two block scales).
-  const bool loads_scales = wave < kGemmWR;
+  const bool loads_scales = wave < Shape::kWR;
   const unsigned s_off =
       unsigned(min(btile0 + wave * 4 + (lane & 3), row_tiles - 1)) *
           unsigned(nchunks * kTileScales * 2) +
@@ -399,30 +407,49 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   // D layout: lane L holds tokens 16 t + 4 (L / 16) + i of weight row L % 16.
   const int sub = lane & 15, quad = lane >> 4;
   const int wtok0 = tok0 + wt * TT * 16;
+  // The lane's token scales (0 past the last token), all loaded before the
+  // first store, and stores without branches (an output outside the
+  // matrix goes to an offset the hardware drops): loads and stores share
+  // one counter, and a load issued after stores, or a branch around them,
+  // makes the compiler wait for every store.
+  const BufferResource scale_res = MakeBuffer(a_scale, unsigned(n) * 4u);
+  const BufferResource y_res = MakeBuffer(y, unsigned(n) * unsigned(ldy) * 4u);
+  float s[TT][4];
+  unsigned token_off[TT][4];
+#pragma unroll
+  for (int t = 0; t < TT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int token = wtok0 + t * 16 + 4 * quad + i;
+      s[t][i] = __uint_as_float(LoadB32(scale_res, unsigned(token) * 4u));
+      token_off[t][i] = token < n ? unsigned(token) * unsigned(ldy) * 4u : kOutOfRange;
+    }
   if constexpr (kSwiGLU) {
     // Each token's max |y| over the block's rows (LDS), stored once per
     // (row block, token) for the down projection's FP16 conversion.
-    __shared__ unsigned s_max[kGemmTokens];
-    for (int i = tid; i < kGemmTokens; i += kGemmThreads)
+    __shared__ unsigned s_max[Shape::kTokens];
+    for (int i = tid; i < Shape::kTokens; i += Shape::kThreads)
       s_max[i] = 0;
     __syncthreads();
     // Tiles (2 j, 2 j + 1) are a (gate, up) pair for output rows j * 16 + n.
+    unsigned row_off[RT / 2];
+#pragma unroll
+    for (int pr = 0; pr < RT / 2; ++pr) {
+      const int row = (tile0 / 2 + pr) * kTileRows + sub;
+      row_off[pr] = row < rows_out ? unsigned(row) * 4u : kOutOfRange;
+    }
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int token = wtok0 + t * 16 + 4 * quad + i;
-        const float s = token < n ? a_scale[token] : 0.0f;
         float m = 0.0f;
 #pragma unroll
         for (int pr = 0; pr < RT / 2; ++pr) {
-          const int row = (tile0 / 2 + pr) * kTileRows + sub;
-          const float g = acc[2 * pr][t][i] * s, u = acc[2 * pr + 1][t][i] * s;
+          const float g = acc[2 * pr][t][i] * s[t][i], u = acc[2 * pr + 1][t][i] * s[t][i];
           const float value = (g * (1.0f / (1.0f + expf(-g)))) * u;
-          if (token < n && row < rows_out) {
-            y[std::size_t(token) * ldy + row] = value;
-            m = fmaxf(m, fabsf(value));
-          }
+          const bool inside = token_off[t][i] != kOutOfRange && row_off[pr] != kOutOfRange;
+          StoreF32(y_res, inside ? token_off[t][i] + row_off[pr] : kOutOfRange, value);
+          m = inside ? fmaxf(m, fabsf(value)) : m;
         }
         m = fmaxf(m, __shfl_xor(m, 8, 64));
         m = fmaxf(m, __shfl_xor(m, 4, 64));
@@ -434,26 +461,27 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
     }
     __syncthreads();
     if (row_max)
-      for (int i = tid; i < kGemmTokens; i += kGemmThreads)
+      for (int i = tid; i < Shape::kTokens; i += Shape::kThreads)
         if (tok0 + i < n)
           row_max[std::size_t(rb) * n + tok0 + i] = s_max[i];
   } else {
+    unsigned row_off[RT];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int token = wtok0 + t * 16 + 4 * quad + i;
-        if (token >= n)
-          continue;
-        const float s = a_scale[token];
-#pragma unroll
-        for (int r = 0; r < RT; ++r) {
-          const int row = (tile0 + r) * kTileRows + sub;
-          if (row < rows_out)
-            y[std::size_t(token) * ldy + row] = acc[r][t][i] * s;
-        }
-      }
+    for (int r = 0; r < RT; ++r) {
+      const int row = (tile0 + r) * kTileRows + sub;
+      row_off[r] = row < rows_out ? unsigned(row) * 4u : kOutOfRange;
     }
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+          StoreF32(y_res,
+                   token_off[t][i] != kOutOfRange && row_off[r] != kOutOfRange
+                       ? token_off[t][i] + row_off[r]
+                       : kOutOfRange,
+                   acc[r][t][i] * s[t][i]);
   }
 }
 
@@ -472,33 +500,52 @@ __global__ void SumPartsKernel(float* __restrict__ y, std::size_t part_stride, i
   p[0] = sum;
 }
 
-// K parts for a prompt GEMM: double while the blocks still fit one round
-// on the 256 CUs (one block each, with a quarter over), keeping at least 4
-// chunks a part, at most 8 parts. Each part costs its consumer one more
-// FP32 output pass.
-int PromptParts(int row_blocks, int token_blocks, int nchunks) {
+// Blocks of one K part of a projection in the given shape.
+template<class Shape>
+int ShapeBlocks(int row_tiles, int tokens) {
+  return (row_tiles + Shape::kTiles - 1) / Shape::kTiles *
+         ((tokens + Shape::kTokens - 1) / Shape::kTokens);
+}
+
+// The block shape of a projection: wide when its blocks alone fill most of
+// the 256 CUs, narrow (two blocks a CU) otherwise.
+bool NarrowGemm(int row_tiles, int tokens) {
+  return ShapeBlocks<WideShape>(row_tiles, tokens) < 192;
+}
+
+// K parts for a prompt GEMM: double while the blocks stay within 320
+// (wide shape: one round on the 256 CUs with a quarter over) or 384
+// (narrow shape) and each part keeps at least 4 chunks, at most 8 parts.
+// Each part costs its consumer one more FP32 output pass; on the model's
+// 512-token projections these limits give the fastest GEMM plus part
+// reads (2048 x 2048: 4 parts; 6144 x 2048: 2; 2048 x 7680: 4).
+int PromptParts(int row_tiles, int tokens, int nchunks) {
+  const bool narrow = NarrowGemm(row_tiles, tokens);
+  const int blocks = narrow ? ShapeBlocks<NarrowShape>(row_tiles, tokens)
+                            : ShapeBlocks<WideShape>(row_tiles, tokens);
+  const int limit = narrow ? 384 : 320;
   int parts = 1;
-  while (parts < 8 && row_blocks * token_blocks * parts * 2 <= 320 &&
-         nchunks / (parts * 2) >= 4)
+  while (parts < 8 && blocks * parts * 2 <= limit && nchunks / (parts * 2) >= 4)
     parts *= 2;
   return parts;
 }
 
-// The kernel addresses codes, scales and activations with 32-bit buffer
-// offsets.
+// The kernel addresses codes, scales, activations and each output part
+// with 32-bit buffer offsets.
 bool GemmOperandsFit(std::uint64_t row_tiles, std::uint64_t nchunks, std::uint64_t tokens,
-                     std::uint64_t lda) {
-  return row_tiles * nchunks * kTileCodeBytes < (1ull << 31) && tokens * lda * 2 < (1ull << 31);
+                     std::uint64_t lda, std::uint64_t ldy) {
+  return row_tiles * nchunks * kTileCodeBytes < (1ull << 31) &&
+         tokens * lda * 2 < (1ull << 31) && tokens * ldy * 4 < (1ull << 31);
 }
 
-template<bool kSwiGLU>
+template<bool kSwiGLU, class Shape>
 void LaunchGemm(const void* codes, const void* scales, int row_tiles, int nchunks,
                 const std::uint16_t* a, std::uint32_t lda, const float* a_scale,
                 std::uint32_t tokens, float* y, std::uint32_t ldy, std::uint32_t rows,
                 int parts, std::size_t part_stride, unsigned* row_max, hipStream_t stream) {
-  const int row_blocks = (row_tiles + kGemmTiles - 1) / kGemmTiles;
-  const int token_blocks = (int(tokens) + kGemmTokens - 1) / kGemmTokens;
-  Q8GemmKernel<kSwiGLU><<<row_blocks * token_blocks * parts, kGemmThreads, 0, stream>>>(
+  const int row_blocks = (row_tiles + Shape::kTiles - 1) / Shape::kTiles;
+  const int token_blocks = (int(tokens) + Shape::kTokens - 1) / Shape::kTokens;
+  Q8GemmKernel<kSwiGLU, Shape><<<row_blocks * token_blocks * parts, Shape::kThreads, 0, stream>>>(
       static_cast<const std::uint8_t*>(codes), static_cast<const Half*>(scales), row_tiles,
       nchunks, reinterpret_cast<const Half*>(a), int(lda), a_scale, int(tokens), y, int(ldy),
       int(rows), row_blocks, token_blocks, parts, part_stride, row_max);
@@ -537,16 +584,14 @@ int lfm3_half_rows(const float* x, std::uint32_t ldx, const unsigned* row_max,
 }
 
 std::uint32_t lfm3_q8_gemm_swiglu_max_blocks(std::uint32_t rows) {
-  return (2 * RowTiles(rows) + kGemmTiles - 1) / kGemmTiles;
+  return (2 * RowTiles(rows) + WideShape::kTiles - 1) / WideShape::kTiles;
 }
 
 std::uint32_t lfm3_q8_gemm_parts(std::uint32_t rows, std::uint32_t cols,
                                  std::uint32_t tokens, int swiglu) {
   if (!rows || !cols || !tokens || swiglu)
     return 1;
-  const int row_blocks = (int(RowTiles(rows)) + kGemmTiles - 1) / kGemmTiles;
-  const int token_blocks = (int(tokens) + kGemmTokens - 1) / kGemmTokens;
-  return std::uint32_t(PromptParts(row_blocks, token_blocks, int(Chunks(cols))));
+  return std::uint32_t(PromptParts(int(RowTiles(rows)), int(tokens), int(Chunks(cols))));
 }
 
 int lfm3_q8_gemm(const void* codes, const void* scales, std::uint32_t rows,
@@ -557,11 +602,13 @@ int lfm3_q8_gemm(const void* codes, const void* scales, std::uint32_t rows,
       cols % 32 || !tokens || lda % 64 || lda < Chunks(cols) * kChunk ||
       ldy < rows || !parts || parts > 8 || parts > Chunks(cols) ||
       (reinterpret_cast<std::uintptr_t>(a) & 15) ||
-      !GemmOperandsFit(RowTiles(rows), Chunks(cols), tokens, lda))
+      !GemmOperandsFit(RowTiles(rows), Chunks(cols), tokens, lda, ldy))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 prompt GEMM shape");
-  LaunchGemm<false>(codes, scales, int(RowTiles(rows)), int(Chunks(cols)), a, lda, a_scale,
-                    tokens, y, ldy, rows, int(parts), std::size_t(ldy) * tokens, nullptr,
-                    static_cast<hipStream_t>(stream));
+  const auto launch = NarrowGemm(int(RowTiles(rows)), int(tokens))
+                          ? LaunchGemm<false, NarrowShape>
+                          : LaunchGemm<false, WideShape>;
+  launch(codes, scales, int(RowTiles(rows)), int(Chunks(cols)), a, lda, a_scale, tokens, y, ldy,
+         rows, int(parts), std::size_t(ldy) * tokens, nullptr, static_cast<hipStream_t>(stream));
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 prompt GEMM launch");
 }
 
@@ -585,9 +632,9 @@ int lfm3_q8_gemm_swiglu(const void* codes, const void* scales,
   if (!codes || !scales || !a || !a_scale || !y || !rows || !cols ||
       cols % 32 || !tokens || lda % 64 || lda < Chunks(cols) * kChunk ||
       ldy < rows || (reinterpret_cast<std::uintptr_t>(a) & 15) ||
-      !GemmOperandsFit(2 * RowTiles(rows), Chunks(cols), tokens, lda))
+      !GemmOperandsFit(2 * RowTiles(rows), Chunks(cols), tokens, lda, ldy))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 prompt SwiGLU shape");
-  LaunchGemm<true>(codes, scales, int(2 * RowTiles(rows)), int(Chunks(cols)), a, lda,
+  LaunchGemm<true, WideShape>(codes, scales, int(2 * RowTiles(rows)), int(Chunks(cols)), a, lda,
                    a_scale, tokens, y, ldy, rows, 1, 0, row_max,
                    static_cast<hipStream_t>(stream));
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 prompt SwiGLU launch");

@@ -84,8 +84,11 @@ def test_gemm_reference_projection_vectors(n):
 
 @pytest.mark.parametrize("M,K,n,parts", [(2048, 2048, 512, None), (3088, 2048, 512, 1),
                                          (6144, 2048, 130, None), (2048, 7680, 512, None),
-                                         (2048, 7680, 64, 3), (48, 96, 17, 2)])
+                                         (2048, 7680, 64, 3), (48, 96, 17, 2),
+                                         (12288, 256, 512, None), (12288, 256, 500, 2)])
 def test_gemm_model_shapes(M, K, n, parts):
+    """Model projections (128-row blocks) and a tall matrix whose 256-row
+    blocks fill the CUs (12288 rows x 500 or 512 tokens: the wide block shape)."""
     w = L.q8(SEED, f"pg.{M}.{K}", M, K)
     x = L.normal(SEED, f"pg.x.{M}.{K}.{n}", n * K).reshape(n, K)
     y = gemm(DeviceMatrix(w, M, K), x, parts)
