@@ -73,10 +73,15 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
   __shared__ float s_alpha[NW][G];
   __shared__ __attribute__((aligned(16))) float s_acc[NW][G][D];
   __shared__ float s_m[NW][G], s_l[NW][G];
+  __shared__ float s_gate[G];
 
   const lfm3_attention_item item = items[blockIdx.x];
   const int g = blockIdx.y, row = int(item.row);
   const int tid = threadIdx.x, lane = tid & 63;
+  // The output gate's divisor, loaded before any store (a load after
+  // stores waits for them) and read from LDS by the epilogue.
+  if (item.parts == 1 && tid < G)
+    s_gate[tid] = 1.0f + expf(-gate[std::size_t(row) * ldg + g * G + tid]);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int stride = kv_heads * D;
   const std::uint32_t cap = capacity[row];
@@ -122,10 +127,18 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
     for (int d = tid; d < D; d += (NW * 64))
       s_kv[1][d] = FloatToHalfBits(v[std::size_t(row) * ld + g * D + d]);
     __syncthreads();
-    if (ke == pos + 1 && tid < D) {  // this span holds the current position
-      const std::size_t at = std::size_t(std::uint32_t(pos) % cap) * stride + g * D + tid;
-      ck[at] = s_kv[0][tid];
-      cv[at] = s_kv[1][tid];
+    if (ke == pos + 1) {  // this span holds the current position
+      // The row goes to the ring and has landed (the store counter at
+      // zero) before any wave of the block reads it back with the other
+      // keys; the block's waves share the CU's L1, and stores write
+      // through it.
+      if (tid < D) {
+        const std::size_t at = std::size_t(std::uint32_t(pos) % cap) * stride + g * D + tid;
+        ck[at] = s_kv[0][tid];
+        cv[at] = s_kv[1][tid];
+      }
+      __builtin_amdgcn_s_waitcnt(WaitVm(0));
+      __syncthreads();
     }
   } else {
     for (int e = tid; e < G * D; e += (NW * 64))
@@ -202,18 +215,6 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
   for (int j = wave; j < ngroups; j += NW) {
     const int base = kb + kGroupKeys * j;
     fetch(j + NW, kn, vn);  // past the span: zeros, no traffic
-    if constexpr (kFused) {
-      // The current key and value come from LDS, never from the ring.
-      if (base + n == pos) {
-#pragma unroll
-        for (int s2 = 0; s2 < S; ++s2)
-          kr[s2] = *reinterpret_cast<const uint4*>(&s_kv[0][32 * s2 + 8 * kg]);
-      }
-#pragma unroll
-      for (int i = 0; i < KPL; ++i)
-        if (base + kq + KG * i == pos)
-          vr[i] = *reinterpret_cast<const uint4*>(&s_kv[1][8 * dg]);
-    }
     f4 sacc = zero;
 #pragma unroll
     for (int s2 = 0; s2 < S; ++s2)
@@ -324,8 +325,7 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
     }
     const int head = g * G + h;
     if (!split) {
-      out[std::size_t(row) * ldo + head * D + d] =
-          (av / l) / (1.0f + expf(-gate[std::size_t(row) * ldg + head]));
+      out[std::size_t(row) * ldo + head * D + d] = (av / l) / s_gate[h];
     } else {
       float* po = part_out + h * (D + 2);
       if (d == 0) {
@@ -349,12 +349,14 @@ __launch_bounds__(kAttnThreads) __global__
                        const float* __restrict__ partial) {
   __shared__ float s_w[kMaxParts][G];
   __shared__ float s_lv[kMaxParts][G];
-  __shared__ float s_top[G], s_den[G];
+  __shared__ float s_top[G], s_den[G], s_gate[G];
   const lfm3_attention_item item = items[blockIdx.x];
   if (item.parts < 2 || item.first_item != blockIdx.x)
     return;
   const int g = blockIdx.y, row = int(item.row), parts = int(item.parts);
   const int tid = threadIdx.x;
+  if (tid < G)  // loaded before the stores, read from LDS
+    s_gate[tid] = 1.0f + expf(-gate[std::size_t(row) * ldg + g * G + tid]);
   const std::size_t span_stride = std::size_t(kv_heads) * G * (D + 2);
   const float* base = partial + (std::size_t(item.first_item) * kv_heads + g) * G * (D + 2);
   for (int e = tid; e < parts * G; e += kAttnThreads) {
@@ -383,16 +385,29 @@ __launch_bounds__(kAttnThreads) __global__
     s_den[tid] = den;
   }
   __syncthreads();
-  for (int e = tid; e < G * D; e += kAttnThreads) {
-    const int h = e / D, d = e % D;
-    const float* po = base + h * (D + 2) + 2 + d;
-    float av = 0.0f;
+  // Every element's sum first, then the stores: a load issued after a
+  // store waits for it.
+  constexpr int EPT = (G * D + kAttnThreads - 1) / kAttnThreads;
+  float av[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = tid + kAttnThreads * j;
+    av[j] = 0.0f;
+    if (e < G * D) {
+      const int h = e / D, d = e % D;
+      const float* po = base + h * (D + 2) + 2 + d;
 #pragma unroll 8
-    for (int s = 0; s < parts; ++s)
-      av = fmaf(po[s * span_stride], s_w[s][h], av);
-    const int head = g * G + h;
-    out[std::size_t(row) * ldo + head * D + d] =
-        (av / s_den[h]) / (1.0f + expf(-gate[std::size_t(row) * ldg + head]));
+      for (int s = 0; s < parts; ++s)
+        av[j] = fmaf(po[s * span_stride], s_w[s][h], av[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = tid + kAttnThreads * j;
+    if (e < G * D) {
+      const int h = e / D, d = e % D;
+      out[std::size_t(row) * ldo + (g * G + h) * D + d] = (av[j] / s_den[h]) / s_gate[h];
+    }
   }
 }
 

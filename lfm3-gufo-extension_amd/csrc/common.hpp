@@ -115,9 +115,40 @@ __device__ __forceinline__ float4 LoadF4(BufferResource res, unsigned offset) {
 __device__ __forceinline__ unsigned LoadB32(BufferResource res, unsigned offset) {
   return __builtin_amdgcn_raw_buffer_load_b32(res, offset, 0, 0);
 }
+// s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt
+// 11:8), issued through the builtin so the compiler's own wait insertion
+// sees them.
+constexpr int WaitVm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kWaitLgkm0 = 15 | (3 << 14) | (7 << 4);
+
+// Per-component select (a select of whole vectors in a register array can
+// become a select of addresses into scratch memory).
+__device__ __forceinline__ uint4 SelectU4(bool p, uint4 a, uint4 b) {
+  return make_uint4(p ? a.x : b.x, p ? a.y : b.y, p ? a.z : b.z, p ? a.w : b.w);
+}
+
 // A store at kOutOfRange (or any offset past the resource) is dropped.
 __device__ __forceinline__ void StoreF32(BufferResource res, unsigned offset, float v) {
   __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), res, offset, 0, 0);
+}
+__device__ __forceinline__ void StoreB32(BufferResource res, unsigned offset, unsigned v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, res, offset, 0, 0);
+}
+__device__ __forceinline__ void StoreB64(BufferResource res, unsigned offset, uint2 v) {
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  const u2 w = {v.x, v.y};
+  __builtin_amdgcn_raw_buffer_store_b64(w, res, offset, 0, 0);
+}
+__device__ __forceinline__ void StoreB128(BufferResource res, unsigned offset, uint4 v) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  const u4 w = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(w, res, offset, 0, 0);
+}
+__device__ __forceinline__ void StoreF4(BufferResource res, unsigned offset, float a, float b,
+                                        float c, float d) {
+  StoreB128(res, offset,
+            make_uint4(__float_as_uint(a), __float_as_uint(b), __float_as_uint(c),
+                       __float_as_uint(d)));
 }
 
 // Greedy-pick order key: the float's bits made monotone as unsigned, then

@@ -95,12 +95,16 @@ __launch_bounds__(kHalfThreads) __global__
     const int per = gridDim.y == 1 ? K / 4 : kHalfThreads * kHalfVec / kHalfSplit;
     const int v0 = blockIdx.y * per;
     const int nv = min(K / 4, v0 + per);
-    const float4* src4 = reinterpret_cast<const float4*>(src);
+    // Loads and stores through buffer resources, without branches (a
+    // branch around a store makes the compiler wait for the stores before
+    // the next one).
+    const BufferResource src_res = MakeBuffer(src, unsigned(K) * 4u);
+    const BufferResource dst_res = MakeBuffer(dst, unsigned((K + kChunk - 1) / kChunk * kChunk) * 2u);
     float4 v[kHalfVec];
 #pragma unroll
     for (int j = 0; j < kHalfVec; ++j) {
       const int i = v0 + tid + kHalfThreads * j;
-      v[j] = i < nv ? src4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      v[j] = LoadF4(src_res, i < nv ? unsigned(i) * 16u : kOutOfRange);
     }
     float maximum;
     if (row_max) {
@@ -116,17 +120,16 @@ __launch_bounds__(kHalfThreads) __global__
     const int e = RowExponent(maximum);
     if (tid == 0 && blockIdx.y == 0)
       scale[row] = ldexpf(1.0f, -e);
-    uint2* dst2 = reinterpret_cast<uint2*>(dst);
 #pragma unroll
     for (int j = 0; j < kHalfVec; ++j) {
       const int i = v0 + tid + kHalfThreads * j;
-      if (i < nv)
-        dst2[i] = make_uint2(unsigned(ScaledHalf(v[j].x, e)) | (unsigned(ScaledHalf(v[j].y, e)) << 16),
-                             unsigned(ScaledHalf(v[j].z, e)) | (unsigned(ScaledHalf(v[j].w, e)) << 16));
+      StoreB64(dst_res, i < nv ? unsigned(i) * 8u : kOutOfRange,
+               make_uint2(unsigned(ScaledHalf(v[j].x, e)) | (unsigned(ScaledHalf(v[j].y, e)) << 16),
+                          unsigned(ScaledHalf(v[j].z, e)) | (unsigned(ScaledHalf(v[j].w, e)) << 16)));
     }
     if (blockIdx.y + 1 == gridDim.y)  // the zero tail of the last chunk
       for (int i = K / 4 + tid; i < (K + kChunk - 1) / kChunk * (kChunk / 4); i += kHalfThreads)
-        dst2[i] = make_uint2(0u, 0u);
+        StoreB64(dst_res, unsigned(i) * 8u, make_uint2(0u, 0u));
   } else {
     float maximum;
     if (row_max) {
@@ -171,11 +174,6 @@ __device__ __forceinline__ void BufferToLds4(BufferResource res, unsigned lane_o
                : "memory");
 }
 
-// s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt
-// 11:8). Issued through the builtin so the compiler's own wait insertion
-// sees them.
-constexpr int WaitVm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-constexpr int kWaitLgkm0 = 15 | (3 << 14) | (7 << 4);
 
 __device__ __forceinline__ void BlockBarrier() {
   asm volatile("" ::: "memory");

@@ -122,6 +122,14 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
     head[ct] = g * G + c % G;
     live[ct] = row[ct] < n;
   }
+  // The output gate's divisor, loaded with the queries: a load after the
+  // output stores would wait for them.
+  float g_scale[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+    g_scale[ct] = partial || !live[ct]
+                      ? 1.0f
+                      : 1.0f + expf(-gate[std::size_t(row[ct]) * ldg + head[ct]]);
 
   // Q^T operands: lane L holds dims 32 s + 8 (L / 16) + j of its column,
   // scaled in FP32 and rounded to F16.
@@ -355,14 +363,13 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
           part[2 + 16 * m + 4 * grp + i] = acc[ct][m][i];
       continue;
     }
-    const float g_scale = 1.0f + expf(-gate[std::size_t(row[ct]) * ldg + head[ct]]);
     float* o = out + std::size_t(row[ct]) * ldo + head[ct] * D;
 #pragma unroll
     for (int m = 0; m < kDimBlocks; ++m) {
       f4 r;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        r[i] = (acc[ct][m][i] / total) / g_scale;
+        r[i] = (acc[ct][m][i] / total) / g_scale[ct];
       *reinterpret_cast<f4*>(o + 16 * m + 4 * grp) = r;
     }
   }

@@ -170,6 +170,15 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
                                              unsigned long long* keys = nullptr) {
   constexpr int T = W * 64;
   const int tid = threadIdx.x;
+  // With T a multiple of 128 a thread stores one token's outputs; its row
+  // pointer is loaded before the reductions, so the load's latency hides
+  // behind them and it does not wait for the keys store.
+  float* yrow = nullptr;
+  if constexpr (!kSwiGLU && T % 128 == 0) {
+    const int tok = (tid % 128) / 16;
+    if (y_rows && tok < B)
+      yrow = y_rows[tok];
+  }
   StoreWaveSums<W, RT>(total, red);
   if (keys) {
     // Greedy candidates: token t's best ArgKey over the block's rows, one
@@ -213,7 +222,7 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
       const int r = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
       const int row = (group * RT + r) * kTileRows + n;
       if (tok < B && row < rows_out)
-        (y_rows ? y_rows[tok] : y + std::size_t(tok) * ldy)[row] =
+        (y_rows ? (T % 128 == 0 ? yrow : y_rows[tok]) : y + std::size_t(tok) * ldy)[row] =
             SumOverWaves<W, RT>(red, r, idx);
     }
   }

@@ -214,6 +214,9 @@ __launch_bounds__(kImageNormThreads) __global__ void NormImageKernel(const NormI
     out[0] = lo.x; out[1] = lo.y; out[2] = lo.z; out[3] = lo.w;
     out[4] = hi.x; out[5] = hi.y; out[6] = hi.z; out[7] = hi.w;
   };
+  // Every load is issued before the first store: loads and stores share
+  // one counter, so a load after stores would wait for all of them.
+  float* const zrow = a.z_rows ? a.z_rows[row] : a.z ? a.z + std::size_t(row) * H : nullptr;
   // The round's first norm gathers its rows from the tiled embedding table
   // (EmbedKernel's layout: columns 8G..8G+7 of row r are 8 consecutive code
   // bytes of one lane word) and writes them to x.
@@ -251,17 +254,6 @@ __launch_bounds__(kImageNormThreads) __global__ void NormImageKernel(const NormI
     load8(w_res, off, nw[i]);
     load8(p_res, off, pw[i]);
   }
-  if (a.tokens) {
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const int g = tid + kImageNormThreads * i;
-      if (g * 8 < H) {
-        float4* xr = reinterpret_cast<float4*>(x + std::size_t(row) * H + g * 8);
-        xr[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
-        xr[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
-      }
-    }
-  }
   if (a.branch) {
 #pragma unroll
     for (int p = 0; p < kNormParts; ++p) {
@@ -281,6 +273,27 @@ __launch_bounds__(kImageNormThreads) __global__ void NormImageKernel(const NormI
             b[p][i][k] = 0.0f;
       }
     }
+  }
+  // Every load has landed before the first store, on every path: stores
+  // and loads share one counter, and a wait the compiler places after a
+  // store (for a load still in flight on another path) drains the stores.
+  __builtin_amdgcn_s_waitcnt(WaitVm(0));
+  // Stores go through buffer resources at offsets that are dropped past
+  // the row, without branches: the compiler's waits after a branch around
+  // a store drain every store in flight.
+  const BufferResource x_out = MakeBuffer(x + std::size_t(row) * H, row_bytes);
+  const auto store8 = [](BufferResource r, unsigned off, const float* in) {
+    StoreF4(r, off, in[0], in[1], in[2], in[3]);
+    StoreF4(r, off + 16, in[4], in[5], in[6], in[7]);
+  };
+  if (a.tokens) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int g = tid + kImageNormThreads * i;
+      store8(x_out, g * 8 < H ? unsigned(g) * 32 : kOutOfRange, v[i]);
+    }
+  }
+  if (a.branch) {
     float squares = 0.0f;
 #pragma unroll
     for (int i = 0; i < G; ++i)
@@ -306,11 +319,7 @@ __launch_bounds__(kImageNormThreads) __global__ void NormImageKernel(const NormI
 #pragma unroll
       for (int k = 0; k < 8; ++k)
         v[i][k] = v[i][k] + b[0][i][k];
-      if (g * 8 < H) {
-        float4* xr = reinterpret_cast<float4*>(x + std::size_t(row) * H + g * 8);
-        xr[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
-        xr[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
-      }
+      store8(x_out, g * 8 < H ? unsigned(g) * 32 : kOutOfRange, v[i]);
     }
   }
   float squares = 0.0f;
@@ -321,8 +330,8 @@ __launch_bounds__(kImageNormThreads) __global__ void NormImageKernel(const NormI
       squares = fmaf(v[i][k], v[i][k], squares);
   const float scale =
       1.0f / sqrtf(SmallBlockSum<kWaves>(squares, s_red[1]) / float(H) + a.eps);
-  float* zrow = a.z_rows ? a.z_rows[row] : a.z ? a.z + std::size_t(row) * H : nullptr;
   float maximum = 0.0f;
+  const BufferResource z_out = MakeBuffer(zrow, zrow ? row_bytes : 0u);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = tid + kImageNormThreads * i;
@@ -331,11 +340,7 @@ __launch_bounds__(kImageNormThreads) __global__ void NormImageKernel(const NormI
       v[i][k] = (v[i][k] * scale) * nw[i][k];  // zero past H
       maximum = fmaxf(maximum, fabsf(v[i][k]));
     }
-    if (zrow && g * 8 < H) {
-      float4* zr = reinterpret_cast<float4*>(zrow + g * 8);
-      zr[0] = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
-      zr[1] = make_float4(v[i][4], v[i][5], v[i][6], v[i][7]);
-    }
+    store8(z_out, g * 8 < H ? unsigned(g) * 32 : kOutOfRange, v[i]);
   }
   maximum = WaveMax(maximum);
   if ((tid & 63) == 0)
@@ -349,37 +354,37 @@ __launch_bounds__(kImageNormThreads) __global__ void NormImageKernel(const NormI
   // Every group of the row's 64-column chunks, zeros past H.
   const int groups = (H + kChunk - 1) / kChunk * 8;
   if (a.image) {
-    if (tid == 0)
-      a.exps[row] = e;
+    // groups / 8 chunks of two 16-byte (hi, lo) planes of 64 lanes.
+    const BufferResource image_out = MakeBuffer(a.image, unsigned(groups) * 256u);
+    StoreB32(MakeBuffer(a.exps + row, 4u), tid == 0 ? 0u : kOutOfRange, unsigned(e));
 #pragma unroll
     for (int i = 0; i < G; ++i) {
       const int cg = tid + kImageNormThreads * i;
-      if (cg >= groups)
-        continue;
       unsigned hi[4], lo[4];
 #pragma unroll
       for (int k = 0; k < 8; k += 2)
         SplitPair(v[i][k], v[i][k + 1], e, hi[k / 2], lo[k / 2]);
-      const int idx = ((cg >> 3) * 2 + ((cg >> 2) & 1)) * 64 + 16 * (cg & 3) + row;
-      a.image[idx] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-      a.image[idx + 8] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+      const unsigned idx = unsigned(((cg >> 3) * 2 + ((cg >> 2) & 1)) * 64 + 16 * (cg & 3) + row);
+      StoreB128(image_out, cg < groups ? idx * 16u : kOutOfRange,
+                make_uint4(hi[0], hi[1], hi[2], hi[3]));
+      StoreB128(image_out, cg < groups ? (idx + 8) * 16u : kOutOfRange,
+                make_uint4(lo[0], lo[1], lo[2], lo[3]));
     }
   }
   if (a.a16) {
     // The prompt GEMM's FP16 row (HalfRowsKernel's expressions).
-    if (tid == 0)
-      a.a_scale[row] = ldexpf(1.0f, -e);
+    const BufferResource a16_out =
+        MakeBuffer(a.a16 + std::size_t(row) * a.lda, unsigned(groups) * 16u);
+    StoreF32(MakeBuffer(a.a_scale + row, 4u), tid == 0 ? 0u : kOutOfRange, ldexpf(1.0f, -e));
 #pragma unroll
     for (int i = 0; i < G; ++i) {
       const int cg = tid + kImageNormThreads * i;
-      if (cg >= groups)
-        continue;
       unsigned h[4];
 #pragma unroll
       for (int k = 0; k < 8; k += 2)
         h[k / 2] = unsigned(ScaledHalf(v[i][k], e)) | (unsigned(ScaledHalf(v[i][k + 1], e)) << 16);
-      *reinterpret_cast<uint4*>(a.a16 + std::size_t(row) * a.lda + cg * 8) =
-          make_uint4(h[0], h[1], h[2], h[3]);
+      StoreB128(a16_out, cg < groups ? unsigned(cg) * 16u : kOutOfRange,
+                make_uint4(h[0], h[1], h[2], h[3]));
     }
   }
 }
