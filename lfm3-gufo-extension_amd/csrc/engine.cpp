@@ -859,16 +859,23 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
     return parts;
   };
   // A mixer's input projection over the last `rows` rows (FP32 rows of z
-  // below kPromptRows, else the FP16 rows the residual norm left in a16),
-  // as one FP32 output.
-  const auto project = [&](const Matrix& w, std::uint32_t rows, float* y, std::uint32_t ldy) {
+  // below kPromptRows, else the FP16 rows the residual norm left in a16).
+  // With `single` one FP32 output (the convolution reads each value up to
+  // width times); otherwise K parts that the heads kernel adds. Returns
+  // the part count.
+  const auto project = [&](const Matrix& w, std::uint32_t rows, float* y, std::uint32_t ldy,
+                           bool single) -> std::uint32_t {
     const std::uint32_t first = n - rows;
     if (rows < kPromptRows) {
       gemv(w, z + std::size_t(first) * H, H, y, ldy, rows, false);
-      return;
+      return 1;
     }
-    const std::uint32_t parts = gemm(w, first, rows, y, ldy);
-    CheckStatus(lfm3_sum_parts(y, std::size_t(ldy) * rows, rows, w.rows, ldy, parts, s));
+    if (!single)
+      return gemm(w, first, rows, y, ldy);
+    CheckStatus(lfm3_q8_gemm(w.codes.p, w.scales.p, w.rows, w.cols,
+                             a16 + std::size_t(first) * lda, lda, scale + first, rows, y, ldy, 1,
+                             s));
+    return 1;
   };
   // Hidden-wide outputs of FP32 rows `in` go to `out` as K parts that the
   // next residual norm adds in part order; returns the part count.
@@ -911,7 +918,7 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
     const std::uint32_t o_in = n - rows_in, o = n - rows_out;
     std::uint32_t parts;
     if (l.type == LFM3_LAYER_CONV) {
-      project(l.in_proj, rows_in, proj, 3 * H);
+      project(l.in_proj, rows_in, proj, 3 * H, true);
       // Rows before the first live one are not read: outputs that would
       // need them are not live either (engine.cpp:386-393).
       float* hist = state.conv.as<float>();
@@ -922,7 +929,7 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
     } else {
       const bool swa = l.type == LFM3_LAYER_SLIDING;
       const std::uint32_t stride = l.kv * D;
-      project(l.qkvg, n, proj, pld);
+      const std::uint32_t qparts = project(l.qkvg, n, proj, pld, false);
       const float* table = swa ? m.freq_sliding.as<float>() : m.freq_global.as<float>();
       const float* factors = swa ? nullptr : m.factors.as<float>();
       auto* ck = state.k.as<std::uint16_t>();
@@ -931,9 +938,11 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
       // sliding ring is written only after attention read its history.
       std::uint16_t* kc = swa ? b.chunk_k.as<std::uint16_t>() : ck + std::size_t(position) * stride;
       std::uint16_t* vc = swa ? b.chunk_v.as<std::uint16_t>() : cv + std::size_t(position) * stride;
-      CheckStatus(lfm3_prompt_heads(proj + l.q_off, proj + l.k_off, proj + l.v_off, pld,
-                                    l.q_norm.as<float>(), l.k_norm.as<float>(), table, factors,
-                                    kc, vc, n, c.heads, l.kv, D, position, c.eps, s));
+      LaunchPromptHeads(proj + l.q_off, proj + l.k_off, proj + l.v_off, pld,
+                        l.q_norm.as<float>(), l.k_norm.as<float>(), table, factors, kc, vc, n,
+                        c.heads, l.kv, D, position, c.eps, qparts, std::size_t(pld) * n,
+                        proj + l.g_off, s);
+      Check(hipGetLastError(), "LFM3 prompt heads launch");
       // Only the last rows_out queries are live.
       const std::uint32_t skip = n - rows_out;
       float* q_rows = proj + std::size_t(skip) * pld + l.q_off;

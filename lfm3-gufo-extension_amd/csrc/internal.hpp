@@ -50,5 +50,14 @@ int LaunchArgmaxKeys(const unsigned long long* keys, std::uint32_t rows, std::ui
 int LaunchScatterRows(const float* src, std::size_t ld, float* const* dst,
                       std::uint32_t rows, std::size_t count,
                       hipStream_t stream);
+// lfm3_prompt_heads over a projection in K parts (part_stride floats
+// apart): the parts are summed in part order, q and the per-head gate g
+// (one float per head at g + row * ld) into part 0.
+void LaunchPromptHeads(float* q, float* k, const float* v, std::uint32_t ld, const float* q_norm,
+                       const float* k_norm, const float* frequencies, const float* factors,
+                       std::uint16_t* k16, std::uint16_t* v16, std::uint32_t rows,
+                       std::uint32_t heads, std::uint32_t kv_heads, std::uint32_t dim,
+                       std::uint32_t position, float eps, std::uint32_t parts,
+                       std::size_t part_stride, float* g, hipStream_t s);
 }  // namespace lfm3amd
 #endif

@@ -459,9 +459,15 @@ __device__ __forceinline__ void NormRotateHead(float* __restrict__ xh,
                                                const float* __restrict__ frequencies,
                                                const float* __restrict__ factors,
                                                std::uint32_t position, float eps, int pair,
-                                               float& r0, float& r1) {
+                                               float& r0, float& r1, int parts = 1,
+                                               std::size_t part_stride = 0) {
   constexpr int P = D / 2;
-  const float x0 = xh[pair], x1 = xh[pair + P];
+  // K parts of the projection added in part order (SumPartsKernel's sum).
+  float x0 = xh[pair], x1 = xh[pair + P];
+  for (int p = 1; p < parts; ++p) {
+    x0 += xh[p * part_stride + pair];
+    x1 += xh[p * part_stride + pair + P];
+  }
   float squares = fmaf(x0, x0, x1 * x1);
 #pragma unroll
   for (int m = P / 2; m; m >>= 1)
@@ -520,7 +526,9 @@ __launch_bounds__(D / 2) __global__
 
 // Prompt heads (hip/ops.hip:2407-2417 PromptHeads): row r of a chunk is at
 // position + r and its K/V go to row r of k16/v16 (kv_heads * D halves a
-// row), which is either a staging chunk or the cache rows themselves.
+// row), which is either a staging chunk or the cache rows themselves. A
+// projection in K parts is summed here in part order: q (rotated) and the
+// per-head gate g land in part 0, K and V go to the F16 rows.
 template<int D>
 __launch_bounds__(D / 2) __global__
     void PromptHeadsKernel(float* __restrict__ q, float* __restrict__ k,
@@ -530,24 +538,37 @@ __launch_bounds__(D / 2) __global__
                            const float* __restrict__ frequencies,
                            const float* __restrict__ factors, Half* __restrict__ k16,
                            Half* __restrict__ v16, int heads, int kv_heads,
-                           std::uint32_t position, float eps) {
+                           std::uint32_t position, float eps, int parts,
+                           std::size_t part_stride, float* __restrict__ g) {
   constexpr int P = D / 2;
   const int head = blockIdx.x, row = blockIdx.y, pair = threadIdx.x;
   const bool is_key = head >= heads;
   const int kvh = head - heads;
   float* xh = is_key ? k + std::size_t(row) * ld + kvh * D
                      : q + std::size_t(row) * ld + head * D;
+  if (!is_key && parts > 1 && pair == 0) {
+    float* gh = g + std::size_t(row) * ld + head;
+    float sum = gh[0];
+    for (int p = 1; p < parts; ++p)
+      sum += gh[p * part_stride];
+    gh[0] = sum;
+  }
   float r0, r1;
   NormRotateHead<D>(xh, is_key ? k_norm : q_norm, frequencies, factors,
-                    position + std::uint32_t(row), eps, pair, r0, r1);
+                    position + std::uint32_t(row), eps, pair, r0, r1, parts, part_stride);
   if (!is_key)
     return;
   const std::size_t slot = (std::size_t(row) * kv_heads + kvh) * D;
   const float* vh = v + std::size_t(row) * ld + kvh * D;
+  float v0 = vh[pair], v1 = vh[pair + P];
+  for (int p = 1; p < parts; ++p) {
+    v0 += vh[p * part_stride + pair];
+    v1 += vh[p * part_stride + pair + P];
+  }
   k16[slot + pair] = FloatToHalfBits(r0);
   k16[slot + pair + P] = FloatToHalfBits(r1);
-  v16[slot + pair] = FloatToHalfBits(vh[pair]);
-  v16[slot + pair + P] = FloatToHalfBits(vh[pair + P]);
+  v16[slot + pair] = FloatToHalfBits(v0);
+  v16[slot + pair + P] = FloatToHalfBits(v1);
 }
 
 // StoreKV (hip/ops.hip:1737-1749, engine.cpp:467-470): rows 0..n-1 of a
@@ -799,6 +820,27 @@ int LaunchScatterRows(const float* src, std::size_t ld, float* const* dst,
 
 }  // namespace lfm3amd
 
+namespace lfm3amd {
+
+void LaunchPromptHeads(float* q, float* k, const float* v, std::uint32_t ld, const float* q_norm,
+                       const float* k_norm, const float* frequencies, const float* factors,
+                       std::uint16_t* k16, std::uint16_t* v16, std::uint32_t rows,
+                       std::uint32_t heads, std::uint32_t kv_heads, std::uint32_t dim,
+                       std::uint32_t position, float eps, std::uint32_t parts,
+                       std::size_t part_stride, float* g, hipStream_t s) {
+  const dim3 grid(heads + kv_heads, rows);
+  if (dim == 128)
+    PromptHeadsKernel<128><<<grid, 64, 0, s>>>(q, k, v, int(ld), q_norm, k_norm, frequencies,
+                                               factors, k16, v16, int(heads), int(kv_heads),
+                                               position, eps, int(parts), part_stride, g);
+  else
+    PromptHeadsKernel<64><<<grid, 32, 0, s>>>(q, k, v, int(ld), q_norm, k_norm, frequencies,
+                                              factors, k16, v16, int(heads), int(kv_heads),
+                                              position, eps, int(parts), part_stride, g);
+}
+
+}  // namespace lfm3amd
+
 using namespace lfm3amd;
 
 extern "C" {
@@ -963,16 +1005,8 @@ int lfm3_prompt_heads(float* q, float* k, const float* v, std::uint32_t ld,
       !heads || !kv_heads || heads % kv_heads || (dim != 64 && dim != 128) ||
       rows > 65535 || std::uint64_t(position) + rows > (1ull << 31))
     return Fail(LFM3_E_INVALID, "LFM3 prompt heads need dimension 64 or 128");
-  const dim3 grid(heads + kv_heads, rows);
-  const auto s = static_cast<hipStream_t>(stream);
-  if (dim == 128)
-    PromptHeadsKernel<128><<<grid, 64, 0, s>>>(q, k, v, int(ld), q_norm, k_norm, frequencies,
-                                               factors, k16, v16, int(heads), int(kv_heads),
-                                               position, eps);
-  else
-    PromptHeadsKernel<64><<<grid, 32, 0, s>>>(q, k, v, int(ld), q_norm, k_norm, frequencies,
-                                              factors, k16, v16, int(heads), int(kv_heads),
-                                              position, eps);
+  LaunchPromptHeads(q, k, v, ld, q_norm, k_norm, frequencies, factors, k16, v16, rows, heads,
+                    kv_heads, dim, position, eps, 1, 0, nullptr, static_cast<hipStream_t>(stream));
   return HipStatus(hipGetLastError(), "LFM3 prompt heads launch");
 }
 

@@ -70,12 +70,18 @@ def test_prompt_matches_oracle_steps(n, start):
 @pytest.mark.parametrize("dims_kw", [dict(heads=8, kv_heads=4, head_dim=64),
                                      dict(heads=16, kv_heads=2, head_dim=64, pattern="GSC"),
                                      dict(pattern="CCSCGCCSCGCCSCGCSCGCSCGG", hidden=256,
-                                          intermediate=512)])
+                                          intermediate=512),
+                                     dict(hidden=512, intermediate=1024)])
 def test_prompt_other_shapes(dims_kw):
-    """Other head shapes, a prompt ending on a convolution layer, and the
+    """Other head shapes, a prompt ending on a convolution layer, the
     24-layer pattern (13 conv, 5 sliding, 6 global; last layer global, so
-    the last layer's FFN runs on the frontier row only)."""
+    the last layer's FFN runs on the frontier row only), and a hidden size
+    of 512, where the attention input projection runs in two K parts that
+    the heads kernel adds."""
     dims = small_dims(**dims_kw)
+    if dims.hidden == 512:
+        qkvg = dims.heads * dims.head_dim + 2 * dims.kv_heads * dims.head_dim + dims.heads
+        assert L.lib().lfm3_q8_gemm_parts(qkvg, dims.hidden, 200, 0) == 2
     w = L.synth_weights(dims, seed=32)
     gm, om = L.Model(w), O.Model(dims, w)
     g, o = gm.session(1024), om.session(1024, f16=True)
