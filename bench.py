@@ -59,8 +59,8 @@ MIXED_DECODE, MIXED_LO, MIXED_HI = 7, 16384, 32768
 # `bench.py --roofline-only` and scaled by what each counter reads for a
 # plain 256 MiB device-to-device copy in the same program (FETCH_SIZE x 2.0,
 # WRITE_SIZE x 1.0). Re-measure after a change to either kernel.
-GEMV_TRAFFIC = {"read": 18_468_416, "write": 262_144}
-GEMM_TRAFFIC = {"read": 52_804_129, "write": 15_851_520}
+GEMV_TRAFFIC = {"read": 18_477_766, "write": 262_144}
+GEMM_TRAFFIC = {"read": 52_777_234, "write": 15_851_520}
 
 
 def log(msg: str):
