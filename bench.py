@@ -196,7 +196,15 @@ def gemm_roofline(copies: int, passes: int):
     u = L.q8(L.SEED, "gemm.up", F, H)
     L.check(L.lib().lfm3_q8_pack_host(L.ptr(g), F, H, L.ptr(codes), L.ptr(scales), 0, 2))
     L.check(L.lib().lfm3_q8_pack_host(L.ptr(u), F, H, L.ptr(codes), L.ptr(scales), 1, 2))
-    mats = [(L.DeviceBuffer.of(codes), L.DeviceBuffer.of(scales)) for _ in range(copies)]
+    # The pass reads FP16 tiles: decoded once from the codes, as the model does.
+    dcodes = L.DeviceBuffer.of(codes)
+    mats = []
+    for _ in range(copies):
+        halves = L.DeviceBuffer(L.lib().lfm3_q8_half_tiles_bytes(2 * F, H))
+        L.check(L.lib().lfm3_q8_half_tiles(dcodes.addr, 2 * F, H, halves.addr, None))
+        mats.append((halves, L.DeviceBuffer.of(scales)))
+    L.synchronize()
+    dcodes.close()
     x = L.DeviceBuffer.of(L.normal(L.SEED, "gemm.x", n * H))
     a16 = L.DeviceBuffer(n * H * 2)
     scale = L.DeviceBuffer(n * 4)
@@ -207,8 +215,8 @@ def gemm_roofline(copies: int, passes: int):
 
     def one_pass():
         for c, s in mats:
-            L.check(L.lib().lfm3_q8_gemm_swiglu(c.addr, s.addr, F, H, a16.addr, H, scale.addr, n,
-                                                y.addr, F, row_max.addr, stream.handle))
+            L.check(L.lib().lfm3_q8_gemm_swiglu_h16(c.addr, s.addr, F, H, a16.addr, H, scale.addr,
+                                                    n, y.addr, F, row_max.addr, stream.handle))
 
     graph = L.Graph(stream, one_pass)
     graph.launch()
@@ -225,7 +233,9 @@ def gemm_roofline(copies: int, passes: int):
     b.close()
     stream.close()
     flops = 2 * n * 2 * F * H
-    nbytes = (q8_bytes(2 * F, H) + n * H * 2 + n * 4 + n * F * 4
+    # FP16 weights (2 bytes each) and their fp16 block scales, the FP16
+    # rows with their scales, the outputs and the row maxima.
+    nbytes = (2 * F * H * 2 + 2 * F * (H // 32) * 2 + n * H * 2 + n * 4 + n * F * 4
               + L.lib().lfm3_q8_gemm_swiglu_max_blocks(F) * n * 4)
     return {"flops": flops, "bytes": nbytes, "us": us, "tflops": flops / (us * 1e-6) / 1e12}
 

@@ -176,6 +176,25 @@ int lfm3_q8_gemm_swiglu(const void* codes, const void* scales, uint32_t rows,
                         uint32_t cols, const uint16_t* a, uint32_t lda,
                         const float* a_scale, uint32_t tokens, float* y,
                         uint32_t ldy, unsigned* row_max, void* stream);
+/* FP16 tiles of a tiled Q8_0 matrix: each code decoded exactly to fp16 in
+   the order the prompt GEMM's MFMA takes it (2 KB per 16-row x 64-column
+   tile; lfm3_q8_half_tiles_bytes). The scales stay in the Q8_0 scale
+   array. Replaces: the per-chunk decode of Codes (q8_prefill.hpp:82-92),
+   done once at load instead of in every prompt GEMM. */
+size_t lfm3_q8_half_tiles_bytes(uint32_t rows, uint32_t cols);
+int lfm3_q8_half_tiles(const void* codes, uint32_t rows, uint32_t cols,
+                       void* halves, void* stream);
+/* lfm3_q8_gemm and lfm3_q8_gemm_swiglu over FP16 tiles (the same
+   operands, products and FP32 block fmas, so the outputs are identical).
+   Replaces: as lfm3_q8_gemm and lfm3_q8_gemm_swiglu. */
+int lfm3_q8_gemm_h16(const void* halves, const void* scales, uint32_t rows,
+                     uint32_t cols, const uint16_t* a, uint32_t lda,
+                     const float* a_scale, uint32_t tokens, float* y, uint32_t ldy,
+                     uint32_t parts, void* stream);
+int lfm3_q8_gemm_swiglu_h16(const void* halves, const void* scales, uint32_t rows,
+                            uint32_t cols, const uint16_t* a, uint32_t lda,
+                            const float* a_scale, uint32_t tokens, float* y,
+                            uint32_t ldy, unsigned* row_max, void* stream);
 
 /* ---------------------------------------------------------------------
  * Row operations.

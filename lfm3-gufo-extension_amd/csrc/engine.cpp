@@ -79,10 +79,13 @@ struct PinnedBuffer {
   PinnedBuffer(const PinnedBuffer&) = delete;
 };
 
-// A tiled Q8_0 matrix of rows x cols (several sources may share it).
+// A tiled Q8_0 matrix of rows x cols (several sources may share it). The
+// gate/up prompt GEMM reads `halves`, the codes decoded to FP16 tiles,
+// made with the model's prompt scratch.
 struct Matrix {
-  Buffer codes, scales;
+  Buffer codes, scales, halves;
   std::uint32_t rows = 0, cols = 0;
+  std::uint32_t tiles = 0;  // row tiles stored (gate/up: two per 16 rows)
 };
 
 Buffer UploadFloats(const float* host, std::size_t n) {
@@ -101,6 +104,7 @@ Matrix PackMatrix(std::initializer_list<Part> parts, std::uint32_t tiles,
   Matrix m;
   m.rows = rows;
   m.cols = cols;
+  m.tiles = tiles;
   const std::size_t chunks = Chunks(cols);
   const std::size_t code_bytes = std::size_t(tiles) * chunks * kTileCodeBytes;
   const std::size_t scale_bytes = std::size_t(tiles) * chunks * kTileScales * 2;
@@ -771,6 +775,20 @@ PromptBuffers& EnsurePromptBuffers(lfm3_model& m) {
   b->one_bytes = Align(4 * sizeof(void*)) + Align(b->one_items * sizeof(lfm3_attention_item));
   b->one_table = Buffer(b->one_bytes);
   b->one_staging = std::make_unique<PinnedBuffer>(b->one_bytes);
+  // FP16 tiles of the gate/up matrices (every stored tile: two per 16
+  // output rows). Their GEMM runs in the wide block shape, where dropping
+  // the per-chunk code decode pays for the doubled tile bytes (about 9% on
+  // the 512-token gate/up GEMM). The other projections run in the narrow
+  // shape, two blocks a CU, where FP16 tiles gain under 1% of the pass (two
+  // LDS stages instead of three) for 1.4 GB more memory: they stay on code
+  // tiles.
+  for (auto& l : m.layers) {
+    Matrix& w = l.ffn;
+    const std::uint32_t rows = w.tiles * kTileRows;
+    w.halves = Buffer(lfm3_q8_half_tiles_bytes(rows, w.cols), false);
+    CheckStatus(lfm3_q8_half_tiles(w.codes.p, rows, w.cols, w.halves.p, m.stream));
+  }
+  Check(hipStreamSynchronize(m.stream), "FP16 tiles");
   m.prompt = std::move(b);
   return *m.prompt;
 }
@@ -850,12 +868,16 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
                                  k, nullptr, 0, s));
     }
   };
-  const auto gemm = [&](const Matrix& w, std::uint32_t a_row, std::uint32_t rows, float* y,
-                        std::uint32_t ldy) -> std::uint32_t {
-    const std::uint32_t parts = lfm3_q8_gemm_parts(w.rows, w.cols, rows, 0);
+  const auto gemm_parts = [&](const Matrix& w, std::uint32_t a_row, std::uint32_t rows,
+                              float* y, std::uint32_t ldy, std::uint32_t parts) {
     CheckStatus(lfm3_q8_gemm(w.codes.p, w.scales.p, w.rows, w.cols,
                              a16 + std::size_t(a_row) * lda, lda, scale + a_row, rows, y, ldy,
                              parts, s));
+  };
+  const auto gemm = [&](const Matrix& w, std::uint32_t a_row, std::uint32_t rows, float* y,
+                        std::uint32_t ldy) -> std::uint32_t {
+    const std::uint32_t parts = lfm3_q8_gemm_parts(w.rows, w.cols, rows, 0);
+    gemm_parts(w, a_row, rows, y, ldy, parts);
     return parts;
   };
   // A mixer's input projection over the last `rows` rows (FP32 rows of z
@@ -872,9 +894,7 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
     }
     if (!single)
       return gemm(w, first, rows, y, ldy);
-    CheckStatus(lfm3_q8_gemm(w.codes.p, w.scales.p, w.rows, w.cols,
-                             a16 + std::size_t(first) * lda, lda, scale + first, rows, y, ldy, 1,
-                             s));
+    gemm_parts(w, first, rows, y, ldy, 1);
     return 1;
   };
   // Hidden-wide outputs of FP32 rows `in` go to `out` as K parts that the
@@ -997,7 +1017,7 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
       gemv(l.ffn, z + std::size_t(o) * H, H, hid, F, rows_out, true);
       parts = dense(l.down, hid, F, rows_out, nullptr);
     } else {
-      CheckStatus(lfm3_q8_gemm_swiglu(l.ffn.codes.p, l.ffn.scales.p, F, H,
+      CheckStatus(lfm3_q8_gemm_swiglu_h16(l.ffn.halves.p, l.ffn.scales.p, F, H,
                                       a16 + std::size_t(o) * lda, lda, scale + o, rows_out, hid,
                                       F, row_max, s));
       parts = dense(l.down, hid, F, rows_out, row_max);

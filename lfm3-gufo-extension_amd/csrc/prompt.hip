@@ -41,18 +41,28 @@ constexpr int kGemmRT = 4, kGemmTT = 4, kGemmStages = 3;
 // distinct banks), the block's weight tiles for the chunk (1 KB each, lane
 // order), and their scales (256 B per group of 4 tiles, row n's 4 tiles at
 // 16 n).
-template<int WR, int WT>
+// With kHalf the weight tiles are FP16 tiles (2 KB: the 16 codes a lane
+// holds, decoded once at load into block 0's eight halves at byte 16 L and
+// block 1's at 1024 + 16 L), so the loop feeds them to the MFMA without the
+// per-chunk decode; the operands, and so every product, are the same.
+template<int WR, int WT, bool kHalf = false, int kStageCount = kGemmStages>
 struct GemmShape {
   static constexpr int kWR = WR, kWT = WT;
+  static constexpr bool kHalfTiles = kHalf;
+  static constexpr int kStages = kStageCount;  // LDS pipeline stages: 2 or 3
   static constexpr int kWaves = WR * WT, kThreads = 64 * kWaves;
   static constexpr int kTiles = WR * kGemmRT;  // weight tiles a block
   static constexpr int kTokens = WT * kGemmTT * 16;
+  static constexpr int kTileW = kHalf ? 2 * kTileCodeBytes : kTileCodeBytes;
   static constexpr int kW = kTokens * 128;
-  static constexpr int kS = kW + kTiles * kTileCodeBytes;
+  static constexpr int kS = kW + kTiles * kTileW;
   static constexpr int kBytes = kS + kTiles * kTileScales * 2;
 };
 using WideShape = GemmShape<4, 2>;
 using NarrowShape = GemmShape<2, 2>;
+using WideHalfShape = GemmShape<4, 2, true>;
+// Two stages, so that two blocks (2 x 65 KB) fit a CU.
+using NarrowHalfShape = GemmShape<2, 2, true, 2>;
 
 // One block per row: row maximum (scanned, or the maximum of max_blocks
 // partial maxima), then fp16(x 2^e) and the scale 2^-e. The vector form
@@ -208,6 +218,8 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   using Stage = Shape;
   constexpr int A_LOADS = Shape::kTokens * 8 / Shape::kThreads;  // 16-byte loads a lane
   constexpr int W_LOADS = Shape::kTiles / Shape::kWaves;         // tiles a wave loads
+  constexpr int kTileW = Shape::kTileW;                           // bytes of a tile's chunk
+  constexpr int W_PIECES = kTileW / kTileCodeBytes;               // 1 KB loads a tile
   static_assert(A_LOADS * Shape::kThreads == Shape::kTokens * 8, "A loads cover the rows");
   static_assert(W_LOADS * Shape::kWaves == Shape::kTiles, "W loads cover the tiles");
   static_assert(RT == 4 && Shape::kWR <= Shape::kWaves, "scale groups of four tiles");
@@ -215,8 +227,8 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   // that a stage's reads never alias the other stages' loads in flight.
   __shared__ __attribute__((aligned(16))) std::uint8_t s_st0[Stage::kBytes];
   __shared__ __attribute__((aligned(16))) std::uint8_t s_st1[Stage::kBytes];
-  __shared__ __attribute__((aligned(16))) std::uint8_t s_st2[Stage::kBytes];
-  static_assert(kGemmStages == 3, "three stage arrays");
+  __shared__ __attribute__((aligned(16))) std::uint8_t s_st2[Shape::kStages == 3 ? Stage::kBytes : 16];
+  static_assert(Shape::kStages == 2 || Shape::kStages == 3, "two or three stage arrays");
 
   const int item = XcdMajorItem(blockIdx.x, gridDim.x);
   const int tb = item % token_blocks, rb = (item / token_blocks) % row_blocks;
@@ -238,7 +250,7 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   const BufferResource a_res = MakeBuffer(a + std::size_t(tok0) * lda,
                                           unsigned(n - tok0) * unsigned(lda) * 2u);
   const BufferResource w_res = MakeBuffer(codes, unsigned(row_tiles) * unsigned(nchunks) *
-                                                     unsigned(kTileCodeBytes));
+                                                     unsigned(kTileW));
   const BufferResource s_res = MakeBuffer(scales, unsigned(row_tiles) * unsigned(nchunks) *
                                                       unsigned(kTileScales * 2));
   unsigned a_off[A_LOADS];
@@ -252,7 +264,7 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
 #pragma unroll
   for (int j = 0; j < W_LOADS; ++j)
     w_tile[j] = unsigned(min(btile0 + wave * W_LOADS + j, row_tiles - 1)) *
-                unsigned(nchunks * kTileCodeBytes);
+                unsigned(nchunks * kTileW);
   const unsigned w_off = unsigned(lane) * 16u;
   // Scales: wave g < Shape::kWR loads group g; lane L brings tile 4 g + L % 4's
   // dword L / 4 (row L / 4's two block scales).
@@ -268,8 +280,10 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
                     stage + (wave * A_LOADS + j) * 1024);
 #pragma unroll
     for (int j = 0; j < W_LOADS; ++j)
-      BufferToLds16(w_res, w_off, w_tile[j] + unsigned(c * kTileCodeBytes),
-                    stage + Stage::kW + (wave * W_LOADS + j) * kTileCodeBytes);
+#pragma unroll
+      for (int piece = 0; piece < W_PIECES; ++piece)
+        BufferToLds16(w_res, w_off, w_tile[j] + unsigned(c * kTileW + piece * kTileCodeBytes),
+                      stage + Stage::kW + (wave * W_LOADS + j) * kTileW + piece * kTileCodeBytes);
     if (loads_scales)
       BufferToLds4(s_res, s_off, unsigned(c * kTileScales * 2),
                    stage + Stage::kS + wave * 4 * kTileScales * 2);
@@ -277,9 +291,9 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   // Waits until at most one chunk's loads of this wave remain in flight.
   const auto wait_all_but_one_chunk = [&]() {
     if (loads_scales)
-      __builtin_amdgcn_s_waitcnt(WaitVm(A_LOADS + W_LOADS + 1));
+      __builtin_amdgcn_s_waitcnt(WaitVm(A_LOADS + W_LOADS * W_PIECES + 1));
     else
-      __builtin_amdgcn_s_waitcnt(WaitVm(A_LOADS + W_LOADS));
+      __builtin_amdgcn_s_waitcnt(WaitVm(A_LOADS + W_LOADS * W_PIECES));
   };
 
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -299,10 +313,12 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   const int a_row = wt * TT * 16 + (lane & 15);
   const auto compute = [&](const std::uint8_t* stage) {
     uint4 q[RT];
+    if constexpr (!Shape::kHalfTiles) {
 #pragma unroll
-    for (int r = 0; r < RT; ++r)
-      q[r] = *reinterpret_cast<const uint4*>(stage + Stage::kW +
-                                             (wr * RT + r) * kTileCodeBytes + lane * 16);
+      for (int r = 0; r < RT; ++r)
+        q[r] = *reinterpret_cast<const uint4*>(stage + Stage::kW +
+                                               (wr * RT + r) * kTileW + lane * 16);
+    }
     const uint4 sc4 = *reinterpret_cast<const uint4*>(
         stage + Stage::kS + wr * RT * kTileScales * 2 + (lane & 15) * 16);
     const unsigned sc[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
@@ -312,7 +328,11 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
       float d[RT];
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
-        w[r] = blk ? EightCodes(q[r].z, q[r].w) : EightCodes(q[r].x, q[r].y);
+        if constexpr (Shape::kHalfTiles)
+          w[r] = *reinterpret_cast<const h8*>(stage + Stage::kW + (wr * RT + r) * kTileW +
+                                              blk * kTileCodeBytes + lane * 16);
+        else
+          w[r] = blk ? EightCodes(q[r].z, q[r].w) : EightCodes(q[r].x, q[r].y);
         // An opaque conversion keeps the scale FMAs as in-place v_fmac_f32
         // (a v_fma_mix_f32 reading the half would write a fresh register).
         asm("v_cvt_f32_f16 %0, %1" : "=v"(d[r]) : "v"(blk ? sc[r] >> 16 : sc[r]));
@@ -375,6 +395,27 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   // with chunk c - 1), issue chunk c + 2 into chunk c - 1's stage, then
   // multiply chunk c. Loads get two chunks' compute to arrive.
   issue(c_begin, s_st0);
+  if constexpr (Shape::kStages == 2) {
+    // Two stages: step c waits for chunk c (the only loads in flight),
+    // barrier (every wave done with chunk c - 1's stage), issues chunk
+    // c + 1 into it, then multiplies chunk c.
+    const auto step2 = [&](int c, std::uint8_t* stage, std::uint8_t* refill) {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(WaitVm(0));
+      BlockBarrier();
+      if (c + 1 < c_end)
+        issue(c + 1, refill);
+      compute(stage);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    int c = c_begin;
+    for (; c + 2 <= c_end; c += 2) {
+      step2(c, s_st0, s_st1);
+      step2(c + 1, s_st1, s_st0);
+    }
+    if (c < c_end)
+      step2(c, s_st0, s_st1);
+  } else {
   if (c_begin + 1 < c_end)
     issue(c_begin + 1, s_st1);
   const auto step = [&](int c, std::uint8_t* stage, std::uint8_t* refill) {
@@ -401,6 +442,7 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
     step(c, s_st0, s_st2);
   if (c + 1 < c_end)
     step(c + 1, s_st1, s_st0);
+  }
 
   // D layout: lane L holds tokens 16 t + 4 (L / 16) + i of weight row L % 16.
   const int sub = lane & 15, quad = lane >> 4;
@@ -483,6 +525,21 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   }
 }
 
+// Code tiles -> FP16 tiles: the 16 codes lane L of a (tile, chunk) holds
+// become block 0's eight halves at byte 16 L and block 1's at 1024 + 16 L
+// of the 2 KB FP16 tile (the prompt GEMM's B operands, decoded once).
+__global__ void HalfTilesKernel(const uint4* __restrict__ codes, uint4* __restrict__ out,
+                                std::size_t units) {
+  const std::size_t u = std::size_t(blockIdx.x) * 256 + threadIdx.x;  // (tile chunk, lane)
+  if (u >= units)
+    return;
+  const uint4 q = codes[u];
+  const std::size_t tc = u / 64;
+  const unsigned lane = unsigned(u % 64);
+  out[tc * 128 + lane] = __builtin_bit_cast(uint4, EightCodes(q.x, q.y));
+  out[tc * 128 + 64 + lane] = __builtin_bit_cast(uint4, EightCodes(q.z, q.w));
+}
+
 // Adds K parts 1..parts-1 into part 0, in part order (the deterministic
 // merge of split-K partial outputs, hip/ops.hip:2019-2119), for consumers
 // that read one FP32 row.
@@ -531,8 +588,8 @@ int PromptParts(int row_tiles, int tokens, int nchunks) {
 // The kernel addresses codes, scales, activations and each output part
 // with 32-bit buffer offsets.
 bool GemmOperandsFit(std::uint64_t row_tiles, std::uint64_t nchunks, std::uint64_t tokens,
-                     std::uint64_t lda, std::uint64_t ldy) {
-  return row_tiles * nchunks * kTileCodeBytes < (1ull << 31) &&
+                     std::uint64_t lda, std::uint64_t ldy, bool half) {
+  return row_tiles * nchunks * kTileCodeBytes * (half ? 2 : 1) < (1ull << 31) &&
          tokens * lda * 2 < (1ull << 31) && tokens * ldy * 4 < (1ull << 31);
 }
 
@@ -592,22 +649,77 @@ std::uint32_t lfm3_q8_gemm_parts(std::uint32_t rows, std::uint32_t cols,
   return std::uint32_t(PromptParts(int(RowTiles(rows)), int(tokens), int(Chunks(cols))));
 }
 
+std::size_t lfm3_q8_half_tiles_bytes(std::uint32_t rows, std::uint32_t cols) {
+  return std::size_t(RowTiles(rows)) * Chunks(cols) * 2 * kTileCodeBytes;
+}
+
+int lfm3_q8_half_tiles(const void* codes, std::uint32_t rows, std::uint32_t cols, void* out,
+                       void* stream) {
+  if (!codes || !out || !rows || !cols || cols % 32 ||
+      (reinterpret_cast<std::uintptr_t>(codes) & 15) ||
+      (reinterpret_cast<std::uintptr_t>(out) & 15))
+    return Fail(LFM3_E_INVALID, "invalid LFM3 FP16 tile conversion");
+  const std::size_t units = std::size_t(RowTiles(rows)) * Chunks(cols) * 64;
+  HalfTilesKernel<<<unsigned((units + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint4*>(codes), static_cast<uint4*>(out), units);
+  return HipStatus(hipGetLastError(), "LFM3 FP16 tile conversion launch");
+}
+
+}  // extern "C"
+
+namespace {
+
+int Gemm(const void* tiles, bool half, const void* scales, std::uint32_t rows,
+         std::uint32_t cols, const std::uint16_t* a, std::uint32_t lda, const float* a_scale,
+         std::uint32_t tokens, float* y, std::uint32_t ldy, std::uint32_t parts,
+         void* stream) {
+  if (!tiles || !scales || !a || !a_scale || !y || !rows || !cols ||
+      cols % 32 || !tokens || lda % 64 || lda < Chunks(cols) * kChunk ||
+      ldy < rows || !parts || parts > 8 || parts > Chunks(cols) ||
+      (reinterpret_cast<std::uintptr_t>(a) & 15) ||
+      !GemmOperandsFit(RowTiles(rows), Chunks(cols), tokens, lda, ldy, half))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 prompt GEMM shape");
+  const bool narrow = NarrowGemm(int(RowTiles(rows)), int(tokens));
+  const auto launch = half ? (narrow ? LaunchGemm<false, NarrowHalfShape>
+                                     : LaunchGemm<false, WideHalfShape>)
+                           : (narrow ? LaunchGemm<false, NarrowShape>
+                                     : LaunchGemm<false, WideShape>);
+  launch(tiles, scales, int(RowTiles(rows)), int(Chunks(cols)), a, lda, a_scale, tokens, y, ldy,
+         rows, int(parts), std::size_t(ldy) * tokens, nullptr, static_cast<hipStream_t>(stream));
+  return HipStatus(hipGetLastError(), "LFM3 Q8_0 prompt GEMM launch");
+}
+
+int GemmSwiGLU(const void* tiles, bool half, const void* scales, std::uint32_t rows,
+               std::uint32_t cols, const std::uint16_t* a, std::uint32_t lda,
+               const float* a_scale, std::uint32_t tokens, float* y, std::uint32_t ldy,
+               unsigned* row_max, void* stream) {
+  if (!tiles || !scales || !a || !a_scale || !y || !rows || !cols ||
+      cols % 32 || !tokens || lda % 64 || lda < Chunks(cols) * kChunk ||
+      ldy < rows || (reinterpret_cast<std::uintptr_t>(a) & 15) ||
+      !GemmOperandsFit(2 * RowTiles(rows), Chunks(cols), tokens, lda, ldy, half))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 prompt SwiGLU shape");
+  const auto launch = half ? LaunchGemm<true, WideHalfShape> : LaunchGemm<true, WideShape>;
+  launch(tiles, scales, int(2 * RowTiles(rows)), int(Chunks(cols)), a, lda, a_scale, tokens, y,
+         ldy, rows, 1, 0, row_max, static_cast<hipStream_t>(stream));
+  return HipStatus(hipGetLastError(), "LFM3 Q8_0 prompt SwiGLU launch");
+}
+
+}  // namespace
+
+extern "C" {
+
 int lfm3_q8_gemm(const void* codes, const void* scales, std::uint32_t rows,
                  std::uint32_t cols, const std::uint16_t* a, std::uint32_t lda,
                  const float* a_scale, std::uint32_t tokens, float* y,
                  std::uint32_t ldy, std::uint32_t parts, void* stream) {
-  if (!codes || !scales || !a || !a_scale || !y || !rows || !cols ||
-      cols % 32 || !tokens || lda % 64 || lda < Chunks(cols) * kChunk ||
-      ldy < rows || !parts || parts > 8 || parts > Chunks(cols) ||
-      (reinterpret_cast<std::uintptr_t>(a) & 15) ||
-      !GemmOperandsFit(RowTiles(rows), Chunks(cols), tokens, lda, ldy))
-    return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 prompt GEMM shape");
-  const auto launch = NarrowGemm(int(RowTiles(rows)), int(tokens))
-                          ? LaunchGemm<false, NarrowShape>
-                          : LaunchGemm<false, WideShape>;
-  launch(codes, scales, int(RowTiles(rows)), int(Chunks(cols)), a, lda, a_scale, tokens, y, ldy,
-         rows, int(parts), std::size_t(ldy) * tokens, nullptr, static_cast<hipStream_t>(stream));
-  return HipStatus(hipGetLastError(), "LFM3 Q8_0 prompt GEMM launch");
+  return Gemm(codes, false, scales, rows, cols, a, lda, a_scale, tokens, y, ldy, parts, stream);
+}
+
+int lfm3_q8_gemm_h16(const void* halves, const void* scales, std::uint32_t rows,
+                     std::uint32_t cols, const std::uint16_t* a, std::uint32_t lda,
+                     const float* a_scale, std::uint32_t tokens, float* y,
+                     std::uint32_t ldy, std::uint32_t parts, void* stream) {
+  return Gemm(halves, true, scales, rows, cols, a, lda, a_scale, tokens, y, ldy, parts, stream);
 }
 
 int lfm3_sum_parts(float* y, std::size_t part_stride, std::uint32_t rows,
@@ -627,15 +739,17 @@ int lfm3_q8_gemm_swiglu(const void* codes, const void* scales,
                         const std::uint16_t* a, std::uint32_t lda,
                         const float* a_scale, std::uint32_t tokens, float* y,
                         std::uint32_t ldy, unsigned* row_max, void* stream) {
-  if (!codes || !scales || !a || !a_scale || !y || !rows || !cols ||
-      cols % 32 || !tokens || lda % 64 || lda < Chunks(cols) * kChunk ||
-      ldy < rows || (reinterpret_cast<std::uintptr_t>(a) & 15) ||
-      !GemmOperandsFit(2 * RowTiles(rows), Chunks(cols), tokens, lda, ldy))
-    return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 prompt SwiGLU shape");
-  LaunchGemm<true, WideShape>(codes, scales, int(2 * RowTiles(rows)), int(Chunks(cols)), a, lda,
-                   a_scale, tokens, y, ldy, rows, 1, 0, row_max,
-                   static_cast<hipStream_t>(stream));
-  return HipStatus(hipGetLastError(), "LFM3 Q8_0 prompt SwiGLU launch");
+  return GemmSwiGLU(codes, false, scales, rows, cols, a, lda, a_scale, tokens, y, ldy, row_max,
+                    stream);
+}
+
+int lfm3_q8_gemm_swiglu_h16(const void* halves, const void* scales,
+                            std::uint32_t rows, std::uint32_t cols,
+                            const std::uint16_t* a, std::uint32_t lda,
+                            const float* a_scale, std::uint32_t tokens, float* y,
+                            std::uint32_t ldy, unsigned* row_max, void* stream) {
+  return GemmSwiGLU(halves, true, scales, rows, cols, a, lda, a_scale, tokens, y, ldy, row_max,
+                    stream);
 }
 
 }  // extern "C"

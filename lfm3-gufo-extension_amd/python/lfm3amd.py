@@ -69,6 +69,10 @@ _SIGS = {
     "lfm3_q8_gemm_parts": (u32, [u32, u32, u32, i32]),
     "lfm3_q8_gemm": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, vp, u32, u32, vp]),
     "lfm3_q8_gemm_swiglu": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, vp, u32, vp, vp]),
+    "lfm3_q8_half_tiles_bytes": (sz, [u32, u32]),
+    "lfm3_q8_half_tiles": (i32, [vp, u32, u32, vp, vp]),
+    "lfm3_q8_gemm_h16": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, vp, u32, u32, vp]),
+    "lfm3_q8_gemm_swiglu_h16": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, vp, u32, vp, vp]),
     "lfm3_q8_gemv_swiglu": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, u32, vp, sz, vp]),
     "lfm3_residual_norm": (i32, [vp, vp, vp, vp, vp, u32, u32, f32, vp]),
     "lfm3_embed": (i32, [vp, vp, u32, u32, vp, u32, vp, vp]),

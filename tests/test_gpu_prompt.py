@@ -44,23 +44,34 @@ def test_half_rows_bit_exact(n, K):
     assert np.array_equal(got.astype(np.float32), inputs)
 
 
-def gemm(m: DeviceMatrix, x, parts=None, swiglu=False):
+def half_tiles(m: DeviceMatrix, rows=None):
+    """The FP16 tiles of a device matrix (lfm3_q8_half_tiles)."""
+    rows = rows or m.rows
+    out = L.DeviceBuffer(L.lib().lfm3_q8_half_tiles_bytes(rows, m.cols))
+    L.check(L.lib().lfm3_q8_half_tiles(m.codes.addr, rows, m.cols, out.addr, None))
+    L.synchronize()
+    return out
+
+
+def gemm(m: DeviceMatrix, x, parts=None, swiglu=False, half=False):
     n, K = x.shape
     da, ds, lda = half_rows_gpu(x)
     M = m.rows
     parts = parts or L.lib().lfm3_q8_gemm_parts(M, K, n, int(swiglu))
+    w = half_tiles(m, 2 * M if swiglu else M) if half else m.codes
     if swiglu:
         dy = L.DeviceBuffer(n * M * 4)
         blocks = L.lib().lfm3_q8_gemm_swiglu_max_blocks(M)
         rm = L.DeviceBuffer(blocks * n * 4)
-        L.check(L.lib().lfm3_q8_gemm_swiglu(m.codes.addr, m.scales.addr, M, K, da.addr, lda, ds.addr,
-                                            n, dy.addr, M, rm.addr, None))
+        fn = L.lib().lfm3_q8_gemm_swiglu_h16 if half else L.lib().lfm3_q8_gemm_swiglu
+        L.check(fn(w.addr, m.scales.addr, M, K, da.addr, lda, ds.addr, n, dy.addr, M, rm.addr,
+                   None))
         L.synchronize()
         return (dy.download(np.float32, n * M).reshape(n, M),
                 rm.download(np.uint32, blocks * n).reshape(blocks, n))
     dy = L.DeviceBuffer(parts * n * M * 4)
-    L.check(L.lib().lfm3_q8_gemm(m.codes.addr, m.scales.addr, M, K, da.addr, lda, ds.addr, n,
-                                 dy.addr, M, parts, None))
+    fn = L.lib().lfm3_q8_gemm_h16 if half else L.lib().lfm3_q8_gemm
+    L.check(fn(w.addr, m.scales.addr, M, K, da.addr, lda, ds.addr, n, dy.addr, M, parts, None))
     L.synchronize()
     y = dy.download(np.float32, parts * n * M).reshape(parts, n, M)
     out = y[0].copy()
@@ -122,3 +133,48 @@ def test_gemm_swiglu_and_row_max(F, K, n):
     db, dt, _ = half_rows_gpu(y, row_max=rm.reshape(-1), max_blocks=parts.shape[0])
     assert np.array_equal(da.download(np.uint16, n * lda), db.download(np.uint16, n * lda))
     assert np.array_equal(ds.download(np.float32, n), dt.download(np.float32, n))
+
+
+@pytest.mark.parametrize("M,K", [(37, 2048), (3088, 2048), (48, 96)])
+def test_half_tiles_layout(M, K):
+    """FP16 tile (t, c), lane L = 16 g + n: row 16 t + n, block 0's elements
+    64 c + 8 g .. + 7 at byte 16 L, block 1's (64 c + 32 + 8 g ..) at
+    1024 + 16 L, each the exact fp16 of the code; padding rows and columns
+    are zero."""
+    w = L.q8(SEED, f"ht.{M}.{K}", M, K)
+    m = DeviceMatrix(w, M, K)
+    got = half_tiles(m).download(np.uint16, L.lib().lfm3_q8_half_tiles_bytes(M, K) // 2)
+    tiles, chunks = -(-M // 16), -(-K // 64)
+    got = got.reshape(tiles, chunks, 2, 4, 16, 8)  # tile, chunk, block, g, n, element
+    codes = np.zeros((tiles * 16, chunks * 64), np.float32)
+    blocks = w.reshape(M, K // 32, 34)
+    codes[:M, :K] = blocks[:, :, 2:].view(np.int8).reshape(M, K).astype(np.float32)
+    want = codes.reshape(tiles, 16, chunks, 2, 4, 8).transpose(0, 2, 3, 4, 1, 5)
+    assert np.array_equal(got, O.float_to_half(np.ascontiguousarray(want)))
+
+
+@pytest.mark.parametrize("M,K,n,parts,swiglu", [(2048, 2048, 512, None, False),
+                                                (3088, 2048, 512, 1, False),
+                                                (6144, 2048, 130, None, False),
+                                                (2048, 7680, 64, 3, False),
+                                                (12288, 256, 500, 2, False),
+                                                (48, 96, 17, 2, False),
+                                                (7680, 2048, 512, None, True),
+                                                (192, 128, 20, None, True)])
+def test_gemm_half_tiles_identical(M, K, n, parts, swiglu):
+    """The GEMM over FP16 tiles takes the same operands, products and block
+    fmas as over code tiles: outputs (and SwiGLU row maxima) bit-exact, and
+    within the gate of FP64 over the same rounded inputs."""
+    g = L.q8(SEED, f"hg.{M}.{K}", M, K)
+    u = L.q8(SEED, f"hu.{M}.{K}", M, K) if swiglu else None
+    m = DeviceMatrix(g, M, K, interleave_with=u) if swiglu else DeviceMatrix(g, M, K)
+    x = L.normal(SEED, f"hg.x.{M}.{K}.{n}", n * K).reshape(n, K)
+    a = gemm(m, x, parts, swiglu=swiglu)
+    b = gemm(m, x, parts, swiglu=swiglu, half=True)
+    if swiglu:
+        assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+        return
+    assert np.array_equal(a, b)
+    inputs, _ = O.half_rows(x)
+    ok, err = within(b, inputs.astype(np.float64) @ L.q8_dequant(g, M, K).T)
+    assert ok, err
