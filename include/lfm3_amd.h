@@ -492,6 +492,18 @@ int lfm3_forward_batch(lfm3_session* const* sessions, size_t n,
    no logits cross PCIe. */
 int lfm3_forward_batch_greedy(lfm3_session* const* sessions, size_t n,
                               const uint32_t* tokens, uint32_t* ids);
+/* Session::ForwardBatchInputs (engine.cpp:1217-1299): the round of
+   lfm3_forward_batch where rows[i], when not NULL, is a device FP32 row of
+   hidden floats that stands in for session i's token embedding (tokens[i]
+   is then not checked); NULL entries use the token. With want_logits 0 the
+   vocabulary head is skipped: only the positions and the frontier rows
+   (LFM3_STATE_FRONTIER, Session::DeviceHidden) advance, and
+   lfm3_session_read_logits refuses until a round with logits. With
+   want_logits set, logits (may be NULL) receive host copies. A device
+   failure poisons every session of the batch. */
+int lfm3_forward_batch_inputs(lfm3_session* const* sessions, size_t n,
+                              const uint32_t* tokens, const float* const* rows,
+                              int want_logits, float* const* logits);
 /* Session::ReadLogits (engine.cpp) into host memory (vocab floats). */
 int lfm3_session_read_logits(const lfm3_session* session, float* logits);
 /* Stream of the model's batch rounds (Session::DeviceStream). */

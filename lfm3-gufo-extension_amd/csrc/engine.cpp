@@ -139,6 +139,7 @@ struct RoundTable {
   std::uint32_t positions[kMaxBatch];
   float* logits[kMaxBatch];
   float* frontier[kMaxBatch];
+  const float* inputs[kMaxBatch];  // FP32 input rows in place of tokens, or null
 };
 
 std::size_t Align(std::size_t n) { return (n + 255) / 256 * 256; }
@@ -566,7 +567,8 @@ namespace {
 
 // One decode round of n rows (engine.cpp:257-527, batch branch).
 void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
-              const std::uint32_t* tokens, bool greedy) {
+              const std::uint32_t* tokens, bool greedy, const float* const* inputs = nullptr,
+              bool head = true) {
   const auto& c = m.config;
   const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
   const std::uint32_t L = c.n_layers;
@@ -599,6 +601,7 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
   for (std::uint32_t i = 0; i < n; ++i) {
     lfm3_session& se = *sessions[i];
     rt->tokens[i] = tokens[i];
+    rt->inputs[i] = inputs ? inputs[i] : nullptr;
     rt->positions[i] = se.position;
     rt->logits[i] = se.logits.as<float>();
     rt->frontier[i] = se.frontier.as<float>();
@@ -670,9 +673,11 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
   na.emb_codes = static_cast<const std::uint8_t*>(m.embedding.codes.p);
   na.emb_scales = static_cast<const std::uint16_t*>(m.embedding.scales.p);
   na.tokens = d_rt->tokens;
+  na.inputs = inputs ? d_rt->inputs : nullptr;
   na.vocab = int(c.vocab);
   norm_image(0, nullptr, m.layers[0].norm.as<float>(), nullptr);
   na.tokens = nullptr;
+  na.inputs = nullptr;
   for (std::uint32_t il = 0; il < L; ++il) {
     const Layer& l = m.layers[il];
     if (l.type == LFM3_LAYER_CONV) {
@@ -713,17 +718,19 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
   }
   // LM head over the final-normed rows into each session's logits row, with
   // per-block greedy candidates; then the greedy ids from the candidates.
-  const Matrix& head = m.head();
-  auto* keys = m.head_keys.as<unsigned long long>();
-  CheckStatus(LaunchHeadGemv(head.codes.p, head.scales.p, head.rows, head.cols, image, exps, n,
-                             d_rt->logits, keys, nullptr, s));
-  if (greedy)
-    CheckStatus(LaunchArgmaxKeys(keys, n, m.head_groups, m.ids.as<std::uint32_t>(), s));
+  if (head) {
+    const Matrix& w = m.head();
+    auto* keys = m.head_keys.as<unsigned long long>();
+    CheckStatus(LaunchHeadGemv(w.codes.p, w.scales.p, w.rows, w.cols, image, exps, n,
+                               d_rt->logits, keys, nullptr, s));
+    if (greedy)
+      CheckStatus(LaunchArgmaxKeys(keys, n, m.head_groups, m.ids.as<std::uint32_t>(), s));
+  }
   Check(hipGetLastError(), "round launch");
   Check(hipStreamSynchronize(s), "round");
   for (std::uint32_t i = 0; i < n; ++i) {
     ++sessions[i]->position;
-    sessions[i]->logits_ready = true;
+    sessions[i]->logits_ready = head;
   }
 }
 
@@ -1042,25 +1049,28 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
 }
 
 // engine.cpp:1178-1195.
+// engine.cpp:1244-1259: a token is checked only where no input row
+// stands in for it.
 void ValidateBatch(lfm3_session* const* sessions, std::size_t n,
-                   const std::uint32_t* tokens) {
+                   const std::uint32_t* tokens, const float* const* inputs = nullptr) {
   if (!sessions || !tokens || n == 0 || n > kMaxBatch)
     Invalid("invalid LFM3 decode batch shape");
   for (std::size_t i = 0; i < n; ++i) {
     lfm3_session* se = sessions[i];
     if (!se || std::find(sessions, sessions + i, se) != sessions + i)
       Invalid("duplicate or null LFM3 batch session");
+    const bool row = inputs && inputs[i];
     if (se->poisoned || se->position >= se->context ||
-        tokens[i] >= se->model->config.vocab || se->model != sessions[0]->model)
+        (!row && tokens[i] >= se->model->config.vocab) || se->model != sessions[0]->model)
       Invalid("incompatible LFM3 batch session");
   }
 }
 
 int BatchEntry(lfm3_session* const* sessions, std::size_t n,
                const std::uint32_t* tokens, float* const* logits,
-               std::uint32_t* ids) {
+               std::uint32_t* ids, const float* const* inputs = nullptr, bool head = true) {
   try {
-    ValidateBatch(sessions, n, tokens);
+    ValidateBatch(sessions, n, tokens, inputs);
     if (logits)
       for (std::size_t i = 0; i < n; ++i)
         if (!logits[i])
@@ -1070,7 +1080,7 @@ int BatchEntry(lfm3_session* const* sessions, std::size_t n,
   }
   lfm3_model& m = *sessions[0]->model;
   try {
-    RunRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr);
+    RunRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr, inputs, head);
     if (logits)
       for (std::size_t i = 0; i < n; ++i)
         CopyLogits(m, logits[i], sessions[i]->logits.p);
@@ -1147,6 +1157,14 @@ int lfm3_forward_batch_greedy(lfm3_session* const* sessions, std::size_t n,
   if (!ids)
     return Fail(LFM3_E_INVALID, "null greedy ids");
   return BatchEntry(sessions, n, tokens, nullptr, ids);
+}
+
+int lfm3_forward_batch_inputs(lfm3_session* const* sessions, std::size_t n,
+                              const std::uint32_t* tokens, const float* const* rows,
+                              int want_logits, float* const* logits) {
+  if (!rows || (logits && !want_logits))
+    return Fail(LFM3_E_INVALID, "invalid LFM3 decode batch shape");
+  return BatchEntry(sessions, n, tokens, logits, nullptr, rows, want_logits != 0);
 }
 
 }  // extern "C"

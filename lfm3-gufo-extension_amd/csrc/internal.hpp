@@ -28,6 +28,9 @@ struct NormImageArgs {
   const std::uint16_t* emb_scales = nullptr;
   const std::uint32_t* tokens = nullptr;
   int vocab = 0;
+  // With tokens: row r's input is inputs[r] (H floats in device memory)
+  // when the table entry is not null, else embedding row tokens[r].
+  const float* const* inputs = nullptr;
   // The prompt GEMM's FP16 rows instead of (or beside) the image.
   std::uint16_t* a16 = nullptr;
   int lda = 0;

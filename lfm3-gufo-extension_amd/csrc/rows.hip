@@ -221,16 +221,22 @@ __launch_bounds__(kImageNormThreads) __global__ void NormImageKernel(const NormI
   // (EmbedKernel's layout: columns 8G..8G+7 of row r are 8 consecutive code
   // bytes of one lane word) and writes them to x.
   std::uint32_t token = 0;
+  const float* input = nullptr;  // an FP32 input row in place of the token
   if (a.tokens) {
     token = a.tokens[row];
     if (token >= std::uint32_t(a.vocab))
       token = 0;  // the host validates ids; never read out of bounds
+    if (a.inputs)
+      input = a.inputs[row];
   }
+  const BufferResource in_res = MakeBuffer(input, input ? row_bytes : 0u);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int g = tid + kImageNormThreads * i;
     const unsigned off = g * 8 < H ? unsigned(g) * 32 : kOutOfRange;
-    if (a.tokens) {
+    if (input) {
+      load8(in_res, off, v[i]);
+    } else if (a.tokens) {
       const int chunk = g / 8, blk = (g % 8) / 4, lg = g % 4;
       const std::size_t tile = std::size_t(token / kTileRows) * ((H + kChunk - 1) / kChunk) + chunk;
       const int nn = int(token % kTileRows);

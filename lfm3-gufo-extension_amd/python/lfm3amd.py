@@ -111,6 +111,7 @@ _SIGS = {
     "lfm3_session_forward": (i32, [vp, vp, sz, vp]),
     "lfm3_forward_batch": (i32, [vp, sz, vp, vp]),
     "lfm3_forward_batch_greedy": (i32, [vp, sz, vp, vp]),
+    "lfm3_forward_batch_inputs": (i32, [vp, sz, vp, vp, i32, vp]),
     "lfm3_session_read_logits": (i32, [vp, vp]),
     "lfm3_synth_key": (u64, [u64, C.c_char_p]),
     "lfm3_synth_normal": (None, [u64, f32, f32, vp, sz]),
@@ -327,6 +328,22 @@ class Model:
 
     def forward_batch_greedy(self, sessions, tokens):
         return self.forward_batch(sessions, tokens, want_logits=False)
+
+    def forward_batch_inputs(self, sessions, tokens, rows, want_logits=True):
+        """Session::ForwardBatchInputs: rows[i] is a device address of an
+        FP32 hidden row standing in for token i, or 0 to use the token.
+        Returns (n, vocab) float32 logits, or None without logits."""
+        n = len(sessions)
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        handles = (vp * max(n, 1))(*[s.handle for s in sessions])
+        inputs = (vp * max(n, 1))(*[r or None for r in rows])
+        out, dst = None, None
+        if want_logits:
+            out = np.empty((n, self.dims.vocab), np.float32)
+            dst = (vp * max(n, 1))(*[out[i].ctypes.data for i in range(n)])
+        check(lib().lfm3_forward_batch_inputs(handles, n, ptr(toks), inputs, int(want_logits),
+                                              dst))
+        return out
 
 
 class Session:

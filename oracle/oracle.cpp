@@ -387,15 +387,20 @@ float* orc_session_v(orc_session* s, uint32_t layer) {
 }
 
 // reference.cpp:72-168.
-int orc_session_step(orc_session* s, uint32_t token, float* logits,
-                     float* hidden) {
+}  // extern "C"
+
+namespace {
+
+// reference.cpp:72-168 from the step's input row x0 (the token's embedding
+// row, or a caller's row in place of it: Session::ForwardBatchInputs,
+// engine.cpp:1217-1299, copies such a row over the embedding).
+int Step(orc_session* s, const float* x0, float* logits, float* hidden) {
   const orc_model& m = *s->model;
   const auto& c = m.config;
-  if (token >= c.vocab || s->position >= s->context)
+  if (s->position >= s->context)
     return -1;
   const uint32_t H = c.hidden, D = c.head_dim;
-  std::vector<float> x(H), z(H), out(H);
-  DecodeRow(m.global(ORC_EMBEDDING), token, x.data());
+  std::vector<float> x(x0, x0 + H), z(H), out(H);
   for (uint32_t il = 0; il < c.n_layers; ++il) {
     auto& st = s->states[il];
     z = x;
@@ -447,15 +452,37 @@ int orc_session_step(orc_session* s, uint32_t token, float* logits,
     for (uint32_t i = 0; i < H; ++i)
       x[i] += out[i];
   }
-  if (logits) {
+  if (logits || hidden) {
     Norm(x.data(), H, static_cast<const float*>(m.global(ORC_OUTPUT_NORM).data),
          c.eps);
     if (hidden)
       std::copy(x.begin(), x.end(), hidden);
-    Mat(m.global(ORC_OUTPUT), x.data(), logits);
+    if (logits)
+      Mat(m.global(ORC_OUTPUT), x.data(), logits);
   }
   ++s->position;
   return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int orc_session_step(orc_session* s, uint32_t token, float* logits,
+                     float* hidden) {
+  const orc_model& m = *s->model;
+  if (token >= m.config.vocab || s->position >= s->context)
+    return -1;
+  std::vector<float> x(m.config.hidden);
+  DecodeRow(m.global(ORC_EMBEDDING), token, x.data());
+  return Step(s, x.data(), logits, hidden);
+}
+
+int orc_session_step_row(orc_session* s, const float* row, float* logits,
+                         float* hidden) {
+  if (!row)
+    return -1;
+  return Step(s, row, logits, hidden);
 }
 
 }  // extern "C"

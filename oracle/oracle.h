@@ -142,10 +142,15 @@ float* orc_session_k(orc_session* s, uint32_t layer);
 float* orc_session_v(orc_session* s, uint32_t layer);
 /* reference.cpp:72-168. Returns 0, or -1 on an invalid step (token out of
    range or context exhausted), leaving state untouched. logits may be NULL.
-   hidden (may be NULL) receives the final-normed row when logits are
-   requested. */
+   hidden (may be NULL) receives the final-normed row. */
 int orc_session_step(orc_session* s, uint32_t token, float* logits,
                      float* hidden);
+/* The same step from a caller's FP32 input row (hidden floats) in place of
+   the token's embedding row (Session::ForwardBatchInputs,
+   engine.cpp:1217-1299). hidden receives the final-normed row whenever it
+   is not NULL. */
+int orc_session_step_row(orc_session* s, const float* row, float* logits,
+                         float* hidden);
 
 #ifdef __cplusplus
 }

@@ -59,6 +59,7 @@ _SIGS = {
     "orc_session_k": (C.POINTER(C.c_float), [vp, u32]),
     "orc_session_v": (C.POINTER(C.c_float), [vp, u32]),
     "orc_session_step": (i32, [vp, u32, vp, vp]),
+    "orc_session_step_row": (i32, [vp, vp, vp, vp]),
 }
 
 _lib = None
@@ -276,3 +277,14 @@ class Session:
         if lib().orc_session_step(self.handle, token, 0 if out is None else _p(out), 0) != 0:
             raise ValueError("invalid oracle step")
         return out
+
+    def step_row(self, row, logits: bool = True):
+        """One step from an FP32 input row in place of a token's embedding
+        row; returns (logits or None, final-normed hidden row)."""
+        row = np.ascontiguousarray(row, np.float32)
+        out = np.empty(self.model.dims.vocab, np.float32) if logits else None
+        hidden = np.empty(self.model.dims.hidden, np.float32)
+        if lib().orc_session_step_row(self.handle, _p(row), 0 if out is None else _p(out),
+                                      _p(hidden)) != 0:
+            raise ValueError("invalid oracle step")
+        return out, hidden

@@ -144,3 +144,60 @@ def test_full_reference_dims_round():
         print(f"row {i}: max |logit - oracle| = {err:.3g}, top-2 margin {margin(want):.3g}")
         assert err < 2e-3
         assert int(np.argmax(logits[i])) == O.argmax(want)
+
+
+def test_forward_batch_inputs_rows_and_tokens():
+    """Session::ForwardBatchInputs (engine.cpp:1217-1299): device FP32 rows
+    stand in for some sessions' token embeddings. Rows equal to the token's
+    dequantized embedding row give the token round exactly; arbitrary rows
+    match the oracle stepping from the same row; out-of-range tokens are
+    accepted where a row replaces them."""
+    dims = small_dims()
+    n = 6
+    positions = L.uniform_u32(SEED, "inp.pos", n, 0, 600)
+    w, gm, om, gs, os_ = build(dims, 31, positions, 1024)
+    _, gm2, _, gs2, _ = build(dims, 31, positions, 1024)
+    emb = L.q8_dequant(w.globals[0][0], dims.vocab, dims.hidden).astype(np.float32)
+    toks = L.uniform_u32(SEED, "inp.tok", n, 0, dims.vocab - 1)
+    # Embedding rows in place of tokens 0, 2, 4: identical to the token round.
+    erows = [L.DeviceBuffer.of(emb[int(toks[i])]) if i % 2 == 0 else None for i in range(n)]
+    want = gm2.forward_batch(gs2, toks)
+    got = gm.forward_batch_inputs(gs, toks, [r.addr if r else 0 for r in erows])
+    assert np.array_equal(got, want)
+    for i in range(n):
+        os_[i].step(int(toks[i]), logits=False)
+    # Arbitrary rows (and a token id past the vocabulary under a row).
+    rows = [L.normal(SEED, f"inp.row{i}", dims.hidden) * np.float32(0.05) for i in range(n)]
+    drows = [L.DeviceBuffer.of(r) if i != 1 else None for i, r in enumerate(rows)]
+    toks2 = L.uniform_u32(SEED, "inp.tok2", n, 0, dims.vocab - 1)
+    toks2[0] = dims.vocab + 5
+    got = gm.forward_batch_inputs(gs, toks2, [r.addr if r else 0 for r in drows])
+    for i in range(n):
+        if drows[i] is None:
+            ref = os_[i].step(int(toks2[i]))
+        else:
+            ref, _ = os_[i].step_row(rows[i])
+        err = float(np.max(np.abs(got[i] - ref)))
+        assert err < 2e-3, (i, err)
+        assert gs[i].position == os_[i].position
+    # Without logits: positions and frontier rows advance, logits are refused.
+    got = gm.forward_batch_inputs(gs, toks, [r.addr if r else 0 for r in drows],
+                                  want_logits=False)
+    assert got is None
+    for i in range(n):
+        _, hidden = (os_[i].step(int(toks[i]), logits=False), None) if drows[i] is None \
+            else os_[i].step_row(rows[i], logits=False)
+        ptr, nbytes = gs[i].state(L.STATE_FRONTIER)
+        front = L.download_from(ptr, np.float32, dims.hidden)
+        if hidden is not None:
+            assert np.max(np.abs(front - hidden)) < 2e-4 * max(1.0, np.max(np.abs(hidden)))
+        assert gs[i].position == os_[i].position
+        with pytest.raises(L.LFM3Error):
+            gs[i].read_logits()
+    # A token past the vocabulary without a row is refused, state untouched.
+    before = [s.position for s in gs]
+    bad = toks.copy()
+    bad[3] = dims.vocab
+    with pytest.raises(L.LFM3Error):
+        gm.forward_batch_inputs(gs, bad, [0] * n)
+    assert [s.position for s in gs] == before and all(s.coherent() for s in gs)

@@ -296,6 +296,31 @@ def test_state_injection_reproduces_stepping():
     model.close()
 
 
+def test_step_row_with_embedding_row_is_the_token_step():
+    """ForwardBatchInputs' row path (engine.cpp:1217-1299 copies the row over
+    the embedding): the step from the token's dequantized embedding row is
+    the token step, bit for bit; the hidden row is the final-normed row the
+    logits come from (the tied head applied to it gives the logits)."""
+    dims = tiny_dims()
+    w = L.synth_weights(dims, seed=13)
+    model = O.Model(dims, w)
+    a, b = model.session(64), model.session(64)
+    emb = L.q8_dequant(w.globals[0][0], dims.vocab, dims.hidden).astype(np.float32)
+    for tok in (3, 200, 17, 299, 0, 42, 8, 91, 150):
+        want = a.step(tok)
+        got, hidden = b.step_row(emb[tok])
+        assert np.array_equal(got, want)
+        head = emb.astype(np.float64) @ hidden.astype(np.float64)
+        assert np.max(np.abs(head - want)) < 1e-4 * max(1.0, np.max(np.abs(want)))
+    # a row that is no embedding row moves the state differently
+    _, h1 = a.step_row(np.full(dims.hidden, 0.25, np.float32))
+    _, h2 = b.step_row(np.full(dims.hidden, -0.25, np.float32))
+    assert not np.array_equal(h1, h2)
+    _, none = b.step_row(np.ones(dims.hidden, np.float32), logits=False)
+    assert none.shape == (dims.hidden,) and a.position == b.position - 1
+    model.close()
+
+
 def test_f16_switch_stores_binary16_rows():
     dims = tiny_dims()
     w = L.synth_weights(dims, seed=13)
