@@ -504,8 +504,25 @@ int lfm3_forward_batch_greedy(lfm3_session* const* sessions, size_t n,
 int lfm3_forward_batch_inputs(lfm3_session* const* sessions, size_t n,
                               const uint32_t* tokens, const float* const* rows,
                               int want_logits, float* const* logits);
-/* Session::ReadLogits (engine.cpp) into host memory (vocab floats). */
+/* Session::ReadLogits (engine.cpp:1433-1463) into host memory (vocab
+   floats). Refuses a poisoned session or one at position 0; after a round
+   or prompt without logits, the vocabulary head first runs on the
+   frontier row (Session::Impl::EnsureLogits, engine.cpp:237-245). */
 int lfm3_session_read_logits(const lfm3_session* session, float* logits);
+/* Snapshot v2 (Session::SnapshotBytes / SaveSnapshot / RestoreSnapshot,
+   engine.cpp:1387-1574), byte-compatible with the reference's: a 32-byte
+   header of little-endian words (0x334d464c, 2, context, position, hidden,
+   vocab, layers, FNV-1a signature of the configuration), the frontier row
+   and the logits (zeros at position 0), then per layer the convolution
+   history or the first min(position, capacity) K ring slots then V slots
+   in physical order. Save refuses a poisoned session (LFM3_E_STATE) and a
+   buffer of another size; restore checks the whole header and the size
+   before it changes anything (LFM3_E_INVALID), and a failed copy poisons
+   the session. */
+size_t lfm3_session_snapshot_bytes(const lfm3_session* session);
+int lfm3_session_save_snapshot(lfm3_session* session, void* out, size_t bytes);
+int lfm3_session_restore_snapshot(lfm3_session* session, const void* data,
+                                  size_t bytes);
 /* Stream of the model's batch rounds (Session::DeviceStream). */
 void* lfm3_model_stream(lfm3_model* model);
 

@@ -550,14 +550,193 @@ int lfm3_session_set_position(lfm3_session* s, std::uint32_t position) {
   return LFM3_OK;
 }
 
+}  // extern "C"
+
+namespace lfm3amd {
+namespace {
+
+// Session::Impl::EnsureLogits (engine.cpp:237-245): a round or prompt that
+// skipped the vocabulary head leaves the frontier row; the head runs on it
+// when logits are first wanted.
+void EnsureLogits(lfm3_session& se) {
+  if (se.logits_ready)
+    return;
+  lfm3_model& m = *se.model;
+  const auto& c = m.config;
+  const Matrix& head = m.head();
+  CheckStatus(lfm3_q8_gemv(head.codes.p, head.scales.p, c.vocab, c.hidden,
+                           se.frontier.as<float>(), c.hidden, se.logits.as<float>(), c.vocab, 1,
+                           nullptr, 0, m.stream));
+  Check(hipStreamSynchronize(m.stream), "logits");
+  se.logits_ready = true;
+}
+
+// Snapshot v2 (engine.cpp:1387-1574): a 32-byte header of little-endian
+// words (magic "LFM3", version 2, context, position, hidden, vocab, layers,
+// configuration signature), the frontier row and the logits (zeros at
+// position 0), then per layer the convolution history [hidden][width - 1]
+// f32, or the K rows then the V rows of the ring's first min(position,
+// capacity) slots in physical order (F16 [slot][kv_heads][head_dim]).
+constexpr std::uint32_t kSnapshotMagic = 0x334d464c, kSnapshotVersion = 2;
+constexpr std::size_t kSnapshotHeaderBytes = 32;
+
+// FNV-1a over the little-endian bytes of the configuration words
+// (engine.cpp ConfigSignature): restores refuse a snapshot of another shape.
+std::uint32_t ConfigSignature(const lfm3_config& c) {
+  std::uint32_t hash = 2166136261u;
+  const auto mix = [&](std::uint32_t value) {
+    for (int i = 0; i < 4; ++i)
+      hash = (hash ^ ((value >> (8 * i)) & 255u)) * 16777619u;
+  };
+  for (std::uint32_t value :
+       {c.hidden, c.intermediate, c.vocab, c.heads, c.head_dim, c.window, c.conv_width,
+        __builtin_bit_cast(std::uint32_t, c.eps), __builtin_bit_cast(std::uint32_t, c.theta),
+        __builtin_bit_cast(std::uint32_t, c.theta_swa)})
+    mix(value);
+  for (std::uint32_t i = 0; i < c.n_layers; ++i) {
+    mix(c.layer_type[i]);
+    mix(c.kv_heads[i]);
+  }
+  return hash;
+}
+
+std::size_t RingBytes(const lfm3_config& c, std::uint32_t layer, std::uint32_t slots) {
+  return std::size_t(slots) * c.kv_heads[layer] * c.head_dim * sizeof(Half);
+}
+
+std::size_t StateBytes(const lfm3_config& c, std::uint32_t position) {
+  std::size_t bytes = kSnapshotHeaderBytes + (std::size_t(c.hidden) + c.vocab) * 4;
+  for (std::uint32_t i = 0; i < c.n_layers; ++i)
+    bytes += c.layer_type[i] == LFM3_LAYER_CONV
+                 ? std::size_t(c.hidden) * (c.conv_width - 1) * 4
+                 : 2 * RingBytes(c, i,
+                                 c.layer_type[i] == LFM3_LAYER_SLIDING
+                                     ? std::min(position, c.window)
+                                     : position);
+  return bytes;
+}
+
+void PutWord(std::uint8_t* p, std::size_t word, std::uint32_t value) {
+  for (int i = 0; i < 4; ++i)
+    p[word * 4 + i] = std::uint8_t(value >> (8 * i));
+}
+std::uint32_t GetWord(const std::uint8_t* p, std::size_t word) {
+  std::uint32_t value = 0;
+  for (int i = 0; i < 4; ++i)
+    value |= std::uint32_t(p[word * 4 + i]) << (8 * i);
+  return value;
+}
+
+}  // namespace
+}  // namespace lfm3amd
+
+extern "C" {
+
 int lfm3_session_read_logits(const lfm3_session* s, float* logits) {
   if (!s || !logits)
     return Fail(LFM3_E_INVALID, "null logits");
-  if (!s->logits_ready)
-    return Fail(LFM3_E_STATE, "LFM3 session has no logits");
+  // engine.cpp Session::ReadLogits: a poisoned session or one without a
+  // frontier row has no logits.
+  if (s->poisoned || !s->position)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 logit frontier");
+  try {
+    EnsureLogits(const_cast<lfm3_session&>(*s));
+  } catch (const Error& e) {
+    return Fail(e.status, e.what());
+  }
   return HipStatus(hipMemcpy(logits, s->logits.p, std::size_t(s->model->config.vocab) * 4,
                              hipMemcpyDeviceToHost),
                    "read logits");
+}
+
+std::size_t lfm3_session_snapshot_bytes(const lfm3_session* s) {
+  return s ? StateBytes(s->model->config, s->position) : 0;
+}
+
+int lfm3_session_save_snapshot(lfm3_session* s, void* out, std::size_t bytes) {
+  if (!s || !out || bytes != lfm3_session_snapshot_bytes(s))
+    return Fail(LFM3_E_INVALID, "invalid LFM3 snapshot buffer");
+  if (s->poisoned)
+    return Fail(LFM3_E_STATE, "cannot snapshot a poisoned LFM3 session");
+  const auto& c = s->model->config;
+  auto* p = static_cast<std::uint8_t*>(out);
+  try {
+    if (s->position)
+      EnsureLogits(*s);
+    const std::uint32_t header[8] = {kSnapshotMagic, kSnapshotVersion, s->context,
+                                     s->position,    c.hidden,         c.vocab,
+                                     c.n_layers,     ConfigSignature(c)};
+    for (std::size_t i = 0; i < 8; ++i)
+      PutWord(p, i, header[i]);
+    std::size_t offset = kSnapshotHeaderBytes;
+    const auto copy = [&](const void* source, std::size_t size) {
+      if (size)
+        Check(hipMemcpy(p + offset, source, size, hipMemcpyDeviceToHost), "snapshot copy");
+      offset += size;
+    };
+    if (s->position) {
+      copy(s->frontier.p, std::size_t(c.hidden) * 4);
+      copy(s->logits.p, std::size_t(c.vocab) * 4);
+    } else {
+      std::memset(p + offset, 0, (std::size_t(c.hidden) + c.vocab) * 4);
+      offset += (std::size_t(c.hidden) + c.vocab) * 4;
+    }
+    for (std::uint32_t i = 0; i < c.n_layers; ++i) {
+      const auto& st = s->states[i];
+      if (st.conv.p) {
+        copy(st.conv.p, std::size_t(c.hidden) * (c.conv_width - 1) * 4);
+      } else {
+        const std::size_t size = RingBytes(c, i, std::min(s->position, st.capacity));
+        copy(st.k.p, size);
+        copy(st.v.p, size);
+      }
+    }
+    return LFM3_OK;
+  } catch (const Error& e) {
+    return Fail(e.status, e.what());
+  }
+}
+
+int lfm3_session_restore_snapshot(lfm3_session* s, const void* data, std::size_t bytes) {
+  if (!s || !data)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 snapshot payload");
+  const auto& c = s->model->config;
+  const auto* p = static_cast<const std::uint8_t*>(data);
+  // The whole header and the size are checked before any state changes.
+  if (bytes < kSnapshotHeaderBytes || GetWord(p, 0) != kSnapshotMagic ||
+      GetWord(p, 1) != kSnapshotVersion || GetWord(p, 2) != s->context ||
+      GetWord(p, 3) > s->context || GetWord(p, 4) != c.hidden || GetWord(p, 5) != c.vocab ||
+      GetWord(p, 6) != c.n_layers || GetWord(p, 7) != ConfigSignature(c) ||
+      bytes != StateBytes(c, GetWord(p, 3)))
+    return Fail(LFM3_E_INVALID, "invalid LFM3 snapshot payload");
+  const std::uint32_t position = GetWord(p, 3);
+  std::size_t offset = kSnapshotHeaderBytes;
+  try {
+    const auto copy = [&](void* destination, std::size_t size) {
+      if (size)
+        Check(hipMemcpy(destination, p + offset, size, hipMemcpyHostToDevice), "restore copy");
+      offset += size;
+    };
+    copy(s->frontier.p, std::size_t(c.hidden) * 4);
+    copy(s->logits.p, std::size_t(c.vocab) * 4);
+    for (std::uint32_t i = 0; i < c.n_layers; ++i) {
+      auto& st = s->states[i];
+      if (st.conv.p) {
+        copy(st.conv.p, std::size_t(c.hidden) * (c.conv_width - 1) * 4);
+      } else {
+        const std::size_t size = RingBytes(c, i, std::min(position, st.capacity));
+        copy(st.k.p, size);
+        copy(st.v.p, size);
+      }
+    }
+  } catch (const Error& e) {
+    s->poisoned = true;  // a partial restore leaves no coherent state
+    return Fail(e.status, e.what());
+  }
+  s->position = position;
+  s->logits_ready = position != 0;
+  s->poisoned = false;
+  return LFM3_OK;
 }
 
 }  // extern "C"
@@ -1048,9 +1227,8 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
   se.logits_ready = want_logits;
 }
 
-// engine.cpp:1178-1195.
-// engine.cpp:1244-1259: a token is checked only where no input row
-// stands in for it.
+// engine.cpp:1178-1195; for ForwardBatchInputs (engine.cpp:1244-1259) a
+// token is checked only where no input row stands in for it.
 void ValidateBatch(lfm3_session* const* sessions, std::size_t n,
                    const std::uint32_t* tokens, const float* const* inputs = nullptr) {
   if (!sessions || !tokens || n == 0 || n > kMaxBatch)

@@ -113,6 +113,9 @@ _SIGS = {
     "lfm3_forward_batch_greedy": (i32, [vp, sz, vp, vp]),
     "lfm3_forward_batch_inputs": (i32, [vp, sz, vp, vp, i32, vp]),
     "lfm3_session_read_logits": (i32, [vp, vp]),
+    "lfm3_session_snapshot_bytes": (sz, [vp]),
+    "lfm3_session_save_snapshot": (i32, [vp, vp, sz]),
+    "lfm3_session_restore_snapshot": (i32, [vp, vp, sz]),
     "lfm3_synth_key": (u64, [u64, C.c_char_p]),
     "lfm3_synth_normal": (None, [u64, f32, f32, vp, sz]),
     "lfm3_synth_uniform_u32": (None, [u64, u32, u32, vp, sz]),
@@ -392,6 +395,18 @@ class Session:
         out = np.empty(self.model.dims.vocab, np.float32)
         check(lib().lfm3_session_read_logits(self.handle, ptr(out)))
         return out
+
+    def save_snapshot(self) -> bytes:
+        """Session::SaveSnapshot: the snapshot v2 bytes."""
+        out = np.empty(lib().lfm3_session_snapshot_bytes(self.handle), np.uint8)
+        check(lib().lfm3_session_save_snapshot(self.handle, ptr(out), out.size))
+        return out.tobytes()
+
+    def restore_snapshot(self, data: bytes):
+        """Session::RestoreSnapshot."""
+        buf = np.frombuffer(data, np.uint8).copy()
+        check(lib().lfm3_session_restore_snapshot(self.handle, ptr(buf) if buf.size else None,
+                                                  buf.size))
 
 
 # ------------------------------------------------------------ device memory

@@ -211,3 +211,20 @@ def test_projection_conv_rejects_bad_shapes():
                                        None) == L.E_INVALID  # width 1
     assert lib.lfm3_q8_gemv_conv_image(1, 1, 2056, 16, 1, 1, 1, 1, 7, 1, 2056,
                                        None) == L.E_INVALID  # 2056 % 16
+
+
+def test_snapshot_signature_is_fnv1a32():
+    """The snapshot's configuration signature is 32-bit FNV-1a
+    (engine.cpp ConfigSignature): the published test vectors, and the word
+    order of the configuration bytes."""
+    import struct
+
+    from snapshot_format import fnv1a32, signature
+    assert fnv1a32(b"") == 0x811C9DC5
+    assert fnv1a32(b"a") == 0xE40C292C
+    assert fnv1a32(b"foobar") == 0xBF9CF968
+    d = L.Dims(hidden=256, intermediate=512, vocab=1000, context=64, heads=8, head_dim=128,
+               kv_heads=2, window=32, pattern="CG")
+    raw = struct.pack("<7I3f", 256, 512, 1000, 8, 128, 32, 7, d.eps, d.theta, d.theta_swa)
+    raw += struct.pack("<4I", L.LAYER_CONV, 0, L.LAYER_FULL, 2)
+    assert signature(d) == fnv1a32(raw)

@@ -180,20 +180,23 @@ def test_forward_batch_inputs_rows_and_tokens():
         err = float(np.max(np.abs(got[i] - ref)))
         assert err < 2e-3, (i, err)
         assert gs[i].position == os_[i].position
-    # Without logits: positions and frontier rows advance, logits are refused.
+    # Without logits: positions and frontier rows advance; reading logits
+    # then runs the head on the frontier row (EnsureLogits, engine.cpp:237-245).
     got = gm.forward_batch_inputs(gs, toks, [r.addr if r else 0 for r in drows],
                                   want_logits=False)
     assert got is None
     for i in range(n):
-        _, hidden = (os_[i].step(int(toks[i]), logits=False), None) if drows[i] is None \
-            else os_[i].step_row(rows[i], logits=False)
+        if drows[i] is None:
+            ref, hidden = os_[i].step(int(toks[i])), None
+        else:
+            ref, hidden = os_[i].step_row(rows[i])
         ptr, nbytes = gs[i].state(L.STATE_FRONTIER)
         front = L.download_from(ptr, np.float32, dims.hidden)
         if hidden is not None:
             assert np.max(np.abs(front - hidden)) < 2e-4 * max(1.0, np.max(np.abs(hidden)))
         assert gs[i].position == os_[i].position
-        with pytest.raises(L.LFM3Error):
-            gs[i].read_logits()
+        err = float(np.max(np.abs(gs[i].read_logits() - ref)))
+        assert err < 2e-3, (i, err)
     # A token past the vocabulary without a row is refused, state untouched.
     before = [s.position for s in gs]
     bad = toks.copy()
