@@ -601,8 +601,11 @@ __global__ void StoreRingKernel(const Half* __restrict__ k16, const Half* __rest
 // [H][L - 1] (oldest first). A thread slides one channel's window down
 // kConvRows rows, forming each B x product once. The window sum keeps
 // ConvStepKernel's expressions and order (reference.cpp:85-101), so n
-// prompt rows give bit-identical outputs to n decode steps; the history
-// moves in a second launch, after every window has read it.
+// prompt rows give bit-identical outputs to n decode steps. For widths up
+// to kConvRows + 1 only the threads of a segment's first row group read its
+// old history, so they also write the new one (the segment's last L - 1
+// products, reaching into the old history when the segment is shorter),
+// after their own reads.
 constexpr int kConvRows = 16;
 constexpr int kMaxConvSegments = 8;
 struct ConvSegments {
@@ -611,10 +614,32 @@ struct ConvSegments {
   int rows[kMaxConvSegments];
 };
 
+// The new history of channel ch of a segment of `rows` rows (ps: its first
+// row of p): hist[j] = the B x product of row rows - (L - 1) + j, or the
+// old entry for a row before the segment. Every old entry is read before
+// the first write.
+template<int kMaxL>
+__device__ __forceinline__ void WriteConvHistory(const float* __restrict__ ps, int ldp, int H,
+                                                 int ch, int rows, float* hist, int L) {
+#pragma clang fp contract(off)
+  float past[kMaxL - 1];
+#pragma unroll
+  for (int j = 0; j < kMaxL - 1; ++j) {
+    const int r = rows - (L - 1) + j;
+    if (j < L - 1)
+      past[j] = r >= 0 ? ps[std::size_t(r) * ldp + ch] * ps[std::size_t(r) * ldp + 2 * H + ch]
+                       : hist[(L - 1) + r];
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxL - 1; ++j)
+    if (j < L - 1)
+      hist[j] = past[j];
+}
+
 template<int L>
 __global__ void PromptConvKernel(const float* __restrict__ p, int ldp,
                                  const float* __restrict__ taps, ConvSegments seg,
-                                 float* __restrict__ y, int ldy, int H) {
+                                 float* __restrict__ y, int ldy, int H, int update_history) {
 #pragma clang fp contract(off)
   const int s = blockIdx.z, ch = blockIdx.x * blockDim.x + threadIdx.x;
   const int first = blockIdx.y * kConvRows, rows = seg.rows[s];
@@ -622,7 +647,7 @@ __global__ void PromptConvKernel(const float* __restrict__ p, int ldp,
     return;
   const float* ps = p + std::size_t(seg.begin[s]) * ldp;
   float* ys = y + std::size_t(seg.begin[s]) * ldy;
-  const float* hist = seg.history[s] + std::size_t(ch) * (L - 1);
+  float* hist = seg.history[s] + std::size_t(ch) * (L - 1);
   // Every load of the thread's rows is issued before any arithmetic: the
   // L - 1 products before the first row (from p, or the history before the
   // segment) and B, C, x of each of its rows.
@@ -664,13 +689,16 @@ __global__ void PromptConvKernel(const float* __restrict__ p, int ldp,
     if (r < rows)
       ys[std::size_t(r) * ldy + ch] = sum * cv[i];
   }
+  if (update_history && first == 0)
+    WriteConvHistory<L>(ps, ldp, H, ch, rows, hist, L);
 }
 
 // Any width: each output recomputes its window's products (same values and
 // order as PromptConvKernel).
 __global__ void PromptConvAnyKernel(const float* __restrict__ p, int ldp,
                                     const float* __restrict__ taps, ConvSegments seg,
-                                    float* __restrict__ y, int ldy, int H, int L) {
+                                    float* __restrict__ y, int ldy, int H, int L,
+                                    int update_history) {
 #pragma clang fp contract(off)
   const int s = blockIdx.z, ch = blockIdx.x * blockDim.x + threadIdx.x;
   const int first = blockIdx.y * kConvRows, rows = seg.rows[s];
@@ -678,7 +706,7 @@ __global__ void PromptConvAnyKernel(const float* __restrict__ p, int ldp,
     return;
   const float* ps = p + std::size_t(seg.begin[s]) * ldp;
   float* ys = y + std::size_t(seg.begin[s]) * ldy;
-  const float* hist = seg.history[s] + std::size_t(ch) * (L - 1);
+  float* hist = seg.history[s] + std::size_t(ch) * (L - 1);
   const int last = min(first + kConvRows, rows);
   for (int r = first; r < last; ++r) {
     float sum = 0.0f;
@@ -691,27 +719,19 @@ __global__ void PromptConvAnyKernel(const float* __restrict__ p, int ldp,
     }
     ys[std::size_t(r) * ldy + ch] = sum * ps[std::size_t(r) * ldp + H + ch];
   }
+  if (update_history && first == 0)
+    WriteConvHistory<32>(ps, ldp, H, ch, rows, hist, L);
 }
 
-// The history after a segment: its last L - 1 B x products, reaching into
-// the old history when the segment is shorter.
+// The history after a segment, as a launch of its own: for widths past
+// kConvRows + 1 the second row group's windows also read the old history.
 __global__ void PromptConvHistoryKernel(const float* __restrict__ p, int ldp,
                                         ConvSegments seg, int H, int L) {
-#pragma clang fp contract(off)
   const int s = blockIdx.y, ch = blockIdx.x * blockDim.x + threadIdx.x;
   if (ch >= H)
     return;
-  const int rows = seg.rows[s];
-  const float* ps = p + std::size_t(seg.begin[s]) * ldp;
-  float* hist = seg.history[s] + std::size_t(ch) * (L - 1);
-  float past[31];
-  for (int j = 0; j < L - 1; ++j) {
-    const int r = rows - (L - 1) + j;
-    past[j] = r >= 0 ? ps[std::size_t(r) * ldp + ch] * ps[std::size_t(r) * ldp + 2 * H + ch]
-                     : hist[(L - 1) + r];
-  }
-  for (int j = 0; j < L - 1; ++j)
-    hist[j] = past[j];
+  WriteConvHistory<32>(p + std::size_t(seg.begin[s]) * ldp, ldp, H, ch, seg.rows[s],
+                       seg.history[s] + std::size_t(ch) * (L - 1), L);
 }
 
 // Greedy argmax: one block per row scans the row with a 64-bit key per
@@ -1048,12 +1068,15 @@ int lfm3_conv_prompt(const float* p, std::uint32_t ldp, const float* taps,
   }
   const auto s = static_cast<hipStream_t>(stream);
   const dim3 grid((hidden + 127) / 128, (most + kConvRows - 1) / kConvRows, segments);
+  // The first row group's threads move the history when only they read it.
+  const bool in_kernel = width - 1 <= std::uint32_t(kConvRows);
   if (width == 7)
-    PromptConvKernel<7><<<grid, 128, 0, s>>>(p, int(ldp), taps, seg, y, int(ldy), int(hidden));
+    PromptConvKernel<7><<<grid, 128, 0, s>>>(p, int(ldp), taps, seg, y, int(ldy), int(hidden),
+                                             update_history);
   else
     PromptConvAnyKernel<<<grid, 128, 0, s>>>(p, int(ldp), taps, seg, y, int(ldy), int(hidden),
-                                             int(width));
-  if (update_history)
+                                             int(width), update_history && in_kernel);
+  if (update_history && !in_kernel)
     PromptConvHistoryKernel<<<dim3((hidden + 127) / 128, segments), 128, 0, s>>>(
         p, int(ldp), seg, int(hidden), int(width));
   return HipStatus(hipGetLastError(), "LFM3 prompt convolution launch");

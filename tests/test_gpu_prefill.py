@@ -43,11 +43,13 @@ def run_conv_prompt(p, ldp, taps, hists, begins, rows, H, Lw, update=True):
     return y, [d.download(np.float32, H * (Lw - 1)) for d in dh]
 
 
-@pytest.mark.parametrize("Lw", [7, 4])
+@pytest.mark.parametrize("Lw", [7, 4, 20])
 def test_conv_prompt_packed_segments_bit_exact(Lw):
     """The packed ragged prefill variant: prompts of 512, 37, 300 and 1 rows
     in one launch, each continuing its own session history; every output
-    and history equals sequential decode steps (the oracle) bit for bit."""
+    and history equals sequential decode steps (the oracle) bit for bit.
+    Width 20 reaches past one 16-row group, where the history moves in a
+    launch of its own."""
     H = 2048
     seg_rows = [512, 37, 300, 1]
     begins = np.cumsum([0] + seg_rows[:-1])
