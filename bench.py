@@ -60,7 +60,7 @@ MIXED_DECODE, MIXED_LO, MIXED_HI = 7, 16384, 32768
 # plain 256 MiB device-to-device copy in the same program (FETCH_SIZE x 2.0,
 # WRITE_SIZE x 1.0). Re-measure after a change to either kernel.
 GEMV_TRAFFIC = {"read": 18_477_766, "write": 262_144}
-GEMM_TRAFFIC = {"read": 52_777_234, "write": 15_851_520}
+GEMM_TRAFFIC = {"read": 86_290_594, "write": 15_851_520}
 
 
 def log(msg: str):
