@@ -265,6 +265,45 @@ def roofline_only():
                       "gemm_flops": m["flops"], "gemm_us": m["us"]}), flush=True)
 
 
+def nominal_round(seed, ctx, tokens0, steps: int, warmup: int):
+    """The same decode round on the BASELINE-nominal dims (FFN 8192, 32q/8kv
+    heads x 64, vocabulary 65536; the other dims as the reference's), with
+    the same contexts: its own random-init model and synthesized state."""
+    dims = L.Dims(intermediate=8192, heads=32, kv_heads=8, head_dim=64, vocab=65536,
+                  context=CTX_HI + warmup + steps + 64)
+    model = L.Model(L.synth_weights(dims, seed=seed))
+    sessions = []
+    for sid, c in enumerate(ctx):
+        s = model.session(int(c) + warmup + steps + 8)
+        L.inject_synth_state(s, dims, seed, sid, int(c) - 1)
+        sessions.append(s)
+    toks = tokens0 % dims.vocab
+    for _ in range(warmup):
+        toks = model.forward_batch_greedy(sessions, toks)
+    L.synchronize()
+    positions = [[s.position + k for s in sessions] for k in range(steps)]
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        toks = model.forward_batch_greedy(sessions, toks)
+    L.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
+    nbytes = statistics.mean(round_bytes(dims, p) for p in positions)
+    for s in sessions:
+        s.close()
+    model.close()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "workload": ("the same round on the nominal dims: FFN 8192, 32q/8kv heads x 64, "
+                     "vocab 65536 (hidden 2048, 24 layers 13/5/6, Q8_0)"),
+        "ms": round(ms, 4),
+        "tok_s": round(SESSIONS / (ms * 1e-3), 1),
+        "bytes": int(nbytes),
+        "weight_bytes": weight_bytes(dims),
+        "achieved_GBps": round(gbs, 1),
+        "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+    }
+
+
 def prefill_and_mixed(model, dims, seed, reps: int, warmup: int):
     """The 512-token pass at depth 24576 alone, then the mixed round (7
     decode sessions at contexts in [16384, 32768] plus the pass). Each
@@ -485,6 +524,10 @@ def main():
                         "GBps": round(g["bytes"] / (g["us"] * 1e-6) / 1e9, 1)}
                        for g in sweep],
     }
+    nominal = nominal_round(seed, ctx, tokens0, args.steps, args.warmup)
+    log(f"nominal-dims round {nominal['ms']:.3f} ms, {nominal['tok_s']:.0f} tok/s, "
+        f"{nominal['achieved_GBps']:.0f} GB/s")
+    result["nominal_round"] = nominal
     if not args.no_prefill:
         log("512-token prompt pass at depth 24576 and the mixed round ...")
         pass_ms, mixed_ms, mixed_ctx = prefill_and_mixed(model, dims, seed, args.prefill_reps, 2)
