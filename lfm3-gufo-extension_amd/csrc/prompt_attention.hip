@@ -385,18 +385,31 @@ __launch_bounds__(D) __global__
   const int rh = blockIdx.x, d = threadIdx.x;
   const int row = rh / heads, head = rh % heads;
   const std::size_t rows = std::size_t(n) * heads;
-  float maximum = -INFINITY;
-  for (int s = 0; s < splits; ++s)
-    maximum = fmaxf(maximum, partial[(s * rows + rh) * (D + 2)]);
-  float sum = 0.0f, acc = 0.0f;
-  for (int s = 0; s < splits; ++s) {
+  // Every load (each span's maximum, sum and output element, and the gate)
+  // is issued before any arithmetic: one memory round trip.
+  float m[kMaxPromptSplits], l[kMaxPromptSplits], a[kMaxPromptSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxPromptSplits; ++s) {
     const float* part = partial + (s * rows + rh) * (D + 2);
-    const float w = __builtin_amdgcn_exp2f(part[0] - maximum);
-    sum = fmaf(part[1], w, sum);
-    acc = fmaf(part[2 + d], w, acc);
+    m[s] = s < splits ? part[0] : -INFINITY;
+    l[s] = s < splits ? part[1] : 0.0f;
+    a[s] = s < splits ? part[2 + d] : 0.0f;
   }
-  out[std::size_t(row) * ldo + head * D + d] =
-      (acc / sum) / (1.0f + expf(-gate[std::size_t(row) * ldg + head]));
+  const float g = gate[std::size_t(row) * ldg + head];
+  float maximum = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kMaxPromptSplits; ++s)
+    maximum = fmaxf(maximum, m[s]);
+  float sum = 0.0f, acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kMaxPromptSplits; ++s) {
+    if (s < splits) {
+      const float w = __builtin_amdgcn_exp2f(m[s] - maximum);
+      sum = fmaf(l[s], w, sum);
+      acc = fmaf(a[s], w, acc);
+    }
+  }
+  out[std::size_t(row) * ldo + head * D + d] = (acc / sum) / (1.0f + expf(-g));
 }
 
 struct PromptArgs {
