@@ -314,7 +314,10 @@ size_t lfm3_attention_workspace_bytes(uint32_t items, uint32_t rows,
    K/V row (lfm3_decode_heads_ragged). q/gate/out rows have strides
    ldq/ldg/ldo floats; items and the per-row tables are in device memory.
    dim 64 or 128; heads % kv_heads == 0 with a group of 2, 4 or 8. Two
-   launches: the spans, then their merge in span order.
+   launches: the spans, then their merge in span order; one when n_items ==
+   rows. `items` must be an lfm3_attention_plan over exactly these `rows`
+   rows: an item list whose count equals `rows` but holds a split row
+   leaves that row's outputs NaN (there is no merge launch to finish it).
    Replaces: gpu::Attention with n == 1 (hip/ops.hip:2289-2315:
    DecodeWaves + DecodeCombine) per session (engine.cpp:430-434). */
 int lfm3_decode_attention_ragged(
@@ -326,10 +329,11 @@ int lfm3_decode_attention_ragged(
     void* stream);
 /* lfm3_decode_heads_ragged and lfm3_decode_attention_ragged in one pass:
    q/k/v are the raw projection rows (stride ld floats, left unchanged);
-   each block norms and rotates its row's queries and key, the block whose
-   span ends at the current position stores the row's F16 K/V to ring slot
-   positions[i] % capacity[i], and the current key is read from that
-   block's registers, never from the ring.
+   each block norms and rotates its row's queries and key; the one block
+   whose span ends at the current position stores the row's F16 K/V to ring
+   slot positions[i] % capacity[i], waits for the stores, and reads the key
+   back through the ring with its other keys (no other span of the row
+   covers that slot; sliding rings hold at least the window).
    Replaces: gpu::DecodeHeads + gpu::Attention (hip/ops.hip:2289-2315,
    2397-2407) per session (engine.cpp:424-436). */
 int lfm3_decode_heads_attention_ragged(
@@ -381,8 +385,10 @@ int lfm3_store_kv(const uint16_t* k16, const uint16_t* v16, uint16_t* cache_k,
                   uint16_t* cache_v, uint32_t rows, uint32_t stride,
                   uint32_t position, uint32_t capacity, void* stream);
 /* Workspace of lfm3_prompt_attention: key spans of long global histories
-   (at least 2048 keys each, at most 8) keep partial sums, rows x heads x
-   (dim + 2) floats a span; 0 when the keys fit one span or window > 0. */
+   (whole 64-key tiles, at least 1024 keys each, at most 16, as many as
+   bring the launch to about one block per CU) keep partial sums, rows x
+   heads x (dim + 2) floats a span; this bounds any head grouping. 0 when
+   the keys fit one span or window > 0. */
 size_t lfm3_prompt_attention_workspace_bytes(uint32_t rows, uint32_t heads,
                                              uint32_t dim, uint32_t position,
                                              uint32_t window);
@@ -467,8 +473,14 @@ enum {
 };
 int lfm3_session_state(lfm3_session* session, int kind, uint32_t layer,
                        void** data, size_t* bytes);
-/* Restores a position after the caller wrote state rows directly
-   (Session::FinishRestore, engine.cpp:1380-1386). */
+/* Session::BeginRestore (engine.cpp:1372-1377): waits for the session's
+   work in flight and refuses further work (poisoned) until
+   lfm3_session_set_position, so a caller can write every state row through
+   lfm3_session_state. */
+int lfm3_session_begin_restore(lfm3_session* session);
+/* Session::FinishRestore (engine.cpp:1378-1384): the session resumes at
+   `position` with the state rows the caller wrote, the logits row included
+   (read_logits returns it as written; position 0 still has no logits). */
 int lfm3_session_set_position(lfm3_session* session, uint32_t position);
 
 /* Session::Forward (engine.cpp:882-938): n tokens of one session in

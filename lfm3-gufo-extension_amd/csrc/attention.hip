@@ -22,9 +22,21 @@
 //
 // With the heads fused in (lfm3_decode_heads_attention_ragged), every block
 // also applies the per-head Q/K RMSNorm and paired RoPE of its row
-// (hip/ops.hip:1072-1134) in its prologue; the block whose span holds the
-// current position stores that row's K/V to its ring slot, and every block
-// reads the current key from LDS, never from the ring being written.
+// (hip/ops.hip:1072-1134) in its prologue. Exactly one block of a row
+// writes the ring: the one whose span ends at the current position. It
+// stores the row's F16 K/V to slot position % capacity, waits for its
+// stores (vmcnt 0) and the block barrier, and then reads that key back
+// through the ring with the rest of its span. No other span of the row
+// covers the current position, so no other block reads the slot being
+// written; on a sliding layer this relies on the ring holding at least the
+// window (capacity = min(context, window) >= keys of any span), so the
+// current slot is not an earlier key of another span.
+//
+// A row with several spans needs the merge launch. The 8-wave whole-row
+// path runs only when the item count equals the row count (every row one
+// item); an item with parts > 1 on that path (an item list that is not a
+// plan over exactly `rows` rows) writes NaN to its row's outputs, so the
+// misuse shows instead of leaving stale rows.
 #include <algorithm>
 #include <cmath>
 
@@ -310,6 +322,8 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
   __syncthreads();
   const bool split = item.parts > 1;
   float* part_out = partial + (std::size_t(blockIdx.x) * kv_heads + g) * G * (D + 2);
+  // The whole-row shape has no merge launch behind it (see the file head).
+  const bool unmerged = split && NW == kWholeRowWaves;
   for (int e = tid; e < G * D; e += (NW * 64)) {
     const int h = e / D, d = e % D;
     float top = -INFINITY;
@@ -324,7 +338,9 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
       av = fmaf(s_acc[w][h][d], wt, av);
     }
     const int head = g * G + h;
-    if (!split) {
+    if (unmerged) {
+      out[std::size_t(row) * ldo + head * D + d] = __builtin_nanf("");
+    } else if (!split) {
       out[std::size_t(row) * ldo + head * D + d] = (av / l) / s_gate[h];
     } else {
       float* po = part_out + h * (D + 2);

@@ -497,18 +497,24 @@ std::uint32_t lfm3_session_ring_capacity(const lfm3_session* s, std::uint32_t la
 }
 
 // engine.cpp:1300-1332: zero the convolution history, position 0, healthy.
+// The session's work runs on the model's non-blocking stream, which is not
+// ordered against the null stream: the clears go on that stream, between
+// two synchronizations, as the reference's Reset does.
 int lfm3_session_reset(lfm3_session* s) {
   if (!s)
     return Fail(LFM3_E_INVALID, "null session");
   const auto& c = s->model->config;
+  const hipStream_t stream = s->model->stream;
+  int e = HipStatus(hipStreamSynchronize(stream), "reset");
   for (auto& st : s->states)
-    if (st.conv.p) {
-      const int e = HipStatus(
-          hipMemset(st.conv.p, 0, std::size_t(c.hidden) * (c.conv_width - 1) * 4),
+    if (!e && st.conv.p)
+      e = HipStatus(
+          hipMemsetAsync(st.conv.p, 0, std::size_t(c.hidden) * (c.conv_width - 1) * 4, stream),
           "reset");
-      if (e)
-        return e;
-    }
+  if (!e)
+    e = HipStatus(hipStreamSynchronize(stream), "reset");
+  if (e)
+    return e;
   s->position = 0;
   s->logits_ready = false;
   s->poisoned = false;
@@ -541,12 +547,26 @@ int lfm3_session_state(lfm3_session* s, int kind, std::uint32_t layer,
   return b->p ? LFM3_OK : Fail(LFM3_E_INVALID, "LFM3 layer has no such state");
 }
 
+// Session::BeginRestore (engine.cpp:1372-1377): work in flight drains, and
+// the session refuses work until lfm3_session_set_position.
+int lfm3_session_begin_restore(lfm3_session* s) {
+  if (!s)
+    return Fail(LFM3_E_INVALID, "null session");
+  const int e = HipStatus(hipStreamSynchronize(s->model->stream), "begin restore");
+  if (e)
+    return e;
+  s->poisoned = true;
+  return LFM3_OK;
+}
+
+// Session::FinishRestore (engine.cpp:1378-1384): the caller wrote every
+// state row, the logits row included, so the logits are served as written.
 int lfm3_session_set_position(lfm3_session* s, std::uint32_t position) {
   if (!s || position > s->context)
     return Fail(LFM3_E_INVALID, "invalid LFM3 position");
   s->position = position;
   s->poisoned = false;
-  s->logits_ready = false;
+  s->logits_ready = true;
   return LFM3_OK;
 }
 
@@ -644,9 +664,13 @@ int lfm3_session_read_logits(const lfm3_session* s, float* logits) {
   } catch (const Error& e) {
     return Fail(e.status, e.what());
   }
-  return HipStatus(hipMemcpy(logits, s->logits.p, std::size_t(s->model->config.vocab) * 4,
-                             hipMemcpyDeviceToHost),
-                   "read logits");
+  const hipStream_t stream = s->model->stream;
+  int e = HipStatus(hipMemcpyAsync(logits, s->logits.p, std::size_t(s->model->config.vocab) * 4,
+                                   hipMemcpyDeviceToHost, stream),
+                    "read logits");
+  if (!e)
+    e = HipStatus(hipStreamSynchronize(stream), "read logits");
+  return e;
 }
 
 std::size_t lfm3_session_snapshot_bytes(const lfm3_session* s) {
@@ -669,9 +693,13 @@ int lfm3_session_save_snapshot(lfm3_session* s, void* out, std::size_t bytes) {
     for (std::size_t i = 0; i < 8; ++i)
       PutWord(p, i, header[i]);
     std::size_t offset = kSnapshotHeaderBytes;
+    // Copies on the session stream, after its work and before the return.
+    const hipStream_t stream = s->model->stream;
+    Check(hipStreamSynchronize(stream), "snapshot");
     const auto copy = [&](const void* source, std::size_t size) {
       if (size)
-        Check(hipMemcpy(p + offset, source, size, hipMemcpyDeviceToHost), "snapshot copy");
+        Check(hipMemcpyAsync(p + offset, source, size, hipMemcpyDeviceToHost, stream),
+              "snapshot copy");
       offset += size;
     };
     if (s->position) {
@@ -691,6 +719,7 @@ int lfm3_session_save_snapshot(lfm3_session* s, void* out, std::size_t bytes) {
         copy(st.v.p, size);
       }
     }
+    Check(hipStreamSynchronize(stream), "snapshot");
     return LFM3_OK;
   } catch (const Error& e) {
     return Fail(e.status, e.what());
@@ -711,10 +740,13 @@ int lfm3_session_restore_snapshot(lfm3_session* s, const void* data, std::size_t
     return Fail(LFM3_E_INVALID, "invalid LFM3 snapshot payload");
   const std::uint32_t position = GetWord(p, 3);
   std::size_t offset = kSnapshotHeaderBytes;
+  const hipStream_t stream = s->model->stream;
   try {
+    Check(hipStreamSynchronize(stream), "restore");
     const auto copy = [&](void* destination, std::size_t size) {
       if (size)
-        Check(hipMemcpy(destination, p + offset, size, hipMemcpyHostToDevice), "restore copy");
+        Check(hipMemcpyAsync(destination, p + offset, size, hipMemcpyHostToDevice, stream),
+              "restore copy");
       offset += size;
     };
     copy(s->frontier.p, std::size_t(c.hidden) * 4);
@@ -729,6 +761,7 @@ int lfm3_session_restore_snapshot(lfm3_session* s, const void* data, std::size_t
         copy(st.v.p, size);
       }
     }
+    Check(hipStreamSynchronize(stream), "restore");
   } catch (const Error& e) {
     s->poisoned = true;  // a partial restore leaves no coherent state
     return Fail(e.status, e.what());
@@ -1262,8 +1295,10 @@ int BatchEntry(lfm3_session* const* sessions, std::size_t n,
     if (logits)
       for (std::size_t i = 0; i < n; ++i)
         CopyLogits(m, logits[i], sessions[i]->logits.p);
-    if (ids)
-      Check(hipMemcpy(ids, m.ids.p, n * 4, hipMemcpyDeviceToHost), "ids copy");
+    if (ids) {
+      Check(hipMemcpyAsync(ids, m.ids.p, n * 4, hipMemcpyDeviceToHost, m.stream), "ids copy");
+      Check(hipStreamSynchronize(m.stream), "ids copy");
+    }
     return LFM3_OK;
   } catch (const Error& e) {
     for (std::size_t i = 0; i < n; ++i)

@@ -26,8 +26,10 @@
 // never cross lanes. A column's softmax state is per lane; its row maximum
 // and final sum combine the 4 lanes of the column (L % 16) with two
 // exchanges. Long global histories split keys across blockIdx.y into spans
-// of at least 2048 keys (at most 8); each split stores its maximum, sum and
-// unnormalized output, merged by CombineSpansKernel.
+// (SpanPlan: enough spans for about one block per CU, whole 64-key tiles,
+// at least 1024 keys and at most 16 spans; the reference's PromptSplits
+// instead fixes spans of at least 2048 keys, at most 8). Each span stores
+// its maximum, sum and unnormalized output, merged by CombineSpansKernel.
 #include <cmath>
 
 #include "common.hpp"
@@ -37,12 +39,34 @@ namespace {
 
 constexpr int kPAWaves = 8, kPAThreads = 64 * kPAWaves;
 constexpr int kPAKeys = 64;             // keys a tile
-constexpr int kMinPromptSpan = 2048, kMaxPromptSplits = 8;
 
-// hip/ops.hip:2275-2280: spans of at least 2048 keys, at most 8 of them.
-int PromptSplits(int keys, int& span) {
-  span = std::max(kMinPromptSpan, (keys + kMaxPromptSplits - 1) / kMaxPromptSplits);
-  return (keys + span - 1) / span;
+// Key spans of a long causal history (blockIdx.y of the tile launch): a
+// launch of row blocks x KV heads blocks per span is cut into spans until
+// it has about one block per CU, each span a whole number of 64-key tiles
+// and at least kSpanFloorTiles tiles long, so the merge launch stays small
+// next to the spans. A sliding window never splits.
+constexpr int kFillBlocks = 256, kSpanFloorTiles = 16, kMaxSpans = 16;
+
+int SpanPlan(int keys, int blocks_per_span, int& span_keys) {
+  const int tiles = (keys + kPAKeys - 1) / kPAKeys;
+  int spans = (kFillBlocks + blocks_per_span - 1) / std::max(blocks_per_span, 1);
+  spans = std::min({spans, kMaxSpans, std::max(1, tiles / kSpanFloorTiles)});
+  span_keys = (tiles + spans - 1) / spans * kPAKeys;
+  return (keys + span_keys - 1) / span_keys;
+}
+
+// Keys visible to a query at absolute position p, clipped to a span
+// [span_lo, span_hi]: the causal window [p + 1 - window, p] (from key 0
+// without a window). Inclusive bounds; empty when lo > hi. Visible(p).lo
+// and Visible(p).hi are both non-decreasing in p, so a run of consecutive
+// queries sees the union {Visible(first).lo, Visible(last).hi} and every
+// query of the run sees {Visible(last).lo, Visible(first).hi}.
+struct KeyRange {
+  int lo, hi;
+};
+__device__ __forceinline__ KeyRange Visible(int p, int window, int span_lo, int span_hi) {
+  const int oldest = window > 0 ? p - window + 1 : 0;
+  return KeyRange{max(oldest, span_lo), min(p, span_hi)};
 }
 
 // Slot of a key row's 16-byte segment: XOR swizzle chosen so that the 16
@@ -56,13 +80,18 @@ __device__ __forceinline__ int KeySwizzle(int key) {
     return ((key >> 1) & 1) | (((key >> 3) & 3) << 1);
 }
 
-// Rows at or after position come from the chunk, earlier rows from the
-// ring (hip/ops.hip:1193-1199).
-__device__ __forceinline__ const Half* KeyRow(const Half* chunk, const Half* ring, int t,
-                                              int position, int capacity, int stride) {
-  return t >= position ? chunk + std::size_t(t - position) * stride
-                       : ring + std::size_t(t % capacity) * stride;
-}
+// The F16 row of key t: the prompt's own keys (t >= position) are chunk
+// rows t - position; older keys sit in ring slot t mod capacity.
+struct KeySource {
+  const Half* chunk;
+  const Half* ring;
+  int position, capacity, stride;
+  __device__ __forceinline__ const Half* Row(int t) const {
+    const bool own = t >= position;
+    const std::size_t slot = own ? std::size_t(t - position) : std::size_t(t % capacity);
+    return (own ? chunk : ring) + slot * stride;
+  }
+};
 
 __device__ __forceinline__ unsigned PackHalves(float a, float b) {
   return unsigned(FloatToHalfBits(a)) | (unsigned(FloatToHalfBits(b)) << 16);
@@ -152,28 +181,23 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
     }
   }
 
-  // Key ranges: each column's own, the block's, and the wave's (open = keys
-  // every column of the wave sees, where tiles skip the mask).
-  const int span_first = split * span, span_last = span_first + span - 1;
-  const auto first_key = [&](int query) {
-    return max(window > 0 ? query + 1 - window : 0, span_first);
-  };
-  int lo[CT], hi[CT];
+  // Visible keys of each column, of the block's rows (the tiles it walks)
+  // and of the wave's rows: their union (tiles the wave computes) and their
+  // intersection (tiles every column sees whole, where the mask is skipped).
+  const int span_lo = split * span, span_hi = span_lo + span - 1;
+  const auto visible = [&](int r) { return Visible(position + r, window, span_lo, span_hi); };
+  KeyRange own[CT];
 #pragma unroll
-  for (int ct = 0; ct < CT; ++ct) {
-    lo[ct] = first_key(position + row[ct]);
-    hi[ct] = min(position + row[ct], span_last);
-  }
-  const int block_last_row = min(q0 + kRows, n) - 1;
-  const int block_first = first_key(position + q0);
-  const int block_last = min(position + block_last_row, span_last);
-  const int w_row0 = q0 + wave * 16 * CT / G;
-  const int w_row1 = min(q0 + (wave * 16 * CT + 16 * CT - 1) / G, n - 1);
-  const bool wave_live = w_row0 < n;
-  const int wave_first = first_key(position + w_row0);
-  const int wave_last = min(position + w_row1, span_last);
-  const int open_first = first_key(position + w_row1);
-  const int open_last = min(position + w_row0, span_last);
+  for (int ct = 0; ct < CT; ++ct)
+    own[ct] = visible(row[ct]);
+  const KeyRange walk{visible(q0).lo, visible(min(q0 + kRows, n) - 1).hi};
+  const int wave_r0 = q0 + wave * 16 * CT / G;
+  const int wave_r1 = min(q0 + (wave * 16 * CT + 16 * CT - 1) / G, n - 1);
+  const bool wave_live = wave_r0 < n;
+  const KeyRange reach{visible(wave_r0).lo, visible(wave_r1).hi};
+  const KeyRange whole{visible(wave_r1).lo, visible(wave_r0).hi};
+  const KeySource keys{k, ck, position, capacity, stride};
+  const KeySource values{v, cv, position, capacity, stride};
 
   // Staging: K segment u of thread tid is (key, seg) = j / kSegs, j % kSegs
   // with j = tid + kPAThreads u; V job j = tid covers keys 2 (j % 32) and
@@ -184,18 +208,15 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
 #pragma unroll
     for (int u = 0; u < kKLoads; ++u) {
       const int j = tid + kPAThreads * u, t = base + j / kSegs;
-      kr[u] = t <= block_last
-                  ? *reinterpret_cast<const uint4*>(
-                        KeyRow(k, ck, t, position, capacity, stride) + (j % kSegs) * 8)
-                  : make_uint4(0, 0, 0, 0);
+      kr[u] = t <= walk.hi ? *reinterpret_cast<const uint4*>(keys.Row(t) + (j % kSegs) * 8)
+                           : make_uint4(0, 0, 0, 0);
     }
     if (tid < kVPairs) {
       const int seg = tid / 32, t = base + 2 * (tid % 32);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
-        vr[i] = t + i <= block_last
-                    ? *reinterpret_cast<const uint4*>(
-                          KeyRow(v, cv, t + i, position, capacity, stride) + seg * 8)
+        vr[i] = t + i <= walk.hi
+                    ? *reinterpret_cast<const uint4*>(values.Row(t + i) + seg * 8)
                     : make_uint4(0, 0, 0, 0);
     }
   };
@@ -254,7 +275,7 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
     }
     // Lane L's value i of block kb is key base + 32 (kb / 2) + 8 (L / 16) +
     // 4 (kb % 2) + i of its column.
-    const bool open = base >= open_first && base + kPAKeys - 1 <= open_last;
+    const bool open = base >= whole.lo && base + kPAKeys - 1 <= whole.hi;
     h8 p[CT][2];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
@@ -271,7 +292,7 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int t = base + 32 * (kb >> 1) + 8 * grp + 4 * (kb & 1) + i;
-            s[ct][kb][i] = (t >= lo[ct] && t <= hi[ct]) ? s[ct][kb][i] : -INFINITY;
+            s[ct][kb][i] = (t >= own[ct].lo && t <= own[ct].hi) ? s[ct][kb][i] : -INFINITY;
             tile_max = fmaxf(tile_max, s[ct][kb][i]);
           }
       }
@@ -297,7 +318,8 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
                       (unsigned(__builtin_bit_cast(Half, b)) << 16);
         }
       sum[ct] = sum[ct] * alpha + local;
-      // An unchanged maximum gives alpha == 1 exactly.
+      // exp2(0) is exactly 1: when no lane's maximum moved, the rescale of
+      // the accumulators is skipped for the whole wave.
       if (__ballot(alpha != 1.0f)) {
 #pragma unroll
         for (int m = 0; m < kDimBlocks; ++m)
@@ -329,16 +351,16 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
   // Tiles: write the prefetched tile to its stage, one barrier (the tile is
   // visible, and every wave is done with the stage written two tiles ago),
   // prefetch the next tile, multiply.
-  if (block_first <= block_last)
-    load(block_first);
+  if (walk.lo <= walk.hi)
+    load(walk.lo);
   int it = 0;
-  for (int base = block_first; base <= block_last; base += kPAKeys, ++it) {
+  for (int base = walk.lo; base <= walk.hi; base += kPAKeys, ++it) {
     const int st = it & 1;
     store(st);
     __syncthreads();
-    if (base + kPAKeys <= block_last)
+    if (base + kPAKeys <= walk.hi)
       load(base + kPAKeys);
-    if (!wave_live || base > wave_last || base + kPAKeys <= wave_first)
+    if (!wave_live || base > reach.hi || base + kPAKeys <= reach.lo)
       continue;
     compute(st, base);
   }
@@ -387,9 +409,9 @@ __launch_bounds__(D) __global__
   const std::size_t rows = std::size_t(n) * heads;
   // Every load (each span's maximum, sum and output element, and the gate)
   // is issued before any arithmetic: one memory round trip.
-  float m[kMaxPromptSplits], l[kMaxPromptSplits], a[kMaxPromptSplits];
+  float m[kMaxSpans], l[kMaxSpans], a[kMaxSpans];
 #pragma unroll
-  for (int s = 0; s < kMaxPromptSplits; ++s) {
+  for (int s = 0; s < kMaxSpans; ++s) {
     const float* part = partial + (s * rows + rh) * (D + 2);
     m[s] = s < splits ? part[0] : -INFINITY;
     l[s] = s < splits ? part[1] : 0.0f;
@@ -398,11 +420,11 @@ __launch_bounds__(D) __global__
   const float g = gate[std::size_t(row) * ldg + head];
   float maximum = -INFINITY;
 #pragma unroll
-  for (int s = 0; s < kMaxPromptSplits; ++s)
+  for (int s = 0; s < kMaxSpans; ++s)
     maximum = fmaxf(maximum, m[s]);
   float sum = 0.0f, acc = 0.0f;
 #pragma unroll
-  for (int s = 0; s < kMaxPromptSplits; ++s) {
+  for (int s = 0; s < kMaxSpans; ++s) {
     if (s < splits) {
       const float w = __builtin_amdgcn_exp2f(m[s] - maximum);
       sum = fmaf(l[s], w, sum);
@@ -427,11 +449,32 @@ struct PromptArgs {
   int n, heads, kv_heads, position, capacity, window, span, splits;
 };
 
+// Long histories: two column tiles a wave (each K / V operand read feeds two
+// MFMAs); windows and short histories: one, for more blocks.
+int ColumnTiles(int position, int n, int window) {
+  return window == 0 && position + n > 4096 ? 2 : 1;
+}
+
+// The span plan of one call: span length and count for the tile launch of
+// the chosen shape (spans > 1 only for a history without a window).
+int PlanCall(int n, int position, int window, int group, int kv_heads, int& span) {
+  const int keys = position + n;
+  span = keys;
+  if (window)
+    return 1;
+  const int rows = 16 * ColumnTiles(position, n, window) * kPAWaves / group;
+  const int blocks_per_span = (n + rows - 1) / rows * kv_heads;
+  const int spans = SpanPlan(keys, blocks_per_span, span);
+  if (spans == 1)
+    span = keys;
+  return spans;
+}
+
 template<int D, int G, int CT>
 void LaunchTiles(const PromptArgs& a, hipStream_t s) {
   constexpr int kRows = 16 * CT * kPAWaves / G;
   const int row_blocks = (a.n + kRows - 1) / kRows;
-  // 8 XCD slots of row_blocks blocks per group of 8 (split, KV head) pairs.
+  // 8 XCD slots of row_blocks blocks per group of 8 (span, KV head) pairs.
   const int pairs = a.splits * a.kv_heads;
   const int blocks = (pairs + 7) / 8 * 8 * row_blocks;
   PromptAttentionKernel<D, G, CT><<<blocks, kPAThreads, 0, s>>>(
@@ -440,11 +483,9 @@ void LaunchTiles(const PromptArgs& a, hipStream_t s) {
       a.window, a.span, row_blocks, a.splits);
 }
 
-// Long histories: two column tiles a wave (each K / V operand read feeds two
-// MFMAs); windows and short histories: one, for more blocks.
 template<int D, int G>
 void LaunchPrompt(const PromptArgs& a, hipStream_t s) {
-  if (a.window == 0 && a.position + a.n > 4096)
+  if (ColumnTiles(a.position, a.n, a.window) == 2)
     LaunchTiles<D, G, 2>(a, s);
   else
     LaunchTiles<D, G, 1>(a, s);
@@ -463,15 +504,12 @@ void LaunchPromptGroup(const PromptArgs& a, int group, hipStream_t s) {
     LaunchPrompt<D, 8>(a, s);
 }
 
-int SplitsFor(std::uint32_t position, std::uint32_t n, std::uint32_t window, int& span) {
-  if (window) {
-    span = int(position + n);
+// Spans any call of these sizes may use, whatever its head grouping.
+int MostSpans(std::uint32_t position, std::uint32_t n, std::uint32_t window) {
+  if (window)
     return 1;
-  }
-  const int splits = PromptSplits(int(position + n), span);
-  if (splits == 1)
-    span = int(position + n);
-  return splits;
+  const int tiles = int((std::uint64_t(position) + n + kPAKeys - 1) / kPAKeys);
+  return std::min(kMaxSpans, std::max(1, tiles / kSpanFloorTiles));
 }
 
 }  // namespace
@@ -484,9 +522,8 @@ extern "C" {
 std::size_t lfm3_prompt_attention_workspace_bytes(std::uint32_t rows, std::uint32_t heads,
                                                   std::uint32_t dim, std::uint32_t position,
                                                   std::uint32_t window) {
-  int span;
-  const int splits = SplitsFor(position, rows, window, span);
-  return splits > 1 ? std::size_t(splits) * rows * heads * (dim + 2) * sizeof(float) : 0;
+  const int spans = MostSpans(position, rows, window);
+  return spans > 1 ? std::size_t(spans) * rows * heads * (dim + 2) * sizeof(float) : 0;
 }
 
 int lfm3_prompt_attention(const float* q, std::uint32_t ldq, const std::uint16_t* k,
@@ -506,7 +543,7 @@ int lfm3_prompt_attention(const float* q, std::uint32_t ldq, const std::uint16_t
       std::uint64_t(position) + rows > (1ull << 31))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt attention shape");
   PromptArgs a{};
-  a.splits = SplitsFor(position, rows, window, a.span);
+  a.splits = PlanCall(int(rows), int(position), int(window), int(group), int(kv_heads), a.span);
   const std::size_t need =
       a.splits > 1 ? std::size_t(a.splits) * rows * heads * (dim + 2) * sizeof(float) : 0;
   if (need && (!workspace || workspace_bytes < need))

@@ -108,6 +108,7 @@ _SIGS = {
     "lfm3_session_ring_capacity": (u32, [vp, u32]),
     "lfm3_session_state": (i32, [vp, i32, u32, C.POINTER(vp), C.POINTER(sz)]),
     "lfm3_session_set_position": (i32, [vp, u32]),
+    "lfm3_session_begin_restore": (i32, [vp]),
     "lfm3_session_forward": (i32, [vp, vp, sz, vp]),
     "lfm3_forward_batch": (i32, [vp, sz, vp, vp]),
     "lfm3_forward_batch_greedy": (i32, [vp, sz, vp, vp]),
@@ -368,6 +369,9 @@ class Session:
 
     def set_position(self, p: int):
         check(lib().lfm3_session_set_position(self.handle, p))
+
+    def begin_restore(self):
+        check(lib().lfm3_session_begin_restore(self.handle))
 
     def reset(self):
         check(lib().lfm3_session_reset(self.handle))

@@ -6,6 +6,8 @@ Gates: the reference's own (ops_test.cpp: projection 1e-4 vs FP64, conv
 apply, and the BASELINE gates elsewhere (1e-3 relative / 1e-4 absolute for
 FP32 GEMV and attention outputs; bit-exact for indexing, ring slots and
 greedy ids)."""
+import zlib
+
 import numpy as np
 import pytest
 
@@ -160,7 +162,8 @@ def test_conv_step_ragged_bit_exact():
 # --------------------------------------------------- heads and attention
 
 def ragged_case(heads, kv, D, window, ctx_hi=4096, n=8, tag="a", global_cap=4096):
-    rng = np.random.default_rng(abs(hash((heads, kv, D, window, tag))) % 2**32)
+    # A stable per-case seed (str hashes are salted per process).
+    rng = np.random.default_rng(zlib.crc32(repr((heads, kv, D, window, tag)).encode()))
     ctx = L.uniform_u32(SEED, f"att.ctx.{tag}", n, 1, ctx_hi)
     positions = (ctx - 1).astype(np.uint32)
     cap = window if window else global_cap

@@ -132,3 +132,37 @@ def test_snapshot_of_another_configuration_is_refused(model):
     for x in (s, t, short):
         x.close()
     other.close()
+
+
+def test_restore_through_state_rows_serves_the_written_logits(model):
+    """Session::BeginRestore / FinishRestore (engine.cpp:1372-1384): a
+    continuation written row by row through the state pointers resumes with
+    the logits row it carried, bit for bit, and decodes as the original."""
+    d, m = model
+    a, b = m.session(1024), m.session(1024)
+    toks = tokens(80, "r")
+    a.forward(toks[:40], want_logits=False)
+    a.forward(toks[40:41])
+    want = a.read_logits()
+    b.forward(tokens(7, "other"))                 # dirty state to overwrite
+    b.begin_restore()
+    assert not b.coherent()
+    with pytest.raises(L.LFM3Error):
+        b.forward(toks[41:42])                    # refused while restoring
+    kinds = [(L.STATE_LOGITS, 0), (L.STATE_FRONTIER, 0)]
+    for i in range(d.n_layers):
+        if d.layer_type(i) == L.LAYER_CONV:
+            kinds.append((L.STATE_CONV, i))
+        else:
+            kinds += [(L.STATE_KEY, i), (L.STATE_VALUE, i)]
+    for kind, layer in kinds:
+        src, nbytes = a.state(kind, layer)
+        dst, nbytes_b = b.state(kind, layer)
+        assert nbytes == nbytes_b
+        L.upload_to(dst, L.download_from(src, np.uint8, nbytes))
+    b.set_position(a.position)
+    assert b.coherent() and b.position == a.position
+    assert np.array_equal(b.read_logits(), want)
+    assert np.array_equal(b.forward(toks[41:44]), a.forward(toks[41:44]))
+    a.close()
+    b.close()
