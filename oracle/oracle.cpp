@@ -6,13 +6,39 @@
 #include "oracle.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <limits>
 #include <new>
+#include <thread>
 #include <vector>
 
 namespace {
+
+// Worker threads of one matrix-vector product or attention read (1: the
+// reference's serial loops). Each output row or head is still one thread's
+// sequential sum in the reference's order, so results do not depend on the
+// count; only the wall time does.
+std::atomic<unsigned> g_threads{1};
+
+// Runs body(begin, end) over [0, n) split into contiguous ranges, one per
+// worker (the calling thread takes the first).
+template<class Body>
+void Split(size_t n, Body body) {
+  const unsigned workers = unsigned(std::min<size_t>(g_threads.load(), n));
+  if (workers <= 1) {
+    body(size_t(0), n);
+    return;
+  }
+  std::vector<std::thread> pool;
+  pool.reserve(workers - 1);
+  for (unsigned w = 1; w < workers; ++w)
+    pool.emplace_back(body, n * w / workers, n * (w + 1) / workers);
+  body(size_t(0), n / workers);
+  for (auto& t : pool)
+    t.join();
+}
 
 // Textbook IEEE binary16 decoding: sign, 5-bit exponent (bias 15), 10-bit
 // fraction; exponent 0 is subnormal (fraction * 2^-24), 31 is Inf/NaN.
@@ -111,15 +137,18 @@ bool DecodeRow(const orc_tensor& t, uint32_t row, float* out) {
 
 // reference.cpp:9-19.
 bool Mat(const orc_tensor& t, const float* x, float* y) {
-  std::vector<float> row(t.cols);
-  for (uint32_t r = 0; r < t.rows; ++r) {
-    if (!DecodeRow(t, r, row.data()))
-      return false;
-    float sum = 0;
-    for (uint32_t k = 0; k < t.cols; ++k)
-      sum += row[k] * x[k];
-    y[r] = sum;
-  }
+  if (t.type != ORC_F32 && t.type != ORC_F16 && !(t.type == ORC_Q8_0 && t.cols % 32 == 0))
+    return false;
+  Split(t.rows, [&](size_t r0, size_t r1) {
+    std::vector<float> row(t.cols);
+    for (size_t r = r0; r < r1; ++r) {
+      DecodeRow(t, uint32_t(r), row.data());
+      float sum = 0;
+      for (uint32_t k = 0; k < t.cols; ++k)
+        sum += row[k] * x[k];
+      y[r] = sum;
+    }
+  });
   return true;
 }
 
@@ -176,30 +205,32 @@ void AttentionRead(const float* q, const float* gate, const float* ck,
   const size_t stride = size_t(kv_heads) * D;
   const uint32_t first =
       window && position + 1 > window ? position + 1 - window : 0;
-  std::vector<float> scores(position + 1 - first);
-  for (uint32_t h = 0; h < heads; ++h) {
-    const uint32_t kh = h / (heads / kv_heads);
-    float max = -std::numeric_limits<float>::infinity();
-    for (uint32_t t = first; t <= position; ++t) {
-      float score = 0;
-      for (uint32_t d = 0; d < D; ++d)
-        score += q[h * D + d] * ck[(t % capacity) * stride + kh * D + d];
-      scores[t - first] = score / std::sqrt(float(D));
-      max = std::max(max, scores[t - first]);
+  Split(heads, [&](size_t h0, size_t h1) {
+    std::vector<float> scores(position + 1 - first);
+    for (uint32_t h = uint32_t(h0); h < h1; ++h) {
+      const uint32_t kh = h / (heads / kv_heads);
+      float max = -std::numeric_limits<float>::infinity();
+      for (uint32_t t = first; t <= position; ++t) {
+        float score = 0;
+        for (uint32_t d = 0; d < D; ++d)
+          score += q[h * D + d] * ck[(t % capacity) * stride + kh * D + d];
+        scores[t - first] = score / std::sqrt(float(D));
+        max = std::max(max, scores[t - first]);
+      }
+      float den = 0;
+      for (auto& score : scores) {
+        score = std::exp(score - max);
+        den += score;
+      }
+      for (uint32_t d = 0; d < D; ++d) {
+        float sum = 0;
+        for (uint32_t t = first; t <= position; ++t)
+          sum += (scores[t - first] / den) *
+                 cv[(t % capacity) * stride + kh * D + d];
+        out[h * D + d] = sum / (1 + std::exp(-gate[h]));
+      }
     }
-    float den = 0;
-    for (auto& score : scores) {
-      score = std::exp(score - max);
-      den += score;
-    }
-    for (uint32_t d = 0; d < D; ++d) {
-      float sum = 0;
-      for (uint32_t t = first; t <= position; ++t)
-        sum += (scores[t - first] / den) *
-               cv[(t % capacity) * stride + kh * D + d];
-      out[h * D + d] = sum / (1 + std::exp(-gate[h]));
-    }
-  }
+  });
 }
 
 }  // namespace
@@ -227,6 +258,9 @@ struct orc_session {
 };
 
 extern "C" {
+
+void orc_set_threads(unsigned threads) { g_threads.store(std::max(1u, threads)); }
+unsigned orc_threads(void) { return g_threads.load(); }
 
 float orc_half_to_float(uint16_t h) { return HalfToFloat(h); }
 uint16_t orc_float_to_half(float f) { return FloatToHalf(f); }

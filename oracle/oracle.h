@@ -73,6 +73,13 @@ typedef struct orc_model orc_model;
 typedef struct orc_session orc_session;
 
 /* IEEE binary16 <-> binary32, round to nearest even. */
+/* Worker threads per matrix-vector product (rows split into contiguous
+   ranges) and per attention read (heads split): 1, the default, is the
+   reference's serial loop. Every output row and head keeps its sequential
+   sum, so results are identical for any count; process-wide. */
+void orc_set_threads(unsigned threads);
+unsigned orc_threads(void);
+
 float orc_half_to_float(uint16_t h);
 uint16_t orc_float_to_half(float f);
 void orc_halves_to_floats(const uint16_t* h, float* f, size_t n);

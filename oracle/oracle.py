@@ -31,6 +31,8 @@ class Tensor(C.Structure):
 
 
 _SIGS = {
+    "orc_set_threads": (None, [u32]),
+    "orc_threads": (u32, []),
     "orc_half_to_float": (f32, [C.c_uint16]),
     "orc_float_to_half": (C.c_uint16, [f32]),
     "orc_halves_to_floats": (None, [vp, vp, sz]),
@@ -95,6 +97,16 @@ def q8_tensor(blob: np.ndarray, rows: int, cols: int) -> Tensor:
 def f32_tensor(a: np.ndarray, rows: int, cols: int) -> Tensor:
     assert a.dtype == np.float32
     return Tensor(_p(a), F32, cols, rows)
+
+
+def set_threads(n: int):
+    """Worker threads per matrix-vector product / attention read (1 = the
+    reference's serial loops; results are identical for any count)."""
+    lib().orc_set_threads(max(1, int(n)))
+
+
+def threads() -> int:
+    return int(lib().orc_threads())
 
 
 def half_to_float(h: np.ndarray) -> np.ndarray:

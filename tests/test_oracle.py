@@ -296,6 +296,27 @@ def test_state_injection_reproduces_stepping():
     model.close()
 
 
+def test_parallel_rows_and_heads_give_identical_steps():
+    """The row-parallel matrix-vector products and head-parallel attention
+    (orc_set_threads) keep every output row's sequential sum: logits are
+    bit-identical to the serial reference loops for any thread count."""
+    dims = tiny_dims()
+    w = L.synth_weights(dims, seed=14)
+    model = O.Model(dims, w)
+    runs = []
+    for threads in (1, 3, 8):
+        O.set_threads(threads)
+        s = model.session(64)
+        runs.append([s.step(tok * 5 % dims.vocab) for tok in range(6)])
+        s.close()
+    O.set_threads(1)
+    assert O.threads() == 1
+    for other in runs[1:]:
+        for a, b in zip(runs[0], other):
+            assert np.array_equal(a, b)
+    model.close()
+
+
 def test_step_row_with_embedding_row_is_the_token_step():
     """ForwardBatchInputs' row path (engine.cpp:1217-1299 copies the row over
     the embedding): the step from the token's dequantized embedding row is
