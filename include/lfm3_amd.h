@@ -27,6 +27,9 @@ extern "C" {
 #define LFM3_E_HIP (-2)
 #define LFM3_E_STATE (-3)
 #define LFM3_E_NOMEM (-4)
+/* A continuation hook refused the call (continuation_hooks.hpp:6-15: a
+   hook may throw to refuse); nothing changed. */
+#define LFM3_E_REFUSED (-5)
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* lfm3_last_error(void);
@@ -376,6 +379,21 @@ int lfm3_prompt_heads(float* q, float* k, const float* v, uint32_t ld,
                       uint16_t* k16, uint16_t* v16, uint32_t rows,
                       uint32_t heads, uint32_t kv_heads, uint32_t dim,
                       uint32_t position, float eps, void* stream);
+/* gpu::RopeFrequencies (hip/ops.hpp:71; hip/ops.hip:1045-1050, 2265-2267):
+   out[i] = fp32(theta^(-2i / dim)) for i < dim / 2, the power in double
+   precision. dim even, at most 1024. */
+int lfm3_rope_frequencies(float* out, uint32_t dim, float theta, void* stream);
+/* gpu::Rope (hip/ops.hpp:72-73; hip/ops.hip:1052-1071, 2268-2274): rotates
+   pairs (i, i + dim / 2) of n x heads rows of dim floats (row (t, h) at
+   x + (t heads + h) dim) by angle (position + t) frequencies[i], divided
+   by factors[i] when factors is not NULL. */
+int lfm3_rope(float* x, const float* frequencies, const float* factors,
+              uint32_t n, uint32_t heads, uint32_t dim, uint32_t position,
+              void* stream);
+/* gpu::PackKV (hip/ops.hpp:107-108; hip/ops.hip:1729-1736, 2387-2390):
+   count values of k and v rounded to F16 (round to nearest even). */
+int lfm3_pack_kv(const float* k, const float* v, uint16_t* k16, uint16_t* v16,
+                 size_t count, void* stream);
 /* Chunk rows 0..rows-1 at positions position + r into the F16 ring: row r
    goes to slot (position + r) % capacity; only the last min(rows, capacity)
    rows are copied (their slots are distinct). stride = kv_heads * dim.
@@ -537,6 +555,88 @@ int lfm3_session_restore_snapshot(lfm3_session* session, const void* data,
                                   size_t bytes);
 /* Stream of the model's batch rounds (Session::DeviceStream). */
 void* lfm3_model_stream(lfm3_model* model);
+
+/* Session::ForwardEmbeddings (engine.hpp:104-110, engine.cpp:939-985):
+   n_rows input rows of hidden floats each in place of token embeddings, in
+   passes of 512 rows (one row: a decode row), on host memory or, with
+   on_device, device memory ordered before the call. logits (vocab floats,
+   may be NULL) receive the last row's logits. Refusals and poisoning as
+   lfm3_session_forward. */
+int lfm3_session_forward_rows(lfm3_session* session, const float* rows,
+                              size_t n_rows, int on_device, float* logits);
+/* Session::Input (engine.hpp:111-115): a run of token ids or of input rows
+   (hidden floats each, host memory); one of the two counts is 0. */
+typedef struct {
+  const uint32_t* tokens;
+  size_t n_tokens;
+  const float* rows;
+  size_t n_rows;
+} lfm3_input;
+/* Session::ForwardInputs (engine.hpp:116-121, engine.cpp:986-1100): the
+   runs in order, adjacent runs sharing their 512-row passes (a prompt that
+   mixes text and embeddings reads the weights once per pass). A run with
+   both tokens and rows, an out-of-range token or an empty total is
+   refused without touching state. */
+int lfm3_session_forward_inputs(lfm3_session* session, const lfm3_input* inputs,
+                                size_t n_inputs, float* logits);
+/* Session::ReadHidden (engine.hpp:122-123): the final-normed hidden row of
+   the last advanced row (hidden floats, host memory). */
+int lfm3_session_read_hidden(const lfm3_session* session, float* hidden);
+
+/* ---------------------------------------------------------------------
+ * Continuation hooks and state layout (continuation_hooks.hpp,
+ * continuation_layout.hpp / .cpp).
+ * ------------------------------------------------------------------- */
+/* ContinuationHooks (continuation_hooks.hpp:6-15): host callbacks that run
+   before the session changes state or submits device work. A nonzero
+   return refuses the call (LFM3_E_REFUSED), leaving the session as it
+   was. before_write gets the rows [first, end) about to be written (every
+   forward entry; each session of a batch round, engine.cpp:1196-1199),
+   before_reset runs first in lfm3_session_reset and before_restore first
+   in lfm3_session_restore_snapshot (engine.cpp:1522-1524). NULL members
+   are skipped; the table is copied. Session::SetContinuationHooks
+   (engine.cpp:1338-1340). */
+typedef struct {
+  void* user;
+  int (*before_write)(void* user, uint32_t first, uint32_t end);
+  int (*before_reset)(void* user);
+  int (*before_restore)(void* user);
+} lfm3_hooks;
+int lfm3_session_set_hooks(lfm3_session* session, const lfm3_hooks* hooks);
+
+/* ContinuationPart (continuation_layout.hpp:12-25). */
+enum {
+  LFM3_PART_LOGITS = 0,
+  LFM3_PART_FRONTIER = 1,
+  LFM3_PART_METADATA = 2,
+  LFM3_PART_CONVOLUTION = 3,
+  LFM3_PART_SLIDING_WINDOW = 4, /* K then V of a sliding ring */
+  LFM3_PART_KEY = 5,            /* full-attention K rows, final once written */
+  LFM3_PART_VALUE = 6
+};
+/* The metadata part's bytes: uint32 version (1), uint32 position, zeros. */
+#define LFM3_CONTINUATION_METADATA_BYTES 16
+/* One component of the state inventory: append rows (row_bytes per
+   position, state_bytes 0) or private state (state_bytes, row_bytes 0).
+   Ids count from 1 in inventory order. */
+typedef struct {
+  uint32_t id, part, layer, reserved;
+  size_t row_bytes, state_bytes;
+} lfm3_continuation_component;
+/* ContinuationLayout (continuation_layout.cpp:6-46): logits, frontier and
+   metadata, then per layer its convolution history, its sliding ring (2 x
+   kv_heads x head_dim x 2 x min(context, window) bytes) or its K and V
+   rows. Writes up to `capacity` components and their total to *count.
+   Refuses an invalid geometry (context 0 or past config->context). */
+int lfm3_continuation_layout(const lfm3_config* config, uint32_t context,
+                             lfm3_continuation_component* out, size_t capacity,
+                             size_t* count);
+/* PrivateBytes / RowBytes(position) (continuation_layout.cpp:56-69): the
+   private state's bytes, and the append rows' bytes at a frontier
+   (position <= context). */
+int lfm3_continuation_bytes(const lfm3_config* config, uint32_t context,
+                            uint32_t position, size_t* private_bytes,
+                            size_t* row_bytes);
 
 /* ---------------------------------------------------------------------
  * Deterministic synthetic inputs (benchmarks and parity tests). No

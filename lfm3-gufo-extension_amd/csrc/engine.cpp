@@ -43,6 +43,12 @@ void CheckStatus(int status) {
     throw Error(status, lfm3_last_error());
 }
 [[noreturn]] void Invalid(const std::string& m) { throw Error(LFM3_E_INVALID, m); }
+// A continuation hook's refusal (a nonzero return) stops the call before
+// the session changes state (continuation_hooks.hpp:6-15: hooks may throw).
+void Hook(int rc, const char* what) {
+  if (rc)
+    throw Error(LFM3_E_REFUSED, std::string("LFM3 continuation hook refused ") + what);
+}
 
 struct Buffer {
   void* p = nullptr;
@@ -174,6 +180,7 @@ struct lfm3_model {
   Buffer x, proj, a, hidden, out, gemv_ws, head_keys, ids;
   std::uint32_t head_groups = 0;
   Buffer image, exps;  // GEMV operand image of the current hidden-wide input
+  Buffer one_row;      // a host input row of a one-row chunk, on the device
   std::size_t proj_ld = 0, gemv_ws_bytes = 0;
   // Per-round device tables: RoundTable, per-layer pointer rows, items.
   Buffer table;
@@ -196,6 +203,8 @@ struct lfm3_session {
   lfm3_model* model = nullptr;
   std::uint32_t context = 0, position = 0;
   bool poisoned = false, logits_ready = false;
+  // Continuation hooks (continuation_hooks.hpp:6-15); null members skip.
+  lfm3_hooks hooks{};
   struct State {
     Buffer conv, k, v;
     std::uint32_t capacity = 0;
@@ -432,6 +441,7 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     m->image = Buffer(lfm3_operand_image_bytes(H));
     m->exps = Buffer(kMaxBatch * sizeof(int));
     m->ids = Buffer(B * 4);
+    m->one_row = Buffer(std::size_t(H) * 4);
     Check(hipDeviceSynchronize(), "model upload");
     *out = m.release();
     return LFM3_OK;
@@ -503,6 +513,8 @@ std::uint32_t lfm3_session_ring_capacity(const lfm3_session* s, std::uint32_t la
 int lfm3_session_reset(lfm3_session* s) {
   if (!s)
     return Fail(LFM3_E_INVALID, "null session");
+  if (s->hooks.before_reset && s->hooks.before_reset(s->hooks.user))
+    return Fail(LFM3_E_REFUSED, "LFM3 continuation hook refused the reset");
   const auto& c = s->model->config;
   const hipStream_t stream = s->model->stream;
   int e = HipStatus(hipStreamSynchronize(stream), "reset");
@@ -729,6 +741,9 @@ int lfm3_session_save_snapshot(lfm3_session* s, void* out, std::size_t bytes) {
 int lfm3_session_restore_snapshot(lfm3_session* s, const void* data, std::size_t bytes) {
   if (!s || !data)
     return Fail(LFM3_E_INVALID, "invalid LFM3 snapshot payload");
+  // engine.cpp:1522-1524: the hook runs before the header is checked.
+  if (s->hooks.before_restore && s->hooks.before_restore(s->hooks.user))
+    return Fail(LFM3_E_REFUSED, "LFM3 continuation hook refused the restore");
   const auto& c = s->model->config;
   const auto* p = static_cast<const std::uint8_t*>(data);
   // The whole header and the size are checked before any state changes.
@@ -1042,8 +1057,18 @@ void PruneRows(const lfm3_config& c, std::uint32_t n, std::vector<std::uint32_t>
 // full-attention K/V rows are written in place into the cache (the ring
 // does not wrap), sliding ones are staged and stored to the ring after
 // attention read its history (engine.cpp:437-470).
-void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std::uint32_t n,
-               bool want_logits) {
+// The input rows of a chunk, in row order: runs of token ids (host memory)
+// and runs of FP32 rows of hidden floats (host memory, or device memory
+// ordered before the call).
+struct ChunkPart {
+  std::uint32_t count = 0;
+  const std::uint32_t* tokens = nullptr;
+  const float* rows = nullptr;
+  bool on_device = false;
+};
+
+void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& input,
+               std::uint32_t n, bool want_logits) {
   const auto& c = m.config;
   const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
   const std::uint32_t L = c.n_layers, position = se.position;
@@ -1145,10 +1170,31 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
                                            z + o * H, rows, H, c.eps, s));
   };
 
-  Check(hipMemcpyAsync(b.tokens.p, tokens, std::size_t(n) * 4, hipMemcpyHostToDevice, s),
-        "token upload");
-  CheckStatus(lfm3_embed(m.embedding.codes.p, m.embedding.scales.p, c.vocab, H,
-                         b.tokens.as<std::uint32_t>(), n, x, s));
+  // x <- the chunk's input rows: token runs embedded from one upload of
+  // their ids, row runs copied into place (engine.cpp:1066-1092). The ids
+  // stay alive until the stream synchronizes at the end.
+  std::vector<std::uint32_t> ids;
+  for (const ChunkPart& part : input)
+    if (part.tokens)
+      ids.insert(ids.end(), part.tokens, part.tokens + part.count);
+  if (!ids.empty())
+    Check(hipMemcpyAsync(b.tokens.p, ids.data(), ids.size() * 4, hipMemcpyHostToDevice, s),
+          "token upload");
+  {
+    std::size_t row = 0, id = 0;
+    for (const ChunkPart& part : input) {
+      if (part.tokens) {
+        CheckStatus(lfm3_embed(m.embedding.codes.p, m.embedding.scales.p, c.vocab, H,
+                               b.tokens.as<std::uint32_t>() + id, part.count, x + row * H, s));
+        id += part.count;
+      } else {
+        Check(hipMemcpyAsync(x + row * H, part.rows, std::size_t(part.count) * H * 4,
+                             part.on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s),
+              "input rows");
+      }
+      row += part.count;
+    }
+  }
   residual_norm(0, nullptr, &m.layers[0].norm, live_in[0], live_in[0]);
   for (std::uint32_t il = 0; il < L; ++il) {
     const Layer& l = m.layers[il];
@@ -1260,6 +1306,97 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::uint32_t* tokens, std
   se.logits_ready = want_logits;
 }
 
+// Session::Forward / ForwardEmbeddings / ForwardInputs (engine.cpp:882-1100):
+// n input rows from `runs`, in chunks of kPrefillChunk rows that runs share
+// (one pass reads the weights once whatever mixes in it); a chunk of one row
+// is a decode row. The vocabulary head runs for the last chunk only when
+// logits are wanted.
+void ForwardRuns(lfm3_session& se, const std::vector<ChunkPart>& runs, std::size_t n,
+                 bool want_logits) {
+  lfm3_model& m = *se.model;
+  const std::size_t H = m.config.hidden;
+  std::size_t run = 0, at = 0;  // next input row: runs[run], row at
+  for (std::size_t done = 0; done < n;) {
+    const auto count = std::uint32_t(std::min<std::size_t>(kPrefillChunk, n - done));
+    std::vector<ChunkPart> parts;
+    for (std::uint32_t row = 0; row < count;) {
+      const ChunkPart& r = runs[run];
+      const auto take = std::uint32_t(std::min<std::size_t>(r.count - at, count - row));
+      if (take) {
+        ChunkPart p = r;
+        p.count = take;
+        if (r.tokens)
+          p.tokens = r.tokens + at;
+        else
+          p.rows = r.rows + at * H;
+        parts.push_back(p);
+      }
+      row += take;
+      at += take;
+      if (at == r.count) {
+        ++run;
+        at = 0;
+      }
+    }
+    const bool head = want_logits && done + count == n;
+    if (count == 1) {
+      // One row is one decode row (engine.cpp:412-436).
+      lfm3_session* one = &se;
+      const ChunkPart& p = parts.front();
+      if (p.tokens) {
+        RunRound(m, &one, 1, p.tokens, false, nullptr, head);
+      } else {
+        const float* row = p.rows;
+        if (!p.on_device) {
+          Check(hipMemcpyAsync(m.one_row.p, p.rows, H * 4, hipMemcpyHostToDevice, m.stream),
+                "input row");
+          row = m.one_row.as<float>();
+        }
+        const std::uint32_t unused = 0;
+        RunRound(m, &one, 1, &unused, false, &row, head);
+      }
+    } else {
+      RunPrompt(m, se, parts, count, head);
+    }
+    done += count;
+  }
+}
+
+// Checks shared by the forward entries (engine.cpp:904-914), then the
+// continuation hook for the rows about to be written.
+void CheckForward(lfm3_session* se, std::size_t n) {
+  if (!se)
+    Invalid("null LFM3 session");
+  if (se->poisoned)
+    throw Error(LFM3_E_STATE, "LFM3 session requires Reset after a device error");
+  if (n == 0 || n > se->context - se->position)
+    Invalid("invalid LFM3 input/logit count or context exhausted");
+}
+void BeforeWrite(lfm3_session& se, std::size_t n) {
+  if (se.hooks.before_write)
+    Hook(se.hooks.before_write(se.hooks.user, se.position, se.position + std::uint32_t(n)),
+         "the write");
+}
+
+// Runs a validated forward; a device failure poisons the session
+// (engine.cpp:924-926).
+int ForwardEntry(lfm3_session* se, const std::vector<ChunkPart>& runs, std::size_t n,
+                 float* logits) {
+  lfm3_model& m = *se->model;
+  try {
+    ForwardRuns(*se, runs, n, logits != nullptr);
+    if (logits)
+      CopyLogits(m, logits, se->logits.p);
+    return LFM3_OK;
+  } catch (const Error& e) {
+    se->poisoned = true;
+    return Fail(e.status, e.what());
+  } catch (const std::exception& e) {
+    se->poisoned = true;
+    return Fail(LFM3_E_HIP, e.what());
+  }
+}
+
 // engine.cpp:1178-1195; for ForwardBatchInputs (engine.cpp:1244-1259) a
 // token is checked only where no input row stands in for it.
 void ValidateBatch(lfm3_session* const* sessions, std::size_t n,
@@ -1286,6 +1423,9 @@ int BatchEntry(lfm3_session* const* sessions, std::size_t n,
       for (std::size_t i = 0; i < n; ++i)
         if (!logits[i])
           Invalid("invalid LFM3 decode batch shape");
+    // engine.cpp:1196-1199: every session's hook before any work.
+    for (std::size_t i = 0; i < n; ++i)
+      BeforeWrite(*sessions[i], 1);
   } catch (const Error& e) {
     return Fail(e.status, e.what());
   }
@@ -1319,43 +1459,163 @@ extern "C" {
 int lfm3_session_forward(lfm3_session* se, const std::uint32_t* tokens, std::size_t n,
                          float* logits) {
   try {
-    if (!se)
-      Invalid("null LFM3 session");
-    const auto& c = se->model->config;
-    if (se->poisoned)
-      throw Error(LFM3_E_STATE, "LFM3 session requires Reset after a device error");
-    if (!tokens || n == 0 || n > se->context - se->position)
+    CheckForward(se, n);
+    if (!tokens)
       Invalid("invalid LFM3 token/logit count or context exhausted");
     for (std::size_t i = 0; i < n; ++i)
-      if (tokens[i] >= c.vocab)
+      if (tokens[i] >= se->model->config.vocab)
         Invalid("LFM3 token out of range");
+    BeforeWrite(*se, n);
   } catch (const Error& e) {
     return Fail(e.status, e.what());
   }
-  lfm3_model& m = *se->model;
+  ChunkPart run;
+  run.count = std::uint32_t(n);
+  run.tokens = tokens;
+  return ForwardEntry(se, {run}, n, logits);
+}
+
+int lfm3_session_forward_rows(lfm3_session* se, const float* rows, std::size_t n_rows,
+                              int on_device, float* logits) {
   try {
-    for (std::size_t offset = 0; offset < n; offset += kPrefillChunk) {
-      const auto count = std::uint32_t(std::min<std::size_t>(kPrefillChunk, n - offset));
-      const bool last = offset + count == n;
-      if (count == 1) {
-        // One token is one decode row (engine.cpp:412-436).
-        lfm3_session* one = se;
-        RunRound(m, &one, 1, tokens + offset, false);
-        se->logits_ready = last && logits;
-      } else {
-        RunPrompt(m, *se, tokens + offset, count, last && logits);
-      }
-    }
-    if (logits)
-      CopyLogits(m, logits, se->logits.p);
-    return LFM3_OK;
+    CheckForward(se, n_rows);
+    if (!rows)
+      Invalid("invalid LFM3 embedding/logit count or context exhausted");
+    BeforeWrite(*se, n_rows);
   } catch (const Error& e) {
-    se->poisoned = true;  // engine.cpp:924-926
     return Fail(e.status, e.what());
-  } catch (const std::exception& e) {
-    se->poisoned = true;
-    return Fail(LFM3_E_HIP, e.what());
   }
+  ChunkPart run;
+  run.count = std::uint32_t(n_rows);
+  run.rows = rows;
+  run.on_device = on_device != 0;
+  return ForwardEntry(se, {run}, n_rows, logits);
+}
+
+int lfm3_session_forward_inputs(lfm3_session* se, const lfm3_input* inputs, std::size_t n_inputs,
+                                float* logits) {
+  std::vector<ChunkPart> runs;
+  std::size_t n = 0;
+  try {
+    if (!se || (!inputs && n_inputs))
+      Invalid("invalid LFM3 inputs");
+    const std::uint32_t vocab = se->model->config.vocab;
+    for (std::size_t i = 0; i < n_inputs; ++i) {
+      const lfm3_input& in = inputs[i];
+      if (in.n_tokens && in.n_rows)
+        Invalid("an LFM3 input run is tokens or rows");
+      if ((in.n_tokens && !in.tokens) || (in.n_rows && !in.rows))
+        Invalid("invalid LFM3 inputs");
+      for (std::size_t t = 0; t < in.n_tokens; ++t)
+        if (in.tokens[t] >= vocab)
+          Invalid("LFM3 token out of range");
+      ChunkPart run;
+      run.count = std::uint32_t(in.n_tokens + in.n_rows);
+      run.tokens = in.n_tokens ? in.tokens : nullptr;
+      run.rows = in.n_rows ? in.rows : nullptr;
+      if (run.count)
+        runs.push_back(run);
+      n += in.n_tokens + in.n_rows;
+    }
+    CheckForward(se, n);
+    BeforeWrite(*se, n);
+  } catch (const Error& e) {
+    return Fail(e.status, e.what());
+  }
+  return ForwardEntry(se, runs, n, logits);
+}
+
+// ContinuationLayout (continuation_layout.cpp:6-46): the state inventory
+// in the reference's order; ids count from 1.
+int lfm3_continuation_layout(const lfm3_config* config, std::uint32_t context,
+                             lfm3_continuation_component* out, std::size_t capacity,
+                             std::size_t* count) {
+  if (!config || !count || (capacity && !out) || !context || context > config->context ||
+      !config->n_layers || !config->hidden || !config->vocab || !config->head_dim ||
+      !config->conv_width || !config->kv_heads || !config->layer_type)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 continuation geometry");
+  const lfm3_config& c = *config;
+  std::size_t n = 0;
+  const auto add = [&](std::uint32_t part, std::size_t row, std::size_t state,
+                       std::uint32_t layer) {
+    if (n < capacity) {
+      lfm3_continuation_component& x = out[n];
+      x.id = std::uint32_t(n + 1);
+      x.part = part;
+      x.layer = layer;
+      x.reserved = 0;
+      x.row_bytes = row;
+      x.state_bytes = state;
+    }
+    ++n;
+  };
+  add(LFM3_PART_LOGITS, 0, std::size_t(c.vocab) * 4, 0);
+  add(LFM3_PART_FRONTIER, 0, std::size_t(c.hidden) * 4, 0);
+  add(LFM3_PART_METADATA, 0, LFM3_CONTINUATION_METADATA_BYTES, 0);
+  for (std::uint32_t l = 0; l < c.n_layers; ++l) {
+    const std::size_t row = std::size_t(c.kv_heads[l]) * c.head_dim * sizeof(Half);
+    switch (c.layer_type[l]) {
+      case LFM3_LAYER_CONV:
+        add(LFM3_PART_CONVOLUTION, 0, std::size_t(c.hidden) * (c.conv_width - 1) * 4, l);
+        break;
+      case LFM3_LAYER_SLIDING:
+        add(LFM3_PART_SLIDING_WINDOW, 0, 2 * row * std::min(context, c.window), l);
+        break;
+      default:
+        add(LFM3_PART_KEY, row, 0, l);
+        add(LFM3_PART_VALUE, row, 0, l);
+        break;
+    }
+  }
+  *count = n;
+  return LFM3_OK;
+}
+
+// PrivateBytes and RowBytes(position) (continuation_layout.cpp:56-69).
+int lfm3_continuation_bytes(const lfm3_config* config, std::uint32_t context,
+                            std::uint32_t position, std::size_t* private_bytes,
+                            std::size_t* row_bytes) {
+  std::size_t n = 0;
+  int e = lfm3_continuation_layout(config, context, nullptr, 0, &n);
+  if (e)
+    return e;
+  if (position > context)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 continuation frontier");
+  std::vector<lfm3_continuation_component> parts(n);
+  e = lfm3_continuation_layout(config, context, parts.data(), n, &n);
+  if (e)
+    return e;
+  std::size_t priv = 0, rows = 0;
+  for (const auto& x : parts) {
+    priv += x.state_bytes;
+    rows += x.row_bytes * position;
+  }
+  if (private_bytes)
+    *private_bytes = priv;
+  if (row_bytes)
+    *row_bytes = rows;
+  return LFM3_OK;
+}
+
+int lfm3_session_set_hooks(lfm3_session* se, const lfm3_hooks* hooks) {
+  if (!se)
+    return Fail(LFM3_E_INVALID, "null session");
+  se->hooks = hooks ? *hooks : lfm3_hooks{};
+  return LFM3_OK;
+}
+
+int lfm3_session_read_hidden(const lfm3_session* se, float* hidden) {
+  if (!se || !hidden)
+    return Fail(LFM3_E_INVALID, "null hidden row");
+  if (se->poisoned || !se->position)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 hidden frontier");
+  const hipStream_t stream = se->model->stream;
+  int e = HipStatus(hipMemcpyAsync(hidden, se->frontier.p, std::size_t(se->model->config.hidden) * 4,
+                                   hipMemcpyDeviceToHost, stream),
+                    "read hidden");
+  if (!e)
+    e = HipStatus(hipStreamSynchronize(stream), "read hidden");
+  return e;
 }
 
 int lfm3_forward_batch(lfm3_session* const* sessions, std::size_t n,

@@ -491,6 +491,50 @@ __device__ __forceinline__ void NormRotateHead(float* __restrict__ xh,
   xh[pair + P] = r1;
 }
 
+// RoPE table (hip/ops.hip:1045-1050): theta^(-2i / dim) as a
+// double-precision power of the FP32 exponent, rounded to FP32.
+__global__ void RopeTableKernel(float* __restrict__ out, int dim, float theta) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dim / 2; i += gridDim.x * blockDim.x) {
+    const float exponent = -2.0f * float(i) / float(dim);
+    out[i] = float(pow(double(theta), double(exponent)));
+  }
+}
+
+// Standalone paired RoPE (hip/ops.hip:1052-1071 semantics): one thread per
+// (row, head, pair) over a grid-stride walk; the pair (i, i + dim / 2) of
+// row (t, h) turns by (position + t) * frequencies[i] (/ factors[i]).
+__global__ void RopeRowsKernel(float* __restrict__ x, const float* __restrict__ frequencies,
+                               const float* __restrict__ factors, std::size_t units,
+                               int heads, int dim, std::uint32_t position) {
+  const int half = dim / 2;
+  for (std::size_t u = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x; u < units;
+       u += std::size_t(gridDim.x) * blockDim.x) {
+    const int pair = int(u % half);
+    const std::size_t head_row = u / half;
+    const std::uint32_t token = std::uint32_t(head_row / heads);
+    float angle = float(position + token) * frequencies[pair];
+    if (factors)
+      angle /= factors[pair];
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
+    float* h = x + head_row * dim;
+    const float a = h[pair], b = h[pair + half];
+    h[pair] = a * cs - b * sn;
+    h[pair + half] = b * cs + a * sn;
+  }
+}
+
+// F16 rounding of K and V rows (round to nearest even), grid-stride.
+__global__ void PackHalvesKernel(const float* __restrict__ k, const float* __restrict__ v,
+                                 Half* __restrict__ k16, Half* __restrict__ v16,
+                                 std::size_t count) {
+  for (std::size_t i = std::size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+       i += std::size_t(gridDim.x) * blockDim.x) {
+    k16[i] = FloatToHalfBits(k[i]);
+    v16[i] = FloatToHalfBits(v[i]);
+  }
+}
+
 // Decode heads: a block is one row (with its own position and ring) and
 // blockIdx.x walks the query heads, then the KV heads, which also store K
 // and V to the row's ring slot position % capacity.
@@ -1034,6 +1078,35 @@ int lfm3_prompt_heads(float* q, float* k, const float* v, std::uint32_t ld,
   LaunchPromptHeads(q, k, v, ld, q_norm, k_norm, frequencies, factors, k16, v16, rows, heads,
                     kv_heads, dim, position, eps, 1, 0, nullptr, static_cast<hipStream_t>(stream));
   return HipStatus(hipGetLastError(), "LFM3 prompt heads launch");
+}
+
+int lfm3_rope_frequencies(float* out, std::uint32_t dim, float theta, void* stream) {
+  if (!out || dim < 2 || dim % 2 || dim > 1024 || !(theta > 0))
+    return Fail(LFM3_E_INVALID, "invalid LFM3 RoPE table");
+  RopeTableKernel<<<1, 512, 0, static_cast<hipStream_t>(stream)>>>(out, int(dim), theta);
+  return HipStatus(hipGetLastError(), "LFM3 RoPE table launch");
+}
+
+int lfm3_rope(float* x, const float* frequencies, const float* factors, std::uint32_t n,
+              std::uint32_t heads, std::uint32_t dim, std::uint32_t position, void* stream) {
+  if (!x || !frequencies || !n || !heads || dim < 2 || dim % 2 || dim > 1024)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 RoPE shape");
+  const std::size_t units = std::size_t(n) * heads * (dim / 2);
+  const unsigned blocks = unsigned(std::min<std::size_t>((units + 255) / 256, 8192));
+  RopeRowsKernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      x, frequencies, factors, units, int(heads), int(dim), position);
+  return HipStatus(hipGetLastError(), "LFM3 RoPE launch");
+}
+
+int lfm3_pack_kv(const float* k, const float* v, std::uint16_t* k16, std::uint16_t* v16,
+                 std::size_t count, void* stream) {
+  if (!count)
+    return LFM3_OK;
+  if (!k || !v || !k16 || !v16)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 K/V pack");
+  const unsigned blocks = unsigned(std::min<std::size_t>((count + 255) / 256, 8192));
+  PackHalvesKernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(k, v, k16, v16, count);
+  return HipStatus(hipGetLastError(), "LFM3 K/V pack launch");
 }
 
 int lfm3_store_kv(const std::uint16_t* k16, const std::uint16_t* v16, std::uint16_t* cache_k,

@@ -14,7 +14,7 @@ import numpy as np
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_DIR, "liblfm3_amd.so")
 
-OK, E_INVALID, E_HIP, E_STATE, E_NOMEM = 0, -1, -2, -3, -4
+OK, E_INVALID, E_HIP, E_STATE, E_NOMEM, E_REFUSED = 0, -1, -2, -3, -4, -5
 LAYER_CONV, LAYER_FULL, LAYER_SLIDING = 0, 1, 2
 TYPE_F32, TYPE_Q8_0 = 0, 8
 STATE_LOGITS, STATE_FRONTIER, STATE_CONV, STATE_KEY, STATE_VALUE = range(5)
@@ -39,6 +39,28 @@ class Config(C.Structure):
 
 class Tensor(C.Structure):
     _fields_ = [("data", vp), ("type", u32), ("cols", u32), ("rows", u32)]
+
+
+class Input(C.Structure):
+    """lfm3_input: a run of token ids or of FP32 input rows."""
+    _fields_ = [("tokens", vp), ("n_tokens", C.c_size_t), ("rows", vp), ("n_rows", C.c_size_t)]
+
+
+WRITE_HOOK = C.CFUNCTYPE(C.c_int, vp, C.c_uint32, C.c_uint32)
+EVENT_HOOK = C.CFUNCTYPE(C.c_int, vp)
+
+
+class Hooks(C.Structure):
+    """lfm3_hooks: continuation callbacks (a nonzero return refuses)."""
+    _fields_ = [("user", vp), ("before_write", WRITE_HOOK), ("before_reset", EVENT_HOOK),
+                ("before_restore", EVENT_HOOK)]
+
+
+class Component(C.Structure):
+    """lfm3_continuation_component."""
+    _fields_ = [("id", C.c_uint32), ("part", C.c_uint32), ("layer", C.c_uint32),
+                ("reserved", C.c_uint32), ("row_bytes", C.c_size_t),
+                ("state_bytes", C.c_size_t)]
 
 
 class AttentionItem(C.Structure):
@@ -109,6 +131,15 @@ _SIGS = {
     "lfm3_session_state": (i32, [vp, i32, u32, C.POINTER(vp), C.POINTER(sz)]),
     "lfm3_session_set_position": (i32, [vp, u32]),
     "lfm3_session_begin_restore": (i32, [vp]),
+    "lfm3_session_forward_rows": (i32, [vp, vp, sz, i32, vp]),
+    "lfm3_session_forward_inputs": (i32, [vp, vp, sz, vp]),
+    "lfm3_session_read_hidden": (i32, [vp, vp]),
+    "lfm3_session_set_hooks": (i32, [vp, vp]),
+    "lfm3_continuation_layout": (i32, [vp, u32, vp, sz, C.POINTER(sz)]),
+    "lfm3_continuation_bytes": (i32, [vp, u32, u32, C.POINTER(sz), C.POINTER(sz)]),
+    "lfm3_rope_frequencies": (i32, [vp, u32, f32, vp]),
+    "lfm3_rope": (i32, [vp, vp, vp, u32, u32, u32, u32, vp]),
+    "lfm3_pack_kv": (i32, [vp, vp, vp, vp, sz, vp]),
     "lfm3_session_forward": (i32, [vp, vp, sz, vp]),
     "lfm3_forward_batch": (i32, [vp, sz, vp, vp]),
     "lfm3_forward_batch_greedy": (i32, [vp, sz, vp, vp]),
@@ -284,6 +315,28 @@ def make_config(dims: Dims):
     return cfg, (kv, lt)
 
 
+PART_LOGITS, PART_FRONTIER, PART_METADATA, PART_CONVOLUTION = 0, 1, 2, 3
+PART_SLIDING_WINDOW, PART_KEY, PART_VALUE = 4, 5, 6
+
+
+def continuation_layout(dims: Dims, context: int):
+    """lfm3_continuation_layout: [(id, part, layer, row_bytes, state_bytes)]."""
+    cfg, keep = make_config(dims)
+    n = sz()
+    check(lib().lfm3_continuation_layout(C.byref(cfg), context, None, 0, C.byref(n)))
+    arr = (Component * n.value)()
+    check(lib().lfm3_continuation_layout(C.byref(cfg), context, arr, n.value, C.byref(n)))
+    return [(c.id, c.part, c.layer, c.row_bytes, c.state_bytes) for c in arr]
+
+
+def continuation_bytes(dims: Dims, context: int, position: int):
+    """lfm3_continuation_bytes: (private bytes, append-row bytes at position)."""
+    cfg, keep = make_config(dims)
+    a, b = sz(), sz()
+    check(lib().lfm3_continuation_bytes(C.byref(cfg), context, position, C.byref(a), C.byref(b)))
+    return a.value, b.value
+
+
 def tensor_array(entries):
     arr = (Tensor * len(entries))()
     for i, e in enumerate(entries):
@@ -399,6 +452,59 @@ class Session:
         out = np.empty(self.model.dims.vocab, np.float32)
         check(lib().lfm3_session_read_logits(self.handle, ptr(out)))
         return out
+
+    def read_hidden(self) -> np.ndarray:
+        out = np.empty(self.model.dims.hidden, np.float32)
+        check(lib().lfm3_session_read_hidden(self.handle, ptr(out)))
+        return out
+
+    def forward_rows(self, rows, want_logits=True, device_addr=None):
+        """Session::ForwardEmbeddings: host rows (n, hidden) float32, or
+        device_addr of n rows (rows is then the row count)."""
+        out = np.empty(self.model.dims.vocab, np.float32) if want_logits else None
+        if device_addr is not None:
+            check(lib().lfm3_session_forward_rows(self.handle, device_addr, int(rows), 1,
+                                                  ptr(out) if want_logits else None))
+        else:
+            r = np.ascontiguousarray(rows, np.float32).reshape(-1, self.model.dims.hidden)
+            check(lib().lfm3_session_forward_rows(self.handle, ptr(r), r.shape[0], 0,
+                                                  ptr(out) if want_logits else None))
+        return out
+
+    def forward_inputs(self, runs, want_logits=True):
+        """Session::ForwardInputs: runs of ("tokens", ids) or ("rows", (n,
+        hidden) float32), in order."""
+        keep = []
+        arr = (Input * max(len(runs), 1))()
+        for i, (kind, data) in enumerate(runs):
+            if kind == "tokens":
+                t = np.ascontiguousarray(data, np.uint32)
+                keep.append(t)
+                arr[i] = Input(ptr(t) if t.size else None, t.size, None, 0)
+            else:
+                r = np.ascontiguousarray(data, np.float32).reshape(-1, self.model.dims.hidden)
+                keep.append(r)
+                arr[i] = Input(None, 0, ptr(r) if r.size else None, r.shape[0])
+        out = np.empty(self.model.dims.vocab, np.float32) if want_logits else None
+        check(lib().lfm3_session_forward_inputs(self.handle, arr, len(runs),
+                                                ptr(out) if want_logits else None))
+        return out
+
+    def set_hooks(self, before_write=None, before_reset=None, before_restore=None):
+        """Continuation hooks: Python callables returning 0 (allow) or
+        nonzero (refuse); None clears them all when every one is None."""
+        if before_write is None and before_reset is None and before_restore is None:
+            self._hooks = None
+            check(lib().lfm3_session_set_hooks(self.handle, None))
+            return
+        h = Hooks(None,
+                  WRITE_HOOK(lambda u, a, b: int(before_write(a, b))) if before_write
+                  else WRITE_HOOK(),
+                  EVENT_HOOK(lambda u: int(before_reset())) if before_reset else EVENT_HOOK(),
+                  EVENT_HOOK(lambda u: int(before_restore())) if before_restore
+                  else EVENT_HOOK())
+        self._hooks = h  # the callbacks must outlive the session's use
+        check(lib().lfm3_session_set_hooks(self.handle, C.byref(h)))
 
     def save_snapshot(self) -> bytes:
         """Session::SaveSnapshot: the snapshot v2 bytes."""

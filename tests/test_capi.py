@@ -228,3 +228,40 @@ def test_snapshot_signature_is_fnv1a32():
     raw = struct.pack("<7I3f", 256, 512, 1000, 8, 128, 32, 7, d.eps, d.theta, d.theta_swa)
     raw += struct.pack("<4I", L.LAYER_CONV, 0, L.LAYER_FULL, 2)
     assert signature(d) == fnv1a32(raw)
+
+
+def test_continuation_layout_follows_the_state_inventory():
+    """continuation_layout.cpp:6-46 restated from the config: logits,
+    frontier and a 16-byte metadata part, then per layer its convolution
+    history, its sliding ring (K and V of min(context, window) slots) or a
+    K and a V row component; ids count from 1. RowBytes(p) is p times the
+    row bytes; invalid geometry and frontiers are refused."""
+    d = L.Dims(context=8192)
+    ctx = 3000
+    comps = L.continuation_layout(d, ctx)
+    want = [(L.PART_LOGITS, 0, 0, d.vocab * 4), (L.PART_FRONTIER, 0, 0, d.hidden * 4),
+            (L.PART_METADATA, 0, 0, 16)]
+    row = d.kv_heads * d.head_dim * 2
+    for l in range(d.n_layers):
+        t = d.layer_type(l)
+        if t == L.LAYER_CONV:
+            want.append((L.PART_CONVOLUTION, l, 0, d.hidden * (d.conv_width - 1) * 4))
+        elif t == L.LAYER_SLIDING:
+            want.append((L.PART_SLIDING_WINDOW, l, 0, 2 * row * min(ctx, d.window)))
+        else:
+            want += [(L.PART_KEY, l, row, 0), (L.PART_VALUE, l, row, 0)]
+    assert [c[1:] for c in comps] == want
+    assert [c[0] for c in comps] == list(range(1, len(want) + 1))
+    assert len(comps) == 3 + 13 + 5 + 2 * 6
+    private, rows = L.continuation_bytes(d, ctx, 1234)
+    assert private == sum(w[3] for w in want)
+    assert rows == 1234 * 2 * 6 * row
+    assert L.continuation_bytes(d, ctx, 0)[1] == 0
+    for bad_ctx in (0, d.context + 1):
+        with pytest.raises(L.LFM3Error):
+            L.continuation_layout(d, bad_ctx)
+    with pytest.raises(L.LFM3Error):
+        L.continuation_bytes(d, ctx, ctx + 1)
+    # A context below the window shrinks the sliding rings to the context.
+    small = L.continuation_layout(d, 100)
+    assert all(c[4] == 2 * row * 100 for c in small if c[1] == L.PART_SLIDING_WINDOW)
