@@ -349,6 +349,28 @@ int lfm3_decode_heads_attention_ragged(
     uint32_t kv_heads, uint32_t dim, float eps, void* workspace,
     size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate
+   device memory (code under HIP graph capture, tight serving loops,
+   harnesses that forbid hipMalloc): lfm3_decode_heads_attention_ragged
+   with the span partials in a library-owned device array of
+   LFM3_ATTENTION_SCRATCH_BYTES per GPU (held until the process ends)
+   instead of a workspace argument; same kernels, same outputs. A plan
+   whose partials (lfm3_attention_workspace_bytes) exceed the array is
+   refused (LFM3_E_INVALID). Nothing in the array needs clearing: every
+   partial a merge reads is written by its span first in the same call.
+   Every call on one GPU shares that GPU's array, so calls that overlap on
+   one GPU (on different streams) race. Allocates nothing: the array's
+   address is looked up once per device (hipGetSymbolAddress). */
+#define LFM3_ATTENTION_SCRATCH_BYTES ((size_t)8 << 20)
+int lfm3_decode_heads_attention_ragged_noalloc(
+    const float* q, const float* k, const float* v, uint32_t ld,
+    const float* gate, uint32_t ldg, const float* q_norm, const float* k_norm,
+    const float* frequencies, const float* factors, uint16_t* const* cache_k,
+    uint16_t* const* cache_v, const uint32_t* positions,
+    const uint32_t* capacity, const lfm3_attention_item* items,
+    uint32_t n_items, float* out, uint32_t ldo, uint32_t rows, uint32_t heads,
+    uint32_t kv_heads, uint32_t dim, float eps, void* stream);
+
 /* ---------------------------------------------------------------------
  * Prompt chunk rows: n consecutive rows of one session (or, for the
  * convolution, packed segments of several sessions).

@@ -38,11 +38,20 @@
 // plan over exactly `rows` rows) writes NaN to its row's outputs, so the
 // misuse shows instead of leaving stale rows.
 #include <algorithm>
+#include <array>
 #include <cmath>
+#include <mutex>
 
 #include "common.hpp"
 
 namespace lfm3amd {
+
+// Span partials of lfm3_decode_heads_attention_ragged_noalloc: a
+// file-scope device array (one copy per GPU, held until the process ends)
+// in place of a caller workspace. Host code reaches it only through the
+// address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) float scratch[LFM3_ATTENTION_SCRATCH_BYTES / sizeof(float)];
+
 namespace {
 
 constexpr int kAttnThreads = 256, kAttnWaves = 4, kGroupKeys = 16, kWholeRowWaves = 8;
@@ -514,6 +523,31 @@ int Launch(const AttentionArgs& a, std::uint32_t n_items, std::uint32_t rows,
   return HipStatus(hipGetLastError(), "LFM3 decode attention launch");
 }
 
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+std::array<void*, kMaxDevices> g_scratch{};
+
+// The current device's copy of `scratch`, looked up once per device.
+int ScratchAddress(void** out) {
+  int device = 0;
+  int e = HipStatus(hipGetDevice(&device), "LFM3 attention scratch device");
+  if (e)
+    return e;
+  if (device < 0 || device >= kMaxDevices)
+    return Fail(LFM3_E_INVALID, "LFM3 attention scratch: device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[device]) {
+    void* p = nullptr;
+    e = HipStatus(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                  "LFM3 attention scratch address");
+    if (e)
+      return e;
+    g_scratch[device] = p;
+  }
+  *out = g_scratch[device];
+  return LFM3_OK;
+}
+
 }  // namespace
 }  // namespace lfm3amd
 
@@ -644,3 +678,27 @@ int lfm3_decode_heads_attention_ragged(
 }
 
 }  // extern "C"
+
+extern "C" int lfm3_decode_heads_attention_ragged_noalloc(
+    const float* q, const float* k, const float* v, std::uint32_t ld, const float* gate,
+    std::uint32_t ldg, const float* q_norm, const float* k_norm, const float* frequencies,
+    const float* factors, std::uint16_t* const* cache_k, std::uint16_t* const* cache_v,
+    const std::uint32_t* positions, const std::uint32_t* capacity,
+    const lfm3_attention_item* items, std::uint32_t n_items, float* out, std::uint32_t ldo,
+    std::uint32_t rows, std::uint32_t heads, std::uint32_t kv_heads, std::uint32_t dim,
+    float eps, void* stream) {
+  const std::size_t need = lfm3_attention_workspace_bytes(n_items, rows, heads, kv_heads, dim);
+  if (need > LFM3_ATTENTION_SCRATCH_BYTES)
+    return Fail(LFM3_E_INVALID,
+                "LFM3 attention plan needs " + std::to_string(need) +
+                    " bytes of span partials, more than the library's " +
+                    std::to_string(LFM3_ATTENTION_SCRATCH_BYTES) + "-byte scratch");
+  void* ws = nullptr;
+  const int e = ScratchAddress(&ws);
+  if (e)
+    return e;
+  return lfm3_decode_heads_attention_ragged(q, k, v, ld, gate, ldg, q_norm, k_norm, frequencies,
+                                            factors, cache_k, cache_v, positions, capacity, items,
+                                            n_items, out, ldo, rows, heads, kv_heads, dim, eps, ws,
+                                            LFM3_ATTENTION_SCRATCH_BYTES, stream);
+}

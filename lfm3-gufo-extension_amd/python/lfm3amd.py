@@ -119,6 +119,9 @@ _SIGS = {
     "lfm3_decode_heads_attention_ragged": (i32, [vp, vp, vp, u32, vp, u32, vp, vp, vp, vp, vp,
                                                  vp, vp, vp, vp, u32, vp, u32, u32, u32, u32,
                                                  u32, f32, vp, sz, vp]),
+    "lfm3_decode_heads_attention_ragged_noalloc": (i32, [vp, vp, vp, u32, vp, u32, vp, vp, vp,
+                                                         vp, vp, vp, vp, vp, vp, u32, vp, u32,
+                                                         u32, u32, u32, u32, f32, vp]),
     "lfm3_model_load": (i32, [C.POINTER(Config), C.POINTER(Tensor), sz, C.POINTER(vp)]),
     "lfm3_model_destroy": (None, [vp]),
     "lfm3_model_stream": (vp, [vp]),
