@@ -578,6 +578,23 @@ int lfm3_session_restore_snapshot(lfm3_session* session, const void* data,
 /* Stream of the model's batch rounds (Session::DeviceStream). */
 void* lfm3_model_stream(lfm3_model* model);
 
+/* One scheduler round (README.md:106-109: the decode batch and a prompt
+   chunk a round): n decode rows of distinct sessions (as
+   lfm3_forward_batch, at most 8; n may be 0) and a prompt of n_prompt
+   tokens of another session of the same model (as lfm3_session_forward;
+   n_prompt may be 0). The decode round runs on the model stream and the
+   prompt pass on the model's second stream, both enqueued before either
+   is waited on. ids (host, may be NULL) get the rows' greedy ids, logits
+   (may be NULL) host copies of their logits; prompt_logits (may be NULL)
+   the prompt's last logits. Every check and hook runs before any work;
+   a device failure of the decode round poisons its sessions, one of the
+   prompt poisons the prompt session. No counterpart call in the
+   reference, whose runner issues the two one after the other. */
+int lfm3_scheduler_round(lfm3_session* const* sessions, size_t n,
+                         const uint32_t* tokens, uint32_t* ids,
+                         float* const* logits, lfm3_session* prompt,
+                         const uint32_t* prompt_tokens, size_t n_prompt,
+                         float* prompt_logits);
 /* Session::ForwardEmbeddings (engine.hpp:104-110, engine.cpp:939-985):
    n_rows input rows of hidden floats each in place of token embeddings, in
    passes of 512 rows (one row: a decode row), on host memory or, with

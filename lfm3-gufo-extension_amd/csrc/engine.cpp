@@ -155,8 +155,10 @@ std::size_t Align(std::size_t n) { return (n + 255) / 256 * 256; }
 struct PromptBuffers {
   Buffer tokens, x, z, a16, scale, proj, mix, hid, out, row_max, chunk_k, chunk_v, attn_ws;
   Buffer one_table;  // one decode-attention row: ring pointers, capacity, position, items
+  Buffer one_ws;     // that row's span partials (apart from the decode round's)
   std::unique_ptr<PinnedBuffer> one_staging;
   std::size_t lda = 0, proj_ld = 0, attn_ws_bytes = 0, one_bytes = 0, one_items = 0;
+  std::size_t one_ws_bytes = 0;
 };
 
 }  // namespace
@@ -175,6 +177,9 @@ struct lfm3_model {
   bool tied = true;
   Buffer output_norm, factors, freq_global, freq_sliding;
   hipStream_t stream = nullptr;
+  // The stream a scheduler round's prompt pass runs on, beside the decode
+  // round on `stream` (both default priority).
+  hipStream_t prompt_stream = nullptr;
   // Round scratch, shared by the model's rounds (calls are serialized, as
   // the Gufo scheduler serializes sessions: engine.cpp:101-113).
   Buffer x, proj, a, hidden, out, gemv_ws, head_keys, ids;
@@ -195,6 +200,8 @@ struct lfm3_model {
   ~lfm3_model() {
     if (stream)
       (void)hipStreamDestroy(stream);
+    if (prompt_stream)
+      (void)hipStreamDestroy(prompt_stream);
   }
   const Matrix& head() const { return tied ? embedding : output; }
 };
@@ -328,6 +335,7 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
     ValidateTensors(c, tensors);
     Check(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "hipStreamCreate");
+    Check(hipStreamCreateWithFlags(&m->prompt_stream, hipStreamNonBlocking), "hipStreamCreate");
 
     const lfm3_tensor& emb = tensors[0];
     CheckTensor(emb, H, c.vocab, true, "token_embd.weight");
@@ -792,10 +800,12 @@ int lfm3_session_restore_snapshot(lfm3_session* s, const void* data, std::size_t
 namespace lfm3amd {
 namespace {
 
-// One decode round of n rows (engine.cpp:257-527, batch branch).
-void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
-              const std::uint32_t* tokens, bool greedy, const float* const* inputs = nullptr,
-              bool head = true) {
+// One decode round of n rows (engine.cpp:257-527, batch branch): every
+// launch, enqueued on the model stream; FinishRound advances the sessions
+// once the stream has drained.
+void EnqueueRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
+                  const std::uint32_t* tokens, bool greedy, const float* const* inputs,
+                  bool head) {
   const auto& c = m.config;
   const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
   const std::uint32_t L = c.n_layers;
@@ -954,11 +964,21 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
       CheckStatus(LaunchArgmaxKeys(keys, n, m.head_groups, m.ids.as<std::uint32_t>(), s));
   }
   Check(hipGetLastError(), "round launch");
-  Check(hipStreamSynchronize(s), "round");
+}
+
+void FinishRound(lfm3_session* const* sessions, std::uint32_t n, bool head) {
   for (std::uint32_t i = 0; i < n; ++i) {
     ++sessions[i]->position;
     sessions[i]->logits_ready = head;
   }
+}
+
+void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
+              const std::uint32_t* tokens, bool greedy, const float* const* inputs = nullptr,
+              bool head = true) {
+  EnqueueRound(m, sessions, n, tokens, greedy, inputs, head);
+  Check(hipStreamSynchronize(m.stream), "round");
+  FinishRound(sessions, n, head);
 }
 
 // Device logits row -> caller's host row through the model's pinned
@@ -1008,6 +1028,11 @@ PromptBuffers& EnsurePromptBuffers(lfm3_model& m) {
   b->one_items = lfm3_attention_max_items(1, c.context);
   b->one_bytes = Align(4 * sizeof(void*)) + Align(b->one_items * sizeof(lfm3_attention_item));
   b->one_table = Buffer(b->one_bytes);
+  b->one_ws_bytes = std::max<std::size_t>(
+      lfm3_attention_workspace_bytes(std::uint32_t(b->one_items), 1, c.heads, c.heads,
+                                     std::uint32_t(D)),
+      256);
+  b->one_ws = Buffer(b->one_ws_bytes);
   b->one_staging = std::make_unique<PinnedBuffer>(b->one_bytes);
   // FP16 tiles of the gate/up matrices (every stored tile: two per 16
   // output rows). Their GEMM runs in the wide block shape, where dropping
@@ -1068,11 +1093,10 @@ struct ChunkPart {
 };
 
 void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& input,
-               std::uint32_t n, bool want_logits) {
+               std::uint32_t n, bool want_logits, hipStream_t s) {
   const auto& c = m.config;
   const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
   const std::uint32_t L = c.n_layers, position = se.position;
-  const hipStream_t s = m.stream;
   PromptBuffers& b = EnsurePromptBuffers(m);
   std::vector<std::uint32_t> live_in, live_out;
   PruneRows(c, n, live_in, live_out);
@@ -1252,15 +1276,15 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
         Check(hipMemcpyAsync(dev, host, b.one_bytes, hipMemcpyHostToDevice, s), "table upload");
         const std::size_t ws = lfm3_attention_workspace_bytes(std::uint32_t(count), 1, c.heads,
                                                               l.kv, D);
-        if (ws > m.attn_ws_bytes)
+        if (ws > b.one_ws_bytes)
           throw Error(LFM3_E_INVALID, "LFM3 attention workspace too small");
         CheckStatus(lfm3_decode_attention_ragged(
             q_rows, pld, g_rows, pld, reinterpret_cast<const std::uint16_t* const*>(dev),
             reinterpret_cast<const std::uint16_t* const*>(dev + sizeof(void*)),
             reinterpret_cast<const std::uint32_t*>(dev + 2 * sizeof(void*)),
             reinterpret_cast<const lfm3_attention_item*>(dev + Align(4 * sizeof(void*))),
-            std::uint32_t(count), a_rows, c.heads * D, 1, c.heads, l.kv, D, m.attn_ws.p,
-            m.attn_ws_bytes, s));
+            std::uint32_t(count), a_rows, c.heads * D, 1, c.heads, l.kv, D, b.one_ws.p,
+            b.one_ws_bytes, s));
         // The staging buffer is reused by the next layer's row.
         Check(hipStreamSynchronize(s), "decode attention row");
       } else {
@@ -1312,8 +1336,10 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
 // is a decode row. The vocabulary head runs for the last chunk only when
 // logits are wanted.
 void ForwardRuns(lfm3_session& se, const std::vector<ChunkPart>& runs, std::size_t n,
-                 bool want_logits) {
+                 bool want_logits, hipStream_t prompt_stream = nullptr) {
   lfm3_model& m = *se.model;
+  if (!prompt_stream)
+    prompt_stream = m.stream;
   const std::size_t H = m.config.hidden;
   std::size_t run = 0, at = 0;  // next input row: runs[run], row at
   for (std::size_t done = 0; done < n;) {
@@ -1356,7 +1382,7 @@ void ForwardRuns(lfm3_session& se, const std::vector<ChunkPart>& runs, std::size
         RunRound(m, &one, 1, &unused, false, &row, head);
       }
     } else {
-      RunPrompt(m, se, parts, count, head);
+      RunPrompt(m, se, parts, count, head, prompt_stream);
     }
     done += count;
   }
@@ -1595,6 +1621,110 @@ int lfm3_continuation_bytes(const lfm3_config* config, std::uint32_t context,
   if (row_bytes)
     *row_bytes = rows;
   return LFM3_OK;
+}
+
+// One scheduler round (README.md:106-109; runner.cpp drives the decode
+// batch and a prompt chunk each round): the decode rows of `sessions` on
+// the model stream and the prompt pass on the model's prompt stream, both
+// enqueued before either is waited on, so the bandwidth-bound decode GEMVs
+// run beside the matrix-core prompt GEMMs. The decode round's greedy ids
+// (ids) and logits (logits) and the prompt's last logits are as from
+// lfm3_forward_batch_greedy / lfm3_forward_batch and lfm3_session_forward.
+int lfm3_scheduler_round(lfm3_session* const* sessions, std::size_t n,
+                         const std::uint32_t* tokens, std::uint32_t* ids, float* const* logits,
+                         lfm3_session* prompt, const std::uint32_t* prompt_tokens,
+                         std::size_t n_prompt, float* prompt_logits) {
+  lfm3_model* model = nullptr;
+  try {
+    if (!n && !n_prompt)
+      Invalid("empty LFM3 scheduler round");
+    if (n) {
+      ValidateBatch(sessions, n, tokens);
+      if (logits)
+        for (std::size_t i = 0; i < n; ++i)
+          if (!logits[i])
+            Invalid("invalid LFM3 decode batch shape");
+      model = sessions[0]->model;
+    }
+    if (n_prompt) {
+      CheckForward(prompt, n_prompt);
+      if (!prompt_tokens)
+        Invalid("invalid LFM3 token/logit count or context exhausted");
+      if (model && prompt->model != model)
+        Invalid("LFM3 prompt session of another model");
+      if (n && std::find(sessions, sessions + n, prompt) != sessions + n)
+        Invalid("an LFM3 session cannot decode and prefill in one round");
+      for (std::size_t i = 0; i < n_prompt; ++i)
+        if (prompt_tokens[i] >= prompt->model->config.vocab)
+          Invalid("LFM3 token out of range");
+      model = prompt->model;
+    }
+    for (std::size_t i = 0; i < n; ++i)
+      BeforeWrite(*sessions[i], 1);
+    if (n_prompt)
+      BeforeWrite(*prompt, n_prompt);
+  } catch (const Error& e) {
+    return Fail(e.status, e.what());
+  }
+  lfm3_model& m = *model;
+  const auto poison_batch = [&] {
+    for (std::size_t i = 0; i < n; ++i)
+      sessions[i]->poisoned = true;
+  };
+  int status = LFM3_OK;
+  std::string message;
+  bool enqueued = false;
+  try {
+    if (n_prompt)
+      EnsurePromptBuffers(m);
+    // A prompt whose last chunk is one row runs that row as a decode round
+    // on the model stream: then the two run one after the other.
+    const bool overlap = n && n_prompt && n_prompt % kPrefillChunk != 1;
+    if (n) {
+      EnqueueRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr, nullptr, true);
+      enqueued = true;
+      if (!overlap) {
+        Check(hipStreamSynchronize(m.stream), "round");
+        FinishRound(sessions, std::uint32_t(n), true);
+        enqueued = false;
+      }
+    }
+    if (n_prompt) {
+      ChunkPart run;
+      run.count = std::uint32_t(n_prompt);
+      run.tokens = prompt_tokens;
+      try {
+        ForwardRuns(*prompt, {run}, n_prompt, prompt_logits != nullptr, m.prompt_stream);
+      } catch (const std::exception& e) {
+        prompt->poisoned = true;  // engine.cpp:924-926
+        (void)hipStreamSynchronize(m.prompt_stream);
+        const auto* err = dynamic_cast<const Error*>(&e);
+        status = err ? err->status : LFM3_E_HIP;
+        message = e.what();
+      }
+    }
+    if (enqueued) {
+      Check(hipStreamSynchronize(m.stream), "round");
+      FinishRound(sessions, std::uint32_t(n), true);
+      enqueued = false;
+    }
+    if (n && logits)
+      for (std::size_t i = 0; i < n; ++i)
+        CopyLogits(m, logits[i], sessions[i]->logits.p);
+    if (n && ids) {
+      Check(hipMemcpyAsync(ids, m.ids.p, n * 4, hipMemcpyDeviceToHost, m.stream), "ids copy");
+      Check(hipStreamSynchronize(m.stream), "ids copy");
+    }
+    if (status == LFM3_OK && n_prompt && prompt_logits)
+      CopyLogits(m, prompt_logits, prompt->logits.p);
+  } catch (const std::exception& e) {
+    if (enqueued)
+      (void)hipStreamSynchronize(m.stream);
+    poison_batch();  // engine.cpp:1205-1208
+    const auto* err = dynamic_cast<const Error*>(&e);
+    return Fail(err ? err->status : LFM3_E_HIP, e.what());
+  }
+  return status == LFM3_OK ? LFM3_OK : Fail(status, message);
 }
 
 int lfm3_session_set_hooks(lfm3_session* se, const lfm3_hooks* hooks) {

@@ -134,6 +134,7 @@ _SIGS = {
     "lfm3_session_state": (i32, [vp, i32, u32, C.POINTER(vp), C.POINTER(sz)]),
     "lfm3_session_set_position": (i32, [vp, u32]),
     "lfm3_session_begin_restore": (i32, [vp]),
+    "lfm3_scheduler_round": (i32, [vp, sz, vp, vp, vp, vp, vp, sz, vp]),
     "lfm3_session_forward_rows": (i32, [vp, vp, sz, i32, vp]),
     "lfm3_session_forward_inputs": (i32, [vp, vp, sz, vp]),
     "lfm3_session_read_hidden": (i32, [vp, vp]),
@@ -388,6 +389,28 @@ class Model:
 
     def forward_batch_greedy(self, sessions, tokens):
         return self.forward_batch(sessions, tokens, want_logits=False)
+
+    def scheduler_round(self, sessions, tokens, prompt=None, prompt_tokens=None,
+                        want_logits=False, want_prompt_logits=True):
+        """lfm3_scheduler_round: decode rows of `sessions` beside a prompt
+        pass of `prompt`. Returns (greedy ids, decode logits or None, prompt
+        logits or None)."""
+        n = len(sessions)
+        toks = np.ascontiguousarray(tokens if n else np.zeros(0), np.uint32)
+        handles = (vp * max(n, 1))(*[s.handle for s in sessions])
+        ids = np.zeros(n, np.uint32)
+        out = np.empty((n, self.dims.vocab), np.float32) if want_logits and n else None
+        dst = (vp * max(n, 1))(*[out[i].ctypes.data for i in range(n)]) if out is not None else None
+        ptoks = np.ascontiguousarray(prompt_tokens if prompt is not None else np.zeros(0),
+                                     np.uint32)
+        pout = (np.empty(self.dims.vocab, np.float32)
+                if prompt is not None and want_prompt_logits else None)
+        check(lib().lfm3_scheduler_round(handles, n, ptr(toks) if n else None,
+                                         ptr(ids) if n else None, dst,
+                                         prompt.handle if prompt is not None else None,
+                                         ptr(ptoks) if ptoks.size else None, ptoks.size,
+                                         ptr(pout) if pout is not None else None))
+        return ids, out, pout
 
     def forward_batch_inputs(self, sessions, tokens, rows, want_logits=True):
         """Session::ForwardBatchInputs: rows[i] is a device address of an

@@ -261,6 +261,7 @@ extern "C" {
 
 void orc_set_threads(unsigned threads) { g_threads.store(std::max(1u, threads)); }
 unsigned orc_threads(void) { return g_threads.load(); }
+unsigned orc_hardware_concurrency(void) { return std::thread::hardware_concurrency(); }
 
 float orc_half_to_float(uint16_t h) { return HalfToFloat(h); }
 uint16_t orc_float_to_half(float f) { return FloatToHalf(f); }

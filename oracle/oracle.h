@@ -79,6 +79,8 @@ typedef struct orc_session orc_session;
    sum, so results are identical for any count; process-wide. */
 void orc_set_threads(unsigned threads);
 unsigned orc_threads(void);
+/* std::thread::hardware_concurrency() of the host. */
+unsigned orc_hardware_concurrency(void);
 
 float orc_half_to_float(uint16_t h);
 uint16_t orc_float_to_half(float f);

@@ -33,6 +33,7 @@ class Tensor(C.Structure):
 _SIGS = {
     "orc_set_threads": (None, [u32]),
     "orc_threads": (u32, []),
+    "orc_hardware_concurrency": (u32, []),
     "orc_half_to_float": (f32, [C.c_uint16]),
     "orc_float_to_half": (C.c_uint16, [f32]),
     "orc_halves_to_floats": (None, [vp, vp, sz]),
@@ -107,6 +108,10 @@ def set_threads(n: int):
 
 def threads() -> int:
     return int(lib().orc_threads())
+
+
+def hardware_concurrency() -> int:
+    return int(lib().orc_hardware_concurrency())
 
 
 def half_to_float(h: np.ndarray) -> np.ndarray:
