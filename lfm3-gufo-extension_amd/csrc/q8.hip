@@ -102,10 +102,13 @@ GemvPlan PlanGemv(std::uint32_t rows, std::uint32_t cols, bool swiglu,
     p.SPW = 5;  // slices of 40 chunks (80 KB of LDS operands), prefetched
   // Two 64 KB blocks fit a CU. Past 256 tiles a block takes two tiles: it
   // stages x and reduces across waves once for both (at 8192 x 2048 this is
-  // about 10% faster than 512 one-tile blocks). A multi-slice block keeps
+  // about 10% faster than 512 one-tile blocks). So does a part of 24 chunks
+  // or more: each tile then costs fewer staged x chunks (2048 x 7680 in 4
+  // parts: 6.8 us against 7.9 us with one tile; 2048 x 2048 in 2 parts,
+  // 16 chunks a part, stays fastest with one). A multi-slice block keeps
   // two slices of weights in registers: one tile (or gate/up pair).
   const int units = p.row_tiles / unit;
-  int per = units > 256 && !swiglu ? 2 : 1;
+  int per = (units > 256 || nloc >= 24) && !swiglu ? 2 : 1;
   if (p.SPW == 5)
     per = 1;
   p.RT = per * unit;
