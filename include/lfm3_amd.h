@@ -248,6 +248,32 @@ size_t lfm3_argmax_workspace_bytes(uint32_t rows);
 int lfm3_argmax(const float* logits, uint32_t rows, uint32_t cols,
                 uint32_t* ids, void* workspace, size_t workspace_bytes,
                 void* stream);
+/* Sampler settings of the serving loop (runner.cpp:31-35 defaults:
+   temperature 0.1, top_k 50, repeat_penalty 1.1). temperature <= 0 or
+   top_k == 1 is the greedy pick; top_k 0 keeps the whole vocabulary. */
+typedef struct {
+  float temperature;
+  uint32_t top_k;
+  float repeat_penalty;
+} lfm3_sampling;
+#define LFM3_SAMPLE_MAX_TOP_K 1024u
+#define LFM3_SAMPLE_MAX_PENALTY 4096u
+#define LFM3_SAMPLE_MAX_COLS 262144u
+/* One token id per logits row (rows of cols floats, ld floats apart), all
+   in device memory. Each row: the repetition penalty over
+   penalty_ids[row * n_penalty ...] (logit l -> l / p if l > 0 else l * p,
+   once per listed token; ids >= cols are padding), the top_k largest
+   logits (ties toward the lower index), weights exp((l - l_max) / T), and
+   the first candidate, in descending logit order (index order when the
+   whole vocabulary is kept), whose running weight sum exceeds
+   uniforms[row] * total. uniforms (in [0, 1)) may be NULL for a greedy
+   pick. No workspace; deterministic for given uniforms.
+   Replaces: sampler.Sample(s.logits) in SelectNext (runner.cpp:300-325),
+   the Gufo host sampler, which the reference does not carry. */
+int lfm3_sample(const float* logits, uint32_t rows, uint32_t cols, uint32_t ld,
+                const lfm3_sampling* params, const uint32_t* penalty_ids,
+                uint32_t n_penalty, const float* uniforms, uint32_t* ids,
+                void* stream);
 
 /* ---------------------------------------------------------------------
  * Ragged decode rows: every row belongs to its own session; per-row
@@ -544,6 +570,17 @@ int lfm3_forward_batch(lfm3_session* const* sessions, size_t n,
    no logits cross PCIe. */
 int lfm3_forward_batch_greedy(lfm3_session* const* sessions, size_t n,
                               const uint32_t* tokens, uint32_t* ids);
+/* The same round with the sampler's pick in place of the greedy one
+   (lfm3_sample over each session's device logits row; the serving loop's
+   SelectNext, runner.cpp:300-325, on the device). Host inputs: row i's
+   penalty list penalty_ids[i * n_penalty ...] (the session's recent
+   tokens; ids >= vocab are padding; may be NULL when n_penalty is 0) and
+   its uniform uniforms[i] in [0, 1) (may be NULL for a greedy setting).
+   ids (host) get the picks. Parameters are checked before any work. */
+int lfm3_forward_batch_sample(lfm3_session* const* sessions, size_t n,
+                              const uint32_t* tokens, const lfm3_sampling* params,
+                              const uint32_t* penalty_ids, uint32_t n_penalty,
+                              const float* uniforms, uint32_t* ids);
 /* Session::ForwardBatchInputs (engine.cpp:1217-1299): the round of
    lfm3_forward_batch where rows[i], when not NULL, is a device FP32 row of
    hidden floats that stands in for session i's token embedding (tokens[i]

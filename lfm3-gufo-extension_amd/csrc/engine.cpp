@@ -191,6 +191,9 @@ struct lfm3_model {
   Buffer table;
   std::unique_ptr<PinnedBuffer> staging;
   std::unique_ptr<PinnedBuffer> logits_host;  // one logits row, pinned
+  // A sampled round's uniforms and penalty lists (made on first use).
+  Buffer sample_table;
+  std::unique_ptr<PinnedBuffer> sample_staging;
   std::size_t table_bytes = 0, items_capacity = 0;
   Buffer attn_ws;
   std::size_t attn_ws_bytes = 0;
@@ -1440,15 +1443,57 @@ void ValidateBatch(lfm3_session* const* sessions, std::size_t n,
   }
 }
 
+// The sampler's inputs for a round (host arrays): row i's penalty list at
+// penalty_ids + i * n_penalty and its uniform at uniforms[i].
+struct SampleArgs {
+  const lfm3_sampling* params = nullptr;
+  const std::uint32_t* penalty_ids = nullptr;
+  std::uint32_t n_penalty = 0;
+  const float* uniforms = nullptr;
+};
+
+// Uploads the sampler's inputs on the model stream and picks each row's id
+// from its session's logits row into m.ids.
+void EnqueueSample(lfm3_model& m, std::uint32_t n, const SampleArgs& a) {
+  const std::size_t uni_bytes = Align(kMaxBatch * 4);
+  const std::size_t bytes = uni_bytes + std::size_t(kMaxBatch) * kSampleMaxPenalty * 4;
+  if (!m.sample_staging) {
+    m.sample_table = Buffer(bytes);
+    m.sample_staging = std::make_unique<PinnedBuffer>(bytes);
+  }
+  auto* host = static_cast<std::uint8_t*>(m.sample_staging->p);
+  if (a.uniforms)
+    std::memcpy(host, a.uniforms, n * 4);
+  if (a.n_penalty)
+    std::memcpy(host + uni_bytes, a.penalty_ids, std::size_t(n) * a.n_penalty * 4);
+  const std::size_t used = uni_bytes + std::size_t(n) * a.n_penalty * 4;
+  auto* dev = m.sample_table.as<std::uint8_t>();
+  Check(hipMemcpyAsync(dev, host, used, hipMemcpyHostToDevice, m.stream), "sampler upload");
+  const auto* rows = reinterpret_cast<const float* const*>(m.table.as<std::uint8_t>() +
+                                                           offsetof(RoundTable, logits));
+  CheckStatus(LaunchSample(nullptr, 0, rows, n, m.config.vocab, *a.params,
+                           a.n_penalty ? reinterpret_cast<const std::uint32_t*>(dev + uni_bytes)
+                                       : nullptr,
+                           a.n_penalty, a.uniforms ? reinterpret_cast<const float*>(dev) : nullptr,
+                           m.ids.as<std::uint32_t>(), m.stream));
+}
+
 int BatchEntry(lfm3_session* const* sessions, std::size_t n,
                const std::uint32_t* tokens, float* const* logits,
-               std::uint32_t* ids, const float* const* inputs = nullptr, bool head = true) {
+               std::uint32_t* ids, const float* const* inputs = nullptr, bool head = true,
+               const SampleArgs* sample = nullptr) {
   try {
     ValidateBatch(sessions, n, tokens, inputs);
     if (logits)
       for (std::size_t i = 0; i < n; ++i)
         if (!logits[i])
           Invalid("invalid LFM3 decode batch shape");
+    if (sample) {
+      if (!sample->params ||
+          CheckSample(*sample->params, sessions[0]->model->config.vocab, sample->n_penalty,
+                      sample->penalty_ids != nullptr, sample->uniforms != nullptr))
+        Invalid("unsupported LFM3 sampling parameters");
+    }
     // engine.cpp:1196-1199: every session's hook before any work.
     for (std::size_t i = 0; i < n; ++i)
       BeforeWrite(*sessions[i], 1);
@@ -1457,7 +1502,14 @@ int BatchEntry(lfm3_session* const* sessions, std::size_t n,
   }
   lfm3_model& m = *sessions[0]->model;
   try {
-    RunRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr, inputs, head);
+    if (sample) {
+      EnqueueRound(m, sessions, std::uint32_t(n), tokens, false, inputs, head);
+      EnqueueSample(m, std::uint32_t(n), *sample);
+      Check(hipStreamSynchronize(m.stream), "round");
+      FinishRound(sessions, std::uint32_t(n), head);
+    } else {
+      RunRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr, inputs, head);
+    }
     if (logits)
       for (std::size_t i = 0; i < n; ++i)
         CopyLogits(m, logits[i], sessions[i]->logits.p);
@@ -1760,6 +1812,20 @@ int lfm3_forward_batch_greedy(lfm3_session* const* sessions, std::size_t n,
   if (!ids)
     return Fail(LFM3_E_INVALID, "null greedy ids");
   return BatchEntry(sessions, n, tokens, nullptr, ids);
+}
+
+int lfm3_forward_batch_sample(lfm3_session* const* sessions, std::size_t n,
+                              const std::uint32_t* tokens, const lfm3_sampling* params,
+                              const std::uint32_t* penalty_ids, std::uint32_t n_penalty,
+                              const float* uniforms, std::uint32_t* ids) {
+  if (!ids || !params)
+    return Fail(LFM3_E_INVALID, "null sampled ids or sampling parameters");
+  SampleArgs a;
+  a.params = params;
+  a.penalty_ids = penalty_ids;
+  a.n_penalty = n_penalty;
+  a.uniforms = uniforms;
+  return BatchEntry(sessions, n, tokens, nullptr, ids, nullptr, true, &a);
 }
 
 int lfm3_forward_batch_inputs(lfm3_session* const* sessions, std::size_t n,

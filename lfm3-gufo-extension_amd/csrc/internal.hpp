@@ -6,6 +6,8 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "../../include/lfm3_amd.h"
+
 namespace lfm3amd {
 // Decode-round residual norm writing the next GEMV's operand image
 // (lfm3_residual_norm_image) with the round's options: z rows through a
@@ -48,6 +50,17 @@ std::uint32_t HeadGemvGroups(std::uint32_t rows, std::uint32_t cols);
 // ids[t] = the first index of token t's maximum from the head's keys.
 int LaunchArgmaxKeys(const unsigned long long* keys, std::uint32_t rows, std::uint32_t groups,
                      std::uint32_t* ids, hipStream_t stream);
+// lfm3_sample's limits, its parameter check (status, with the error text
+// set) and its launch over rows given by a device pointer table (row_ptrs)
+// or by a base and stride (logits, ld).
+constexpr int kSampleMaxCols = LFM3_SAMPLE_MAX_COLS, kSampleMaxTopK = LFM3_SAMPLE_MAX_TOP_K;
+constexpr int kSampleMaxPenalty = LFM3_SAMPLE_MAX_PENALTY;
+int CheckSample(const lfm3_sampling& p, std::uint32_t cols, std::uint32_t n_penalty,
+                bool have_penalty, bool have_uniforms);
+int LaunchSample(const float* logits, std::uint32_t ld, const float* const* row_ptrs,
+                 std::uint32_t rows, std::uint32_t cols, const lfm3_sampling& p,
+                 const std::uint32_t* penalty_ids, std::uint32_t n_penalty,
+                 const float* uniforms, std::uint32_t* ids, hipStream_t stream);
 // dst[i][0..count) = src + i * ld for rows i < rows, with dst pointers read
 // from a device table (per-session logits / frontier rows of a round).
 int LaunchScatterRows(const float* src, std::size_t ld, float* const* dst,

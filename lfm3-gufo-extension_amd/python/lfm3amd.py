@@ -63,6 +63,14 @@ class Component(C.Structure):
                 ("state_bytes", C.c_size_t)]
 
 
+class Sampling(C.Structure):
+    """lfm3_sampling (runner.cpp:31-35 defaults: 0.1, 50, 1.1)."""
+    _fields_ = [("temperature", f32), ("top_k", u32), ("repeat_penalty", f32)]
+
+
+SAMPLE_MAX_TOP_K, SAMPLE_MAX_PENALTY, SAMPLE_MAX_COLS = 1024, 4096, 262144
+
+
 class AttentionItem(C.Structure):
     _fields_ = [("row", u32), ("key_begin", u32), ("key_end", u32),
                 ("first_item", u32), ("parts", u32), ("reserved", u32 * 3)]
@@ -100,6 +108,7 @@ _SIGS = {
     "lfm3_embed": (i32, [vp, vp, u32, u32, vp, u32, vp, vp]),
     "lfm3_argmax_workspace_bytes": (sz, [u32]),
     "lfm3_argmax": (i32, [vp, u32, u32, vp, vp, sz, vp]),
+    "lfm3_sample": (i32, [vp, u32, u32, u32, vp, vp, u32, vp, vp, vp]),
     "lfm3_conv_step_ragged": (i32, [vp, u32, vp, vp, vp, u32, u32, u32, u32, vp]),
     "lfm3_decode_heads_ragged": (i32, [vp, vp, vp, u32, vp, vp, vp, vp, vp, vp, vp, vp,
                                        u32, u32, u32, u32, f32, vp]),
@@ -147,6 +156,7 @@ _SIGS = {
     "lfm3_session_forward": (i32, [vp, vp, sz, vp]),
     "lfm3_forward_batch": (i32, [vp, sz, vp, vp]),
     "lfm3_forward_batch_greedy": (i32, [vp, sz, vp, vp]),
+    "lfm3_forward_batch_sample": (i32, [vp, sz, vp, vp, vp, u32, vp, vp]),
     "lfm3_forward_batch_inputs": (i32, [vp, sz, vp, vp, i32, vp]),
     "lfm3_session_read_logits": (i32, [vp, vp]),
     "lfm3_session_snapshot_bytes": (sz, [vp]),
@@ -389,6 +399,21 @@ class Model:
 
     def forward_batch_greedy(self, sessions, tokens):
         return self.forward_batch(sessions, tokens, want_logits=False)
+
+    def forward_batch_sample(self, sessions, tokens, params, uniforms=None, penalty=None):
+        """lfm3_forward_batch_sample: one round, then the sampler's pick per
+        row. penalty: (n, m) uint32 recent-token lists (ids >= vocab pad)."""
+        n = len(sessions)
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        handles = (vp * max(n, 1))(*[s.handle for s in sessions])
+        ids = np.empty(n, np.uint32)
+        uni = None if uniforms is None else np.ascontiguousarray(uniforms, np.float32)
+        pen = None if penalty is None else np.ascontiguousarray(penalty, np.uint32).reshape(n, -1)
+        check(lib().lfm3_forward_batch_sample(
+            handles, n, ptr(toks), C.byref(params), ptr(pen) if pen is not None else None,
+            pen.shape[1] if pen is not None else 0, ptr(uni) if uni is not None else None,
+            ptr(ids)))
+        return ids
 
     def scheduler_round(self, sessions, tokens, prompt=None, prompt_tokens=None,
                         want_logits=False, want_prompt_logits=True):

@@ -352,6 +352,48 @@ uint32_t orc_argmax(const float* x, size_t n) {
   return uint32_t(std::max_element(x, x + n) - x);
 }
 
+uint32_t orc_sample(const float* logits, size_t n, float temperature, uint32_t top_k,
+                    float repeat_penalty, const uint32_t* penalty_ids, size_t n_penalty,
+                    float u) {
+  std::vector<float> l(logits, logits + n);
+  std::vector<bool> hit(n, false);
+  for (size_t i = 0; i < n_penalty; ++i)
+    if (penalty_ids[i] < n && !hit[penalty_ids[i]]) {
+      hit[penalty_ids[i]] = true;
+      float& v = l[penalty_ids[i]];
+      v = v > 0 ? v / repeat_penalty : v * repeat_penalty;
+    }
+  if (!(temperature > 0) || top_k == 1)
+    return uint32_t(std::max_element(l.begin(), l.end()) - l.begin());
+  const float top = *std::max_element(l.begin(), l.end());
+  std::vector<uint32_t> order(n);
+  for (size_t i = 0; i < n; ++i)
+    order[i] = uint32_t(i);
+  size_t k = n;
+  if (top_k != 0 && top_k < n) {
+    k = top_k;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](uint32_t a, uint32_t b) { return l[a] > l[b]; });
+    order.resize(k);
+  }
+  const float inv_t = 1.0f / temperature;
+  float total = 0;
+  for (size_t i = 0; i < k; ++i)
+    total += std::exp((l[order[i]] - top) * inv_t);
+  const float target = u * total;
+  float run = 0;
+  size_t pick = 0;
+  for (size_t i = 0; i < k; ++i) {
+    const float w = std::exp((l[order[i]] - top) * inv_t);
+    if (w > 0)
+      pick = i;
+    run += w;
+    if (w > 0 && run > target)
+      break;
+  }
+  return order[pick];
+}
+
 orc_model* orc_model_create(const orc_config* config, const orc_tensor* tensors,
                             size_t count) {
   if (!config || count != ORC_GLOBALS + size_t(config->n_layers) * ORC_PER_LAYER)

@@ -132,6 +132,22 @@ void orc_half_rows(const float* x, size_t rows, size_t cols, float* inputs,
 void orc_swiglu(float* gate, const float* up, size_t n);
 /* First index of the maximum (std::max_element). */
 uint32_t orc_argmax(const float* x, size_t n);
+/* Token selection of the serving loop (SelectNext, runner.cpp:300-325;
+   defaults temperature 0.1, top_k 50, repeat_penalty 1.1 at
+   runner.cpp:31-35). The reference's sampler (Gufo's
+   sampling::SamplerState) is not vendored, so this follows the common
+   definition, step by step:
+   repetition penalty over penalty_ids (l -> l / p if l > 0 else l * p,
+   once per listed id < n), the top_k largest (ties: lower index; 0 or
+   >= n keeps all), weights exp((l - max) / T) in float, then the first
+   candidate (descending logit order, or index order when all are kept)
+   whose running float sum exceeds u * total. T <= 0 or top_k == 1: the
+   first index of the maximum. Parity unpinned against the Gufo sampler
+   itself; pinned by the greedy cases and by frequency/closed-form checks
+   in the tests. */
+uint32_t orc_sample(const float* logits, size_t n, float temperature,
+                    uint32_t top_k, float repeat_penalty,
+                    const uint32_t* penalty_ids, size_t n_penalty, float u);
 
 orc_model* orc_model_create(const orc_config* config,
                             const orc_tensor* tensors, size_t count);

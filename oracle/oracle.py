@@ -50,6 +50,7 @@ _SIGS = {
     "orc_half_rows": (None, [vp, sz, sz, vp, vp]),
     "orc_swiglu": (None, [vp, vp, sz]),
     "orc_argmax": (u32, [vp, sz]),
+    "orc_sample": (u32, [vp, sz, f32, u32, f32, vp, sz, f32]),
     "orc_model_create": (vp, [C.POINTER(Config), C.POINTER(Tensor), sz]),
     "orc_model_destroy": (None, [vp]),
     "orc_session_create": (vp, [vp, u32, i32]),
@@ -214,6 +215,16 @@ def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
 
 def argmax(x: np.ndarray) -> int:
     return int(lib().orc_argmax(_p(np.ascontiguousarray(x, np.float32)), x.size))
+
+
+def sample(x: np.ndarray, temperature: float, top_k: int, repeat_penalty: float = 1.0,
+           penalty_ids=None, u: float = 0.0) -> int:
+    """orc_sample: one row's pick (runner.cpp:300-325 SelectNext semantics)."""
+    x = np.ascontiguousarray(x, np.float32)
+    pen = (np.zeros(0, np.uint32) if penalty_ids is None
+           else np.ascontiguousarray(penalty_ids, np.uint32))
+    return int(lib().orc_sample(_p(x), x.size, temperature, top_k, repeat_penalty,
+                                _p(pen) if pen.size else None, pen.size, u))
 
 
 class Model:

@@ -1,0 +1,199 @@
+"""The sampler on the GPU (lfm3_sample, lfm3_forward_batch_sample) against
+the oracle's orc_sample and the float64 definition.
+
+The reference's own sampler (Gufo's, behind SelectNext, runner.cpp:300-325)
+is not vendored, so parity with it is unpinned beyond the greedy pick;
+bars here:
+  * greedy settings (T <= 0, top_k 1): bit-exact first index of the maximum
+    of the penalized row, as lfm3_argmax / std::max_element;
+  * sampled settings: the oracle's pick on the same row and uniform, or,
+    where float rounding of the running sums differs between the two, a
+    pick whose cumulative interval holds the target within 2e-5 of the
+    total (sample_util.consistent);
+  * a uniform grid over one row hits each candidate in proportion to its
+    float64 probability, within two grid cells;
+  * the engine's sampled round picks what lfm3_sample picks on the logits
+    that lfm3_forward_batch returns on twin sessions.
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+import lfm3amd as L
+import oracle as O
+from sample_util import consistent, probabilities
+
+pytestmark = pytest.mark.gpu
+SEED = L.SEED
+
+
+def rows_of(name, rows, cols, scale=4.0):
+    return (scale * L.normal(SEED, name, rows * cols)).reshape(rows, cols).astype(np.float32)
+
+
+def sample(x, t, k, p=1.0, pen=None, u=None, ld=None):
+    rows, cols = x.shape
+    ld = ld or cols
+    host = np.zeros((rows, ld), np.float32)
+    host[:, :cols] = x
+    dx = L.DeviceBuffer.of(host)
+    dpen = L.DeviceBuffer.of(np.ascontiguousarray(pen, np.uint32)) if pen is not None else None
+    du = L.DeviceBuffer.of(np.ascontiguousarray(u, np.float32)) if u is not None else None
+    ids = L.DeviceBuffer(rows * 4)
+    params = L.Sampling(t, k, p)
+    L.check(L.lib().lfm3_sample(dx.addr, rows, cols, ld, L.C.byref(params),
+                                dpen.addr if dpen else None,
+                                pen.shape[1] if pen is not None else 0,
+                                du.addr if du else None, ids.addr, None))
+    L.synchronize()
+    return ids.download(np.uint32, rows)
+
+
+@pytest.mark.parametrize("t,k", [(0.0, 50), (0.7, 1), (-1.0, 0)])
+def test_greedy_settings_are_argmax(t, k):
+    rows, V = 8, 65536
+    x = rows_of(f"sample.greedy.{t}.{k}", rows, V)
+    x[0, 9] = x[0, 60000] = 40.0      # tie: first index
+    x[1, :] = -2.0                    # all equal: index 0
+    x[2, V - 1] = 50.0
+    pen = L.uniform_u32(SEED, f"sample.gpen.{t}", rows * 64, 0, V + 100).reshape(rows, 64)
+    pen[3, 0] = int(np.argmax(x[3]))  # the leader penalized
+    got = sample(x, t, k, 1.1, pen, np.full(rows, 0.5, np.float32))
+    for r in range(rows):
+        assert got[r] == O.sample(x[r], t, k, 1.1, pen[r]), r
+    plain = sample(x, t, k)
+    assert [int(v) for v in plain] == [O.argmax(x[r]) for r in range(rows)]
+    assert plain[0] == 9 and plain[1] == 0 and plain[2] == V - 1
+
+
+CASES = [  # vocabulary, rows, temperature, top_k, penalty, penalty list length
+    (65536, 8, 0.1, 50, 1.1, 64),      # the serving loop's defaults
+    (65536, 8, 1.0, 1024, 1.0, 0),
+    (65536, 4, 0.8, 0, 1.1, 256),      # whole vocabulary
+    (128000, 3, 0.5, 7, 1.3, 4096),
+    (1000, 8, 2.0, 999, 1.1, 16),
+    (1000, 8, 1.5, 1000, 1.0, 0),      # k == cols: whole vocabulary
+    (37, 5, 0.3, 5, 1.1, 3),
+    (262144, 1, 1.0, 2, 1.0, 0),
+]
+
+
+@pytest.mark.parametrize("V,rows,t,k,p,np_", CASES)
+def test_sampled_picks_match_the_oracle(V, rows, t, k, p, np_):
+    name = f"sample.{V}.{rows}.{k}.{np_}"
+    x = rows_of(name, rows, V, 2.0 + 4.0 * (zlib.crc32(name.encode()) % 3))
+    pen = (L.uniform_u32(SEED, name + ".pen", rows * np_, 0, V + 50).reshape(rows, np_)
+           if np_ else None)
+    u = np.random.default_rng(zlib.crc32(name.encode())).random(rows).astype(np.float32)
+    for ld in (V, V + 4):
+        got = sample(x, t, k, p, pen, u, ld)
+        exact = 0
+        for r in range(rows):
+            ids = pen[r] if pen is not None else None
+            want = O.sample(x[r], t, k, p, ids, float(u[r]))
+            exact += int(got[r] == want)
+            assert got[r] == want or consistent(x[r], t, k, p, ids, float(u[r]), int(got[r])), \
+                (r, int(got[r]), want)
+        assert exact >= rows - 1
+
+
+@pytest.mark.parametrize("t,k", [(0.7, 8), (1.0, 0), (0.25, 64)])
+def test_uniform_grid_frequencies(t, k):
+    """One row repeated over a grid of uniforms: each candidate's count is
+    its float64 probability times the grid, within two cells."""
+    V, grid = 4096, 8192
+    base = rows_of(f"sample.freq.{k}", 1, V, 1.0)[0]
+    base[:16] += 3.0                 # a few heavy candidates
+    x = np.tile(base, (grid, 1))
+    u = ((np.arange(grid) + 0.5) / grid).astype(np.float32)
+    got = sample(x, t, k, 1.0, None, u)
+    order, prob = probabilities(base, t, k)
+    want = np.zeros(V)
+    want[order] = prob * grid
+    counts = np.bincount(got, minlength=V)
+    assert np.max(np.abs(counts - want)) <= 2.0
+    assert counts[np.setdiff1d(np.arange(V), order)].sum() == 0
+
+
+def test_topk_ties_and_all_equal_rows():
+    V = 5000
+    x = np.full((3, V), -1.0, np.float32)
+    x[0, [10, 20, 30, 40]] = 2.0        # four tied leaders, k = 2: 10 and 20 kept
+    x[1, :] = 0.5                       # all tied, k = 3: the first three
+    x[2, [4999, 7]] = 9.0               # two tied at the top across the row, k = 2
+    grid = 2000
+    seen = [set(), set(), set()]
+    for i in range(0, grid, 50):
+        u = np.full(3, (i + 0.5) / grid, np.float32)
+        got = sample(x, 1.0, 2, 1.0, None, u)
+        seen[0].add(int(got[0]))
+        seen[2].add(int(got[2]))
+        got = sample(x, 1.0, 3, 1.0, None, u)
+        seen[1].add(int(got[1]))
+    assert seen[0] == {10, 20}
+    assert seen[1] == {0, 1, 2}
+    assert seen[2] == {7, 4999}
+
+
+def test_refusals():
+    x = L.DeviceBuffer(4 * 1000)
+    ids = L.DeviceBuffer(16)
+    u = L.DeviceBuffer(16)
+    bad = [
+        (L.Sampling(1.0, 1025, 1.0), 1000, 1000, 0, u.addr),        # k above the maximum
+        (L.Sampling(1.0, 5, 1.0), 1000, 1000, 0, None),             # no uniforms
+        (L.Sampling(1.0, 5, 0.0), 1000, 1000, 0, u.addr),           # penalty <= 0
+        (L.Sampling(float("nan"), 5, 1.0), 1000, 1000, 0, u.addr),
+        (L.Sampling(1.0, 5, 1.0), 1000, 999, 0, u.addr),            # ld < cols
+        (L.Sampling(1.0, 5, 1.0), 1000, 1000, 4097, u.addr),        # penalty list too long
+        (L.Sampling(1.0, 5, 1.0), 300000, 300000, 0, u.addr),       # cols above the maximum
+    ]
+    for params, cols, ld, n_pen, uni in bad:
+        st = L.lib().lfm3_sample(x.addr, 1, cols, ld, L.C.byref(params), None, n_pen, uni,
+                                 ids.addr, None)
+        assert st == L.E_INVALID, (params.temperature, params.top_k, cols, ld, n_pen)
+
+
+def small_dims():
+    return L.Dims(hidden=256, intermediate=512, vocab=1000, context=512, heads=8, head_dim=128,
+                  kv_heads=2, window=32, pattern="CSGC")
+
+
+def test_engine_sampled_round_matches_lfm3_sample():
+    dims = small_dims()
+    w = L.synth_weights(dims, seed=71)
+    gm = L.Model(w)
+    a = [gm.session(512) for _ in range(5)]
+    b = [gm.session(512) for _ in range(5)]
+    prompt = L.uniform_u32(SEED, "sample.engine.p", 30, 0, dims.vocab - 1)
+    for i in range(5):
+        a[i].forward(prompt[: 5 + i])
+        b[i].forward(prompt[: 5 + i])
+    params = L.Sampling(0.1, 50, 1.1)
+    rng = np.random.default_rng(71)
+    toks = L.uniform_u32(SEED, "sample.engine.t", 5, 0, dims.vocab - 1)
+    for rnd in range(4):
+        pen = rng.integers(0, dims.vocab + 5, size=(5, 32)).astype(np.uint32)
+        u = rng.random(5).astype(np.float32)
+        ids = gm.forward_batch_sample(a, toks, params, u, pen)
+        logits = gm.forward_batch(b, toks)
+        want = sample(logits, 0.1, 50, 1.1, pen, u)
+        assert np.array_equal(ids, want), rnd
+        assert [s.position for s in a] == [s.position for s in b]
+        toks = ids
+    # greedy settings give the greedy round's ids
+    g = gm.forward_batch_sample(a, toks, L.Sampling(0.0, 50, 1.0))
+    assert np.array_equal(g, gm.forward_batch_greedy(b, toks))
+    # refused before any work: positions stay
+    before = [s.position for s in a]
+    for bad in (L.Sampling(1.0, 5000, 1.0), L.Sampling(1.0, 5, -1.0)):
+        with pytest.raises(L.LFM3Error) as e:
+            gm.forward_batch_sample(a, toks, bad, np.full(5, 0.5, np.float32))
+        assert e.value.status == L.E_INVALID
+    with pytest.raises(L.LFM3Error):
+        gm.forward_batch_sample(a, toks, params)     # sampled setting without uniforms
+    assert [s.position for s in a] == before
+    for s in a + b:
+        s.close()
+    gm.close()
