@@ -60,8 +60,9 @@ MIXED_DECODE, MIXED_LO, MIXED_HI = 7, 16384, 32768
 # plain 256 MiB device-to-device copy in the same program (FETCH_SIZE x 2.0,
 # WRITE_SIZE x 1.0). Re-measure after a change to either kernel.
 GEMV_TRAFFIC = {"read": 18_477_766, "write": 262_144}
-# The same for the SwiGLU operand-image GEMV (2 x 7680 x 2048, 8 rows).
-SWIGLU_TRAFFIC = {"read": None, "write": None}
+# The same for the SwiGLU operand-image GEMV (2 x 7680 x 2048, 8 rows):
+# 1.017 x its algorithmic bytes.
+SWIGLU_TRAFFIC = {"read": 34_044_181, "write": 245_760}
 GEMM_TRAFFIC = {"read": 86_290_594, "write": 15_851_520}
 
 
