@@ -88,10 +88,13 @@ struct PinnedBuffer {
 // A tiled Q8_0 matrix of rows x cols (several sources may share it). The
 // gate/up prompt GEMM reads `halves`, the codes decoded to FP16 tiles,
 // made with the model's prompt scratch.
+// A BF16 matrix (bf16 set) keeps its tiles in `codes` (lfm3_bf16_pack_host
+// layout) and has no scales.
 struct Matrix {
   Buffer codes, scales, halves;
   std::uint32_t rows = 0, cols = 0;
   std::uint32_t tiles = 0;  // row tiles stored (gate/up: two per 16 rows)
+  bool bf16 = false;
 };
 
 Buffer UploadFloats(const float* host, std::size_t n) {
@@ -111,6 +114,17 @@ Matrix PackMatrix(std::initializer_list<Part> parts, std::uint32_t tiles,
   m.rows = rows;
   m.cols = cols;
   m.tiles = tiles;
+  if (parts.begin()->t->type == LFM3_TYPE_BF16) {
+    m.bf16 = true;
+    const std::size_t bytes = lfm3_bf16_tiled_bytes(tiles * kTileRows, cols);
+    std::vector<std::uint8_t> host(bytes, 0);
+    for (const auto& part : parts)
+      CheckStatus(lfm3_bf16_pack_host(part.t->data, part.t->rows, part.t->cols, host.data(),
+                                      part.tile_offset, part.tile_stride));
+    m.codes = Buffer(bytes, false);
+    Check(hipMemcpy(m.codes.p, host.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy");
+    return m;
+  }
   const std::size_t chunks = Chunks(cols);
   const std::size_t code_bytes = std::size_t(tiles) * chunks * kTileCodeBytes;
   const std::size_t scale_bytes = std::size_t(tiles) * chunks * kTileScales * 2;
@@ -183,6 +197,11 @@ struct lfm3_model {
   // Round scratch, shared by the model's rounds (calls are serialized, as
   // the Gufo scheduler serializes sessions: engine.cpp:101-113).
   Buffer x, proj, a, hidden, out, gemv_ws, head_keys, ids;
+  // BF16 models (bf16 set): every projection is an exact BF16 x FP32 GEMV
+  // from FP32 normed rows z; the head writes head_out, then the rows go to
+  // the sessions' logits.
+  bool bf16 = false;
+  Buffer z, head_out;
   std::uint32_t head_groups = 0;
   Buffer image, exps;  // GEMV operand image of the current hidden-wide input
   Buffer one_row;      // a host input row of a one-row chunk, on the device
@@ -244,21 +263,31 @@ void ValidateConfig(const lfm3_config& c) {
   }
 }
 
+// `type` is LFM3_TYPE_F32 for vectors, else the model's matrix type.
 void CheckTensor(const lfm3_tensor& t, std::uint32_t cols, std::uint32_t rows,
-                 bool q8, const char* name) {
-  if (!t.data || t.cols != cols || t.rows != rows ||
-      t.type != (q8 ? LFM3_TYPE_Q8_0 : LFM3_TYPE_F32))
+                 std::uint32_t type, const char* name) {
+  if (!t.data || t.cols != cols || t.rows != rows || t.type != type)
     Invalid(std::string("invalid LFM3 tensor: ") + name);
+}
+
+// The model's matrix type: the embedding's, Q8_0 or BF16; every projection
+// matrix must share it (one engine path per precision).
+std::uint32_t MatrixType(const lfm3_tensor* tensors) {
+  const std::uint32_t t = tensors[0].type;
+  if (t != LFM3_TYPE_Q8_0 && t != LFM3_TYPE_BF16)
+    Invalid("invalid LFM3 tensor: token_embd.weight (Q8_0 or BF16)");
+  return t;
 }
 
 // weights.cpp:10-100 binding rules, checked before anything is uploaded.
 void ValidateTensors(const lfm3_config& c, const lfm3_tensor* tensors) {
   const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
-  CheckTensor(tensors[0], H, c.vocab, true, "token_embd.weight");
+  const std::uint32_t mt = MatrixType(tensors);
+  CheckTensor(tensors[0], H, c.vocab, mt, "token_embd.weight");
   if (tensors[1].data && tensors[1].data != tensors[0].data)
-    CheckTensor(tensors[1], H, c.vocab, true, "output.weight");
-  CheckTensor(tensors[2], H, 1, false, "output_norm.weight");
-  CheckTensor(tensors[3], D / 2, 1, false, "rope_freqs.weight");
+    CheckTensor(tensors[1], H, c.vocab, mt, "output.weight");
+  CheckTensor(tensors[2], H, 1, LFM3_TYPE_F32, "output_norm.weight");
+  CheckTensor(tensors[3], D / 2, 1, LFM3_TYPE_F32, "rope_freqs.weight");
   for (std::uint32_t i = 0; i < D / 2; ++i) {
     const float f = static_cast<const float*>(tensors[3].data)[i];
     if (!std::isfinite(f) || !(f > 0))
@@ -266,30 +295,30 @@ void ValidateTensors(const lfm3_config& c, const lfm3_tensor* tensors) {
   }
   for (std::uint32_t i = 0; i < c.n_layers; ++i) {
     const lfm3_tensor* t = tensors + LFM3_GLOBAL_TENSORS + std::size_t(i) * LFM3_LAYER_TENSORS;
-    CheckTensor(t[0], H, 1, false, "attn_norm.weight");
-    CheckTensor(t[1], H, 1, false, "ffn_norm.weight");
+    CheckTensor(t[0], H, 1, LFM3_TYPE_F32, "attn_norm.weight");
+    CheckTensor(t[1], H, 1, LFM3_TYPE_F32, "ffn_norm.weight");
     if (bool(t[2].data) != bool(t[3].data))
       Invalid("LFM3 requires both post norms or neither");
     if (t[2].data) {
-      CheckTensor(t[2], H, 1, false, "post_attention_norm.weight");
-      CheckTensor(t[3], H, 1, false, "post_ffw_norm.weight");
+      CheckTensor(t[2], H, 1, LFM3_TYPE_F32, "post_attention_norm.weight");
+      CheckTensor(t[3], H, 1, LFM3_TYPE_F32, "post_ffw_norm.weight");
     }
-    CheckTensor(t[4], H, F, true, "ffn_gate.weight");
-    CheckTensor(t[5], H, F, true, "ffn_up.weight");
-    CheckTensor(t[6], F, H, true, "ffn_down.weight");
+    CheckTensor(t[4], H, F, mt, "ffn_gate.weight");
+    CheckTensor(t[5], H, F, mt, "ffn_up.weight");
+    CheckTensor(t[6], F, H, mt, "ffn_down.weight");
     if (c.layer_type[i] == LFM3_LAYER_CONV) {
-      CheckTensor(t[7], c.conv_width, H, false, "shortconv.conv.weight");
-      CheckTensor(t[8], H, 3 * H, true, "shortconv.in_proj.weight");
-      CheckTensor(t[9], H, H, true, "shortconv.out_proj.weight");
+      CheckTensor(t[7], c.conv_width, H, LFM3_TYPE_F32, "shortconv.conv.weight");
+      CheckTensor(t[8], H, 3 * H, mt, "shortconv.in_proj.weight");
+      CheckTensor(t[9], H, H, mt, "shortconv.out_proj.weight");
     } else {
       const std::uint32_t qr = c.heads * D, kr = c.kv_heads[i] * D;
-      CheckTensor(t[10], H, qr, true, "attn_q.weight");
-      CheckTensor(t[11], H, kr, true, "attn_k.weight");
-      CheckTensor(t[12], H, kr, true, "attn_v.weight");
-      CheckTensor(t[13], D, 1, false, "attn_q_norm.weight");
-      CheckTensor(t[14], D, 1, false, "attn_k_norm.weight");
-      CheckTensor(t[15], H, c.heads, true, "attn_gate.weight");
-      CheckTensor(t[16], qr, H, true, "attn_output.weight");
+      CheckTensor(t[10], H, qr, mt, "attn_q.weight");
+      CheckTensor(t[11], H, kr, mt, "attn_k.weight");
+      CheckTensor(t[12], H, kr, mt, "attn_v.weight");
+      CheckTensor(t[13], D, 1, LFM3_TYPE_F32, "attn_q_norm.weight");
+      CheckTensor(t[14], D, 1, LFM3_TYPE_F32, "attn_k_norm.weight");
+      CheckTensor(t[15], H, c.heads, mt, "attn_gate.weight");
+      CheckTensor(t[16], qr, H, mt, "attn_output.weight");
     }
   }
 }
@@ -337,21 +366,23 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     m->config.layer_type = m->layer_type.data();
     const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
     ValidateTensors(c, tensors);
+    const std::uint32_t mt = MatrixType(tensors);
+    m->bf16 = mt == LFM3_TYPE_BF16;
     Check(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "hipStreamCreate");
     Check(hipStreamCreateWithFlags(&m->prompt_stream, hipStreamNonBlocking), "hipStreamCreate");
 
     const lfm3_tensor& emb = tensors[0];
-    CheckTensor(emb, H, c.vocab, true, "token_embd.weight");
+    CheckTensor(emb, H, c.vocab, mt, "token_embd.weight");
     m->embedding = PackMatrix({{&emb, 0, 1}}, RowTiles(c.vocab), c.vocab, H);
     const lfm3_tensor& outw = tensors[1];
     m->tied = !outw.data || outw.data == emb.data;
     if (!m->tied) {
-      CheckTensor(outw, H, c.vocab, true, "output.weight");
+      CheckTensor(outw, H, c.vocab, mt, "output.weight");
       m->output = PackMatrix({{&outw, 0, 1}}, RowTiles(c.vocab), c.vocab, H);
     }
-    CheckTensor(tensors[2], H, 1, false, "output_norm.weight");
+    CheckTensor(tensors[2], H, 1, LFM3_TYPE_F32, "output_norm.weight");
     m->output_norm = UploadFloats(static_cast<const float*>(tensors[2].data), H);
-    CheckTensor(tensors[3], D / 2, 1, false, "rope_freqs.weight");
+    CheckTensor(tensors[3], D / 2, 1, LFM3_TYPE_F32, "rope_freqs.weight");
     const auto* factors = static_cast<const float*>(tensors[3].data);
     for (std::uint32_t i = 0; i < D / 2; ++i)
       if (!std::isfinite(factors[i]) || !(factors[i] > 0))
@@ -372,40 +403,40 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
       Layer l;
       l.type = c.layer_type[i];
       l.kv = c.kv_heads[i];
-      CheckTensor(t[0], H, 1, false, "attn_norm.weight");
-      CheckTensor(t[1], H, 1, false, "ffn_norm.weight");
+      CheckTensor(t[0], H, 1, LFM3_TYPE_F32, "attn_norm.weight");
+      CheckTensor(t[1], H, 1, LFM3_TYPE_F32, "ffn_norm.weight");
       l.norm = UploadFloats(static_cast<const float*>(t[0].data), H);
       l.ffn_norm = UploadFloats(static_cast<const float*>(t[1].data), H);
       if (bool(t[2].data) != bool(t[3].data))
         Invalid("LFM3 requires both post norms or neither");
       if (t[2].data) {
-        CheckTensor(t[2], H, 1, false, "post_attention_norm.weight");
-        CheckTensor(t[3], H, 1, false, "post_ffw_norm.weight");
+        CheckTensor(t[2], H, 1, LFM3_TYPE_F32, "post_attention_norm.weight");
+        CheckTensor(t[3], H, 1, LFM3_TYPE_F32, "post_ffw_norm.weight");
         l.post_norm = UploadFloats(static_cast<const float*>(t[2].data), H);
         l.post_ffn_norm = UploadFloats(static_cast<const float*>(t[3].data), H);
       }
-      CheckTensor(t[4], H, F, true, "ffn_gate.weight");
-      CheckTensor(t[5], H, F, true, "ffn_up.weight");
-      CheckTensor(t[6], F, H, true, "ffn_down.weight");
+      CheckTensor(t[4], H, F, mt, "ffn_gate.weight");
+      CheckTensor(t[5], H, F, mt, "ffn_up.weight");
+      CheckTensor(t[6], F, H, mt, "ffn_down.weight");
       l.ffn = PackMatrix({{&t[4], 0, 2}, {&t[5], 1, 2}}, 2 * RowTiles(F), F, H);
       l.down = PackMatrix({{&t[6], 0, 1}}, RowTiles(H), H, F);
       if (l.type == LFM3_LAYER_CONV) {
-        CheckTensor(t[7], c.conv_width, H, false, "shortconv.conv.weight");
-        CheckTensor(t[8], H, 3 * H, true, "shortconv.in_proj.weight");
-        CheckTensor(t[9], H, H, true, "shortconv.out_proj.weight");
+        CheckTensor(t[7], c.conv_width, H, LFM3_TYPE_F32, "shortconv.conv.weight");
+        CheckTensor(t[8], H, 3 * H, mt, "shortconv.in_proj.weight");
+        CheckTensor(t[9], H, H, mt, "shortconv.out_proj.weight");
         l.conv = UploadFloats(static_cast<const float*>(t[7].data),
                               std::size_t(H) * c.conv_width);
         l.in_proj = PackMatrix({{&t[8], 0, 1}}, RowTiles(3 * H), 3 * H, H);
         l.out_proj = PackMatrix({{&t[9], 0, 1}}, RowTiles(H), H, H);
       } else {
         const std::uint32_t qr = c.heads * D, kr = l.kv * D;
-        CheckTensor(t[10], H, qr, true, "attn_q.weight");
-        CheckTensor(t[11], H, kr, true, "attn_k.weight");
-        CheckTensor(t[12], H, kr, true, "attn_v.weight");
-        CheckTensor(t[13], D, 1, false, "attn_q_norm.weight");
-        CheckTensor(t[14], D, 1, false, "attn_k_norm.weight");
-        CheckTensor(t[15], H, c.heads, true, "attn_gate.weight");
-        CheckTensor(t[16], qr, H, true, "attn_output.weight");
+        CheckTensor(t[10], H, qr, mt, "attn_q.weight");
+        CheckTensor(t[11], H, kr, mt, "attn_k.weight");
+        CheckTensor(t[12], H, kr, mt, "attn_v.weight");
+        CheckTensor(t[13], D, 1, LFM3_TYPE_F32, "attn_q_norm.weight");
+        CheckTensor(t[14], D, 1, LFM3_TYPE_F32, "attn_k_norm.weight");
+        CheckTensor(t[15], H, c.heads, mt, "attn_gate.weight");
+        CheckTensor(t[16], qr, H, mt, "attn_output.weight");
         const std::uint32_t tq = RowTiles(qr), tk = RowTiles(kr), tg = RowTiles(c.heads);
         l.q_off = 0;
         l.k_off = tq * kTileRows;
@@ -432,6 +463,13 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     std::size_t out_parts = lfm3_q8_gemv_parts(H, F);
     out_parts = std::max<std::size_t>(out_parts, lfm3_q8_gemv_parts(H, H));
     out_parts = std::max<std::size_t>(out_parts, lfm3_q8_gemv_parts(H, c.heads * D));
+    if (m->bf16) {
+      out_parts = std::max<std::size_t>(out_parts, lfm3_bf16_gemv_parts(H, F, B));
+      out_parts = std::max<std::size_t>(out_parts, lfm3_bf16_gemv_parts(H, H, B));
+      out_parts = std::max<std::size_t>(out_parts, lfm3_bf16_gemv_parts(H, c.heads * D, B));
+      m->z = Buffer(B * H * 4);
+      m->head_out = Buffer(B * std::size_t(c.vocab) * 4);
+    }
     m->out = Buffer(out_parts * B * H * 4);
     std::size_t ws = lfm3_gemv_workspace_bytes(c.vocab, H, B);
     for (const auto& l : m->layers) {
@@ -598,6 +636,18 @@ int lfm3_session_set_position(lfm3_session* s, std::uint32_t position) {
 namespace lfm3amd {
 namespace {
 
+// The vocabulary head on one FP32 row (the frontier), on stream s.
+void HeadRow(lfm3_model& m, const float* row, float* logits, hipStream_t s) {
+  const auto& c = m.config;
+  const Matrix& head = m.head();
+  if (head.bf16)
+    CheckStatus(lfm3_bf16_gemv(head.codes.p, c.vocab, c.hidden, row, c.hidden, logits, c.vocab,
+                               1, 1, 0, s));
+  else
+    CheckStatus(lfm3_q8_gemv(head.codes.p, head.scales.p, c.vocab, c.hidden, row, c.hidden,
+                             logits, c.vocab, 1, nullptr, 0, s));
+}
+
 // Session::Impl::EnsureLogits (engine.cpp:237-245): a round or prompt that
 // skipped the vocabulary head leaves the frontier row; the head runs on it
 // when logits are first wanted.
@@ -605,11 +655,7 @@ void EnsureLogits(lfm3_session& se) {
   if (se.logits_ready)
     return;
   lfm3_model& m = *se.model;
-  const auto& c = m.config;
-  const Matrix& head = m.head();
-  CheckStatus(lfm3_q8_gemv(head.codes.p, head.scales.p, c.vocab, c.hidden,
-                           se.frontier.as<float>(), c.hidden, se.logits.as<float>(), c.vocab, 1,
-                           nullptr, 0, m.stream));
+  HeadRow(m, se.frontier.as<float>(), se.logits.as<float>(), m.stream);
   Check(hipStreamSynchronize(m.stream), "logits");
   se.logits_ready = true;
 }
@@ -873,6 +919,80 @@ void EnqueueRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
   float* out = m.out.as<float>();
   const std::uint32_t pld = std::uint32_t(m.proj_ld);
 
+  if (m.bf16) {
+    // The reference-precision round (every projection an exact BF16 x FP32
+    // GEMV, hip/ops.hip:2230-2244): FP32 normed rows z feed the GEMVs;
+    // narrow outputs split K into parts that the next norm adds.
+    float* z = m.z.as<float>();
+    const auto bgemv = [&](const Matrix& w, const float* in, std::uint32_t ldx, float* y,
+                           std::uint32_t ldy, std::uint32_t parts, bool swiglu) {
+      CheckStatus(lfm3_bf16_gemv(w.codes.p, w.rows, w.cols, in, ldx, y, ldy, n, parts,
+                                 swiglu ? 1 : 0, s));
+    };
+    const auto bparts = [&](const Matrix& w, const float* in, std::uint32_t ldx) {
+      const std::uint32_t parts = lfm3_bf16_gemv_parts(w.rows, w.cols, n);
+      bgemv(w, in, ldx, out, H, parts, false);
+      return parts;
+    };
+    const auto norm = [&](std::uint32_t parts, const float* post, const float* weight) {
+      CheckStatus(lfm3_residual_norm_parts(parts ? out : nullptr, parts ? parts : 1,
+                                           std::size_t(n) * H, parts ? post : nullptr, x, weight,
+                                           z, n, H, c.eps, s));
+    };
+    CheckStatus(lfm3_bf16_embed(m.embedding.codes.p, c.vocab, H, d_rt->tokens,
+                                inputs ? d_rt->inputs : nullptr, n, x, s));
+    norm(0, nullptr, m.layers[0].norm.as<float>());
+    for (std::uint32_t il = 0; il < L; ++il) {
+      const Layer& l = m.layers[il];
+      std::uint32_t parts;
+      if (l.type == LFM3_LAYER_CONV) {
+        bgemv(l.in_proj, z, H, proj, 3 * H, 1, false);
+        CheckStatus(lfm3_conv_step_ragged(
+            proj, 3 * H, l.conv.as<float>(),
+            reinterpret_cast<float* const*>(dev + conv_off) + il * kMaxBatch, a, H, n, H,
+            c.conv_width, s));
+        parts = bparts(l.out_proj, a, H);
+      } else {
+        const bool swa = l.type == LFM3_LAYER_SLIDING;
+        bgemv(l.qkvg, z, H, proj, pld, 1, false);
+        const auto* kp = reinterpret_cast<std::uint16_t* const*>(dev + k_off) + il * kMaxBatch;
+        const auto* vp = reinterpret_cast<std::uint16_t* const*>(dev + v_off) + il * kMaxBatch;
+        const auto* cp = reinterpret_cast<const std::uint32_t*>(dev + cap_off) + il * kMaxBatch;
+        const auto* items = reinterpret_cast<const lfm3_attention_item*>(
+            dev + (swa ? items_swa_off : items_full_off));
+        CheckStatus(lfm3_decode_heads_attention_ragged(
+            proj + l.q_off, proj + l.k_off, proj + l.v_off, pld, proj + l.g_off, pld,
+            l.q_norm.as<float>(), l.k_norm.as<float>(),
+            swa ? m.freq_sliding.as<float>() : m.freq_global.as<float>(),
+            swa ? nullptr : m.factors.as<float>(), kp, vp, d_rt->positions, cp, items,
+            std::uint32_t(swa ? n_swa : n_full), a, c.heads * D, n, c.heads, l.kv, D, c.eps,
+            m.attn_ws.p, m.attn_ws_bytes, s));
+        parts = bparts(l.attn_out, a, c.heads * D);
+      }
+      norm(parts, l.post_norm.as<float>(), l.ffn_norm.as<float>());
+      bgemv(l.ffn, z, H, hid, F, 1, true);
+      parts = bparts(l.down, hid, F);
+      const bool last = il + 1 == L;
+      norm(parts, l.post_ffn_norm.as<float>(),
+           last ? m.output_norm.as<float>() : m.layers[il + 1].norm.as<float>());
+    }
+    // The final normed rows are the frontier rows (engine.cpp:505-511).
+    CheckStatus(LaunchScatterRows(z, H, d_rt->frontier, n, H, s));
+    if (head) {
+      const Matrix& w = m.head();
+      float* logits = m.head_out.as<float>();
+      bgemv(w, z, H, logits, c.vocab, 1, false);
+      CheckStatus(LaunchScatterRows(logits, c.vocab, d_rt->logits, n, c.vocab, s));
+      if (greedy) {
+        lfm3_sampling pick{0.0f, 1, 1.0f};
+        CheckStatus(LaunchSample(logits, c.vocab, nullptr, n, c.vocab, pick, nullptr, 0,
+                                 nullptr, m.ids.as<std::uint32_t>(), s));
+      }
+    }
+    Check(hipGetLastError(), "round launch");
+    return;
+  }
+
   // Narrow matrices (hidden rows) split K into parts whose partial sums the
   // following residual norm adds in part order.
   const auto partials = [&](const Matrix& w, const float* in,
@@ -1046,6 +1166,8 @@ PromptBuffers& EnsurePromptBuffers(lfm3_model& m) {
   // tiles.
   for (auto& l : m.layers) {
     Matrix& w = l.ffn;
+    if (w.bf16)
+      continue;
     const std::uint32_t rows = w.tiles * kTileRows;
     w.halves = Buffer(lfm3_q8_half_tiles_bytes(rows, w.cols), false);
     CheckStatus(lfm3_q8_half_tiles(w.codes.p, rows, w.cols, w.halves.p, m.stream));
@@ -1126,8 +1248,16 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
     CheckStatus(lfm3_half_rows(in, ldx, rmax, rmax ? max_blocks : 0, a16, lda, scale, rows,
                                cols, s));
   };
+  // BF16 models run every projection through the exact BF16 GEMV over all
+  // rows at once (hip/ops.hip:2230-2244 for BF16 tensors).
+  const std::uint32_t mfma_rows = m.bf16 ? 0xffffffffu : kPromptRows;
   const auto gemv = [&](const Matrix& w, const float* in, std::uint32_t ldx, float* y,
                         std::uint32_t ldy, std::uint32_t rows, bool swiglu) {
+    if (w.bf16) {
+      CheckStatus(lfm3_bf16_gemv(w.codes.p, swiglu ? F : w.rows, w.cols, in, ldx, y, ldy, rows,
+                                 1, swiglu ? 1 : 0, s));
+      return;
+    }
     for (std::uint32_t r = 0; r < rows; r += kMaxBatch) {
       const std::uint32_t k = std::min(kMaxBatch, rows - r);
       if (swiglu)
@@ -1159,7 +1289,7 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
   const auto project = [&](const Matrix& w, std::uint32_t rows, float* y, std::uint32_t ldy,
                            bool single) -> std::uint32_t {
     const std::uint32_t first = n - rows;
-    if (rows < kPromptRows) {
+    if (rows < mfma_rows) {
       gemv(w, z + std::size_t(first) * H, H, y, ldy, rows, false);
       return 1;
     }
@@ -1172,7 +1302,7 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
   // next residual norm adds in part order; returns the part count.
   const auto dense = [&](const Matrix& w, const float* in, std::uint32_t ldx,
                          std::uint32_t rows, const unsigned* rmax) -> std::uint32_t {
-    if (rows < kPromptRows) {
+    if (rows < mfma_rows) {
       gemv(w, in, ldx, out, H, rows, false);
       return 1;
     }
@@ -1187,7 +1317,7 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
     const std::size_t o = n - rows;
     const float* branch = parts ? out : nullptr;
     const float* pn = post && post->p ? post->as<float>() : nullptr;
-    if (next && consumer_rows >= kPromptRows)
+    if (next && consumer_rows >= mfma_rows)
       CheckStatus(lfm3_residual_norm_half(branch, parts ? parts : 1, std::size_t(rows) * H, pn,
                                           x + o * H, next->as<float>(), nullptr, a16 + o * lda,
                                           lda, scale + o, rows, H, c.eps, s));
@@ -1210,7 +1340,12 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
   {
     std::size_t row = 0, id = 0;
     for (const ChunkPart& part : input) {
-      if (part.tokens) {
+      if (part.tokens && m.bf16) {
+        CheckStatus(lfm3_bf16_embed(m.embedding.codes.p, c.vocab, H,
+                                    b.tokens.as<std::uint32_t>() + id, nullptr, part.count,
+                                    x + row * H, s));
+        id += part.count;
+      } else if (part.tokens) {
         CheckStatus(lfm3_embed(m.embedding.codes.p, m.embedding.scales.p, c.vocab, H,
                                b.tokens.as<std::uint32_t>() + id, part.count, x + row * H, s));
         id += part.count;
@@ -1305,7 +1440,7 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
     residual_norm(parts, &l.post_norm, &l.ffn_norm, rows_out, rows_out);
     // FFN over the live rows: SwiGLU (with each row's max |y| per block of
     // output rows for the down projection's FP16 conversion), then down.
-    if (rows_out < kPromptRows) {
+    if (rows_out < mfma_rows) {
       gemv(l.ffn, z + std::size_t(o) * H, H, hid, F, rows_out, true);
       parts = dense(l.down, hid, F, rows_out, nullptr);
     } else {
@@ -1322,11 +1457,8 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
   CheckStatus(lfm3_residual_norm(nullptr, nullptr, x + std::size_t(n - 1) * H,
                                  m.output_norm.as<float>(), se.frontier.as<float>(), 1, H,
                                  c.eps, s));
-  if (want_logits) {
-    const Matrix& head = m.head();
-    CheckStatus(lfm3_q8_gemv(head.codes.p, head.scales.p, c.vocab, H, se.frontier.as<float>(),
-                             H, se.logits.as<float>(), c.vocab, 1, nullptr, 0, s));
-  }
+  if (want_logits)
+    HeadRow(m, se.frontier.as<float>(), se.logits.as<float>(), s);
   Check(hipGetLastError(), "prompt launch");
   Check(hipStreamSynchronize(s), "prompt");
   se.position += n;

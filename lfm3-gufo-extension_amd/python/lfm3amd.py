@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(PKG_DIR, "liblfm3_amd.so")
 
 OK, E_INVALID, E_HIP, E_STATE, E_NOMEM, E_REFUSED = 0, -1, -2, -3, -4, -5
 LAYER_CONV, LAYER_FULL, LAYER_SLIDING = 0, 1, 2
-TYPE_F32, TYPE_Q8_0 = 0, 8
+TYPE_F32, TYPE_Q8_0, TYPE_BF16 = 0, 8, 30
 STATE_LOGITS, STATE_FRONTIER, STATE_CONV, STATE_KEY, STATE_VALUE = range(5)
 GLOBAL_TENSORS, LAYER_TENSORS = 4, 17
 MAX_BATCH = 8
@@ -104,6 +104,11 @@ _SIGS = {
     "lfm3_q8_gemm_h16": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, vp, u32, u32, vp]),
     "lfm3_q8_gemm_swiglu_h16": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, vp, u32, vp, vp]),
     "lfm3_q8_gemv_swiglu": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, u32, vp, sz, vp]),
+    "lfm3_bf16_tiled_bytes": (sz, [u32, u32]),
+    "lfm3_bf16_pack_host": (i32, [vp, u32, u32, vp, u32, u32]),
+    "lfm3_bf16_gemv_parts": (u32, [u32, u32, u32]),
+    "lfm3_bf16_gemv": (i32, [vp, u32, u32, vp, u32, vp, u32, u32, u32, i32, vp]),
+    "lfm3_bf16_embed": (i32, [vp, u32, u32, vp, vp, u32, vp, vp]),
     "lfm3_residual_norm": (i32, [vp, vp, vp, vp, vp, u32, u32, f32, vp]),
     "lfm3_embed": (i32, [vp, vp, u32, u32, vp, u32, vp, vp]),
     "lfm3_argmax_workspace_bytes": (sz, [u32]),
@@ -233,6 +238,23 @@ def q8(seed: int, name: str, rows: int, cols: int, d_std=0.02) -> np.ndarray:
     return out
 
 
+def bf16(seed: int, name: str, rows: int, cols: int, std=0.0116) -> np.ndarray:
+    """Random BF16 matrix (GGUF row-major uint16 bit patterns), N(0, std)
+    rounded to nearest even; std matches the synthetic Q8_0 weights."""
+    return to_bf16(normal(seed, name, rows * cols, 0.0, std))
+
+
+def to_bf16(x: np.ndarray) -> np.ndarray:
+    """FP32 -> BF16 bit patterns, round to nearest even."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    return b.astype(np.uint16)
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
 def q8_dequant(blob: np.ndarray, rows: int, cols: int) -> np.ndarray:
     """float64 d * q of GGUF Q8_0 rows (test helper)."""
     blocks = blob.reshape(rows, cols // 32, 34)
@@ -283,14 +305,16 @@ class Weights:
         return self.globals + [t for layer in self.layers for t in layer]
 
 
-def synth_weights(dims: Dims, seed: int = SEED, masked_rope=True) -> Weights:
-    """Random-init Q8_0 model of the given dims (GGUF layouts)."""
+def synth_weights(dims: Dims, seed: int = SEED, masked_rope=True, bf16_weights=False) -> Weights:
+    """Random-init model of the given dims (GGUF layouts): Q8_0 matrices, or
+    BF16 ones with bf16_weights."""
     H, F, D, V = dims.hidden, dims.intermediate, dims.head_dim, dims.vocab
     w = Weights(dims)
+    mat, mtype = (bf16, TYPE_BF16) if bf16_weights else (q8, TYPE_Q8_0)
     factors = np.ones(D // 2, np.float32)
     if masked_rope:
         factors[D // 4:] = 1e30
-    w.globals = [(q8(seed, "token_embd", V, H), TYPE_Q8_0, H, V), None,
+    w.globals = [(mat(seed, "token_embd", V, H), mtype, H, V), None,
                  (normal(seed, "output_norm", H, 1.0, 0.02), TYPE_F32, H, 1),
                  (factors, TYPE_F32, D // 2, 1)]
     for i in range(dims.n_layers):
@@ -298,23 +322,23 @@ def synth_weights(dims: Dims, seed: int = SEED, masked_rope=True) -> Weights:
         t = [None] * LAYER_TENSORS
         for j, name in enumerate(["attn_norm", "ffn_norm", "post_attention_norm", "post_ffw_norm"]):
             t[j] = (normal(seed, p + name, H, 1.0, 0.02), TYPE_F32, H, 1)
-        t[4] = (q8(seed, p + "ffn_gate", F, H), TYPE_Q8_0, H, F)
-        t[5] = (q8(seed, p + "ffn_up", F, H), TYPE_Q8_0, H, F)
-        t[6] = (q8(seed, p + "ffn_down", H, F), TYPE_Q8_0, F, H)
+        t[4] = (mat(seed, p + "ffn_gate", F, H), mtype, H, F)
+        t[5] = (mat(seed, p + "ffn_up", F, H), mtype, H, F)
+        t[6] = (mat(seed, p + "ffn_down", H, F), mtype, F, H)
         if dims.layer_type(i) == LAYER_CONV:
             t[7] = (normal(seed, p + "shortconv.conv", H * dims.conv_width, 0.0, 0.1), TYPE_F32,
                     dims.conv_width, H)
-            t[8] = (q8(seed, p + "shortconv.in_proj", 3 * H, H), TYPE_Q8_0, H, 3 * H)
-            t[9] = (q8(seed, p + "shortconv.out_proj", H, H), TYPE_Q8_0, H, H)
+            t[8] = (mat(seed, p + "shortconv.in_proj", 3 * H, H), mtype, H, 3 * H)
+            t[9] = (mat(seed, p + "shortconv.out_proj", H, H), mtype, H, H)
         else:
             kv = dims.kv_heads
-            t[10] = (q8(seed, p + "attn_q", dims.heads * D, H), TYPE_Q8_0, H, dims.heads * D)
-            t[11] = (q8(seed, p + "attn_k", kv * D, H), TYPE_Q8_0, H, kv * D)
-            t[12] = (q8(seed, p + "attn_v", kv * D, H), TYPE_Q8_0, H, kv * D)
+            t[10] = (mat(seed, p + "attn_q", dims.heads * D, H), mtype, H, dims.heads * D)
+            t[11] = (mat(seed, p + "attn_k", kv * D, H), mtype, H, kv * D)
+            t[12] = (mat(seed, p + "attn_v", kv * D, H), mtype, H, kv * D)
             t[13] = (normal(seed, p + "attn_q_norm", D, 1.0, 0.02), TYPE_F32, D, 1)
             t[14] = (normal(seed, p + "attn_k_norm", D, 1.0, 0.02), TYPE_F32, D, 1)
-            t[15] = (q8(seed, p + "attn_gate", dims.heads, H), TYPE_Q8_0, H, dims.heads)
-            t[16] = (q8(seed, p + "attn_output", H, dims.heads * D), TYPE_Q8_0, dims.heads * D, H)
+            t[15] = (mat(seed, p + "attn_gate", dims.heads, H), mtype, H, dims.heads)
+            t[16] = (mat(seed, p + "attn_output", H, dims.heads * D), mtype, dims.heads * D, H)
         w.layers.append(t)
     return w
 

@@ -107,7 +107,8 @@ struct Q8Block {
 };
 static_assert(sizeof(Q8Block) == 34, "Q8_0 block is 34 bytes");
 
-// weights.cpp:101-125 (Q8_0 via ggml's d * q, F32 by copy).
+// weights.cpp:101-125 (Q8_0 via ggml's d * q, F32 by copy, F16 and BF16
+// widened).
 bool DecodeRow(const orc_tensor& t, uint32_t row, float* out) {
   if (row >= t.rows)
     return false;
@@ -120,6 +121,14 @@ bool DecodeRow(const orc_tensor& t, uint32_t row, float* out) {
     const auto* h = static_cast<const uint16_t*>(t.data) + size_t(row) * t.cols;
     for (uint32_t i = 0; i < t.cols; ++i)
       out[i] = HalfToFloat(h[i]);
+    return true;
+  }
+  if (t.type == ORC_BF16) {  // weights.cpp:116-117: the high half of an FP32
+    const auto* h = static_cast<const uint16_t*>(t.data) + size_t(row) * t.cols;
+    for (uint32_t i = 0; i < t.cols; ++i) {
+      const uint32_t bits = uint32_t(h[i]) << 16;
+      std::memcpy(&out[i], &bits, 4);
+    }
     return true;
   }
   if (t.type == ORC_Q8_0 && t.cols % 32 == 0) {
@@ -137,7 +146,8 @@ bool DecodeRow(const orc_tensor& t, uint32_t row, float* out) {
 
 // reference.cpp:9-19.
 bool Mat(const orc_tensor& t, const float* x, float* y) {
-  if (t.type != ORC_F32 && t.type != ORC_F16 && !(t.type == ORC_Q8_0 && t.cols % 32 == 0))
+  if (t.type != ORC_F32 && t.type != ORC_F16 && t.type != ORC_BF16 &&
+      !(t.type == ORC_Q8_0 && t.cols % 32 == 0))
     return false;
   Split(t.rows, [&](size_t r0, size_t r1) {
     std::vector<float> row(t.cols);

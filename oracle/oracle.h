@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8 };
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_BF16 = 30 };
 enum { ORC_CONV = 0, ORC_FULL = 1, ORC_SLIDING = 2 };
 
 typedef struct {

@@ -14,7 +14,7 @@ import numpy as np
 ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
 
-F32, F16, Q8_0 = 0, 1, 8
+F32, F16, Q8_0, BF16 = 0, 1, 8, 30
 CONV, FULL, SLIDING = 0, 1, 2
 vp, u32, f32, sz, i32 = C.c_void_p, C.c_uint32, C.c_float, C.c_size_t, C.c_int
 
@@ -94,6 +94,12 @@ def _p(a: np.ndarray) -> int:
 
 def q8_tensor(blob: np.ndarray, rows: int, cols: int) -> Tensor:
     return Tensor(_p(blob), Q8_0, cols, rows)
+
+
+def bf16_tensor(h: np.ndarray, rows: int, cols: int) -> Tensor:
+    """GGUF BF16 rows (uint16 bit patterns)."""
+    assert h.dtype == np.uint16 and h.size == rows * cols
+    return Tensor(_p(h), BF16, cols, rows)
 
 
 def f32_tensor(a: np.ndarray, rows: int, cols: int) -> Tensor:
@@ -245,7 +251,7 @@ class Model:
         for i, e in enumerate(entries):
             if e is not None:
                 data, typ, cols, rows = e
-                self._tensors[i] = Tensor(_p(data), Q8_0 if typ == 8 else F32, cols, rows)
+                self._tensors[i] = Tensor(_p(data), typ, cols, rows)  # GGML type ids
         self._weights = weights
         self.handle = lib().orc_model_create(C.byref(self.config), self._tensors, len(entries))
         if not self.handle:
