@@ -74,27 +74,32 @@ def q8_bytes(rows: int, cols: int) -> int:
     return rows * (cols // 32) * 34
 
 
-def weight_bytes(d: L.Dims) -> int:
-    """Q8_0 weight bytes one decode round streams (the tied vocabulary head
-    included, the 8 embedding rows not)."""
+def bf16_bytes(rows: int, cols: int) -> int:
+    return rows * cols * 2
+
+
+def weight_bytes(d: L.Dims, bf16: bool = False) -> int:
+    """Weight bytes one decode round streams (Q8_0, or BF16 with bf16; the
+    tied vocabulary head included, the 8 embedding rows not)."""
     H, F, D = d.hidden, d.intermediate, d.head_dim
-    total = q8_bytes(d.vocab, H)
+    mb = bf16_bytes if bf16 else q8_bytes
+    total = mb(d.vocab, H)
     for i in range(d.n_layers):
-        total += 2 * q8_bytes(F, H) + q8_bytes(H, F)
+        total += 2 * mb(F, H) + mb(H, F)
         if d.layer_type(i) == L.LAYER_CONV:
-            total += q8_bytes(3 * H, H) + q8_bytes(H, H)
+            total += mb(3 * H, H) + mb(H, H)
         else:
-            total += q8_bytes(d.heads * D, H) + 2 * q8_bytes(d.kv_heads * D, H)
-            total += q8_bytes(d.heads, H) + q8_bytes(H, d.heads * D)
+            total += mb(d.heads * D, H) + 2 * mb(d.kv_heads * D, H)
+            total += mb(d.heads, H) + mb(H, d.heads * D)
     return total
 
 
-def round_bytes(d: L.Dims, positions) -> int:
+def round_bytes(d: L.Dims, positions, bf16: bool = False) -> int:
     """Algorithmic HBM bytes of one round at the given positions: weights,
     K/V rows read (keys [first, p]) and written, conv histories read and
     written."""
     kv_row = 2 * d.kv_heads * d.head_dim * 2  # K + V, F16
-    total = weight_bytes(d)
+    total = weight_bytes(d, bf16)
     for p in positions:
         for i in range(d.n_layers):
             t = d.layer_type(i)
@@ -146,6 +151,26 @@ def gemv_roofline(batch: int, copies: int, passes: int):
     stream.close()
     nbytes = q8_bytes(M, K) + batch * K * 4 + batch * M * 4
     return {"batch": batch, "bytes": nbytes, "us": us}
+
+
+def bf16_gemv_roofline(batch: int, copies: int, passes: int):
+    """The exact BF16 GEMV at config 1's shape (W 8192 x 2048 BF16, `batch`
+    FP32 rows) over `copies` rotated weight buffers (32 MB each, past the
+    MALL), replayed from a HIP graph."""
+    M, K = 8192, 2048
+    h = L.bf16(L.SEED, "bf16.gemv.W", M, K)
+    tiles = np.zeros(L.lib().lfm3_bf16_tiled_bytes(M, K) // 2, np.uint16)
+    L.check(L.lib().lfm3_bf16_pack_host(L.ptr(h), M, K, L.ptr(tiles), 0, 1))
+    mats = [L.DeviceBuffer.of(tiles) for _ in range(copies)]
+    x = L.DeviceBuffer.of(L.normal(L.SEED, f"bf16.gemv.X{batch}", batch * K))
+    y = L.DeviceBuffer(batch * M * 4)
+    us = time_launches(lambda i, st: L.check(L.lib().lfm3_bf16_gemv(
+        mats[i].addr, M, K, x.addr, K, y.addr, M, batch, 1, 0, st)), copies, passes)
+    nbytes = bf16_bytes(M, K) + batch * K * 4 + batch * M * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"kernel": "exact BF16 x FP32 GEMV, W 8192 x 2048 BF16", "batch": batch,
+            "us": round(us, 3), "bytes": nbytes, "GBps": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def packed_copies(parts, rows_total: int, cols: int, copies: int):
@@ -479,13 +504,12 @@ def roofline_only():
                       "gemm_flops": m["flops"], "gemm_us": m["us"]}), flush=True)
 
 
-def nominal_round(seed, ctx, tokens0, steps: int, warmup: int):
-    """The same decode round on the BASELINE-nominal dims (FFN 8192, 32q/8kv
-    heads x 64, vocabulary 65536; the other dims as the reference's), with
-    the same contexts: its own random-init model and synthesized state."""
-    dims = L.Dims(intermediate=8192, heads=32, kv_heads=8, head_dim=64, vocab=65536,
-                  context=CTX_HI + warmup + steps + 64)
-    model = L.Model(L.synth_weights(dims, seed=seed))
+def variant_round(dims: L.Dims, seed, ctx, tokens0, steps: int, warmup: int, workload: str,
+                  bf16: bool = False):
+    """The decode round of 8 sessions at the same contexts on another model:
+    its own random-init weights (Q8_0, or BF16 with bf16) and synthesized
+    state, greedy ids fed back."""
+    model = L.Model(L.synth_weights(dims, seed=seed, bf16_weights=bf16))
     sessions = []
     for sid, c in enumerate(ctx):
         s = model.session(int(c) + warmup + steps + 8)
@@ -501,18 +525,17 @@ def nominal_round(seed, ctx, tokens0, steps: int, warmup: int):
         toks = model.forward_batch_greedy(sessions, toks)
     L.synchronize()
     ms = (time.perf_counter() - t0) * 1000.0 / steps
-    nbytes = statistics.mean(round_bytes(dims, p) for p in positions)
+    nbytes = statistics.mean(round_bytes(dims, p, bf16) for p in positions)
     for s in sessions:
         s.close()
     model.close()
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {
-        "workload": ("the same round on the nominal dims: FFN 8192, 32q/8kv heads x 64, "
-                     "vocab 65536 (hidden 2048, 24 layers 13/5/6, Q8_0)"),
+        "workload": workload,
         "ms": round(ms, 4),
         "tok_s": round(SESSIONS / (ms * 1e-3), 1),
         "bytes": int(nbytes),
-        "weight_bytes": weight_bytes(dims),
+        "weight_bytes": weight_bytes(dims, bf16),
         "achieved_GBps": round(gbs, 1),
         "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
     }
@@ -722,7 +745,7 @@ def main():
     tokens0 = L.uniform_u32(seed, "bench.tokens", SESSIONS, 0, dims.vocab - 1)
     sessions = []
     for sid, c in enumerate(ctx):
-        s = model.session(int(c) + args.warmup + args.steps + 8)
+        s = model.session(int(c) + args.warmup + 2 * args.steps + 8)
         L.inject_synth_state(s, dims, seed, sid, int(c) - 1)
         sessions.append(s)
     log(f"sessions at contexts {ctx.tolist()}")
@@ -751,6 +774,21 @@ def main():
     rbytes = statistics.mean(round_bytes(dims, p) for p in positions)
     round_gbs = rbytes / (ms_per_step / 1000.0) / 1e9
     log(f"round {ms_per_step:.3f} ms, {value:.1f} tok/s, {round_gbs:.0f} GB/s")
+
+    # The same rounds with the serving loop's sampler (runner.cpp:31-35
+    # defaults) in place of the greedy pick: the last 64 ids of each session
+    # as its penalty list, seeded uniforms.
+    params = L.Sampling(0.1, 50, 1.1)
+    rng = np.random.default_rng(seed)
+    recent = np.full((SESSIONS, 64), dims.vocab, np.uint32)  # ids >= vocab pad
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        recent[:, k % 64] = toks
+        toks = model.forward_batch_sample(sessions, toks, params,
+                                          rng.random(SESSIONS, dtype=np.float32), recent)
+    L.synchronize()
+    sampled_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    log(f"sampled round {sampled_ms:.3f} ms")
 
     # The round's kernels alone at their round shapes; the first (the SwiGLU
     # operand-image GEMV, the largest share of the round) is the roofline.
@@ -806,6 +844,13 @@ def main():
             "frac_of_peak": round(round_gbs / HBM_PEAK_GBS, 4),
             "gpu_ms_per_step": round(ev0.elapsed_ms(ev1) / args.steps, 4),
         },
+        "sampled_round": {
+            "workload": ("the same round with lfm3_forward_batch_sample at the serving "
+                         "loop's defaults (temperature 0.1, top_k 50, repeat_penalty 1.1 "
+                         "over the last 64 ids) instead of the greedy pick"),
+            "ms": round(sampled_ms, 4),
+            "tok_s": round(SESSIONS / (sampled_ms * 1e-3), 1),
+        },
         "config1_gemv": {
             "kernel": "Q8_0 skinny GEMV, W 8192 x 2048 on FP32 rows (BASELINE config 1)",
             "sweep": [{"batch": g["batch"], "us": round(g["us"], 3), "bytes": g["bytes"],
@@ -815,10 +860,25 @@ def main():
             "traffic_read_write": [GEMV_TRAFFIC["read"], GEMV_TRAFFIC["write"]],
         },
     }
-    nominal = nominal_round(seed, ctx, tokens0, args.steps, args.warmup)
+    span = CTX_HI + args.warmup + args.steps + 64
+    nominal = variant_round(
+        L.Dims(intermediate=8192, heads=32, kv_heads=8, head_dim=64, vocab=65536, context=span),
+        seed, ctx, tokens0, args.steps, args.warmup,
+        "the same round on the nominal dims: FFN 8192, 32q/8kv heads x 64, vocab 65536 "
+        "(hidden 2048, 24 layers 13/5/6, Q8_0)")
     log(f"nominal-dims round {nominal['ms']:.3f} ms, {nominal['tok_s']:.0f} tok/s, "
         f"{nominal['achieved_GBps']:.0f} GB/s")
     result["nominal_round"] = nominal
+    bf16 = variant_round(
+        L.Dims(context=span), seed, ctx, tokens0, args.steps, args.warmup,
+        "the same round with BF16 weights (the reference precision: exact BF16 x FP32 "
+        "projections), reference dims", bf16=True)
+    log(f"BF16-weights round {bf16['ms']:.3f} ms, {bf16['tok_s']:.0f} tok/s, "
+        f"{bf16['achieved_GBps']:.0f} GB/s")
+    bf16["gemv"] = bf16_gemv_roofline(8, 16, 6)
+    log(f"BF16 GEMV 8192 x 2048, 8 rows: {bf16['gemv']['us']:.2f} us, "
+        f"{bf16['gemv']['GBps']:.0f} GB/s")
+    result["bf16_round"] = bf16
     if not args.no_prefill:
         log("512-token prompt pass at depth 24576 and the mixed round ...")
         pass_ms, mixed, mixed_ctx = prefill_and_mixed(model, dims, seed, args.prefill_reps, 2)

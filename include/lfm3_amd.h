@@ -301,13 +301,17 @@ typedef struct {
    the first candidate, in descending logit order (index order when the
    whole vocabulary is kept), whose running weight sum exceeds
    uniforms[row] * total. uniforms (in [0, 1)) may be NULL for a greedy
-   pick. No workspace; deterministic for given uniforms.
+   pick. Deterministic for given uniforms. The workspace (device memory,
+   lfm3_sample_workspace_bytes(rows, cols, top_k) bytes) holds each
+   4096-logit slice's statistics and top-k candidates between the two
+   launches.
    Replaces: sampler.Sample(s.logits) in SelectNext (runner.cpp:300-325),
    the Gufo host sampler, which the reference does not carry. */
+size_t lfm3_sample_workspace_bytes(uint32_t rows, uint32_t cols, uint32_t top_k);
 int lfm3_sample(const float* logits, uint32_t rows, uint32_t cols, uint32_t ld,
                 const lfm3_sampling* params, const uint32_t* penalty_ids,
                 uint32_t n_penalty, const float* uniforms, uint32_t* ids,
-                void* stream);
+                void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------
  * Ragged decode rows: every row belongs to its own session; per-row

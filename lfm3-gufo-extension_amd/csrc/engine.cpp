@@ -210,8 +210,10 @@ struct lfm3_model {
   Buffer table;
   std::unique_ptr<PinnedBuffer> staging;
   std::unique_ptr<PinnedBuffer> logits_host;  // one logits row, pinned
-  // A sampled round's uniforms and penalty lists (made on first use).
-  Buffer sample_table;
+  // A sampled round's uniforms and penalty lists (made on first use), and
+  // the sampler's workspace (greedy size at load, grown for top-k).
+  Buffer sample_table, sample_ws;
+  std::size_t sample_ws_bytes = 0;
   std::unique_ptr<PinnedBuffer> sample_staging;
   std::size_t table_bytes = 0, items_capacity = 0;
   Buffer attn_ws;
@@ -490,6 +492,8 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     m->image = Buffer(lfm3_operand_image_bytes(H));
     m->exps = Buffer(kMaxBatch * sizeof(int));
     m->ids = Buffer(B * 4);
+    m->sample_ws_bytes = SampleWorkspaceBytes(kMaxBatch, c.vocab, 1);
+    m->sample_ws = Buffer(m->sample_ws_bytes);
     m->one_row = Buffer(std::size_t(H) * 4);
     Check(hipDeviceSynchronize(), "model upload");
     *out = m.release();
@@ -986,7 +990,8 @@ void EnqueueRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
       if (greedy) {
         lfm3_sampling pick{0.0f, 1, 1.0f};
         CheckStatus(LaunchSample(logits, c.vocab, nullptr, n, c.vocab, pick, nullptr, 0,
-                                 nullptr, m.ids.as<std::uint32_t>(), s));
+                                 nullptr, m.ids.as<std::uint32_t>(), m.sample_ws.p,
+                                 m.sample_ws_bytes, s));
       }
     }
     Check(hipGetLastError(), "round launch");
@@ -1601,13 +1606,20 @@ void EnqueueSample(lfm3_model& m, std::uint32_t n, const SampleArgs& a) {
   const std::size_t used = uni_bytes + std::size_t(n) * a.n_penalty * 4;
   auto* dev = m.sample_table.as<std::uint8_t>();
   Check(hipMemcpyAsync(dev, host, used, hipMemcpyHostToDevice, m.stream), "sampler upload");
+  const std::size_t ws = SampleWorkspaceBytes(kMaxBatch, m.config.vocab, a.params->top_k);
+  if (ws > m.sample_ws_bytes) {
+    Check(hipStreamSynchronize(m.stream), "sampler workspace");
+    m.sample_ws = Buffer(ws);
+    m.sample_ws_bytes = ws;
+  }
   const auto* rows = reinterpret_cast<const float* const*>(m.table.as<std::uint8_t>() +
                                                            offsetof(RoundTable, logits));
   CheckStatus(LaunchSample(nullptr, 0, rows, n, m.config.vocab, *a.params,
                            a.n_penalty ? reinterpret_cast<const std::uint32_t*>(dev + uni_bytes)
                                        : nullptr,
                            a.n_penalty, a.uniforms ? reinterpret_cast<const float*>(dev) : nullptr,
-                           m.ids.as<std::uint32_t>(), m.stream));
+                           m.ids.as<std::uint32_t>(), m.sample_ws.p, m.sample_ws_bytes,
+                           m.stream));
 }
 
 int BatchEntry(lfm3_session* const* sessions, std::size_t n,

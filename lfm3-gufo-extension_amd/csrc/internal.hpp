@@ -51,16 +51,18 @@ std::uint32_t HeadGemvGroups(std::uint32_t rows, std::uint32_t cols);
 int LaunchArgmaxKeys(const unsigned long long* keys, std::uint32_t rows, std::uint32_t groups,
                      std::uint32_t* ids, hipStream_t stream);
 // lfm3_sample's limits, its parameter check (status, with the error text
-// set) and its launch over rows given by a device pointer table (row_ptrs)
-// or by a base and stride (logits, ld).
+// set), its workspace size and its launch over rows given by a device
+// pointer table (row_ptrs) or by a base and stride (logits, ld).
 constexpr int kSampleMaxCols = LFM3_SAMPLE_MAX_COLS, kSampleMaxTopK = LFM3_SAMPLE_MAX_TOP_K;
 constexpr int kSampleMaxPenalty = LFM3_SAMPLE_MAX_PENALTY;
 int CheckSample(const lfm3_sampling& p, std::uint32_t cols, std::uint32_t n_penalty,
                 bool have_penalty, bool have_uniforms);
+std::size_t SampleWorkspaceBytes(std::uint32_t rows, std::uint32_t cols, std::uint32_t top_k);
 int LaunchSample(const float* logits, std::uint32_t ld, const float* const* row_ptrs,
                  std::uint32_t rows, std::uint32_t cols, const lfm3_sampling& p,
                  const std::uint32_t* penalty_ids, std::uint32_t n_penalty,
-                 const float* uniforms, std::uint32_t* ids, hipStream_t stream);
+                 const float* uniforms, std::uint32_t* ids, void* workspace,
+                 std::size_t workspace_bytes, hipStream_t stream);
 // dst[i][0..count) = src + i * ld for rows i < rows, with dst pointers read
 // from a device table (per-session logits / frontier rows of a round).
 int LaunchScatterRows(const float* src, std::size_t ld, float* const* dst,

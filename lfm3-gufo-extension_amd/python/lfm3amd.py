@@ -113,7 +113,8 @@ _SIGS = {
     "lfm3_embed": (i32, [vp, vp, u32, u32, vp, u32, vp, vp]),
     "lfm3_argmax_workspace_bytes": (sz, [u32]),
     "lfm3_argmax": (i32, [vp, u32, u32, vp, vp, sz, vp]),
-    "lfm3_sample": (i32, [vp, u32, u32, u32, vp, vp, u32, vp, vp, vp]),
+    "lfm3_sample_workspace_bytes": (sz, [u32, u32, u32]),
+    "lfm3_sample": (i32, [vp, u32, u32, u32, vp, vp, u32, vp, vp, vp, sz, vp]),
     "lfm3_conv_step_ragged": (i32, [vp, u32, vp, vp, vp, u32, u32, u32, u32, vp]),
     "lfm3_decode_heads_ragged": (i32, [vp, vp, vp, u32, vp, vp, vp, vp, vp, vp, vp, vp,
                                        u32, u32, u32, u32, f32, vp]),
@@ -246,8 +247,11 @@ def bf16(seed: int, name: str, rows: int, cols: int, std=0.0116) -> np.ndarray:
 
 def to_bf16(x: np.ndarray) -> np.ndarray:
     """FP32 -> BF16 bit patterns, round to nearest even."""
-    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
-    b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    b = np.array(x, np.float32).view(np.uint32)   # a copy, rounded in place
+    r = (b >> 16) & 1
+    r += 0x7FFF
+    b += r          # finite values cannot carry out of 32 bits
+    b >>= 16
     return b.astype(np.uint16)
 
 

@@ -42,10 +42,11 @@ def sample(x, t, k, p=1.0, pen=None, u=None, ld=None):
     du = L.DeviceBuffer.of(np.ascontiguousarray(u, np.float32)) if u is not None else None
     ids = L.DeviceBuffer(rows * 4)
     params = L.Sampling(t, k, p)
+    ws = L.DeviceBuffer(L.lib().lfm3_sample_workspace_bytes(rows, cols, k))
     L.check(L.lib().lfm3_sample(dx.addr, rows, cols, ld, L.C.byref(params),
                                 dpen.addr if dpen else None,
                                 pen.shape[1] if pen is not None else 0,
-                                du.addr if du else None, ids.addr, None))
+                                du.addr if du else None, ids.addr, ws.addr, ws.nbytes, None))
     L.synchronize()
     return ids.download(np.uint32, rows)
 
@@ -76,6 +77,9 @@ CASES = [  # vocabulary, rows, temperature, top_k, penalty, penalty list length
     (1000, 8, 1.5, 1000, 1.0, 0),      # k == cols: whole vocabulary
     (37, 5, 0.3, 5, 1.1, 3),
     (262144, 1, 1.0, 2, 1.0, 0),
+    (262144, 2, 0.7, 1024, 1.1, 4096),   # 64 slices of 1024 candidates
+    (4097, 3, 1.0, 1000, 1.0, 0),        # a one-element last slice (shorter than k)
+    (8192, 4, 0.5, 0, 1.2, 100),         # whole vocabulary over two slices
 ]
 
 
@@ -134,12 +138,21 @@ def test_topk_ties_and_all_equal_rows():
     assert seen[0] == {10, 20}
     assert seen[1] == {0, 1, 2}
     assert seen[2] == {7, 4999}
+    # ties spread over slices of 4096: the lowest indices win across slices
+    V = 20000
+    x = np.full((1, V), -1.0, np.float32)
+    x[0, [19999, 12000, 8191, 4096, 4095, 3]] = 5.0
+    seen = set()
+    for i in range(0, grid, 40):
+        seen.add(int(sample(x, 1.0, 4, 1.0, None, np.full(1, (i + 0.5) / grid, np.float32))[0]))
+    assert seen == {3, 4095, 4096, 8191}
 
 
 def test_refusals():
     x = L.DeviceBuffer(4 * 1000)
     ids = L.DeviceBuffer(16)
     u = L.DeviceBuffer(16)
+    ws = L.DeviceBuffer(L.lib().lfm3_sample_workspace_bytes(1, 262144, 1024))
     bad = [
         (L.Sampling(1.0, 1025, 1.0), 1000, 1000, 0, u.addr),        # k above the maximum
         (L.Sampling(1.0, 5, 1.0), 1000, 1000, 0, None),             # no uniforms
@@ -151,8 +164,13 @@ def test_refusals():
     ]
     for params, cols, ld, n_pen, uni in bad:
         st = L.lib().lfm3_sample(x.addr, 1, cols, ld, L.C.byref(params), None, n_pen, uni,
-                                 ids.addr, None)
+                                 ids.addr, ws.addr, ws.nbytes, None)
         assert st == L.E_INVALID, (params.temperature, params.top_k, cols, ld, n_pen)
+    # a workspace smaller than lfm3_sample_workspace_bytes asks for
+    need = L.lib().lfm3_sample_workspace_bytes(1, 1000, 50)
+    st = L.lib().lfm3_sample(x.addr, 1, 1000, 1000, L.C.byref(L.Sampling(1.0, 50, 1.0)), None, 0,
+                             u.addr, ids.addr, ws.addr, need - 1, None)
+    assert st == L.E_INVALID
 
 
 def small_dims():
