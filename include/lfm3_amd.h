@@ -371,7 +371,10 @@ int lfm3_attention_plan(const uint32_t* positions, uint32_t rows,
 /* An item-list capacity that fits any plan of `rows` rows whose positions
    are at most max_position. */
 size_t lfm3_attention_max_items(uint32_t rows, uint32_t max_position);
-/* Partial sums of multi-span rows: items x heads x (dim + 2) floats. */
+/* The decode attention workspace: 64 KiB of arrival counters (one per
+   (first item, KV head) of a plan; they must be zero before a workspace's
+   first call, and every call leaves them zero), then the partial sums of
+   multi-span rows, items x heads x (dim + 2) floats. */
 size_t lfm3_attention_workspace_bytes(uint32_t items, uint32_t rows,
                                       uint32_t heads, uint32_t kv_heads,
                                       uint32_t dim);
@@ -380,11 +383,13 @@ size_t lfm3_attention_workspace_bytes(uint32_t items, uint32_t rows,
    q holds normed, rotated queries and the ring already holds the current
    K/V row (lfm3_decode_heads_ragged). q/gate/out rows have strides
    ldq/ldg/ldo floats; items and the per-row tables are in device memory.
-   dim 64 or 128; heads % kv_heads == 0 with a group of 2, 4 or 8. Two
-   launches: the spans, then their merge in span order; one when n_items ==
-   rows. `items` must be an lfm3_attention_plan over exactly these `rows`
-   rows: an item list whose count equals `rows` but holds a split row
-   leaves that row's outputs NaN (there is no merge launch to finish it).
+   dim 64 or 128; heads % kv_heads == 0 with a group of 2, 4 or 8. One
+   launch: the last span block of a split row (counted with an agent-scope
+   atomic in the workspace) merges the row's spans in span order, so
+   outputs do not depend on scheduling. `items` must be an
+   lfm3_attention_plan over exactly these `rows` rows: an item list whose
+   count equals `rows` but holds a split row leaves that row's outputs NaN
+   (the whole-row path has no merge).
    Replaces: gpu::Attention with n == 1 (hip/ops.hip:2289-2315:
    DecodeWaves + DecodeCombine) per session (engine.cpp:430-434). */
 int lfm3_decode_attention_ragged(
@@ -421,7 +426,9 @@ int lfm3_decode_heads_attention_ragged(
    instead of a workspace argument; same kernels, same outputs. A plan
    whose partials (lfm3_attention_workspace_bytes) exceed the array is
    refused (LFM3_E_INVALID). Nothing in the array needs clearing: every
-   partial a merge reads is written by its span first in the same call.
+   partial a merge reads is written by its span first in the same call, and
+   the arrival counters (the array's first 64 KiB, zero at load) return to
+   zero at the end of every call.
    Every call on one GPU shares that GPU's array, so calls that overlap on
    one GPU (on different streams) race. Allocates nothing: the array's
    address is looked up once per device (hipGetSymbolAddress). */

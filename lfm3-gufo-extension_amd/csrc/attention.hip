@@ -17,8 +17,13 @@
 // key), with the probabilities broadcast through LDS. The next group's K
 // and V loads are issued before the current group is computed. Waves merge
 // through LDS; rows with several spans leave per-span (max, sum, acc)
-// partials that a second launch merges in span order, so results do not
-// depend on block scheduling and no device-scope fence is needed.
+// partials, and the last span block of a (row, KV head) to arrive merges
+// them in span order, so results do not depend on block scheduling. The
+// partials go out as agent-scope stores (written through the XCD's L2),
+// each thread waits for its stores, and one agent-scope atomic per block
+// counts the arrivals; the block that brings the count to the row's span
+// count resets it to zero and reads every span's partials with
+// agent-scope loads. No device-scope fence is needed.
 //
 // With the heads fused in (lfm3_decode_heads_attention_ragged), every block
 // also applies the per-head Q/K RMSNorm and paired RoPE of its row
@@ -32,11 +37,15 @@
 // window (capacity = min(context, window) >= keys of any span), so the
 // current slot is not an earlier key of another span.
 //
-// A row with several spans needs the merge launch. The 8-wave whole-row
-// path runs only when the item count equals the row count (every row one
-// item); an item with parts > 1 on that path (an item list that is not a
-// plan over exactly `rows` rows) writes NaN to its row's outputs, so the
-// misuse shows instead of leaving stale rows.
+// A row with several spans needs the merge. The 8-wave whole-row path runs
+// only when the item count equals the row count (every row one item); an
+// item with parts > 1 on that path (an item list that is not a plan over
+// exactly `rows` rows) writes NaN to its row's outputs, so the misuse shows
+// instead of leaving stale rows.
+//
+// Workspace: kCounterBytes of arrival counters (one per (first item, KV
+// head); zero before the first call, and every call leaves them zero),
+// then the span partials.
 #include <algorithm>
 #include <array>
 #include <cmath>
@@ -57,6 +66,75 @@ namespace {
 constexpr int kAttnThreads = 256, kAttnWaves = 4, kGroupKeys = 16, kWholeRowWaves = 8;
 constexpr std::uint32_t kTargetItems = 128, kMinSpan = 64, kMaxSpan = 1024;
 constexpr std::uint32_t kMaxParts = 256;
+constexpr std::size_t kCounterBytes = 64 << 10;
+
+__device__ __forceinline__ void AgentStore(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float AgentLoad(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The merge of a multi-span row's partials in span order (the last span
+// block of (row, KV head g) runs it): span maxima, weights and
+// denominators staged in LDS, then every output element sums its spans.
+template<int D, int G, int T>
+__device__ void MergeSpans(const lfm3_attention_item& item, int g, int kv_heads,
+                           const float* partial, const float* s_gate, float* out, int ldo,
+                           float (*s_w)[G], float (*s_lv)[G], float* s_top, float* s_den) {
+  const int row = int(item.row), parts = int(item.parts), tid = threadIdx.x;
+  const std::size_t span_stride = std::size_t(kv_heads) * G * (D + 2);
+  const float* base = partial + (std::size_t(item.first_item) * kv_heads + g) * G * (D + 2);
+  for (int e = tid; e < parts * G; e += T) {
+    const int s = e / G, h = e % G;
+    const float* po = base + s * span_stride + h * (D + 2);
+    s_w[s][h] = AgentLoad(po);
+    s_lv[s][h] = AgentLoad(po + 1);
+  }
+  __syncthreads();
+  if (tid < G) {
+    float top = -INFINITY;
+    for (int s = 0; s < parts; ++s)
+      top = fmaxf(top, s_w[s][tid]);
+    s_top[tid] = top;
+  }
+  __syncthreads();
+  for (int e = tid; e < parts * G; e += T) {
+    const int s = e / G, h = e % G;
+    s_w[s][h] = expf(s_w[s][h] - s_top[h]);
+  }
+  __syncthreads();
+  if (tid < G) {
+    float den = 0.0f;
+    for (int s = 0; s < parts; ++s)
+      den = fmaf(s_lv[s][tid], s_w[s][tid], den);
+    s_den[tid] = den;
+  }
+  __syncthreads();
+  // Every element's sum first, then the stores.
+  constexpr int EPT = (G * D + T - 1) / T;
+  float av[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = tid + T * j;
+    av[j] = 0.0f;
+    if (e < G * D) {
+      const int h = e / D, d = e % D;
+      const float* po = base + h * (D + 2) + 2 + d;
+#pragma unroll 8
+      for (int s = 0; s < parts; ++s)
+        av[j] = fmaf(AgentLoad(po + s * span_stride), s_w[s][h], av[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int e = tid + T * j;
+    if (e < G * D) {
+      const int h = e / D, d = e % D;
+      out[std::size_t(row) * ldo + (g * G + h) * D + d] = (av[j] / s_den[h]) / s_gate[h];
+    }
+  }
+}
 
 // Orders this wave's LDS writes before its later LDS reads by other lanes.
 // The hardware keeps a wave's LDS operations in order; the fence stops the
@@ -82,7 +160,8 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
     const std::uint32_t* __restrict__ positions,
     const std::uint32_t* __restrict__ capacity,
     const lfm3_attention_item* __restrict__ items, float* __restrict__ out,
-    int ldo, int kv_heads, float eps, float* __restrict__ partial) {
+    int ldo, int kv_heads, float eps, float* __restrict__ partial,
+    unsigned* __restrict__ counters) {
   static_assert(D == 64 || D == 128, "head dimension 64 or 128");
   static_assert(2 * G <= 16, "hi and lo rows of the group fit one MFMA tile");
   constexpr int S = D / 32;                // MFMA steps per key row
@@ -100,8 +179,8 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
   const int g = blockIdx.y, row = int(item.row);
   const int tid = threadIdx.x, lane = tid & 63;
   // The output gate's divisor, loaded before any store (a load after
-  // stores waits for them) and read from LDS by the epilogue.
-  if (item.parts == 1 && tid < G)
+  // stores waits for them) and read from LDS by the epilogue or the merge.
+  if (tid < G)
     s_gate[tid] = 1.0f + expf(-gate[std::size_t(row) * ldg + g * G + tid]);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int stride = kv_heads * D;
@@ -354,84 +433,32 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
     } else {
       float* po = part_out + h * (D + 2);
       if (d == 0) {
-        po[0] = top;
-        po[1] = l;
+        AgentStore(po, top);
+        AgentStore(po + 1, l);
       }
-      po[2 + d] = av;
+      AgentStore(po + 2 + d, av);
     }
   }
-}
-
-// Merges the spans of every multi-span row in span order: block = (first
-// item of a row, KV head); other items exit. Span maxima, weights and
-// denominators are staged in LDS, then every output element sums its
-// spans with independent loads.
-template<int D, int G>
-__launch_bounds__(kAttnThreads) __global__
-    void CombineKernel(const float* __restrict__ gate, int ldg,
-                       const lfm3_attention_item* __restrict__ items,
-                       float* __restrict__ out, int ldo, int kv_heads,
-                       const float* __restrict__ partial) {
-  __shared__ float s_w[kMaxParts][G];
-  __shared__ float s_lv[kMaxParts][G];
-  __shared__ float s_top[G], s_den[G], s_gate[G];
-  const lfm3_attention_item item = items[blockIdx.x];
-  if (item.parts < 2 || item.first_item != blockIdx.x)
-    return;
-  const int g = blockIdx.y, row = int(item.row), parts = int(item.parts);
-  const int tid = threadIdx.x;
-  if (tid < G)  // loaded before the stores, read from LDS
-    s_gate[tid] = 1.0f + expf(-gate[std::size_t(row) * ldg + g * G + tid]);
-  const std::size_t span_stride = std::size_t(kv_heads) * G * (D + 2);
-  const float* base = partial + (std::size_t(item.first_item) * kv_heads + g) * G * (D + 2);
-  for (int e = tid; e < parts * G; e += kAttnThreads) {
-    const int s = e / G, h = e % G;
-    const float* po = base + s * span_stride + h * (D + 2);
-    s_w[s][h] = po[0];
-    s_lv[s][h] = po[1];
-  }
-  __syncthreads();
-  if (tid < G) {
-    float top = -INFINITY;
-    for (int s = 0; s < parts; ++s)
-      top = fmaxf(top, s_w[s][tid]);
-    s_top[tid] = top;
-  }
-  __syncthreads();
-  for (int e = tid; e < parts * G; e += kAttnThreads) {
-    const int s = e / G, h = e % G;
-    s_w[s][h] = expf(s_w[s][h] - s_top[h]);
-  }
-  __syncthreads();
-  if (tid < G) {
-    float den = 0.0f;
-    for (int s = 0; s < parts; ++s)
-      den = fmaf(s_lv[s][tid], s_w[s][tid], den);
-    s_den[tid] = den;
-  }
-  __syncthreads();
-  // Every element's sum first, then the stores: a load issued after a
-  // store waits for it.
-  constexpr int EPT = (G * D + kAttnThreads - 1) / kAttnThreads;
-  float av[EPT];
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int e = tid + kAttnThreads * j;
-    av[j] = 0.0f;
-    if (e < G * D) {
-      const int h = e / D, d = e % D;
-      const float* po = base + h * (D + 2) + 2 + d;
-#pragma unroll 8
-      for (int s = 0; s < parts; ++s)
-        av[j] = fmaf(po[s * span_stride], s_w[s][h], av[j]);
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int e = tid + kAttnThreads * j;
-    if (e < G * D) {
-      const int h = e / D, d = e % D;
-      out[std::size_t(row) * ldo + (g * G + h) * D + d] = (av[j] / s_den[h]) / s_gate[h];
+  if constexpr (NW == kAttnWaves) {
+    if (split) {  // uniform over the block
+      __shared__ int s_last;
+      __shared__ float s_w[kMaxParts][G], s_lv[kMaxParts][G], s_top[G], s_den[G];
+      // Every thread's partial stores have completed before the arrival.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (tid == 0) {
+        unsigned* c = counters + std::size_t(item.first_item) * kv_heads + g;
+        const unsigned arrived =
+            __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+        const bool last = arrived == item.parts;
+        if (last)
+          __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+      }
+      __syncthreads();
+      if (s_last)
+        MergeSpans<D, G, NW * 64>(item, g, kv_heads, partial, s_gate, out, ldo, s_w, s_lv,
+                                  s_top, s_den);
     }
   }
 }
@@ -451,6 +478,7 @@ struct AttentionArgs {
   int ldo = 0, kv = 0;
   float eps = 0.0f;
   float* partial = nullptr;
+  unsigned* counters = nullptr;
 };
 
 template<int D, int G, int NW>
@@ -459,27 +487,24 @@ void LaunchWaves(const AttentionArgs& a, dim3 grid, hipStream_t s, bool fused) {
     DecodeAttentionKernel<D, G, true, NW><<<grid, NW * 64, 0, s>>>(
         a.q, a.k, a.v, a.ld, a.gate, a.ldg, a.q_norm, a.k_norm, a.frequencies,
         a.factors, a.ck, a.cv, a.positions, a.capacity, a.items, a.out, a.ldo,
-        a.kv, a.eps, a.partial);
+        a.kv, a.eps, a.partial, a.counters);
   else
     DecodeAttentionKernel<D, G, false, NW><<<grid, NW * 64, 0, s>>>(
         a.q, a.k, a.v, a.ld, a.gate, a.ldg, a.q_norm, a.k_norm, a.frequencies,
         a.factors, a.ck, a.cv, a.positions, a.capacity, a.items, a.out, a.ldo,
-        a.kv, a.eps, a.partial);
+        a.kv, a.eps, a.partial, a.counters);
 }
 
 // Every row in one item (sliding windows, short histories): 8-wave
-// blocks (two 16-key groups per wave for a 256-key window) and no merge
-// launch. Otherwise 4-wave blocks over the spans, then the merge.
+// blocks (two 16-key groups per wave for a 256-key window) and no merge.
+// Otherwise 4-wave blocks over the spans, each row's last span block
+// merging.
 template<int D, int G>
 void LaunchGroup(const AttentionArgs& a, dim3 grid, hipStream_t s, bool fused, bool whole_rows) {
-  if (whole_rows) {
+  if (whole_rows)
     LaunchWaves<D, G, kWholeRowWaves>(a, grid, s, fused);
-    return;
-  }
-  LaunchWaves<D, G, kAttnWaves>(a, grid, s, fused);
-  CombineKernel<D, G><<<grid, kAttnThreads, 0, s>>>(a.gate, a.ldg, a.items,
-                                                     a.out, a.ldo, a.kv,
-                                                     a.partial);
+  else
+    LaunchWaves<D, G, kAttnWaves>(a, grid, s, fused);
 }
 
 template<int D>
@@ -508,9 +533,12 @@ int Launch(const AttentionArgs& a, std::uint32_t n_items, std::uint32_t rows,
   if (!workspace || workspace_bytes < lfm3_attention_workspace_bytes(
                                           n_items, rows, heads, kv_heads, dim))
     return Fail(LFM3_E_INVALID, "LFM3 attention workspace too small");
+  if (std::size_t(n_items) * kv_heads * sizeof(unsigned) > kCounterBytes)
+    return Fail(LFM3_E_INVALID, "LFM3 attention plan has too many items for its counters");
   AttentionArgs args = a;
   args.kv = int(kv_heads);
-  args.partial = static_cast<float*>(workspace);
+  args.counters = static_cast<unsigned*>(workspace);
+  args.partial = reinterpret_cast<float*>(static_cast<std::uint8_t*>(workspace) + kCounterBytes);
   const dim3 grid(n_items, kv_heads);
   const auto s = static_cast<hipStream_t>(stream);
   // Every plan item covers at least one row, so n_items == rows means one
@@ -618,7 +646,7 @@ std::size_t lfm3_attention_workspace_bytes(std::uint32_t items,
                                            std::uint32_t dim) {
   (void)rows;
   (void)kv_heads;
-  return std::size_t(items) * heads * (dim + 2) * sizeof(float);
+  return kCounterBytes + std::size_t(items) * heads * (dim + 2) * sizeof(float);
 }
 
 int lfm3_decode_attention_ragged(
