@@ -492,11 +492,13 @@ def copy_calibration(nbytes: int, reps: int):
 def roofline_only():
     """The roofline kernels and the copy calibration, nothing else: the
     program that rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE run (the
-    decode round's kernels at their round shapes, config 1's GEMV at 8
-    rows, the prompt pass's SwiGLU GEMM)."""
+    decode round's kernels at their round shapes, the attention at the
+    bench's contexts included, config 1's GEMV at 8 rows, the prompt
+    pass's SwiGLU GEMM)."""
     copy_bytes = 256 << 20
     copy_calibration(copy_bytes, 4)
-    kernels = round_kernels(L.Dims(), None, passes=2)
+    ctx = L.uniform_u32(L.SEED, "bench.ctx", SESSIONS, CTX_LO, CTX_HI)
+    kernels = round_kernels(L.Dims(), [int(c) - 1 for c in ctx], passes=2)
     g = gemv_roofline(8, 32, 2)
     m = gemm_roofline(8, 2)
     print(json.dumps({"copy_bytes": copy_bytes, "round_kernels": kernels,
