@@ -293,8 +293,8 @@ typedef struct {
 #define LFM3_SAMPLE_MAX_TOP_K 1024u
 #define LFM3_SAMPLE_MAX_PENALTY 4096u
 #define LFM3_SAMPLE_MAX_COLS 262144u
-/* One token id per logits row (rows of cols floats, ld floats apart), all
-   in device memory. Each row: the repetition penalty over
+/* One token id per logits row (at most 65535 rows of cols floats, ld
+   floats apart), all in device memory. Each row: the repetition penalty over
    penalty_ids[row * n_penalty ...] (logit l -> l / p if l > 0 else l * p,
    once per listed token; ids >= cols are padding), the top_k largest
    logits (ties toward the lower index), weights exp((l - l_max) / T), and

@@ -538,7 +538,8 @@ int LaunchSample(const float* logits, std::uint32_t ld, const float* const* row_
                  std::size_t workspace_bytes, hipStream_t stream) {
   if (const int e = CheckSample(p, cols, n_penalty, penalty_ids != nullptr, uniforms != nullptr))
     return e;
-  if ((!logits && !row_ptrs) || !ids || !rows || (logits && ld < cols) || !workspace ||
+  if ((!logits && !row_ptrs) || !ids || !rows || rows > 65535 || (logits && ld < cols) ||
+      !workspace ||
       workspace_bytes < SampleWorkspaceBytes(rows, cols, p.top_k))
     return Fail(LFM3_E_INVALID, "invalid LFM3 sampling shape or workspace");
   const int mode = ModeOf(p, cols);
