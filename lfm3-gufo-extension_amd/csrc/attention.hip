@@ -111,20 +111,36 @@ __device__ void MergeSpans(const lfm3_attention_item& item, int g, int kv_heads,
     s_den[tid] = den;
   }
   __syncthreads();
-  // Every element's sum first, then the stores.
-  constexpr int EPT = (G * D + T - 1) / T;
+  // Every element's sum first, then the stores. The loads of kBatch spans
+  // of every element a thread owns go out together (one memory round trip
+  // a batch); the sums then run in span order. A batch's loads past the
+  // last span repeat the last one and are not added.
+  constexpr int EPT = (G * D + T - 1) / T, kBatch = 16;
   float av[EPT];
+  const float* po[EPT];
+  int hh[EPT];
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
-    const int e = tid + T * j;
+    const int e = tid + T * j < G * D ? tid + T * j : 0;
+    hh[j] = e / D;
+    po[j] = base + hh[j] * (D + 2) + 2 + e % D;
     av[j] = 0.0f;
-    if (e < G * D) {
-      const int h = e / D, d = e % D;
-      const float* po = base + h * (D + 2) + 2 + d;
-#pragma unroll 8
-      for (int s = 0; s < parts; ++s)
-        av[j] = fmaf(AgentLoad(po + s * span_stride), s_w[s][h], av[j]);
+  }
+  for (int s0 = 0; s0 < parts; s0 += kBatch) {
+    float v[kBatch][EPT];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int s = min(s0 + b, parts - 1);
+#pragma unroll
+      for (int j = 0; j < EPT; ++j)
+        v[b][j] = AgentLoad(po[j] + s * span_stride);
     }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b)
+      if (s0 + b < parts)
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+          av[j] = fmaf(v[b][j], s_w[s0 + b][hh[j]], av[j]);
   }
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
