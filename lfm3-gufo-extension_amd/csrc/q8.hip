@@ -654,8 +654,12 @@ void LaunchImageRT(const GemvPlan& p, const std::uint8_t* c, const Half* s,
 GemvPlan PlanImage(std::uint32_t rows, std::uint32_t cols, bool swiglu, std::uint32_t parts) {
   GemvPlan p = PlanGemv(rows, cols, swiglu, int(parts));
   // Rounds of W * 4 chunks need no LDS: keep two tiles (one SwiGLU pair)
-  // at most, so two blocks of eight waves fit a CU.
-  p.RT = swiglu ? 2 : std::min(p.RT, 2);
+  // at most, so two blocks of eight waves fit a CU. With no operand
+  // staging, a second tile only shares the cross-wave reduction, which
+  // pays once the tiles outnumber the CUs: at 193 tiles (q | k | v | gate,
+  // 3088 x 2048, 8 rows) one tile a block takes 4.8 us against 5.8 us with
+  // two; at 8000 tiles (the vocabulary head) two take 60 us against 73 us.
+  p.RT = swiglu ? 2 : p.row_tiles > 256 ? 2 : 1;
   p.groups = (p.row_tiles + p.RT - 1) / p.RT;
   return p;
 }
