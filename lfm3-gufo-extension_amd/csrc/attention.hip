@@ -302,30 +302,43 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
   const BufferResource k_res = MakeBuffer(ck, ring_bytes);
   const BufferResource v_res = MakeBuffer(cv, ring_bytes);
   const int n = lane & 15, kg = lane >> 4;
-  // Ring slot of key base + o (o < 16): one (wave-uniform) division per
-  // group, then the wrap as a subtraction (rings of 16 slots or more).
-  const auto slot_of = [&](int base, int o) -> unsigned {
-    const unsigned sl = unsigned(base) % cap + unsigned(o);
-    return cap >= 16 ? (sl >= cap ? sl - cap : sl) : sl % cap;
-  };
+  // Ring slots of keys base + o (o < 16) for the lane's K row (o = n) and V
+  // rows (o = kq + KG i): one wave-uniform division per group, then the
+  // wrap as an unsigned minimum (rings of 16 slots or more; smaller rings
+  // take the remainder). Keys past the span, and groups past the wave's
+  // last, read zeros from an offset the hardware drops (no traffic). The
+  // offsets are selects, not branches around the loads.
+  const int ngroups = ngroups_of(kb, ke);
+  const unsigned row_bytes = unsigned(stride) * 2;
+  const unsigned k_lane = unsigned(g * D + 8 * kg) * 2, v_lane = unsigned(g * D + 8 * dg) * 2;
   const auto fetch = [&](int j, uint4 (&kr)[S], uint4 (&vr)[KPL]) {
     const int base = kb + kGroupKeys * j;
-    const bool kvalid = j < ngroups_of(kb, ke) && base + n < ke;
-    const unsigned koff = kvalid ? (slot_of(base, n) * unsigned(stride) + g * D + 8 * kg) * 2
-                                 : kOutOfRange;
+    const int rem = j < ngroups ? ke - base : 0;  // keys of the group inside the span
+    const unsigned b0 = unsigned(base) % cap;
+    unsigned sk = b0 + unsigned(n), sv[KPL];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i)
+      sv[i] = b0 + unsigned(kq + KG * i);
+    if (cap >= 16) {
+      sk = min(sk, sk - cap);
+#pragma unroll
+      for (int i = 0; i < KPL; ++i)
+        sv[i] = min(sv[i], sv[i] - cap);
+    } else {
+      sk %= cap;
+#pragma unroll
+      for (int i = 0; i < KPL; ++i)
+        sv[i] %= cap;
+    }
+    const unsigned koff = n < rem ? sk * row_bytes + k_lane : kOutOfRange;
 #pragma unroll
     for (int s2 = 0; s2 < S; ++s2)
       kr[s2] = LoadB128(k_res, koff + 64 * s2);
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) {
-      const int o = kq + KG * i;
-      const bool vvalid = j < ngroups_of(kb, ke) && base + o < ke;
-      vr[i] = LoadB128(v_res, vvalid ? (slot_of(base, o) * unsigned(stride) + g * D + 8 * dg) * 2
-                                     : kOutOfRange);
-    }
+    for (int i = 0; i < KPL; ++i)
+      vr[i] = LoadB128(v_res, kq + KG * i < rem ? sv[i] * row_bytes + v_lane : kOutOfRange);
   };
 
-  const int ngroups = ngroups_of(kb, ke);
   uint4 kr[S], vr[KPL], kn[S], vn[KPL];
   fetch(wave, kr, vr);
   for (int j = wave; j < ngroups; j += NW) {
