@@ -489,6 +489,53 @@ def copy_calibration(nbytes: int, reps: int):
     dst.close()
 
 
+def device_ceilings(read_bytes: int = 2 << 30, reps: int = 8):
+    """What this MI355X delivers to a kernel, beside the published peaks: a
+    plain streaming read of a 2 GiB buffer (lfm3_measure_stream_read, best
+    of four grid sizes) and a register-only f16 MFMA loop
+    (lfm3_measure_mfma_f16, 4 waves a SIMD), each timed with HIP events over
+    `reps` back-to-back launches on its own stream after one untimed
+    launch."""
+    lib = L.lib()
+    stream = L.Stream()
+
+    def timed(launch) -> float:
+        launch()
+        stream.synchronize()
+        a, b = L.Event(), L.Event()
+        a.record(stream.handle)
+        for _ in range(reps):
+            launch()
+        b.record(stream.handle)
+        b.synchronize()
+        ms = a.elapsed_ms(b) / reps
+        a.close()
+        b.close()
+        return ms
+
+    buf = L.DeviceBuffer(read_bytes)
+    L.hip_check(L.hip().hipMemset(buf.addr, 0x5a, read_bytes))
+    sink = L.DeviceBuffer(65535 * 4 * 4)
+    best, best_blocks = 0.0, 0
+    for blocks in (1024, 2048, 4096, 8192):
+        ms = timed(lambda: L.check(lib.lfm3_measure_stream_read(
+            buf.addr, read_bytes, sink.addr, blocks, stream.handle)))
+        if read_bytes / (ms * 1e-3) / 1e9 > best:
+            best, best_blocks = read_bytes / (ms * 1e-3) / 1e9, blocks
+    buf.close()
+    iters, blocks = 4096, 1024
+    ms = timed(lambda: L.check(lib.lfm3_measure_mfma_f16(iters, blocks, sink.addr,
+                                                         stream.handle)))
+    tflops = lib.lfm3_measure_mfma_f16_flops(iters, blocks) / (ms * 1e-3) / 1e12
+    sink.close()
+    stream.close()
+    return {"stream_read_GBps": round(best, 1), "stream_read_bytes": read_bytes,
+            "stream_read_blocks": best_blocks,
+            "mfma_f16_TFLOPs": round(tflops, 1),
+            "stream_read_frac_of_peak": round(best / HBM_PEAK_GBS, 4),
+            "mfma_f16_frac_of_peak": round(tflops / MFMA_PEAK_TFLOPS, 4)}
+
+
 def roofline_only():
     """The roofline kernels and the copy calibration, nothing else: the
     program that rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE run (the
@@ -765,8 +812,11 @@ def main():
     ev0, ev1 = L.Event(), L.Event()
     ev0.record(stream)
     t0 = time.perf_counter()
+    step_ms = []
     for _ in range(args.steps):
-        toks = model.forward_batch_greedy(sessions, toks)
+        ts = time.perf_counter()
+        toks = model.forward_batch_greedy(sessions, toks)  # returns after the ids land
+        step_ms.append((time.perf_counter() - ts) * 1000.0)
     L.synchronize()
     wall = time.perf_counter() - t0
     ev1.record(stream)
@@ -845,6 +895,9 @@ def main():
             "achieved_GBps": round(round_gbs, 1),
             "frac_of_peak": round(round_gbs / HBM_PEAK_GBS, 4),
             "gpu_ms_per_step": round(ev0.elapsed_ms(ev1) / args.steps, 4),
+            "step_ms_median": round(float(np.median(step_ms)), 4),
+            "step_ms_p10": round(float(np.percentile(step_ms, 10)), 4),
+            "step_ms_p90": round(float(np.percentile(step_ms, 90)), 4),
         },
         "sampled_round": {
             "workload": ("the same round with lfm3_forward_batch_sample at the serving "
@@ -862,6 +915,12 @@ def main():
             "traffic_read_write": [GEMV_TRAFFIC["read"], GEMV_TRAFFIC["write"]],
         },
     }
+    ceilings = device_ceilings()
+    log(f"measured ceilings: streaming read {ceilings['stream_read_GBps']:.0f} GB/s, "
+        f"f16 MFMA loop {ceilings['mfma_f16_TFLOPs']:.0f} TFLOP/s")
+    result["measured_ceilings"] = ceilings
+    result["roofline"]["frac_of_measured"] = round(top["GBps"] / ceilings["stream_read_GBps"], 4)
+    result["round"]["frac_of_measured"] = round(round_gbs / ceilings["stream_read_GBps"], 4)
     span = CTX_HI + args.warmup + args.steps + 64
     nominal = variant_round(
         L.Dims(intermediate=8192, heads=32, kv_heads=8, head_dim=64, vocab=65536, context=span),
@@ -900,6 +959,7 @@ def main():
             "flops_without_pruning": int(flops_full),
             "tflops": round(tflops, 1),
             "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+            "mfma_frac_of_measured": round(tflops / ceilings["mfma_f16_TFLOPs"], 4),
             "reps": args.prefill_reps,
             "roofline": {
                 "bound": "mfma",
@@ -908,6 +968,7 @@ def main():
                 "peak": MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": round(gemm["tflops"] / MFMA_PEAK_TFLOPS, 4),
+                "frac_of_measured": round(gemm["tflops"] / ceilings["mfma_f16_TFLOPs"], 4),
                 "traffic": GEMM_TRAFFIC["read"] + GEMM_TRAFFIC["write"],
                 "traffic_read_write": [GEMM_TRAFFIC["read"], GEMM_TRAFFIC["write"]],
                 "algorithmic_bytes": gemm["bytes"],

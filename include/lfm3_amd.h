@@ -777,6 +777,25 @@ void lfm3_synth_half_normal(uint64_t key, uint16_t* out, size_t n);
 void lfm3_synth_q8(uint64_t key, uint32_t rows, uint32_t cols, float d_std,
                    void* out);
 
+/* ---------------------------------------------------------------------
+ * Device ceilings for the benchmark, reported beside the published peaks.
+ * No counterpart in the reference (its benchmarks quote spec bandwidth).
+ * ------------------------------------------------------------------- */
+/* A streaming read of `bytes` (a multiple of 16, 16-byte aligned device
+   memory) by `blocks` 512-thread blocks; sink[b] (device, `blocks` words)
+   gets the XOR of every 32-bit word block b read, so the XOR over sink
+   equals the XOR over the buffer. */
+int lfm3_measure_stream_read(const void* buffer, size_t bytes, unsigned* sink,
+                             uint32_t blocks, void* stream);
+/* A register-only f16 MFMA loop: `blocks` blocks of 4 waves, each wave
+   running 8 independent v_mfma_f32_16x16x32_f16 chains for `iterations`
+   steps (at most 16384) over all-ones operands; sink (device, 4 * blocks
+   floats) gets each wave's 1024 * iterations exactly. */
+int lfm3_measure_mfma_f16(uint32_t iterations, uint32_t blocks, float* sink,
+                          void* stream);
+/* FLOPs of one lfm3_measure_mfma_f16 launch. */
+uint64_t lfm3_measure_mfma_f16_flops(uint32_t iterations, uint32_t blocks);
+
 #ifdef __cplusplus
 }
 #endif

@@ -173,6 +173,9 @@ _SIGS = {
     "lfm3_synth_uniform_u32": (None, [u64, u32, u32, vp, sz]),
     "lfm3_synth_half_normal": (None, [u64, vp, sz]),
     "lfm3_synth_q8": (None, [u64, u32, u32, f32, vp]),
+    "lfm3_measure_stream_read": (i32, [vp, sz, vp, u32, vp]),
+    "lfm3_measure_mfma_f16": (i32, [u32, u32, vp, vp]),
+    "lfm3_measure_mfma_f16_flops": (u64, [u32, u32]),
 }
 
 _lib = None

@@ -265,3 +265,15 @@ def test_continuation_layout_follows_the_state_inventory():
     # A context below the window shrinks the sliding rings to the context.
     small = L.continuation_layout(d, 100)
     assert all(c[4] == 2 * row * 100 for c in small if c[1] == L.PART_SLIDING_WINDOW)
+
+
+def test_measurement_probes_refuse_bad_arguments():
+    """Refused before any launch: no device memory is touched."""
+    lib = L.lib()
+    fake = C.c_void_p(1 << 20)
+    assert lib.lfm3_measure_stream_read(fake, 40, fake, 4, None) == L.E_INVALID  # bytes % 16
+    assert lib.lfm3_measure_stream_read(C.c_void_p((1 << 20) + 4), 64, fake, 4,
+                                        None) == L.E_INVALID                    # alignment
+    assert lib.lfm3_measure_stream_read(fake, 64, fake, 0, None) == L.E_INVALID
+    assert lib.lfm3_measure_mfma_f16(1 << 15, 4, fake, None) == L.E_INVALID       # exactness cap
+    assert lib.lfm3_measure_mfma_f16(0, 4, fake, None) == L.E_INVALID
