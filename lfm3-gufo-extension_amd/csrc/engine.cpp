@@ -210,6 +210,10 @@ struct lfm3_model {
   Buffer table;
   std::unique_ptr<PinnedBuffer> staging;
   std::unique_ptr<PinnedBuffer> logits_host;  // one logits row, pinned
+  // A round's ids and logits rows on their way to the caller (pinned,
+  // made on first use): copied on the model stream behind the round, so
+  // the round and its results take one synchronization.
+  std::unique_ptr<PinnedBuffer> ids_host, rows_host;
   // A sampled round's uniforms and penalty lists (made on first use), and
   // the sampler's workspace (greedy size at load, grown for top-k).
   Buffer sample_table, sample_ws;
@@ -1121,6 +1125,39 @@ void CopyLogits(lfm3_model& m, float* host, const void* device) {
   std::memcpy(host, m.logits_host->p, bytes);
 }
 
+// The round's ids (m.ids) and the sessions' logits rows into pinned
+// staging, on the model stream behind the round's kernels; the caller
+// synchronizes the stream once and then calls DeliverReadback.
+void EnqueueReadback(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
+                     bool ids, bool logits) {
+  if (ids) {
+    if (!m.ids_host)
+      m.ids_host = std::make_unique<PinnedBuffer>(kMaxBatch * 4);
+    Check(hipMemcpyAsync(m.ids_host->p, m.ids.p, std::size_t(n) * 4, hipMemcpyDeviceToHost,
+                         m.stream),
+          "ids copy");
+  }
+  if (logits) {
+    const std::size_t bytes = std::size_t(m.config.vocab) * 4;
+    if (!m.rows_host)
+      m.rows_host = std::make_unique<PinnedBuffer>(kMaxBatch * bytes);
+    for (std::uint32_t i = 0; i < n; ++i)
+      Check(hipMemcpyAsync(static_cast<std::uint8_t*>(m.rows_host->p) + i * bytes,
+                           sessions[i]->logits.p, bytes, hipMemcpyDeviceToHost, m.stream),
+            "logits copy");
+  }
+}
+
+void DeliverReadback(lfm3_model& m, std::uint32_t n, std::uint32_t* ids, float* const* logits) {
+  if (ids)
+    std::memcpy(ids, m.ids_host->p, std::size_t(n) * 4);
+  if (logits) {
+    const std::size_t bytes = std::size_t(m.config.vocab) * 4;
+    for (std::uint32_t i = 0; i < n; ++i)
+      std::memcpy(logits[i], static_cast<const std::uint8_t*>(m.rows_host->p) + i * bytes, bytes);
+  }
+}
+
 PromptBuffers& EnsurePromptBuffers(lfm3_model& m) {
   if (m.prompt)
     return *m.prompt;
@@ -1646,21 +1683,16 @@ int BatchEntry(lfm3_session* const* sessions, std::size_t n,
   }
   lfm3_model& m = *sessions[0]->model;
   try {
-    if (sample) {
-      EnqueueRound(m, sessions, std::uint32_t(n), tokens, false, inputs, head);
+    // The round, the pick, and the copies of its ids and logits rows; one
+    // synchronization for all of them (engine.cpp:1201-1204 syncs, then
+    // copies each logits row synchronously).
+    EnqueueRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr && !sample, inputs, head);
+    if (sample)
       EnqueueSample(m, std::uint32_t(n), *sample);
-      Check(hipStreamSynchronize(m.stream), "round");
-      FinishRound(sessions, std::uint32_t(n), head);
-    } else {
-      RunRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr, inputs, head);
-    }
-    if (logits)
-      for (std::size_t i = 0; i < n; ++i)
-        CopyLogits(m, logits[i], sessions[i]->logits.p);
-    if (ids) {
-      Check(hipMemcpyAsync(ids, m.ids.p, n * 4, hipMemcpyDeviceToHost, m.stream), "ids copy");
-      Check(hipStreamSynchronize(m.stream), "ids copy");
-    }
+    EnqueueReadback(m, sessions, std::uint32_t(n), ids != nullptr, logits != nullptr);
+    Check(hipStreamSynchronize(m.stream), "round");
+    FinishRound(sessions, std::uint32_t(n), head);
+    DeliverReadback(m, std::uint32_t(n), ids, logits);
     return LFM3_OK;
   } catch (const Error& e) {
     for (std::size_t i = 0; i < n; ++i)
@@ -1878,6 +1910,7 @@ int lfm3_scheduler_round(lfm3_session* const* sessions, std::size_t n,
     const bool overlap = n && n_prompt && n_prompt % kPrefillChunk != 1;
     if (n) {
       EnqueueRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr, nullptr, true);
+      EnqueueReadback(m, sessions, std::uint32_t(n), ids != nullptr, logits != nullptr);
       enqueued = true;
       if (!overlap) {
         Check(hipStreamSynchronize(m.stream), "round");
@@ -1904,13 +1937,8 @@ int lfm3_scheduler_round(lfm3_session* const* sessions, std::size_t n,
       FinishRound(sessions, std::uint32_t(n), true);
       enqueued = false;
     }
-    if (n && logits)
-      for (std::size_t i = 0; i < n; ++i)
-        CopyLogits(m, logits[i], sessions[i]->logits.p);
-    if (n && ids) {
-      Check(hipMemcpyAsync(ids, m.ids.p, n * 4, hipMemcpyDeviceToHost, m.stream), "ids copy");
-      Check(hipStreamSynchronize(m.stream), "ids copy");
-    }
+    if (n)
+      DeliverReadback(m, std::uint32_t(n), ids, logits);
     if (status == LFM3_OK && n_prompt && prompt_logits)
       CopyLogits(m, prompt_logits, prompt->logits.p);
   } catch (const std::exception& e) {
