@@ -794,7 +794,7 @@ def main():
     tokens0 = L.uniform_u32(seed, "bench.tokens", SESSIONS, 0, dims.vocab - 1)
     sessions = []
     for sid, c in enumerate(ctx):
-        s = model.session(int(c) + args.warmup + 2 * args.steps + 8)
+        s = model.session(int(c) + 2 * (args.warmup + args.steps) + 8)
         L.inject_synth_state(s, dims, seed, sid, int(c) - 1)
         sessions.append(s)
     log(f"sessions at contexts {ctx.tolist()}")
@@ -833,8 +833,12 @@ def main():
     params = L.Sampling(0.1, 50, 1.1)
     rng = np.random.default_rng(seed)
     recent = np.full((SESSIONS, 64), dims.vocab, np.uint32)  # ids >= vocab pad
+    for k in range(args.warmup):  # untimed, as for the greedy rounds
+        recent[:, k % 64] = toks
+        toks = model.forward_batch_sample(sessions, toks, params,
+                                          rng.random(SESSIONS, dtype=np.float32), recent)
     t0 = time.perf_counter()
-    for k in range(args.steps):
+    for k in range(args.warmup, args.warmup + args.steps):
         recent[:, k % 64] = toks
         toks = model.forward_batch_sample(sessions, toks, params,
                                           rng.random(SESSIONS, dtype=np.float32), recent)

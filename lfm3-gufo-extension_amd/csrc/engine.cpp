@@ -164,6 +164,12 @@ struct RoundTable {
 
 std::size_t Align(std::size_t n) { return (n + 255) / 256 * 256; }
 
+// A sampled round's uploaded inputs: kMaxBatch uniforms, then up to
+// kSampleMaxPenalty penalty ids a row.
+inline std::size_t SampleTableBytes() {
+  return Align(kMaxBatch * 4) + std::size_t(kMaxBatch) * kSampleMaxPenalty * 4;
+}
+
 // Scratch of one prompt chunk (kPrefillChunk rows), made on the first
 // prompt and shared by the model's prompts (calls are serialized).
 struct PromptBuffers {
@@ -496,8 +502,12 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     m->image = Buffer(lfm3_operand_image_bytes(H));
     m->exps = Buffer(kMaxBatch * sizeof(int));
     m->ids = Buffer(B * 4);
-    m->sample_ws_bytes = SampleWorkspaceBytes(kMaxBatch, c.vocab, 1);
+    // The sampler's workspace at its largest top-k (2 MB at vocab 128000)
+    // and its input staging, made here so that no round allocates.
+    m->sample_ws_bytes = SampleWorkspaceBytes(kMaxBatch, c.vocab, kSampleMaxTopK);
     m->sample_ws = Buffer(m->sample_ws_bytes);
+    m->sample_table = Buffer(SampleTableBytes());
+    m->sample_staging = std::make_unique<PinnedBuffer>(SampleTableBytes());
     m->one_row = Buffer(std::size_t(H) * 4);
     Check(hipDeviceSynchronize(), "model upload");
     *out = m.release();
@@ -1630,11 +1640,6 @@ struct SampleArgs {
 // from its session's logits row into m.ids.
 void EnqueueSample(lfm3_model& m, std::uint32_t n, const SampleArgs& a) {
   const std::size_t uni_bytes = Align(kMaxBatch * 4);
-  const std::size_t bytes = uni_bytes + std::size_t(kMaxBatch) * kSampleMaxPenalty * 4;
-  if (!m.sample_staging) {
-    m.sample_table = Buffer(bytes);
-    m.sample_staging = std::make_unique<PinnedBuffer>(bytes);
-  }
   auto* host = static_cast<std::uint8_t*>(m.sample_staging->p);
   if (a.uniforms)
     std::memcpy(host, a.uniforms, n * 4);
