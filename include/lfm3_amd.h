@@ -133,35 +133,55 @@ int lfm3_q8_gemv_swiglu(const void* codes, const void* scales, uint32_t rows,
                         size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------
- * BF16 weights, exact BF16 x FP32 products (the reference precision,
- * README.md:24-27).
+ * Float weights (BF16, F16, F32): exact products with FP32 inputs. BF16 is
+ * the reference precision (README.md:24-27); F16 and F32 are the other
+ * float formats the reference binds (weights.cpp:30-37).
  *
- * GGUF BF16 rows are repacked at load into tiles of 16 rows x 32 columns
- * (1 KB; lane L = 16 g + n holds row n, columns 8g..8g+7), rows padded to
- * 16 and columns to 32 with zeros; the tile offset / stride arguments work
- * as for lfm3_q8_pack_host. The GEMV splits each FP32 input exactly into
- * three BF16 parts (hi + mid + lo) so that every product is exact; sums
- * are FP32 in block order. Any batch (tokens in groups of 16); cols % 32
- * == 0, ldx % 4 == 0, x 16-byte aligned. parts > 1 splits K as
- * lfm3_q8_gemv_partials does (part p at y + p * batch * ldy);
- * lfm3_bf16_gemv_parts gives this library's choice. swiglu: the tiles
- * hold gate/up pairs (tile stride 2), rows is the rows of each, and
- * y = silu(gate) * up (parts must be 1).
+ * `type` is LFM3_TYPE_BF16, LFM3_TYPE_F16 or LFM3_TYPE_F32. GGUF rows are
+ * repacked at load into tiles of 16 rows x 32 columns (lane L = 16 g + n
+ * holds row n, columns 8g..8g+7: one 1 KB plane for the 16-bit formats;
+ * two for F32, columns 8g..8g+3 then 8g+4..8g+7), rows padded to 16 and
+ * columns to 32 with zeros; the tile offset / stride arguments work as for
+ * lfm3_q8_pack_host. The GEMV splits each FP32 input exactly into three
+ * BF16 parts (hi + mid + lo) and each weight into one (BF16), two (F16) or
+ * three (F32) BF16 parts, so that every product is exact on the BF16
+ * matrix cores; sums are FP32 in block order. Any batch (tokens in groups
+ * of 16); cols % 32 == 0, ldx % 4 == 0, x 16-byte aligned. parts > 1
+ * splits K as lfm3_q8_gemv_partials does (part p at y + p * batch * ldy);
+ * lfm3_bf16_gemv_parts gives this library's choice for any float type.
+ * swiglu: the tiles hold gate/up pairs (tile stride 2), rows is the rows
+ * of each, and y = silu(gate) * up (parts must be 1).
  * Replaces: gpu::LaunchExactBf16GEMMFp32SmallBatch (hip/ops.hip:1917-2005),
- * the BF16 branch of gpu::LaunchGEMV (hip/ops.hip:1816-1825) and of
- * gpu::Dense (hip/ops.hip:2243-2244).
+ * F16Dense (hip/ops.hip:876-890), the F32 / F16 / BF16 branches of
+ * gpu::LaunchGEMV (hip/ops.hip:1799-1825) and of gpu::Dense
+ * (hip/ops.hip:2230-2249).
  * ------------------------------------------------------------------- */
+/* 0 for a type that is not a float format. */
+size_t lfm3_float_tiled_bytes(uint32_t type, uint32_t rows, uint32_t cols);
+int lfm3_float_pack_host(uint32_t type, const void* src, uint32_t rows,
+                         uint32_t cols, void* tiles, uint32_t tile_offset,
+                         uint32_t tile_stride);
+uint32_t lfm3_bf16_gemv_parts(uint32_t rows, uint32_t cols, uint32_t batch);
+int lfm3_float_gemv(uint32_t type, const void* tiles, uint32_t rows,
+                    uint32_t cols, const float* x, uint32_t ldx, float* y,
+                    uint32_t ldy, uint32_t batch, uint32_t parts, int swiglu,
+                    void* stream);
+/* out[i] = row tokens[i] of a tiled table as FP32 (vocab rows of cols), or
+   inputs[i] (device FP32 rows) where the device pointer table inputs (may
+   be NULL) has an entry. Ids >= vocab give zero rows.
+   Replaces: gpu::Embedding on an F32, F16 or BF16 table
+   (hip/ops.hip:858-875). */
+int lfm3_float_embed(uint32_t type, const void* tiles, uint32_t vocab,
+                     uint32_t cols, const uint32_t* tokens,
+                     const float* const* inputs, uint32_t n, float* out,
+                     void* stream);
+/* The BF16 forms of the above (type LFM3_TYPE_BF16). */
 size_t lfm3_bf16_tiled_bytes(uint32_t rows, uint32_t cols);
 int lfm3_bf16_pack_host(const void* src, uint32_t rows, uint32_t cols,
                         void* tiles, uint32_t tile_offset, uint32_t tile_stride);
-uint32_t lfm3_bf16_gemv_parts(uint32_t rows, uint32_t cols, uint32_t batch);
 int lfm3_bf16_gemv(const void* tiles, uint32_t rows, uint32_t cols,
                    const float* x, uint32_t ldx, float* y, uint32_t ldy,
                    uint32_t batch, uint32_t parts, int swiglu, void* stream);
-/* out[i] = row tokens[i] of a tiled BF16 table as FP32 (vocab rows of
-   cols), or inputs[i] (device FP32 rows) where the device pointer table
-   inputs (may be NULL) has an entry. Ids >= vocab give zero rows.
-   Replaces: gpu::Embedding on a BF16 table (hip/ops.hip:858-875). */
 int lfm3_bf16_embed(const void* tiles, uint32_t vocab, uint32_t cols,
                     const uint32_t* tokens, const float* const* inputs,
                     uint32_t n, float* out, void* stream);
@@ -529,8 +549,9 @@ int lfm3_prompt_attention(const float* q, uint32_t ldq, const uint16_t* k,
  * ------------------------------------------------------------------- */
 enum { LFM3_LAYER_CONV = 0, LFM3_LAYER_FULL = 1, LFM3_LAYER_SLIDING = 2 };
 /* GGML type ids (core::GgmlType). A model's projection matrices and its
-   embedding are all Q8_0 or all BF16. */
-enum { LFM3_TYPE_F32 = 0, LFM3_TYPE_Q8_0 = 8, LFM3_TYPE_BF16 = 30 };
+   embedding all share one of Q8_0, BF16, F16 or F32 (one engine path per
+   precision); norms, RoPE factors and convolution taps are F32. */
+enum { LFM3_TYPE_F32 = 0, LFM3_TYPE_F16 = 1, LFM3_TYPE_Q8_0 = 8, LFM3_TYPE_BF16 = 30 };
 
 /* config.hpp:9-20. */
 typedef struct {
@@ -544,7 +565,7 @@ typedef struct {
 /* weights.hpp:7-12 tensor view in host memory (GGUF layout). */
 typedef struct {
   const void* data;
-  uint32_t type; /* LFM3_TYPE_F32 / LFM3_TYPE_Q8_0 / LFM3_TYPE_BF16 */
+  uint32_t type; /* LFM3_TYPE_F32 / _F16 / _Q8_0 / _BF16 */
   uint32_t cols, rows;
 } lfm3_tensor;
 

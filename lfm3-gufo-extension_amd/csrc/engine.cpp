@@ -88,13 +88,14 @@ struct PinnedBuffer {
 // A tiled Q8_0 matrix of rows x cols (several sources may share it). The
 // gate/up prompt GEMM reads `halves`, the codes decoded to FP16 tiles,
 // made with the model's prompt scratch.
-// A BF16 matrix (bf16 set) keeps its tiles in `codes` (lfm3_bf16_pack_host
-// layout) and has no scales.
+// A float matrix (BF16, F16 or F32: `exact` set, `type` its format) keeps
+// its tiles in `codes` (lfm3_float_pack_host layout) and has no scales.
 struct Matrix {
   Buffer codes, scales, halves;
   std::uint32_t rows = 0, cols = 0;
   std::uint32_t tiles = 0;  // row tiles stored (gate/up: two per 16 rows)
-  bool bf16 = false;
+  bool exact = false;
+  std::uint32_t type = LFM3_TYPE_Q8_0;
 };
 
 Buffer UploadFloats(const float* host, std::size_t n) {
@@ -114,13 +115,15 @@ Matrix PackMatrix(std::initializer_list<Part> parts, std::uint32_t tiles,
   m.rows = rows;
   m.cols = cols;
   m.tiles = tiles;
-  if (parts.begin()->t->type == LFM3_TYPE_BF16) {
-    m.bf16 = true;
-    const std::size_t bytes = lfm3_bf16_tiled_bytes(tiles * kTileRows, cols);
+  const std::uint32_t type = parts.begin()->t->type;
+  if (type != LFM3_TYPE_Q8_0) {
+    m.exact = true;
+    m.type = type;
+    const std::size_t bytes = lfm3_float_tiled_bytes(type, tiles * kTileRows, cols);
     std::vector<std::uint8_t> host(bytes, 0);
     for (const auto& part : parts)
-      CheckStatus(lfm3_bf16_pack_host(part.t->data, part.t->rows, part.t->cols, host.data(),
-                                      part.tile_offset, part.tile_stride));
+      CheckStatus(lfm3_float_pack_host(type, part.t->data, part.t->rows, part.t->cols,
+                                       host.data(), part.tile_offset, part.tile_stride));
     m.codes = Buffer(bytes, false);
     Check(hipMemcpy(m.codes.p, host.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy");
     return m;
@@ -203,10 +206,11 @@ struct lfm3_model {
   // Round scratch, shared by the model's rounds (calls are serialized, as
   // the Gufo scheduler serializes sessions: engine.cpp:101-113).
   Buffer x, proj, a, hidden, out, gemv_ws, head_keys, ids;
-  // BF16 models (bf16 set): every projection is an exact BF16 x FP32 GEMV
-  // from FP32 normed rows z; the head writes head_out, then the rows go to
-  // the sessions' logits.
-  bool bf16 = false;
+  // Float-weight models (exact set: BF16, F16 or F32 matrices): every
+  // projection is an exact float x FP32 GEMV from FP32 normed rows z; the
+  // head writes head_out, then the rows go to the sessions' logits.
+  bool exact = false;
+  std::uint32_t wtype = LFM3_TYPE_Q8_0;
   Buffer z, head_out;
   std::uint32_t head_groups = 0;
   Buffer image, exps;  // GEMV operand image of the current hidden-wide input
@@ -282,12 +286,13 @@ void CheckTensor(const lfm3_tensor& t, std::uint32_t cols, std::uint32_t rows,
     Invalid(std::string("invalid LFM3 tensor: ") + name);
 }
 
-// The model's matrix type: the embedding's, Q8_0 or BF16; every projection
-// matrix must share it (one engine path per precision).
+// The model's matrix type: the embedding's, one of Q8_0, BF16, F16 and
+// F32 (weights.cpp:30-37); every projection matrix must share it (one
+// engine path per precision).
 std::uint32_t MatrixType(const lfm3_tensor* tensors) {
   const std::uint32_t t = tensors[0].type;
-  if (t != LFM3_TYPE_Q8_0 && t != LFM3_TYPE_BF16)
-    Invalid("invalid LFM3 tensor: token_embd.weight (Q8_0 or BF16)");
+  if (t != LFM3_TYPE_Q8_0 && t != LFM3_TYPE_BF16 && t != LFM3_TYPE_F16 && t != LFM3_TYPE_F32)
+    Invalid("invalid LFM3 tensor: token_embd.weight (Q8_0, BF16, F16 or F32)");
   return t;
 }
 
@@ -379,7 +384,8 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     const std::uint32_t H = c.hidden, F = c.intermediate, D = c.head_dim;
     ValidateTensors(c, tensors);
     const std::uint32_t mt = MatrixType(tensors);
-    m->bf16 = mt == LFM3_TYPE_BF16;
+    m->exact = mt != LFM3_TYPE_Q8_0;
+    m->wtype = mt;
     Check(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "hipStreamCreate");
     Check(hipStreamCreateWithFlags(&m->prompt_stream, hipStreamNonBlocking), "hipStreamCreate");
 
@@ -475,7 +481,7 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     std::size_t out_parts = lfm3_q8_gemv_parts(H, F);
     out_parts = std::max<std::size_t>(out_parts, lfm3_q8_gemv_parts(H, H));
     out_parts = std::max<std::size_t>(out_parts, lfm3_q8_gemv_parts(H, c.heads * D));
-    if (m->bf16) {
+    if (m->exact) {
       out_parts = std::max<std::size_t>(out_parts, lfm3_bf16_gemv_parts(H, F, B));
       out_parts = std::max<std::size_t>(out_parts, lfm3_bf16_gemv_parts(H, H, B));
       out_parts = std::max<std::size_t>(out_parts, lfm3_bf16_gemv_parts(H, c.heads * D, B));
@@ -658,9 +664,9 @@ namespace {
 void HeadRow(lfm3_model& m, const float* row, float* logits, hipStream_t s) {
   const auto& c = m.config;
   const Matrix& head = m.head();
-  if (head.bf16)
-    CheckStatus(lfm3_bf16_gemv(head.codes.p, c.vocab, c.hidden, row, c.hidden, logits, c.vocab,
-                               1, 1, 0, s));
+  if (head.exact)
+    CheckStatus(lfm3_float_gemv(head.type, head.codes.p, c.vocab, c.hidden, row, c.hidden,
+                                logits, c.vocab, 1, 1, 0, s));
   else
     CheckStatus(lfm3_q8_gemv(head.codes.p, head.scales.p, c.vocab, c.hidden, row, c.hidden,
                              logits, c.vocab, 1, nullptr, 0, s));
@@ -937,15 +943,15 @@ void EnqueueRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
   float* out = m.out.as<float>();
   const std::uint32_t pld = std::uint32_t(m.proj_ld);
 
-  if (m.bf16) {
-    // The reference-precision round (every projection an exact BF16 x FP32
-    // GEMV, hip/ops.hip:2230-2244): FP32 normed rows z feed the GEMVs;
-    // narrow outputs split K into parts that the next norm adds.
+  if (m.exact) {
+    // The float-weight round (every projection an exact float x FP32 GEMV,
+    // hip/ops.hip:2230-2249): FP32 normed rows z feed the GEMVs; narrow
+    // outputs split K into parts that the next norm adds.
     float* z = m.z.as<float>();
     const auto bgemv = [&](const Matrix& w, const float* in, std::uint32_t ldx, float* y,
                            std::uint32_t ldy, std::uint32_t parts, bool swiglu) {
-      CheckStatus(lfm3_bf16_gemv(w.codes.p, w.rows, w.cols, in, ldx, y, ldy, n, parts,
-                                 swiglu ? 1 : 0, s));
+      CheckStatus(lfm3_float_gemv(w.type, w.codes.p, w.rows, w.cols, in, ldx, y, ldy, n, parts,
+                                  swiglu ? 1 : 0, s));
     };
     const auto bparts = [&](const Matrix& w, const float* in, std::uint32_t ldx) {
       const std::uint32_t parts = lfm3_bf16_gemv_parts(w.rows, w.cols, n);
@@ -957,8 +963,8 @@ void EnqueueRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
                                            std::size_t(n) * H, parts ? post : nullptr, x, weight,
                                            z, n, H, c.eps, s));
     };
-    CheckStatus(lfm3_bf16_embed(m.embedding.codes.p, c.vocab, H, d_rt->tokens,
-                                inputs ? d_rt->inputs : nullptr, n, x, s));
+    CheckStatus(lfm3_float_embed(m.wtype, m.embedding.codes.p, c.vocab, H, d_rt->tokens,
+                                 inputs ? d_rt->inputs : nullptr, n, x, s));
     norm(0, nullptr, m.layers[0].norm.as<float>());
     for (std::uint32_t il = 0; il < L; ++il) {
       const Layer& l = m.layers[il];
@@ -1218,7 +1224,7 @@ PromptBuffers& EnsurePromptBuffers(lfm3_model& m) {
   // tiles.
   for (auto& l : m.layers) {
     Matrix& w = l.ffn;
-    if (w.bf16)
+    if (w.exact)
       continue;
     const std::uint32_t rows = w.tiles * kTileRows;
     w.halves = Buffer(lfm3_q8_half_tiles_bytes(rows, w.cols), false);
@@ -1300,14 +1306,14 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
     CheckStatus(lfm3_half_rows(in, ldx, rmax, rmax ? max_blocks : 0, a16, lda, scale, rows,
                                cols, s));
   };
-  // BF16 models run every projection through the exact BF16 GEMV over all
-  // rows at once (hip/ops.hip:2230-2244 for BF16 tensors).
-  const std::uint32_t mfma_rows = m.bf16 ? 0xffffffffu : kPromptRows;
+  // Float-weight models run every projection through the exact float GEMV
+  // over all rows at once (hip/ops.hip:2230-2249 for float tensors).
+  const std::uint32_t mfma_rows = m.exact ? 0xffffffffu : kPromptRows;
   const auto gemv = [&](const Matrix& w, const float* in, std::uint32_t ldx, float* y,
                         std::uint32_t ldy, std::uint32_t rows, bool swiglu) {
-    if (w.bf16) {
-      CheckStatus(lfm3_bf16_gemv(w.codes.p, swiglu ? F : w.rows, w.cols, in, ldx, y, ldy, rows,
-                                 1, swiglu ? 1 : 0, s));
+    if (w.exact) {
+      CheckStatus(lfm3_float_gemv(w.type, w.codes.p, swiglu ? F : w.rows, w.cols, in, ldx, y,
+                                  ldy, rows, 1, swiglu ? 1 : 0, s));
       return;
     }
     for (std::uint32_t r = 0; r < rows; r += kMaxBatch) {
@@ -1392,10 +1398,10 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
   {
     std::size_t row = 0, id = 0;
     for (const ChunkPart& part : input) {
-      if (part.tokens && m.bf16) {
-        CheckStatus(lfm3_bf16_embed(m.embedding.codes.p, c.vocab, H,
-                                    b.tokens.as<std::uint32_t>() + id, nullptr, part.count,
-                                    x + row * H, s));
+      if (part.tokens && m.exact) {
+        CheckStatus(lfm3_float_embed(m.wtype, m.embedding.codes.p, c.vocab, H,
+                                     b.tokens.as<std::uint32_t>() + id, nullptr, part.count,
+                                     x + row * H, s));
         id += part.count;
       } else if (part.tokens) {
         CheckStatus(lfm3_embed(m.embedding.codes.p, m.embedding.scales.p, c.vocab, H,

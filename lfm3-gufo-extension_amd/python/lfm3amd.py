@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(PKG_DIR, "liblfm3_amd.so")
 
 OK, E_INVALID, E_HIP, E_STATE, E_NOMEM, E_REFUSED = 0, -1, -2, -3, -4, -5
 LAYER_CONV, LAYER_FULL, LAYER_SLIDING = 0, 1, 2
-TYPE_F32, TYPE_Q8_0, TYPE_BF16 = 0, 8, 30
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_BF16 = 0, 1, 8, 30
 STATE_LOGITS, STATE_FRONTIER, STATE_CONV, STATE_KEY, STATE_VALUE = range(5)
 GLOBAL_TENSORS, LAYER_TENSORS = 4, 17
 MAX_BATCH = 8
@@ -109,6 +109,10 @@ _SIGS = {
     "lfm3_bf16_gemv_parts": (u32, [u32, u32, u32]),
     "lfm3_bf16_gemv": (i32, [vp, u32, u32, vp, u32, vp, u32, u32, u32, i32, vp]),
     "lfm3_bf16_embed": (i32, [vp, u32, u32, vp, vp, u32, vp, vp]),
+    "lfm3_float_tiled_bytes": (sz, [u32, u32, u32]),
+    "lfm3_float_pack_host": (i32, [u32, vp, u32, u32, vp, u32, u32]),
+    "lfm3_float_gemv": (i32, [u32, vp, u32, u32, vp, u32, vp, u32, u32, u32, i32, vp]),
+    "lfm3_float_embed": (i32, [u32, vp, u32, u32, vp, vp, u32, vp, vp]),
     "lfm3_residual_norm": (i32, [vp, vp, vp, vp, vp, u32, u32, f32, vp]),
     "lfm3_embed": (i32, [vp, vp, u32, u32, vp, u32, vp, vp]),
     "lfm3_argmax_workspace_bytes": (sz, [u32]),
@@ -262,6 +266,26 @@ def bf16_to_f32(h: np.ndarray) -> np.ndarray:
     return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def f16(seed: int, name: str, rows: int, cols: int, std=0.0116) -> np.ndarray:
+    """Random F16 matrix (GGUF row-major uint16 bit patterns), N(0, std)
+    rounded to nearest even by numpy."""
+    return normal(seed, name, rows * cols, 0.0, std).astype(np.float16).view(np.uint16)
+
+
+def f32(seed: int, name: str, rows: int, cols: int, std=0.0116) -> np.ndarray:
+    """Random F32 matrix (GGUF row-major), N(0, std)."""
+    return normal(seed, name, rows * cols, 0.0, std).astype(np.float32)
+
+
+def float_to_f32(data: np.ndarray, type_id: int) -> np.ndarray:
+    """FP32 values of a float-format matrix's elements (BF16, F16 or F32)."""
+    if type_id == TYPE_BF16:
+        return bf16_to_f32(data)
+    if type_id == TYPE_F16:
+        return np.asarray(data, np.uint16).view(np.float16).astype(np.float32)
+    return np.asarray(data, np.float32)
+
+
 def q8_dequant(blob: np.ndarray, rows: int, cols: int) -> np.ndarray:
     """float64 d * q of GGUF Q8_0 rows (test helper)."""
     blocks = blob.reshape(rows, cols // 32, 34)
@@ -312,12 +336,15 @@ class Weights:
         return self.globals + [t for layer in self.layers for t in layer]
 
 
-def synth_weights(dims: Dims, seed: int = SEED, masked_rope=True, bf16_weights=False) -> Weights:
+def synth_weights(dims: Dims, seed: int = SEED, masked_rope=True, bf16_weights=False,
+                  weight_type=None) -> Weights:
     """Random-init model of the given dims (GGUF layouts): Q8_0 matrices, or
-    BF16 ones with bf16_weights."""
+    BF16 ones with bf16_weights, or any of TYPE_Q8_0 / TYPE_BF16 / TYPE_F16
+    / TYPE_F32 as weight_type."""
     H, F, D, V = dims.hidden, dims.intermediate, dims.head_dim, dims.vocab
     w = Weights(dims)
-    mat, mtype = (bf16, TYPE_BF16) if bf16_weights else (q8, TYPE_Q8_0)
+    mtype = weight_type if weight_type is not None else TYPE_BF16 if bf16_weights else TYPE_Q8_0
+    mat = {TYPE_Q8_0: q8, TYPE_BF16: bf16, TYPE_F16: f16, TYPE_F32: f32}[mtype]
     factors = np.ones(D // 2, np.float32)
     if masked_rope:
         factors[D // 4:] = 1e30

@@ -102,6 +102,12 @@ def bf16_tensor(h: np.ndarray, rows: int, cols: int) -> Tensor:
     return Tensor(_p(h), BF16, cols, rows)
 
 
+def f16_tensor(h: np.ndarray, rows: int, cols: int) -> Tensor:
+    """GGUF F16 rows (uint16 bit patterns)."""
+    assert h.dtype == np.uint16 and h.size == rows * cols
+    return Tensor(_p(h), F16, cols, rows)
+
+
 def f32_tensor(a: np.ndarray, rows: int, cols: int) -> Tensor:
     assert a.dtype == np.float32
     return Tensor(_p(a), F32, cols, rows)
