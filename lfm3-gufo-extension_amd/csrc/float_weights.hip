@@ -124,17 +124,17 @@ __launch_bounds__(kThreads) __global__
   const int kb0 = p0 + wave * (p1 - p0) / kWaves, kb1 = p0 + (wave + 1) * (p1 - p0) / kWaves;
   const float* xr = x + std::size_t(live ? token : 0) * ldx + 8 * g;
   constexpr int NW = WordsOf(WF), NP = PartsOf(WF);
-  const uint4* w = tiles + (std::size_t(tile0) * nkb) * 64 * NW + lane;
-  bool have[RT];
+  // Tiles past the last one read the last one (unconditional 16-byte
+  // loads); their rows are past out_rows, so their sums are never stored.
+  const uint4* wt[RT];
 #pragma unroll
   for (int r = 0; r < RT; ++r)
-    have[r] = tile0 + r < row_tiles;
+    wt[r] = tiles + (std::size_t(min(tile0 + r, row_tiles - 1)) * nkb) * 64 * NW + lane;
 
   f32x4 acc[3][RT];
 #pragma unroll
   for (int r = 0; r < RT; ++r)
     acc[0][r] = acc[1][r] = acc[2][r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
   const float4 zerof = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   // One block ahead: the next weights and inputs load while this block's
   // MFMAs run.
@@ -144,7 +144,7 @@ __launch_bounds__(kThreads) __global__
     for (int r = 0; r < RT; ++r)
 #pragma unroll
       for (int q = 0; q < NW; ++q)
-        dst[r][q] = have[r] ? w[(std::size_t(r) * nkb + kb) * 64 * NW + 64 * q] : zero4;
+        dst[r][q] = wt[r][std::size_t(kb) * 64 * NW + 64 * q];
   };
   float4 xa = zerof, xb = zerof;
   if (kb0 < kb1) {
