@@ -403,7 +403,8 @@ size_t lfm3_attention_workspace_bytes(uint32_t items, uint32_t rows,
    q holds normed, rotated queries and the ring already holds the current
    K/V row (lfm3_decode_heads_ragged). q/gate/out rows have strides
    ldq/ldg/ldo floats; items and the per-row tables are in device memory.
-   dim 64 or 128; heads % kv_heads == 0 with a group of 2, 4 or 8. One
+   dim 64 or 128; heads % kv_heads == 0 with a group of 2, 4 or 8; each
+   ring (capacity x kv_heads x dim F16) under 2 GiB. One
    launch: the last span block of a split row (counted with an agent-scope
    atomic in the workspace) merges the row's spans in span order, so
    outputs do not depend on scheduling. `items` must be an
@@ -532,7 +533,8 @@ size_t lfm3_prompt_attention_workspace_bytes(uint32_t rows, uint32_t heads,
    q holds normed, rotated queries; q/gate/out rows have strides
    ldq/ldg/ldo floats (multiples of 4, 16-byte aligned rows). F16 Q (with
    the base-2 softmax scale), K, V and probabilities on the matrix cores,
-   FP32 scores, sums and outputs. dim 64 or 128; group 2, 4 or 8.
+   FP32 scores, sums and outputs. dim 64 or 128; group 2, 4 or 8; the
+   chunk (rows) and the ring (capacity) each under 2 GiB of F16 rows.
    Replaces: gpu::Attention with n > 1 (hip/ops.hip:2316-2332: WmmaAttn +
    PromptCombine; engine.cpp:451-466). */
 int lfm3_prompt_attention(const float* q, uint32_t ldq, const uint16_t* k,

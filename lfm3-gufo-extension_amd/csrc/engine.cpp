@@ -276,6 +276,10 @@ void ValidateConfig(const lfm3_config& c) {
         (h && (c.heads % h || (c.heads / h != 2 && c.heads / h != 4 &&
                                c.heads / h != 8))))
       Invalid("invalid LFM3 layer heads/window");
+    // The attention kernels address a layer's F16 K/V ring with 32-bit
+    // buffer offsets: a ring of the full context stays under 2 GiB.
+    if (h && !BufferFits(std::size_t(c.context) * h * c.head_dim * 2))
+      Invalid("LFM3 context too long for its K/V rings");
   }
 }
 

@@ -80,19 +80,6 @@ __device__ __forceinline__ int KeySwizzle(int key) {
     return ((key >> 1) & 1) | (((key >> 3) & 3) << 1);
 }
 
-// The F16 row of key t: the prompt's own keys (t >= position) are chunk
-// rows t - position; older keys sit in ring slot t mod capacity.
-struct KeySource {
-  const Half* chunk;
-  const Half* ring;
-  int position, capacity, stride;
-  __device__ __forceinline__ const Half* Row(int t) const {
-    const bool own = t >= position;
-    const std::size_t slot = own ? std::size_t(t - position) : std::size_t(t % capacity);
-    return (own ? chunk : ring) + slot * stride;
-  }
-};
-
 __device__ __forceinline__ unsigned PackHalves(float a, float b) {
   return unsigned(FloatToHalfBits(a)) | (unsigned(FloatToHalfBits(b)) << 16);
 }
@@ -137,10 +124,6 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
     return;
   const int g = pair / splits, split = pair % splits, q0 = rb * kRows;
   const int stride = kv_heads * D;
-  k += g * D;
-  v += g * D;
-  ck += g * D;
-  cv += g * D;
   // Column tile ct of this wave: columns wave 16 CT + 16 ct + L % 16.
   int row[CT], head[CT];
   bool live[CT];
@@ -196,29 +179,68 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
   const bool wave_live = wave_r0 < n;
   const KeyRange reach{visible(wave_r0).lo, visible(wave_r1).hi};
   const KeyRange whole{visible(wave_r1).lo, visible(wave_r0).hi};
-  const KeySource keys{k, ck, position, capacity, stride};
-  const KeySource values{v, cv, position, capacity, stride};
 
-  // Staging: K segment u of thread tid is (key, seg) = j / kSegs, j % kSegs
-  // with j = tid + kPAThreads u; V job j = tid covers keys 2 (j % 32) and
-  // 2 (j % 32) + 1 of segment j / 32. Keys past the block's last are zero,
-  // so masked probabilities (zero) meet finite V.
+  // Staging jobs of this thread: K job u is (key, segment) = (j / kSegs,
+  // j % kSegs) with j = tid + kPAThreads u; V job i (threads below kVPairs)
+  // is key 2 (tid % 32) + i of segment tid / 32. Keys at or after position
+  // are the prompt's own rows (row t - position), older keys sit in ring
+  // slot t mod capacity. Both are read as buffers: a key past the block's
+  // last, or one that lies in the other source, gets an offset the hardware
+  // drops and reads zeros, without a branch. Tiles are loaded in order, so
+  // each job's ring offset advances by one tile's keys (mod the ring) with
+  // an add and a conditional subtract instead of a division per load.
+  constexpr int kJobs = kKLoads + 2;
+  const unsigned row_bytes = unsigned(stride) * 2;
+  const unsigned ring_bytes = unsigned(capacity) * row_bytes;
+  const BufferResource rk = MakeBuffer(k, unsigned(n) * row_bytes);
+  const BufferResource rv = MakeBuffer(v, unsigned(n) * row_bytes);
+  const BufferResource rck = MakeBuffer(ck, ring_bytes);
+  const BufferResource rcv = MakeBuffer(cv, ring_bytes);
+  int job_key[kJobs];
+  unsigned job_seg[kJobs], job_ring[kJobs];
+#pragma unroll
+  for (int u = 0; u < kKLoads; ++u) {
+    const int j = tid + kPAThreads * u;
+    job_key[u] = j / kSegs;
+    job_seg[u] = unsigned(g * D + (j % kSegs) * 8) * 2;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    job_key[kKLoads + i] = 2 * (tid % 32) + i;
+    job_seg[kKLoads + i] = unsigned(g * D + (tid / 32 % kSegs) * 8) * 2;
+  }
+#pragma unroll
+  for (int u = 0; u < kJobs; ++u)
+    job_ring[u] = unsigned((walk.lo + job_key[u]) % capacity) * row_bytes + job_seg[u];
+  const unsigned ring_step = unsigned(kPAKeys % capacity) * row_bytes;
   uint4 kr[kKLoads], vr[2];
   const auto load = [&](int base) {
+    const int last = walk.hi - base, own = position - base;  // key offsets in the tile
+    const bool from_ring = own > 0, mixed = own > 0 && own < kPAKeys;
+    const BufferResource src_k = from_ring ? rck : rk;
+    const BufferResource src_v = from_ring ? rcv : rv;
+    const unsigned chunk0 = unsigned(base - position) * row_bytes;
+    uint4 r[kJobs];
 #pragma unroll
-    for (int u = 0; u < kKLoads; ++u) {
-      const int j = tid + kPAThreads * u, t = base + j / kSegs;
-      kr[u] = t <= walk.hi ? *reinterpret_cast<const uint4*>(keys.Row(t) + (j % kSegs) * 8)
-                           : make_uint4(0, 0, 0, 0);
+    for (int u = 0; u < kJobs; ++u) {
+      const int key = job_key[u];
+      const unsigned chunk = chunk0 + unsigned(key) * row_bytes + job_seg[u];
+      const bool live = (u < kKLoads || tid < kVPairs) && key <= last, ring = key < own;
+      const unsigned off = !live ? kOutOfRange : from_ring ? (ring ? job_ring[u] : kOutOfRange)
+                                                           : chunk;
+      r[u] = LoadB128(u < kKLoads ? src_k : src_v, off);
+      if (mixed) {
+        const uint4 c = LoadB128(u < kKLoads ? rk : rv, live && !ring ? chunk : kOutOfRange);
+        r[u] = make_uint4(r[u].x | c.x, r[u].y | c.y, r[u].z | c.z, r[u].w | c.w);
+      }
+      job_ring[u] += ring_step;
+      job_ring[u] -= job_ring[u] >= ring_bytes ? ring_bytes : 0u;
     }
-    if (tid < kVPairs) {
-      const int seg = tid / 32, t = base + 2 * (tid % 32);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        vr[i] = t + i <= walk.hi
-                    ? *reinterpret_cast<const uint4*>(values.Row(t + i) + seg * 8)
-                    : make_uint4(0, 0, 0, 0);
-    }
+    for (int u = 0; u < kKLoads; ++u)
+      kr[u] = r[u];
+    vr[0] = r[kKLoads];
+    vr[1] = r[kKLoads + 1];
   };
   const auto store = [&](int st) {
 #pragma unroll
@@ -302,22 +324,24 @@ __launch_bounds__(kPAThreads) __global__ void PromptAttentionKernel(
       const float shift = next == -INFINITY ? 0.0f : next;
       const float alpha = __builtin_amdgcn_exp2f(maximum[ct] - shift);
       maximum[ct] = next;
-      // Probabilities round to F16 once; the sum adds the rounded values.
+      // Probabilities round to F16 once (two a v_cvt_pk_f16_f32); the sum
+      // adds the rounded values, two a v_dot2 against (1, 1), whose
+      // products are exact, in two chains.
+      const h2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
       unsigned pw[4][2];
-      float local = 0.0f;
+      float local[2] = {0.0f, 0.0f};
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const _Float16 a =
-              static_cast<_Float16>(__builtin_amdgcn_exp2f(s[ct][kb][2 * j] - shift));
-          const _Float16 b =
-              static_cast<_Float16>(__builtin_amdgcn_exp2f(s[ct][kb][2 * j + 1] - shift));
-          local += float(a) + float(b);
-          pw[kb][j] = unsigned(__builtin_bit_cast(Half, a)) |
-                      (unsigned(__builtin_bit_cast(Half, b)) << 16);
+          typedef float f2 __attribute__((ext_vector_type(2)));
+          const f2 e = {__builtin_amdgcn_exp2f(s[ct][kb][2 * j] - shift),
+                        __builtin_amdgcn_exp2f(s[ct][kb][2 * j + 1] - shift)};
+          const h2 ph = __builtin_convertvector(e, h2);
+          local[j] = __builtin_amdgcn_fdot2(ph, ones, local[j], false);
+          pw[kb][j] = __builtin_bit_cast(unsigned, ph);
         }
-      sum[ct] = sum[ct] * alpha + local;
+      sum[ct] = sum[ct] * alpha + (local[0] + local[1]);
       // exp2(0) is exactly 1: when no lane's maximum moved, the rescale of
       // the accumulators is skipped for the whole wave.
       if (__ballot(alpha != 1.0f)) {
@@ -540,7 +564,9 @@ int lfm3_prompt_attention(const float* q, std::uint32_t ldq, const std::uint16_t
       ldq < heads * dim || ldo < heads * dim || ldg < heads || ldq % 4 || ldo % 4 ||
       (position && (!cache_k || !cache_v || !capacity)) ||
       (!window && position && capacity < position) ||
-      std::uint64_t(position) + rows > (1ull << 31))
+      std::uint64_t(position) + rows > (1ull << 31) ||
+      !BufferFits(std::size_t(rows) * kv_heads * dim * 2) ||
+      !BufferFits(std::size_t(capacity) * kv_heads * dim * 2))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt attention shape");
   PromptArgs a{};
   a.splits = PlanCall(int(rows), int(position), int(window), int(group), int(kv_heads), a.span);

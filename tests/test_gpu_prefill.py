@@ -270,6 +270,33 @@ def test_prompt_attention_reference_vectors(n, window, P, H, KH):
         assert np.array_equal(dck.download(np.uint16, cap * stride).reshape(cap, stride), ring_k)
 
 
+@pytest.mark.parametrize("n,window,P,cap,D", [(9, 256, 37, 46, 128), (8, 0, 40, 50, 128),
+                                               (5, 256, 30, 35, 64), (33, 0, 20, 60, 128),
+                                               (70, 256, 100, 171, 64), (40, 256, 300, 340, 128)])
+def test_prompt_attention_short_rings(n, window, P, cap, D):
+    """Sessions whose context is below the window (or a tile) keep rings of
+    fewer than 64 slots or of an odd size: ring slots t % cap past a tile's
+    worth of keys, tiles straddling the first chunk key, against the FP64
+    formula at 1e-3."""
+    H, KH = 16, 4
+    stride = KH * D
+    tag = f"{n}.{window}.{P}.{cap}.{D}"
+    q = L.normal(SEED, f"pring.q.{tag}", n * H * D).reshape(n, H * D)
+    gates = L.normal(SEED, f"pring.g.{tag}", n * H).reshape(n, H)
+    kbits = L.half_normal(SEED, f"pring.k.{tag}", n * stride)
+    vbits = L.half_normal(SEED, f"pring.v.{tag}", n * stride)
+    ckbits = L.half_normal(SEED, f"pring.ck.{tag}", cap * stride)
+    cvbits = L.half_normal(SEED, f"pring.cv.{tag}", cap * stride)
+    print(f"[prompt attention] short ring {tag}", flush=True)
+    out, _ = run_prompt_attention(q, gates, kbits, vbits, ckbits, cvbits, n, H, KH, D, P, cap,
+                                  window)
+    want = prompt_attention_fp64(q, gates, O.half_to_float(kbits), O.half_to_float(vbits),
+                                 O.half_to_float(ckbits), O.half_to_float(cvbits), n, H, KH, D,
+                                 P, cap, window)
+    assert np.all(np.isfinite(out))
+    assert np.max(np.abs(out - want)) < 1e-3
+
+
 @pytest.mark.parametrize("window", [0, 256])
 @pytest.mark.parametrize("P", [0, 700])
 def test_prompt_attention_baseline_heads_dim64(window, P):
