@@ -199,6 +199,23 @@ def test_prompt_attention_rejects_bad_shapes():
     # a split history without its workspace
     assert lib.lfm3_prompt_attention(1, 512, 1, 1, 1, 4, 1, 1, 1, 512, 40, 4, 2, 128, 17000,
                                      17040, 0, None, 0, None) == L.E_INVALID
+    # a ring of 2 GiB (2^21 slots x 4 KV heads x 128 dims x 2 bytes): the
+    # kernel addresses rings with 32-bit buffer offsets
+    assert lib.lfm3_prompt_attention(1, 2048, 1, 1, 1, 16, 1, 1, 1, 2048, 40, 16, 4, 128, 100,
+                                     1 << 21, 256, None, 0, None) == L.E_INVALID
+    assert b"prompt attention" in lib.lfm3_last_error()
+
+
+def test_model_load_refuses_rings_past_2gib():
+    """A context whose full K/V ring of one layer reaches 2 GiB is refused
+    before any device work."""
+    dims = L.Dims(hidden=128, intermediate=192, vocab=300, context=64, heads=4, head_dim=64,
+                  kv_heads=2, window=8, pattern="CSG")
+    w = L.synth_weights(dims, seed=1)
+    huge = L.Dims(**{**dims.__dict__, "context": 1 << 23})  # 2^23 x 2 x 64 x 2 B = 2 GiB
+    with pytest.raises(L.LFM3Error) as e:
+        L.Model(L.Weights(huge, w.globals, w.layers))
+    assert e.value.status == L.E_INVALID and "context" in str(e.value)
 
 
 def test_projection_conv_rejects_bad_shapes():
