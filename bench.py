@@ -154,7 +154,7 @@ def gemv_roofline(batch: int, copies: int, passes: int):
 
 
 def bf16_gemv_roofline(batch: int, copies: int, passes: int):
-    """The exact BF16 GEMV at config 1's shape (W 8192 x 2048 BF16, `batch`
+    """The exact BF16 GEMV at the single-GEMV shape (W 8192 x 2048 BF16, `batch`
     FP32 rows) over `copies` rotated weight buffers (32 MB each, past the
     MALL), replayed from a HIP graph."""
     M, K = 8192, 2048
@@ -540,7 +540,7 @@ def roofline_only():
     """The roofline kernels and the copy calibration, nothing else: the
     program that rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE run (the
     decode round's kernels at their round shapes, the attention at the
-    bench's contexts included, config 1's GEMV at 8 rows, the prompt
+    bench's contexts included, the 8192 x 2048 GEMV at 8 rows, the prompt
     pass's SwiGLU GEMM)."""
     copy_bytes = 256 << 20
     copy_calibration(copy_bytes, 4)
@@ -661,7 +661,7 @@ def cpu_model() -> str:
 def cpu_baseline(dims, weights, ctx, tokens, seed):
     """The CPU oracle (a scalar FP32 restatement of reference.cpp) decoding
     the same eight sessions from the same synthesized state, each session's
-    greedy id fed back as its next token, in three modes (BASELINE.md plan):
+    greedy id fed back as its next token, in three modes:
 
       faithful      one round, sessions one after another on one thread
                     (reference.cpp has no threads);
@@ -853,7 +853,7 @@ def main():
     for k in kernels:
         log(f"{k['kernel']}: {k['us']:.2f} us, {k['GBps']:.0f} GB/s ({100 * k['frac']:.1f}%), "
             f"x{k['per_round']} a round")
-    # Config 1: the Q8_0 GEMV W 8192 x 2048 on FP32 rows, B = 1, 2, 4, 8.
+    # The single Q8_0 GEMV, W 8192 x 2048 on FP32 rows, B = 1, 2, 4, 8.
     sweep = [gemv_roofline(b, args.gemv_copies, 8) for b in (1, 2, 4, 8)]
     for g in sweep:
         log(f"gemv B={g['batch']}: {g['us']:.2f} us/launch, "
@@ -910,8 +910,8 @@ def main():
             "ms": round(sampled_ms, 4),
             "tok_s": round(SESSIONS / (sampled_ms * 1e-3), 1),
         },
-        "config1_gemv": {
-            "kernel": "Q8_0 skinny GEMV, W 8192 x 2048 on FP32 rows (BASELINE config 1)",
+        "gemv_8192x2048": {
+            "kernel": "Q8_0 skinny GEMV, W 8192 x 2048 on FP32 rows (single-GEMV workload)",
             "sweep": [{"batch": g["batch"], "us": round(g["us"], 3), "bytes": g["bytes"],
                        "GBps": round(g["bytes"] / (g["us"] * 1e-6) / 1e9, 1),
                        "frac": round(g["bytes"] / (g["us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}

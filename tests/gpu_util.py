@@ -56,7 +56,7 @@ def gemv(m: DeviceMatrix, x: np.ndarray, swiglu=False, ldy=None):
 
 
 def within(got, want, rtol=1e-3, atol=1e-4):
-    """BASELINE gate: |got - want| <= atol + rtol |want| elementwise."""
+    """FP32 parity gate: |got - want| <= atol + rtol |want| elementwise."""
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     bad = np.abs(got - want) > atol + rtol * np.abs(want)

@@ -1,7 +1,7 @@
-"""BASELINE configs 4 and 5 at their own sizes on the GPU, against the CPU
-oracle (reference.cpp restated).
+"""The full-dims decode round and the mixed round's depths at their own
+sizes on the GPU, against the CPU oracle (reference.cpp restated).
 
-Config 4: the full 24-layer model at the reference checkpoint's dims (13
+The decode round: the full 24-layer model at the reference checkpoint's dims (13
 conv, 5 sliding-256, 6 global; hidden 2048, FFN 7680, 16q/4kv x 128, vocab
 128000, random-init Q8_0) with 8 sessions at the benchmark's contexts,
 uniform in [128, 8192]: one ForwardBatch round. Logits within 2e-3 of the
@@ -9,7 +9,7 @@ oracle, the same greedy id wherever the oracle's top-2 margin exceeds 4e-3
 (session_test.cpp:268-272 gates a batch against serial sessions the same
 way).
 
-Config 5 at depth: decode attention of 7 rows at contexts uniform in
+The mixed round's depths: decode attention of 7 rows at contexts uniform in
 [16384, 32768] (sliding and global), the 512-row prompt attention at depth
 24576 (16/4 heads x 128, sliding and global) against an FP64 softmax over
 the F16-rounded keys at 1e-3 (ops_test.cpp:203), and a full-dims
@@ -53,7 +53,7 @@ def inject_both(g, o, dims, seed, sid, position):
     o.set_position(position)
 
 
-def test_config4_full_dims_eight_sessions():
+def test_full_dims_round_eight_sessions():
     ctx = L.uniform_u32(SEED, "bench.ctx", 8, 128, 8192)
     dims = L.Dims(context=8192 + 64)
     w = L.synth_weights(dims, seed=SEED)

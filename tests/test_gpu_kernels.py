@@ -3,7 +3,7 @@ the same seeded inputs, through the C-ABI.
 
 Gates: the reference's own (ops_test.cpp: projection 1e-4 vs FP64, conv
 1e-7 with exact history, decode attention 2e-6 vs FP64) where its vectors
-apply, and the BASELINE gates elsewhere (1e-3 relative / 1e-4 absolute for
+apply, and the FP32 parity gates elsewhere (1e-3 relative / 1e-4 absolute for
 FP32 GEMV and attention outputs; bit-exact for indexing, ring slots and
 greedy ids)."""
 import zlib

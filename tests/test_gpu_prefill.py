@@ -300,7 +300,7 @@ def test_prompt_attention_short_rings(n, window, P, cap, D):
 @pytest.mark.parametrize("window", [0, 256])
 @pytest.mark.parametrize("P", [0, 700])
 def test_prompt_attention_baseline_heads_dim64(window, P):
-    """The BASELINE nominal heads (32 query / 8 KV x 64) on random inputs,
+    """The nominal LFM3-1.7B heads (32 query / 8 KV x 64) on random inputs,
     against the FP64 formula and, row by row, the oracle's FP32 attention
     read over the same keys (reference.cpp:117-144), both within the
     prompt gate of 1e-3."""
