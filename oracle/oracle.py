@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (liboracle.so): TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's CPU baseline use this
-module, as the checker; the product never imports it.
+module, to compare the library's results with; the product never imports it.
 """
 from __future__ import annotations
 

@@ -1,5 +1,5 @@
 """Helpers shared by the GPU parity tests (device buffers, packing, state
-injection). The oracle is the checker; the library does the work."""
+injection). The oracle gives the expected results; the library does the work."""
 import ctypes as C
 
 import numpy as np
