@@ -294,3 +294,18 @@ def test_measurement_probes_refuse_bad_arguments():
     assert lib.lfm3_measure_stream_read(fake, 64, fake, 0, None) == L.E_INVALID
     assert lib.lfm3_measure_mfma_f16(1 << 15, 4, fake, None) == L.E_INVALID       # exactness cap
     assert lib.lfm3_measure_mfma_f16(0, 4, fake, None) == L.E_INVALID
+
+def test_batch_entries_refuse_empty_and_oversized_batches():
+    """engine.cpp:1178-1180: an empty batch or one past kMaxBatch (8) is an
+    invalid shape, refused before any device work, by every batch entry."""
+    lib = L.lib()
+    toks = (C.c_uint32 * 9)()
+    ids = (C.c_uint32 * 9)()
+    sessions = (C.c_void_p * 9)()
+    for n in (0, 9):
+        assert lib.lfm3_forward_batch(sessions, n, toks, None) == L.E_INVALID
+        assert b"decode batch shape" in lib.lfm3_last_error()
+        assert lib.lfm3_forward_batch_greedy(sessions, n, toks, ids) == L.E_INVALID
+    # null session pointers are refused too
+    assert lib.lfm3_forward_batch_greedy(sessions, 2, toks, ids) == L.E_INVALID
+    assert b"null" in lib.lfm3_last_error()

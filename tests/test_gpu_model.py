@@ -116,6 +116,21 @@ def test_invalid_batches_are_refused_without_mutation():
     assert a.position == 1 and b.position == 1
 
 
+def test_batch_of_two_models_is_refused():
+    """engine.cpp:1188-1192: every session of a batch must belong to the
+    front session's model; a mixed batch is refused and nothing moves."""
+    dims = small_dims()
+    g1 = L.Model(L.synth_weights(dims, seed=31))
+    g2 = L.Model(L.synth_weights(dims, seed=32))
+    a, b = g1.session(16), g2.session(16)
+    with pytest.raises(L.LFM3Error) as e:
+        g1.forward_batch([a, b], np.array([1, 2], np.uint32))
+    assert e.value.status == L.E_INVALID and "incompatible" in str(e.value)
+    assert a.position == 0 and b.position == 0
+    g1.forward_batch([a], np.array([1], np.uint32))
+    assert a.position == 1
+
+
 def test_sliding_ring_wraps_across_rounds():
     """Ten rounds past a 32-slot ring: logits keep matching the oracle."""
     dims = small_dims(pattern="SCS")
