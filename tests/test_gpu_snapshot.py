@@ -113,6 +113,42 @@ def test_intermediate_and_empty_snapshots(model):
     b.close()
 
 
+def test_reset_reproduces_exact_logits(model):
+    """session_test.cpp:145-147: after a reset the same prompt gives the
+    same logits bit for bit, and so does the decode row that follows."""
+    d, m = model
+    a = m.session(1024)
+    toks = tokens(300, "reset")
+    first = a.forward(toks[:290])
+    step = m.forward_batch([a], toks[290:291])
+    a.reset()
+    assert a.position == 0
+    assert np.array_equal(a.forward(toks[:290]), first)
+    assert np.array_equal(m.forward_batch([a], toks[290:291]), step)
+    a.close()
+
+
+def test_batch_lane_snapshot_restores_its_row(model):
+    """session_test.cpp:274-283: the snapshot of a batch lane, restored into
+    a fresh session, serves exactly the logits row the batch returned, and
+    both continue identically."""
+    d, m = model
+    lanes = [m.session(1024) for _ in range(3)]
+    for i, s in enumerate(lanes):
+        s.forward(tokens(20 + 7 * i, f"lane{i}"), want_logits=False)
+    rows = m.forward_batch(lanes, tokens(3, "batchrow"))
+    saved = lanes[1].save_snapshot()
+    control = m.session(1024)
+    control.restore_snapshot(saved)
+    assert control.position == lanes[1].position
+    assert np.array_equal(control.read_logits(), rows[1])
+    nxt = tokens(2, "after")
+    assert np.array_equal(m.forward_batch([control], nxt[:1]),
+                          m.forward_batch([lanes[1]], nxt[:1]))
+    for s in lanes + [control]:
+        s.close()
+
+
 def test_snapshot_of_another_configuration_is_refused(model):
     d, m = model
     other_dims = dims(theta_swa=2e4)             # same sizes, another signature
