@@ -73,16 +73,21 @@ __device__ __forceinline__ unsigned OrderedBits(float v) {
 
 __device__ __forceinline__ float Penalized(float l, float p) { return l > 0.0f ? l / p : l * p; }
 
-// Exclusive prefix over the block of one flag per thread, in thread order;
+// Exclusive prefix over the block of one count per thread, in thread order;
 // returns the thread's offset and writes the block total.
 template<int kThreads>
-__device__ __forceinline__ unsigned BlockPrefix(bool flag, unsigned* s_wave, unsigned* total) {
+__device__ __forceinline__ unsigned BlockScan(unsigned count, unsigned* s_wave, unsigned* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const unsigned long long m = __ballot(flag);
-  const unsigned below = __popcll(m & ((1ull << lane) - 1ull));
+  unsigned incl = count;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const unsigned v = __shfl_up(incl, off, 64);
+    if (lane >= off)
+      incl += v;
+  }
   __syncthreads();
-  if (lane == 0)
-    s_wave[wave] = __popcll(m);
+  if (lane == 63)
+    s_wave[wave] = incl;
   __syncthreads();
   unsigned before = 0, all = 0;
   for (int w = 0; w < kThreads / 64; ++w) {
@@ -91,8 +96,13 @@ __device__ __forceinline__ unsigned BlockPrefix(bool flag, unsigned* s_wave, uns
     all += c;
   }
   *total = all;
-  return before + below;
+  return before + incl - count;
 }
+
+// Counts packed for one scan: keys above the k-th (fewer than k <= 1024)
+// in bits 20 and up, keys equal to it (at most 2^17) below.
+constexpr int kUpShift = 20;
+constexpr unsigned kEqMask = (1u << kUpShift) - 1u;
 
 // Radix select over n keys key(i): the key of the k-th largest and how many
 // keys equal to it are kept (the rest of the k are above it). Four passes
@@ -202,7 +212,7 @@ struct SliceArgs {
 
 // One slice of one row (blockIdx.x, blockIdx.y).
 __launch_bounds__(kSliceThreads) __global__ void SliceKernel(SliceArgs a) {
-  __shared__ float s_v[kSliceLen];
+  __shared__ __attribute__((aligned(16))) float s_v[kSliceLen];
   __shared__ unsigned s_bits[kSliceLen / 32];
   __shared__ unsigned s_hist[256];
   __shared__ unsigned s_sel[2];
@@ -276,24 +286,47 @@ __launch_bounds__(kSliceThreads) __global__ void SliceKernel(SliceArgs a) {
   unsigned kth, ties;
   SelectKth<kSliceThreads>(len, unsigned(k), [&](int i) { return OrderedBits(s_v[i]); },
                            s_hist, s_sel, kth, ties);
-  unsigned above = 0, equal = 0;
-  for (int base = 0; base < len; base += kSliceThreads) {
-    const int i = base + tid;
-    const unsigned key = i < len ? OrderedBits(s_v[i]) : 0u;
-    const bool up = i < len && key > kth, eq = i < len && key == kth;
-    unsigned n_up, n_eq;
-    const unsigned au = BlockPrefix<kSliceThreads>(up, s_wave, &n_up);
-    if (up) {
-      out_v[above + au] = s_v[i];
-      out_i[above + au] = unsigned(begin + i);
+  // Thread t owns the kOwn consecutive elements from kOwn t: it counts its
+  // keys above the k-th and equal to it, one block scan of the packed
+  // counts gives its output offsets, and it writes its winners in index
+  // order (the lowest-index ties first).
+  constexpr int kOwn = kSliceLen / kSliceThreads;
+  float vals[kOwn];
+#pragma unroll
+  for (int q = 0; q < kOwn / 4; ++q) {
+    const float4 f = *reinterpret_cast<const float4*>(&s_v[tid * kOwn + 4 * q]);
+    vals[4 * q] = f.x;
+    vals[4 * q + 1] = f.y;
+    vals[4 * q + 2] = f.z;
+    vals[4 * q + 3] = f.w;
+  }
+  unsigned counts = 0;
+#pragma unroll
+  for (int j = 0; j < kOwn; ++j) {
+    const unsigned key = OrderedBits(vals[j]);
+    const bool live = tid * kOwn + j < len;
+    counts += live && key > kth ? (1u << kUpShift) : live && key == kth ? 1u : 0u;
+  }
+  unsigned total;
+  const unsigned at = BlockScan<kSliceThreads>(counts, s_wave, &total);
+  unsigned up = at >> kUpShift, eq = at & kEqMask;
+#pragma unroll
+  for (int j = 0; j < kOwn; ++j) {
+    const int i = tid * kOwn + j;
+    const unsigned key = OrderedBits(vals[j]);
+    if (i >= len)
+      continue;
+    if (key > kth) {
+      out_v[up] = vals[j];
+      out_i[up] = unsigned(begin + i);
+      ++up;
+    } else if (key == kth) {
+      if (eq < ties) {
+        out_v[unsigned(k) - ties + eq] = vals[j];
+        out_i[unsigned(k) - ties + eq] = unsigned(begin + i);
+      }
+      ++eq;
     }
-    const unsigned ae = BlockPrefix<kSliceThreads>(eq, s_wave, &n_eq);
-    if (eq && equal + ae < ties) {
-      out_v[unsigned(k) - ties + equal + ae] = s_v[i];
-      out_i[unsigned(k) - ties + equal + ae] = unsigned(begin + i);
-    }
-    above += n_up;
-    equal += n_eq;
   }
 }
 
@@ -443,67 +476,122 @@ __launch_bounds__(kPickThreads) __global__ void PickKernel(PickArgs a) {
                     std::size_t(row) * a.slices * k;
   const unsigned* ci = reinterpret_cast<const unsigned*>(a.ws + a.layout.indices) +
                        std::size_t(row) * a.slices * k;
+  // The candidates' keys are read from the workspace once into LDS when
+  // they fit, so the select's passes and the compaction read LDS.
+  constexpr int kStagedKeys = 8192;
+  __shared__ unsigned s_cand[kStagedKeys];
+  const bool staged = n <= kStagedKeys;
+  if (staged) {
+    for (int i = tid; i < n; i += kPickThreads)
+      s_cand[i] = OrderedBits(cv[i]);
+    __syncthreads();
+  }
+  const auto key_of = [&](int i) { return staged ? s_cand[i] : OrderedBits(cv[i]); };
   unsigned kth, ties;
-  SelectKth<kPickThreads>(n, unsigned(k), [&](int i) { return OrderedBits(cv[i]); }, s_hist,
-                          s_sel, kth, ties);
-  unsigned above = 0, equal = 0;
-  for (int base = 0; base < n; base += kPickThreads) {
-    const int i = base + tid;
-    const float v = i < n ? cv[i] : 0.0f;
-    const unsigned key = i < n ? OrderedBits(v) : 0u;
-    const bool up = i < n && key > kth, eq = i < n && key == kth;
-    unsigned n_up, n_eq;
-    const unsigned au = BlockPrefix<kPickThreads>(up, s_wave, &n_up);
-    if (up) {
-      s_val[above + au] = v;
-      s_idx[above + au] = ci[i];
+  SelectKth<kPickThreads>(n, unsigned(k), key_of, s_hist, s_sel, kth, ties);
+  // Thread t owns `per` consecutive candidates (the slices' candidates in
+  // slice order, so in global index order where keys tie): counts, one
+  // block scan, then the winners in order.
+  const int per = (n + kPickThreads - 1) / kPickThreads, i0 = tid * per;
+  unsigned counts = 0;
+  for (int j = 0; j < per; ++j) {
+    const int i = i0 + j;
+    if (i < n) {
+      const unsigned key = key_of(i);
+      counts += key > kth ? (1u << kUpShift) : key == kth ? 1u : 0u;
     }
-    const unsigned ae = BlockPrefix<kPickThreads>(eq, s_wave, &n_eq);
-    if (eq && equal + ae < ties) {
-      s_val[unsigned(k) - ties + equal + ae] = v;
-      s_idx[unsigned(k) - ties + equal + ae] = ci[i];
+  }
+  unsigned total;
+  const unsigned at = BlockScan<kPickThreads>(counts, s_wave, &total);
+  unsigned up = at >> kUpShift, eq = at & kEqMask;
+  for (int j = 0; j < per; ++j) {
+    const int i = i0 + j;
+    if (i >= n)
+      break;
+    const unsigned key = key_of(i);
+    if (key > kth) {
+      s_val[up] = cv[i];
+      s_idx[up] = ci[i];
+      ++up;
+    } else if (key == kth) {
+      if (eq < ties) {
+        s_val[unsigned(k) - ties + eq] = cv[i];
+        s_idx[unsigned(k) - ties + eq] = ci[i];
+      }
+      ++eq;
     }
-    above += n_up;
-    equal += n_eq;
   }
   __syncthreads();
-  // Bitonic sort of the k winners: value descending, index ascending.
+  // Bitonic sort of the k winners: value descending, index ascending. Up to
+  // 64 winners sort in one wave's registers (lane p holds position p;
+  // exchanges by lane shuffles, no barriers); more sort in LDS.
   int size = 1;
   while (size < k)
     size <<= 1;
-  for (int i = k + tid; i < size; i += kPickThreads) {
-    s_val[i] = -INFINITY;
-    s_idx[i] = kPadIndex;
-  }
-  __syncthreads();
-  const auto first = [&](int p, int q) {
-    return s_val[p] > s_val[q] || (s_val[p] == s_val[q] && s_idx[p] < s_idx[q]);
-  };
-  for (int len = 2; len <= size; len <<= 1)
-    for (int stride = len >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < size; i += kPickThreads) {
-        const int j = i ^ stride;
-        if (j > i && ((i & len) == 0 ? first(j, i) : first(i, j))) {
-          const float tv = s_val[i];
-          s_val[i] = s_val[j];
-          s_val[j] = tv;
-          const unsigned ti = s_idx[i];
-          s_idx[i] = s_idx[j];
-          s_idx[j] = ti;
+  if (size <= 64) {
+    if (tid < 64) {
+      float v = tid < k ? s_val[tid] : -INFINITY;
+      unsigned ix = tid < k ? s_idx[tid] : kPadIndex;
+      for (int len = 2; len <= 64; len <<= 1)
+        for (int stride = len >> 1; stride > 0; stride >>= 1) {
+          const float ov = __shfl_xor(v, stride, 64);
+          const unsigned oi = unsigned(__shfl_xor(int(ix), stride, 64));
+          // The lower lane of a pair keeps the first of the two in an
+          // ascending run ((p & len) == 0), the upper lane in a descending one.
+          const bool wants_first = ((tid & stride) == 0) == ((tid & len) == 0);
+          const bool mine_first = v > ov || (v == ov && ix < oi);
+          if (wants_first != mine_first) {
+            v = ov;
+            ix = oi;
+          }
         }
+      if (tid < k) {
+        s_val[tid] = v;
+        s_idx[tid] = ix;
       }
-      __syncthreads();
     }
+    __syncthreads();
+  } else {
+    for (int i = k + tid; i < size; i += kPickThreads) {
+      s_val[i] = -INFINITY;
+      s_idx[i] = kPadIndex;
+    }
+    __syncthreads();
+    const auto first = [&](int p, int q) {
+      return s_val[p] > s_val[q] || (s_val[p] == s_val[q] && s_idx[p] < s_idx[q]);
+    };
+    for (int len = 2; len <= size; len <<= 1)
+      for (int stride = len >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < size; i += kPickThreads) {
+          const int j = i ^ stride;
+          if (j > i && ((i & len) == 0 ? first(j, i) : first(i, j))) {
+            const float tv = s_val[i];
+            s_val[i] = s_val[j];
+            s_val[j] = tv;
+            const unsigned ti = s_idx[i];
+            s_idx[i] = s_idx[j];
+            s_idx[j] = ti;
+          }
+        }
+        __syncthreads();
+      }
+  }
+  // The weights in parallel (the sorted maximum first), then the running
+  // sums in candidate order on one thread.
+  __shared__ float s_w[kSampleMaxTopK];
+  const float top = s_val[0];
+  for (int i = tid; i < k; i += kPickThreads)
+    s_w[i] = expf((s_val[i] - top) * a.inv_t);
+  __syncthreads();
   if (tid == 0) {
-    const float top = s_val[0];
     float total = 0.0f;
     for (int i = 0; i < k; ++i)
-      total += expf((s_val[i] - top) * a.inv_t);
+      total += s_w[i];
     const float target = u * total;
     float run = 0.0f;
     int pick = 0;
     for (int i = 0; i < k; ++i) {
-      const float w = expf((s_val[i] - top) * a.inv_t);
+      const float w = s_w[i];
       if (w > 0.0f)
         pick = i;  // the last candidate with weight, should the sums round
       run += w;
