@@ -205,7 +205,7 @@ struct lfm3_model {
   hipStream_t prompt_stream = nullptr;
   // Round scratch, shared by the model's rounds (calls are serialized, as
   // the Gufo scheduler serializes sessions: engine.cpp:101-113).
-  Buffer x, proj, a, hidden, out, gemv_ws, head_keys, ids;
+  Buffer x, proj, a, hidden, out, gemv_ws, head_keys;
   // Float-weight models (exact set: BF16, F16 or F32 matrices): every
   // projection is an exact float x FP32 GEMV from FP32 normed rows z; the
   // head writes head_out, then the rows go to the sessions' logits.
@@ -220,10 +220,13 @@ struct lfm3_model {
   Buffer table;
   std::unique_ptr<PinnedBuffer> staging;
   std::unique_ptr<PinnedBuffer> logits_host;  // one logits row, pinned
-  // A round's ids and logits rows on their way to the caller (pinned,
-  // made on first use): copied on the model stream behind the round, so
-  // the round and its results take one synchronization.
+  // A round's ids, written by its last kernel (the argmax or the sampler's
+  // pick) straight into pinned host memory the device addresses, and the
+  // logits rows on their way to the caller (pinned, made on first use,
+  // copied on the model stream behind the round): the round and its
+  // results take one synchronization and no copy for the ids.
   std::unique_ptr<PinnedBuffer> ids_host, rows_host;
+  std::uint32_t* ids() const { return static_cast<std::uint32_t*>(ids_host->p); }
   // A sampled round's uniforms and penalty lists (made on first use), and
   // the sampler's workspace (greedy size at load, grown for top-k).
   Buffer sample_table, sample_ws;
@@ -511,7 +514,7 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     m->head_keys = Buffer(std::size_t(B) * m->head_groups * sizeof(unsigned long long));
     m->image = Buffer(lfm3_operand_image_bytes(H));
     m->exps = Buffer(kMaxBatch * sizeof(int));
-    m->ids = Buffer(B * 4);
+    m->ids_host = std::make_unique<PinnedBuffer>(std::size_t(B) * 4);
     // The sampler's workspace at its largest top-k (2 MB at vocab 128000)
     // and its input staging, made here so that no round allocates.
     m->sample_ws_bytes = SampleWorkspaceBytes(kMaxBatch, c.vocab, kSampleMaxTopK);
@@ -1014,7 +1017,7 @@ void EnqueueRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
       if (greedy) {
         lfm3_sampling pick{0.0f, 1, 1.0f};
         CheckStatus(LaunchSample(logits, c.vocab, nullptr, n, c.vocab, pick, nullptr, 0,
-                                 nullptr, m.ids.as<std::uint32_t>(), m.sample_ws.p,
+                                 nullptr, m.ids(), m.sample_ws.p,
                                  m.sample_ws_bytes, s));
       }
     }
@@ -1113,7 +1116,7 @@ void EnqueueRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
     CheckStatus(LaunchHeadGemv(w.codes.p, w.scales.p, w.rows, w.cols, image, exps, n,
                                d_rt->logits, keys, nullptr, s));
     if (greedy)
-      CheckStatus(LaunchArgmaxKeys(keys, n, m.head_groups, m.ids.as<std::uint32_t>(), s));
+      CheckStatus(LaunchArgmaxKeys(keys, n, m.head_groups, m.ids(), s));
   }
   Check(hipGetLastError(), "round launch");
 }
@@ -1145,18 +1148,13 @@ void CopyLogits(lfm3_model& m, float* host, const void* device) {
   std::memcpy(host, m.logits_host->p, bytes);
 }
 
-// The round's ids (m.ids) and the sessions' logits rows into pinned
-// staging, on the model stream behind the round's kernels; the caller
-// synchronizes the stream once and then calls DeliverReadback.
+// The sessions' logits rows into pinned staging, on the model stream
+// behind the round's kernels (the round's ids are already written to
+// pinned memory by its last kernel); the caller synchronizes the stream
+// once and then calls DeliverReadback.
 void EnqueueReadback(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
                      bool ids, bool logits) {
-  if (ids) {
-    if (!m.ids_host)
-      m.ids_host = std::make_unique<PinnedBuffer>(kMaxBatch * 4);
-    Check(hipMemcpyAsync(m.ids_host->p, m.ids.p, std::size_t(n) * 4, hipMemcpyDeviceToHost,
-                         m.stream),
-          "ids copy");
-  }
+  (void)ids;  // the ids are already in pinned memory when the stream drains
   if (logits) {
     const std::size_t bytes = std::size_t(m.config.vocab) * 4;
     if (!m.rows_host)
@@ -1647,7 +1645,7 @@ struct SampleArgs {
 };
 
 // Uploads the sampler's inputs on the model stream and picks each row's id
-// from its session's logits row into m.ids.
+// from its session's logits row into the pinned ids (m.ids()).
 void EnqueueSample(lfm3_model& m, std::uint32_t n, const SampleArgs& a) {
   const std::size_t uni_bytes = Align(kMaxBatch * 4);
   auto* host = static_cast<std::uint8_t*>(m.sample_staging->p);
@@ -1670,7 +1668,7 @@ void EnqueueSample(lfm3_model& m, std::uint32_t n, const SampleArgs& a) {
                            a.n_penalty ? reinterpret_cast<const std::uint32_t*>(dev + uni_bytes)
                                        : nullptr,
                            a.n_penalty, a.uniforms ? reinterpret_cast<const float*>(dev) : nullptr,
-                           m.ids.as<std::uint32_t>(), m.sample_ws.p, m.sample_ws_bytes,
+                           m.ids(), m.sample_ws.p, m.sample_ws_bytes,
                            m.stream));
 }
 
