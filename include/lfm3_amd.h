@@ -548,6 +548,15 @@ int lfm3_prompt_attention(const float* q, uint32_t ldq, const uint16_t* k,
 
 /* ---------------------------------------------------------------------
  * Engine: Model / Session (engine.hpp:17-163).
+ *
+ * Threading: a model's sessions share its two streams and its round and
+ * prompt scratch (the reference gives each session its own stream and
+ * workspaces, engine.cpp:47-54, 180-190). Every engine call that uses
+ * them takes the model's lock, so calls on sessions of one model may come
+ * from several host threads and run one at a time, each with the results
+ * it has alone. Continuation hooks run before the lock is taken and may
+ * call back into the library. One session must not be used by two calls
+ * at once (as in the reference, sessions are not thread-safe).
  * ------------------------------------------------------------------- */
 enum { LFM3_LAYER_CONV = 0, LFM3_LAYER_FULL = 1, LFM3_LAYER_SLIDING = 2 };
 /* GGML type ids (core::GgmlType). A model's projection matrices and its
@@ -656,8 +665,9 @@ int lfm3_forward_batch_sample(lfm3_session* const* sessions, size_t n,
    hidden floats that stands in for session i's token embedding (tokens[i]
    is then not checked); NULL entries use the token. With want_logits 0 the
    vocabulary head is skipped: only the positions and the frontier rows
-   (LFM3_STATE_FRONTIER, Session::DeviceHidden) advance, and
-   lfm3_session_read_logits refuses until a round with logits. With
+   (LFM3_STATE_FRONTIER, Session::DeviceHidden) advance, and the head runs
+   on the frontier row when logits are first wanted
+   (lfm3_session_prepare_logits, lfm3_session_read_logits). With
    want_logits set, logits (may be NULL) receive host copies. A device
    failure poisons every session of the batch. */
 int lfm3_forward_batch_inputs(lfm3_session* const* sessions, size_t n,
@@ -668,6 +678,15 @@ int lfm3_forward_batch_inputs(lfm3_session* const* sessions, size_t n,
    or prompt without logits, the vocabulary head first runs on the
    frontier row (Session::Impl::EnsureLogits, engine.cpp:237-245). */
 int lfm3_session_read_logits(const lfm3_session* session, float* logits);
+/* Session::PrepareLogits (engine.hpp:146, engine.cpp:1369-1373): after a
+   round or prompt that skipped the vocabulary head, runs the head on the
+   frontier row on the model stream and waits for it, so the device logits
+   row (LFM3_STATE_LOGITS) holds the frontier's logits; nothing is copied
+   to the host, and logits already current cost nothing. Refuses a
+   poisoned session or one at position 0. The continuation adapter calls
+   it before it captures the logits component
+   (continuation_adapter.cpp:369-370). */
+int lfm3_session_prepare_logits(lfm3_session* session);
 /* Snapshot v2 (Session::SnapshotBytes / SaveSnapshot / RestoreSnapshot,
    engine.cpp:1387-1574), byte-compatible with the reference's: a 32-byte
    header of little-endian words (0x334d464c, 2, context, position, hidden,

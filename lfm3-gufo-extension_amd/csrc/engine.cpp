@@ -15,6 +15,7 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -76,8 +77,13 @@ struct Buffer {
 };
 
 struct PinnedBuffer {
-  void* p = nullptr;
-  explicit PinnedBuffer(std::size_t n) { Check(hipHostMalloc(&p, n, 0), "hipHostMalloc"); }
+  void* p = nullptr;       // host address
+  void* device = nullptr;  // the address kernels use (mapped buffers)
+  explicit PinnedBuffer(std::size_t n, unsigned flags = hipHostMallocDefault) {
+    Check(hipHostMalloc(&p, n, flags), "hipHostMalloc");
+    if (flags & hipHostMallocMapped)
+      Check(hipHostGetDevicePointer(&device, p, 0), "hipHostGetDevicePointer");
+  }
   ~PinnedBuffer() {
     if (p)
       (void)hipHostFree(p);
@@ -174,7 +180,7 @@ inline std::size_t SampleTableBytes() {
 }
 
 // Scratch of one prompt chunk (kPrefillChunk rows), made on the first
-// prompt and shared by the model's prompts (calls are serialized).
+// prompt and shared by the model's prompts (under the model's lock).
 struct PromptBuffers {
   Buffer tokens, x, z, a16, scale, proj, mix, hid, out, row_max, chunk_k, chunk_v, attn_ws;
   Buffer one_table;  // one decode-attention row: ring pointers, capacity, position, items
@@ -203,8 +209,14 @@ struct lfm3_model {
   // The stream a scheduler round's prompt pass runs on, beside the decode
   // round on `stream` (both default priority).
   hipStream_t prompt_stream = nullptr;
-  // Round scratch, shared by the model's rounds (calls are serialized, as
-  // the Gufo scheduler serializes sessions: engine.cpp:101-113).
+  // Serializes every call that uses the model's streams or scratch, so
+  // calls on sessions of one model may come from several host threads;
+  // they run one at a time. (The reference gives each session its own
+  // stream and workspaces, engine.cpp:47-54, 180-190; here the round and
+  // prompt scratch are the model's.) Continuation hooks run before the
+  // lock is taken, so a hook may call back into the library.
+  std::mutex lock;
+  // Round scratch, shared by the model's rounds (under `lock`).
   Buffer x, proj, a, hidden, out, gemv_ws, head_keys;
   // Float-weight models (exact set: BF16, F16 or F32 matrices): every
   // projection is an exact float x FP32 GEMV from FP32 normed rows z; the
@@ -226,7 +238,9 @@ struct lfm3_model {
   // copied on the model stream behind the round): the round and its
   // results take one synchronization and no copy for the ids.
   std::unique_ptr<PinnedBuffer> ids_host, rows_host;
-  std::uint32_t* ids() const { return static_cast<std::uint32_t*>(ids_host->p); }
+  // The device's address of the ids. They are written by a kernel and read
+  // on the host only after the model stream is synchronized (DeliverReadback).
+  std::uint32_t* ids() const { return static_cast<std::uint32_t*>(ids_host->device); }
   // A sampled round's uniforms and penalty lists (made on first use), and
   // the sampler's workspace (greedy size at load, grown for top-k).
   Buffer sample_table, sample_ws;
@@ -514,7 +528,11 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     m->head_keys = Buffer(std::size_t(B) * m->head_groups * sizeof(unsigned long long));
     m->image = Buffer(lfm3_operand_image_bytes(H));
     m->exps = Buffer(kMaxBatch * sizeof(int));
-    m->ids_host = std::make_unique<PinnedBuffer>(std::size_t(B) * 4);
+    // Mapped and coherent (fine-grained): the last kernel's stores reach
+    // host memory without a cache flush; the host reads them after the
+    // stream synchronization that ends the round.
+    m->ids_host = std::make_unique<PinnedBuffer>(std::size_t(B) * 4,
+                                                 hipHostMallocMapped | hipHostMallocCoherent);
     // The sampler's workspace at its largest top-k (2 MB at vocab 128000)
     // and its input staging, made here so that no round allocates.
     m->sample_ws_bytes = SampleWorkspaceBytes(kMaxBatch, c.vocab, kSampleMaxTopK);
@@ -566,6 +584,7 @@ int lfm3_session_create(lfm3_model* m, std::uint32_t context, lfm3_session** out
     }
     s->logits = Buffer(std::size_t(c.vocab) * 4);
     s->frontier = Buffer(std::size_t(c.hidden) * 4);
+    std::lock_guard<std::mutex> guard(m->lock);
     EnsureRoundBuffers(*m, context);
     *out = s.release();
     return LFM3_OK;
@@ -597,6 +616,7 @@ int lfm3_session_reset(lfm3_session* s) {
     return Fail(LFM3_E_REFUSED, "LFM3 continuation hook refused the reset");
   const auto& c = s->model->config;
   const hipStream_t stream = s->model->stream;
+  std::lock_guard<std::mutex> guard(s->model->lock);
   int e = HipStatus(hipStreamSynchronize(stream), "reset");
   for (auto& st : s->states)
     if (!e && st.conv.p)
@@ -644,6 +664,7 @@ int lfm3_session_state(lfm3_session* s, int kind, std::uint32_t layer,
 int lfm3_session_begin_restore(lfm3_session* s) {
   if (!s)
     return Fail(LFM3_E_INVALID, "null session");
+  std::lock_guard<std::mutex> guard(s->model->lock);
   const int e = HipStatus(hipStreamSynchronize(s->model->stream), "begin restore");
   if (e)
     return e;
@@ -759,6 +780,7 @@ int lfm3_session_read_logits(const lfm3_session* s, float* logits) {
   // frontier row has no logits.
   if (s->poisoned || !s->position)
     return Fail(LFM3_E_INVALID, "invalid LFM3 logit frontier");
+  std::lock_guard<std::mutex> guard(s->model->lock);
   try {
     EnsureLogits(const_cast<lfm3_session&>(*s));
   } catch (const Error& e) {
@@ -773,6 +795,26 @@ int lfm3_session_read_logits(const lfm3_session* s, float* logits) {
   return e;
 }
 
+// Session::PrepareLogits (engine.hpp:146, engine.cpp:1369-1373): after a
+// round or prompt that skipped the vocabulary head, the head runs on the
+// frontier row on the model stream, so the device logits row
+// (LFM3_STATE_LOGITS) holds the frontier's logits; nothing is copied to
+// the host. The continuation adapter calls it before it captures the
+// logits component (continuation_adapter.cpp:369-370).
+int lfm3_session_prepare_logits(lfm3_session* s) {
+  if (!s)
+    return Fail(LFM3_E_INVALID, "null session");
+  if (s->poisoned || !s->position)
+    return Fail(LFM3_E_INVALID, "invalid LFM3 logit frontier");
+  std::lock_guard<std::mutex> guard(s->model->lock);
+  try {
+    EnsureLogits(*s);
+  } catch (const Error& e) {
+    return Fail(e.status, e.what());
+  }
+  return LFM3_OK;
+}
+
 std::size_t lfm3_session_snapshot_bytes(const lfm3_session* s) {
   return s ? StateBytes(s->model->config, s->position) : 0;
 }
@@ -784,6 +826,7 @@ int lfm3_session_save_snapshot(lfm3_session* s, void* out, std::size_t bytes) {
     return Fail(LFM3_E_STATE, "cannot snapshot a poisoned LFM3 session");
   const auto& c = s->model->config;
   auto* p = static_cast<std::uint8_t*>(out);
+  std::lock_guard<std::mutex> guard(s->model->lock);
   try {
     if (s->position)
       EnsureLogits(*s);
@@ -844,6 +887,7 @@ int lfm3_session_restore_snapshot(lfm3_session* s, const void* data, std::size_t
   const std::uint32_t position = GetWord(p, 3);
   std::size_t offset = kSnapshotHeaderBytes;
   const hipStream_t stream = s->model->stream;
+  std::lock_guard<std::mutex> guard(s->model->lock);
   try {
     Check(hipStreamSynchronize(stream), "restore");
     const auto copy = [&](void* destination, std::size_t size) {
@@ -1153,8 +1197,7 @@ void CopyLogits(lfm3_model& m, float* host, const void* device) {
 // pinned memory by its last kernel); the caller synchronizes the stream
 // once and then calls DeliverReadback.
 void EnqueueReadback(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
-                     bool ids, bool logits) {
-  (void)ids;  // the ids are already in pinned memory when the stream drains
+                     bool logits) {
   if (logits) {
     const std::size_t bytes = std::size_t(m.config.vocab) * 4;
     if (!m.rows_host)
@@ -1166,6 +1209,9 @@ void EnqueueReadback(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t
   }
 }
 
+// Call only after the model stream has been synchronized: the ids are
+// written by the round's last kernel, the logits rows by copies on the
+// stream.
 void DeliverReadback(lfm3_model& m, std::uint32_t n, std::uint32_t* ids, float* const* logits) {
   if (ids)
     std::memcpy(ids, m.ids_host->p, std::size_t(n) * 4);
@@ -1604,6 +1650,7 @@ void BeforeWrite(lfm3_session& se, std::size_t n) {
 int ForwardEntry(lfm3_session* se, const std::vector<ChunkPart>& runs, std::size_t n,
                  float* logits) {
   lfm3_model& m = *se->model;
+  std::lock_guard<std::mutex> guard(m.lock);
   try {
     ForwardRuns(*se, runs, n, logits != nullptr);
     if (logits)
@@ -1695,6 +1742,7 @@ int BatchEntry(lfm3_session* const* sessions, std::size_t n,
     return Fail(e.status, e.what());
   }
   lfm3_model& m = *sessions[0]->model;
+  std::lock_guard<std::mutex> guard(m.lock);
   try {
     // The round, the pick, and the copies of its ids and logits rows; one
     // synchronization for all of them (engine.cpp:1201-1204 syncs, then
@@ -1702,7 +1750,7 @@ int BatchEntry(lfm3_session* const* sessions, std::size_t n,
     EnqueueRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr && !sample, inputs, head);
     if (sample)
       EnqueueSample(m, std::uint32_t(n), *sample);
-    EnqueueReadback(m, sessions, std::uint32_t(n), ids != nullptr, logits != nullptr);
+    EnqueueReadback(m, sessions, std::uint32_t(n), logits != nullptr);
     Check(hipStreamSynchronize(m.stream), "round");
     FinishRound(sessions, std::uint32_t(n), head);
     DeliverReadback(m, std::uint32_t(n), ids, logits);
@@ -1908,6 +1956,7 @@ int lfm3_scheduler_round(lfm3_session* const* sessions, std::size_t n,
     return Fail(e.status, e.what());
   }
   lfm3_model& m = *model;
+  std::lock_guard<std::mutex> guard(m.lock);
   const auto poison_batch = [&] {
     for (std::size_t i = 0; i < n; ++i)
       sessions[i]->poisoned = true;
@@ -1923,7 +1972,7 @@ int lfm3_scheduler_round(lfm3_session* const* sessions, std::size_t n,
     const bool overlap = n && n_prompt && n_prompt % kPrefillChunk != 1;
     if (n) {
       EnqueueRound(m, sessions, std::uint32_t(n), tokens, ids != nullptr, nullptr, true);
-      EnqueueReadback(m, sessions, std::uint32_t(n), ids != nullptr, logits != nullptr);
+      EnqueueReadback(m, sessions, std::uint32_t(n), logits != nullptr);
       enqueued = true;
       if (!overlap) {
         Check(hipStreamSynchronize(m.stream), "round");
@@ -1976,6 +2025,7 @@ int lfm3_session_read_hidden(const lfm3_session* se, float* hidden) {
     return Fail(LFM3_E_INVALID, "null hidden row");
   if (se->poisoned || !se->position)
     return Fail(LFM3_E_INVALID, "invalid LFM3 hidden frontier");
+  std::lock_guard<std::mutex> guard(se->model->lock);
   const hipStream_t stream = se->model->stream;
   int e = HipStatus(hipMemcpyAsync(hidden, se->frontier.p, std::size_t(se->model->config.hidden) * 4,
                                    hipMemcpyDeviceToHost, stream),

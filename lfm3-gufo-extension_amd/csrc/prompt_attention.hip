@@ -564,6 +564,9 @@ int lfm3_prompt_attention(const float* q, std::uint32_t ldq, const std::uint16_t
       ldq < heads * dim || ldo < heads * dim || ldg < heads || ldq % 4 || ldo % 4 ||
       (position && (!cache_k || !cache_v || !capacity)) ||
       (!window && position && capacity < position) ||
+      // A sliding row at `position` reads the ring's last min(window - 1,
+      // position) keys; a shorter ring would have overwritten some of them.
+      (window && position && capacity < std::min(window - 1, position)) ||
       std::uint64_t(position) + rows > (1ull << 31) ||
       !BufferFits(std::size_t(rows) * kv_heads * dim * 2) ||
       !BufferFits(std::size_t(capacity) * kv_heads * dim * 2))

@@ -169,6 +169,7 @@ _SIGS = {
     "lfm3_forward_batch_sample": (i32, [vp, sz, vp, vp, vp, u32, vp, vp]),
     "lfm3_forward_batch_inputs": (i32, [vp, sz, vp, vp, i32, vp]),
     "lfm3_session_read_logits": (i32, [vp, vp]),
+    "lfm3_session_prepare_logits": (i32, [vp]),
     "lfm3_session_snapshot_bytes": (sz, [vp]),
     "lfm3_session_save_snapshot": (i32, [vp, vp, sz]),
     "lfm3_session_restore_snapshot": (i32, [vp, vp, sz]),
@@ -561,6 +562,11 @@ class Session:
         out = np.empty(self.model.dims.vocab, np.float32)
         check(lib().lfm3_session_read_logits(self.handle, ptr(out)))
         return out
+
+    def prepare_logits(self):
+        """Session::PrepareLogits: the head on the frontier row, into the
+        device logits row (no host copy)."""
+        check(lib().lfm3_session_prepare_logits(self.handle))
 
     def read_hidden(self) -> np.ndarray:
         out = np.empty(self.model.dims.hidden, np.float32)

@@ -144,6 +144,63 @@ bool DecodeRow(const orc_tensor& t, uint32_t row, float* out) {
   return false;
 }
 
+bool Decodable(const orc_tensor& t) {
+  return t.type == ORC_F32 || t.type == ORC_F16 || t.type == ORC_BF16 ||
+         (t.type == ORC_Q8_0 && t.cols % 32 == 0);
+}
+
+// reference.cpp:9-19 over n input rows at once: each weight row is decoded
+// once and dotted with every input row. Every output is still its own
+// sequential sum over k in the reference's order (sum += w[k] * x[k], no
+// contraction), so each row's result is bit-identical to Mat on that row;
+// only the loop order across independent sums differs. Tiles of 16 weight
+// rows x 64 input rows keep the operands in cache; the inputs are
+// transposed so the inner loop runs across input rows (vectorizable).
+bool MatRows(const orc_tensor& t, const float* x, uint32_t n, float* y) {
+  if (!Decodable(t))
+    return false;
+  constexpr uint32_t kRows = 16, kCols = 64;
+  const size_t K = t.cols;
+  const uint32_t col_blocks = (n + kCols - 1) / kCols;
+  std::vector<float> xt(K * size_t(col_blocks) * kCols, 0.0F);
+  // xt[block][k][j] = x[block * 64 + j][k]
+  for (uint32_t i = 0; i < n; ++i)
+    for (size_t k = 0; k < K; ++k)
+      xt[(size_t(i / kCols) * K + k) * kCols + i % kCols] = x[size_t(i) * K + k];
+  const size_t row_blocks = (t.rows + kRows - 1) / kRows;
+  Split(row_blocks, [&](size_t b0, size_t b1) {
+    std::vector<float> rows(kRows * K);
+    for (size_t b = b0; b < b1; ++b) {
+      const uint32_t r0 = uint32_t(b * kRows);
+      const uint32_t nr = std::min<uint32_t>(kRows, t.rows - r0);
+      std::fill(rows.begin(), rows.end(), 0.0F);
+      for (uint32_t rr = 0; rr < nr; ++rr)
+        DecodeRow(t, r0 + rr, rows.data() + rr * K);
+      for (uint32_t cb = 0; cb < col_blocks; ++cb) {
+        const float* xb = xt.data() + size_t(cb) * K * kCols;
+        const uint32_t nc = std::min<uint32_t>(kCols, n - cb * kCols);
+        for (uint32_t rr0 = 0; rr0 < nr; rr0 += 4) {
+          // 4 weight rows x 64 input rows of sums, held in registers.
+          float acc[4][kCols] = {};
+          const float* w0 = rows.data() + rr0 * K;
+          for (size_t k = 0; k < K; ++k) {
+            const float* xk = xb + k * kCols;
+            for (uint32_t q = 0; q < 4; ++q) {
+              const float w = w0[q * K + k];
+              for (uint32_t j = 0; j < kCols; ++j)
+                acc[q][j] += w * xk[j];
+            }
+          }
+          for (uint32_t q = 0; q < 4 && rr0 + q < nr; ++q)
+            for (uint32_t j = 0; j < nc; ++j)
+              y[size_t(cb * kCols + j) * t.rows + r0 + rr0 + q] = acc[q][j];
+        }
+      }
+    }
+  });
+  return true;
+}
+
 // reference.cpp:9-19.
 bool Mat(const orc_tensor& t, const float* x, float* y) {
   if (t.type != ORC_F32 && t.type != ORC_F16 && t.type != ORC_BF16 &&
@@ -215,34 +272,160 @@ void AttentionRead(const float* q, const float* gate, const float* ck,
   const size_t stride = size_t(kv_heads) * D;
   const uint32_t first =
       window && position + 1 > window ? position + 1 - window : 0;
+  // Every score is its own sequential sum over d, and every output element
+  // its own sequential sum over t, exactly as in the reference's loops; the
+  // loops are only nested so the inner one runs across independent sums
+  // (16 keys, or the D output elements), which the compiler vectorizes.
+  const uint32_t count = position + 1 - first;
   Split(heads, [&](size_t h0, size_t h1) {
-    std::vector<float> scores(position + 1 - first);
+    std::vector<float> scores(count), sums(D);
+    constexpr uint32_t kKeys = 16;
     for (uint32_t h = uint32_t(h0); h < h1; ++h) {
       const uint32_t kh = h / (heads / kv_heads);
-      float max = -std::numeric_limits<float>::infinity();
-      for (uint32_t t = first; t <= position; ++t) {
-        float score = 0;
+      const float* qh = q + size_t(h) * D;
+      for (uint32_t t0 = 0; t0 < count; t0 += kKeys) {
+        const uint32_t m = std::min(kKeys, count - t0);
+        const float* rows[kKeys];
+        float acc[kKeys];
+        for (uint32_t j = 0; j < m; ++j) {
+          rows[j] = ck + size_t((first + t0 + j) % capacity) * stride + kh * D;
+          acc[j] = 0;
+        }
         for (uint32_t d = 0; d < D; ++d)
-          score += q[h * D + d] * ck[(t % capacity) * stride + kh * D + d];
-        scores[t - first] = score / std::sqrt(float(D));
-        max = std::max(max, scores[t - first]);
+          for (uint32_t j = 0; j < m; ++j)
+            acc[j] += qh[d] * rows[j][d];
+        for (uint32_t j = 0; j < m; ++j)
+          scores[t0 + j] = acc[j] / std::sqrt(float(D));
       }
+      float max = -std::numeric_limits<float>::infinity();
+      for (uint32_t t = 0; t < count; ++t)
+        max = std::max(max, scores[t]);
       float den = 0;
       for (auto& score : scores) {
         score = std::exp(score - max);
         den += score;
       }
-      for (uint32_t d = 0; d < D; ++d) {
-        float sum = 0;
-        for (uint32_t t = first; t <= position; ++t)
-          sum += (scores[t - first] / den) *
-                 cv[(t % capacity) * stride + kh * D + d];
-        out[h * D + d] = sum / (1 + std::exp(-gate[h]));
+      std::fill(sums.begin(), sums.end(), 0.0F);
+      for (uint32_t t = 0; t < count; ++t) {
+        const float p = scores[t] / den;
+        const float* vt = cv + size_t((first + t) % capacity) * stride + kh * D;
+        for (uint32_t d = 0; d < D; ++d)
+          sums[d] += p * vt[d];
       }
+      for (uint32_t d = 0; d < D; ++d)
+        out[h * D + d] = sums[d] / (1 + std::exp(-gate[h]));
     }
   });
 }
 
+
+// The reference's prompt-path attention read (hip/ops.hip:1355-1561
+// WmmaAttn for n > 1 rows): q scaled by log2(e) / sqrt(D) in FP32 and
+// rounded to F16; scores are sums of the F16 query times the F16 keys in
+// base-2 units; probabilities exp2(s - max) rounded to F16, their sum and
+// the weighted values taken over the rounded probabilities; out =
+// (sum_t p_t v_t / sum_t p_t) / (1 + e^-gate). (The kernel rounds each
+// probability against the running maximum of its 64-key tile walk; this
+// restatement uses the row's final maximum, which moves a probability by at
+// most its rounding.) Keys as AttentionRead's.
+void AttentionReadPrompt(const float* q, const float* gate, const float* ck,
+                         const float* cv, uint32_t heads, uint32_t kv_heads,
+                         uint32_t D, uint32_t position, uint32_t capacity,
+                         uint32_t window, float* out) {
+  const size_t stride = size_t(kv_heads) * D;
+  const uint32_t first =
+      window && position + 1 > window ? position + 1 - window : 0;
+  const uint32_t count = position + 1 - first;
+  const float scale = (1.0F / std::sqrt(float(D))) * 1.44269504088896341F;
+  Split(heads, [&](size_t h0, size_t h1) {
+    std::vector<float> scores(count), sums(D), qs(D);
+    constexpr uint32_t kKeys = 16;
+    for (uint32_t h = uint32_t(h0); h < h1; ++h) {
+      const uint32_t kh = h / (heads / kv_heads);
+      for (uint32_t d = 0; d < D; ++d)
+        qs[d] = HalfToFloat(FloatToHalf(q[size_t(h) * D + d] * scale));
+      for (uint32_t t0 = 0; t0 < count; t0 += kKeys) {
+        const uint32_t m = std::min(kKeys, count - t0);
+        const float* rows[kKeys];
+        float acc[kKeys];
+        for (uint32_t j = 0; j < m; ++j) {
+          rows[j] = ck + size_t((first + t0 + j) % capacity) * stride + kh * D;
+          acc[j] = 0;
+        }
+        for (uint32_t d = 0; d < D; ++d)
+          for (uint32_t j = 0; j < m; ++j)
+            acc[j] += qs[d] * rows[j][d];
+        for (uint32_t j = 0; j < m; ++j)
+          scores[t0 + j] = acc[j];
+      }
+      float max = -std::numeric_limits<float>::infinity();
+      for (uint32_t t = 0; t < count; ++t)
+        max = std::max(max, scores[t]);
+      float den = 0;
+      for (auto& score : scores) {
+        score = HalfToFloat(FloatToHalf(std::exp2(score - max)));
+        den += score;
+      }
+      std::fill(sums.begin(), sums.end(), 0.0F);
+      for (uint32_t t = 0; t < count; ++t) {
+        const float p = scores[t];
+        const float* vt = cv + size_t((first + t) % capacity) * stride + kh * D;
+        for (uint32_t d = 0; d < D; ++d)
+          sums[d] += p * vt[d];
+      }
+      for (uint32_t d = 0; d < D; ++d)
+        out[h * D + d] = (sums[d] / den) / (1 + std::exp(-gate[h]));
+    }
+  });
+}
+
+// reference.cpp:102-146: per-head norms, RoPE and the F16 ring store, then
+// the read (the prompt path's with `prompt_read`).
+void AttentionStep(float* q, float* k, const float* v, const float* gate,
+                   const float* q_norm, const float* k_norm,
+                   const float* factors, float* ck, float* cv, uint32_t heads,
+                   uint32_t kv_heads, uint32_t D, uint32_t position,
+                   uint32_t capacity, uint32_t window, float theta,
+                   bool sliding, float eps, bool f16, bool prompt_read,
+                   float* out) {
+  for (uint32_t h = 0; h < heads; ++h)
+    Norm(q + size_t(h) * D, D, q_norm, eps);
+  for (uint32_t h = 0; h < kv_heads; ++h)
+    Norm(k + size_t(h) * D, D, k_norm, eps);
+  Rope(q, heads, D, position, theta, sliding, factors);
+  Rope(k, kv_heads, D, position, theta, sliding, factors);
+  const size_t stride = size_t(kv_heads) * D;
+  const size_t slot = position % capacity;
+  for (size_t i = 0; i < stride; ++i) {
+    ck[slot * stride + i] = f16 ? HalfToFloat(FloatToHalf(k[i])) : k[i];
+    cv[slot * stride + i] = f16 ? HalfToFloat(FloatToHalf(v[i])) : v[i];
+  }
+  (prompt_read ? AttentionReadPrompt : AttentionRead)(
+      q, gate, ck, cv, heads, kv_heads, D, position, capacity,
+      sliding ? window : 0, out);
+}
+
+// Trailing-row pruning (engine.cpp:304-323): a prompt chunk's last layers
+// compute only the rows later layers read. Walking back from the last
+// layer: a sliding layer keeps every row; a full-attention layer keeps only
+// the rows needed after it (its K/V still come from every row); a
+// convolution needs width - 1 earlier rows. Layer i reads live_in[i] rows
+// and produces live_out[i] (the last rows of the chunk).
+void PruneRows(const orc_config& c, uint32_t n, std::vector<uint32_t>& live_in,
+               std::vector<uint32_t>& live_out) {
+  live_in.assign(c.n_layers, n);
+  live_out.assign(c.n_layers, n);
+  uint32_t need = 1;
+  for (uint32_t i = c.n_layers; i-- > 0;) {
+    if (c.layer_type[i] == ORC_SLIDING)
+      break;
+    live_out[i] = std::min(n, need);
+    if (c.layer_type[i] == ORC_FULL)
+      break;
+    need = std::min(n, need + c.conv_width - 1);
+    live_in[i] = need;
+  }
+}
 }  // namespace
 
 struct orc_model {
@@ -292,10 +475,9 @@ int orc_mat(const orc_tensor* t, const float* x, float* y) {
 }
 int orc_mat_batch(const orc_tensor* t, const float* x, float* y,
                   uint32_t batch) {
-  for (uint32_t b = 0; b < batch; ++b)
-    if (!Mat(*t, x + size_t(b) * t->cols, y + size_t(b) * t->rows))
-      return -1;
-  return 0;
+  if (batch == 0)
+    return 0;
+  return MatRows(*t, x, batch, y) ? 0 : -1;
 }
 void orc_norm(float* x, size_t n, const float* weight, float eps) {
   Norm(x, n, weight, eps);
@@ -323,20 +505,17 @@ void orc_attention_step(float* q, float* k, const float* v, const float* gate,
                         uint32_t position, uint32_t capacity, uint32_t window,
                         float theta, int sliding, float eps, int f16,
                         float* out) {
-  for (uint32_t h = 0; h < heads; ++h)
-    Norm(q + size_t(h) * D, D, q_norm, eps);
-  for (uint32_t h = 0; h < kv_heads; ++h)
-    Norm(k + size_t(h) * D, D, k_norm, eps);
-  Rope(q, heads, D, position, theta, sliding != 0, factors);
-  Rope(k, kv_heads, D, position, theta, sliding != 0, factors);
-  const size_t stride = size_t(kv_heads) * D;
-  const size_t slot = position % capacity;
-  for (size_t i = 0; i < stride; ++i) {
-    ck[slot * stride + i] = f16 ? HalfToFloat(FloatToHalf(k[i])) : k[i];
-    cv[slot * stride + i] = f16 ? HalfToFloat(FloatToHalf(v[i])) : v[i];
-  }
-  AttentionRead(q, gate, ck, cv, heads, kv_heads, D, position, capacity,
-                sliding ? window : 0, out);
+  AttentionStep(q, k, v, gate, q_norm, k_norm, factors, ck, cv, heads, kv_heads,
+                D, position, capacity, window, theta, sliding != 0, eps,
+                f16 != 0, false, out);
+}
+void orc_attention_read_prompt(const float* q, const float* gate,
+                               const float* ck, const float* cv,
+                               uint32_t heads, uint32_t kv_heads, uint32_t dim,
+                               uint32_t position, uint32_t capacity,
+                               uint32_t window, float* out) {
+  AttentionReadPrompt(q, gate, ck, cv, heads, kv_heads, dim, position,
+                      capacity, window, out);
 }
 void orc_half_rows(const float* x, size_t rows, size_t cols, float* inputs,
                    int* exps) {
@@ -551,6 +730,119 @@ int Step(orc_session* s, const float* x0, float* logits, float* hidden) {
   return 0;
 }
 
+// reference.cpp:72-168 applied to n input rows in order, one layer at a time
+// (the reference steps them one token at a time). Every row's arithmetic is
+// Step's: its norms, its products (MatRows gives each row Mat's sums), its
+// convolution step and its attention step at position + i. Rows meet only
+// through the session state (conv history, K/V ring), which each layer
+// reads and writes in row order, as n steps would. So the final state and
+// the last row's logits are bit-identical to n calls of Step.
+//
+// With `prompt` set (and n > 1), the chunk takes the reference's prompt-path
+// numerics (Session::Forward's chunk of n rows, engine.cpp:257-527): a
+// projection over 16 rows or more (hip/ops.hpp:32) reads its inputs as FP16
+// row-scaled values (orc_half_rows, q8_prefill.hpp:27-51), fewer rows stay
+// FP32; the rows each layer computes follow the trailing-row pruning rule
+// (PruneRows), which decides those counts; attention reads through the
+// prompt path's F16 arithmetic (AttentionReadPrompt), except a full-attention
+// layer left with one live row, which reads as a decode row (FP32). Rows
+// that pruning drops are still computed here; nothing reads them.
+int Steps(orc_session* s, const float* x0, uint32_t n, float* logits,
+          float* hidden, bool prompt) {
+  const orc_model& m = *s->model;
+  const auto& c = m.config;
+  if (n == 0 || s->position > s->context || n > s->context - s->position)
+    return -1;
+  if (n == 1)
+    prompt = false;  // a one-row chunk is a decode row
+  const uint32_t H = c.hidden, D = c.head_dim, base = s->position;
+  constexpr uint32_t kPromptRows = 16;
+  std::vector<uint32_t> live_in, live_out;
+  PruneRows(c, n, live_in, live_out);
+  std::vector<float> x(x0, x0 + size_t(n) * H), z(x.size()), out(x.size());
+  auto norm_rows = [&](std::vector<float>& rows, const orc_tensor& w) {
+    for (uint32_t i = 0; i < n; ++i)
+      Norm(rows.data() + size_t(i) * H, H, static_cast<const float*>(w.data),
+           c.eps);
+  };
+  // A projection's input rows as the chunk's path feeds them.
+  auto input = [&](std::vector<float>& rows, size_t cols, uint32_t live) {
+    if (prompt && live >= kPromptRows)
+      orc_half_rows(rows.data(), n, cols, rows.data(), nullptr);
+    return rows.data();
+  };
+  for (uint32_t il = 0; il < c.n_layers; ++il) {
+    auto& st = s->states[il];
+    const uint32_t rows_in = live_in[il], rows_out = live_out[il];
+    z = x;
+    norm_rows(z, m.layer(il, ORC_L_NORM));
+    input(z, H, rows_in);
+    if (c.layer_type[il] == ORC_CONV) {
+      std::vector<float> p(size_t(n) * 3 * H), conv(size_t(n) * H);
+      MatRows(m.layer(il, ORC_L_IN_PROJ), z.data(), n, p.data());
+      for (uint32_t i = 0; i < n; ++i)
+        ConvStep(p.data() + size_t(i) * 3 * H,
+                 static_cast<const float*>(m.layer(il, ORC_L_CONV).data),
+                 st.conv.data(), conv.data() + size_t(i) * H, H, c.conv_width);
+      MatRows(m.layer(il, ORC_L_OUT_PROJ), input(conv, H, rows_out), n,
+              out.data());
+    } else {
+      const uint32_t kv = c.kv_heads[il];
+      const size_t qn = size_t(c.heads) * D, kn = size_t(kv) * D;
+      std::vector<float> q(n * qn), k(n * kn), v(n * kn), gate(size_t(n) * c.heads),
+          a(n * qn);
+      MatRows(m.layer(il, ORC_L_Q), z.data(), n, q.data());
+      MatRows(m.layer(il, ORC_L_K), z.data(), n, k.data());
+      MatRows(m.layer(il, ORC_L_V), z.data(), n, v.data());
+      MatRows(m.layer(il, ORC_L_ATTN_GATE), z.data(), n, gate.data());
+      const bool sliding = c.layer_type[il] == ORC_SLIDING;
+      const bool prompt_read = prompt && !(rows_out == 1 && !sliding);
+      for (uint32_t i = 0; i < n; ++i)
+        AttentionStep(
+            q.data() + i * qn, k.data() + i * kn, v.data() + i * kn,
+            gate.data() + size_t(i) * c.heads,
+            static_cast<const float*>(m.layer(il, ORC_L_Q_NORM).data),
+            static_cast<const float*>(m.layer(il, ORC_L_K_NORM).data),
+            static_cast<const float*>(m.global(ORC_ROPE_FREQS).data),
+            st.k.data(), st.v.data(), c.heads, kv, D, base + i, st.capacity,
+            c.window, sliding ? c.theta_swa : c.theta, sliding, c.eps, s->f16,
+            prompt_read, a.data() + i * qn);
+      MatRows(m.layer(il, ORC_L_ATTN_OUT), input(a, qn, rows_out), n, out.data());
+    }
+    const auto& post = m.layer(il, ORC_L_POST_NORM);
+    if (post.data)
+      norm_rows(out, post);
+    for (size_t i = 0; i < x.size(); ++i)
+      x[i] += out[i];
+    z = x;
+    norm_rows(z, m.layer(il, ORC_L_FFN_NORM));
+    input(z, H, rows_out);
+    std::vector<float> gate(size_t(n) * c.intermediate), up(gate.size());
+    MatRows(m.layer(il, ORC_L_GATE), z.data(), n, gate.data());
+    MatRows(m.layer(il, ORC_L_UP), z.data(), n, up.data());
+    for (size_t i = 0; i < gate.size(); ++i)
+      gate[i] = (gate[i] / (1 + std::exp(-gate[i]))) * up[i];
+    MatRows(m.layer(il, ORC_L_DOWN), input(gate, c.intermediate, rows_out), n,
+            out.data());
+    const auto& post_ffn = m.layer(il, ORC_L_POST_FFN_NORM);
+    if (post_ffn.data)
+      norm_rows(out, post_ffn);
+    for (size_t i = 0; i < x.size(); ++i)
+      x[i] += out[i];
+  }
+  if (logits || hidden) {
+    float* last = x.data() + size_t(n - 1) * H;
+    Norm(last, H, static_cast<const float*>(m.global(ORC_OUTPUT_NORM).data),
+         c.eps);
+    if (hidden)
+      std::copy(last, last + H, hidden);
+    if (logits)
+      Mat(m.global(ORC_OUTPUT), last, logits);
+  }
+  s->position += n;
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -570,6 +862,27 @@ int orc_session_step_row(orc_session* s, const float* row, float* logits,
   if (!row)
     return -1;
   return Step(s, row, logits, hidden);
+}
+
+int orc_session_steps_rows(orc_session* s, const float* rows, uint32_t n,
+                           float* logits, float* hidden, int prompt_path) {
+  if (!rows || n == 0)
+    return -1;
+  return Steps(s, rows, n, logits, hidden, prompt_path != 0);
+}
+
+int orc_session_steps(orc_session* s, const uint32_t* tokens, uint32_t n,
+                      float* logits, float* hidden, int prompt_path) {
+  const orc_model& m = *s->model;
+  if (!tokens || n == 0)
+    return -1;
+  std::vector<float> x(size_t(n) * m.config.hidden);
+  for (uint32_t i = 0; i < n; ++i)
+    if (tokens[i] >= m.config.vocab ||
+        !DecodeRow(m.global(ORC_EMBEDDING), tokens[i],
+                   x.data() + size_t(i) * m.config.hidden))
+      return -1;
+  return Steps(s, x.data(), n, logits, hidden, prompt_path != 0);
 }
 
 }  // extern "C"

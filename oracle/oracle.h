@@ -176,6 +176,32 @@ int orc_session_step(orc_session* s, uint32_t token, float* logits,
    is not NULL. */
 int orc_session_step_row(orc_session* s, const float* row, float* logits,
                          float* hidden);
+/* n tokens in order (a prompt), computed one layer at a time over all n
+   rows: bit-identical to n calls of orc_session_step (each row's arithmetic
+   is the step's; the state is read and written in row order). logits and
+   hidden (each may be NULL) receive the last row's. Returns -1, leaving the
+   state untouched, for n = 0, a token out of range or too short a context.
+   With prompt_path set and n > 1, the n rows are one prompt chunk with the
+   reference's prompt-path numerics (engine.cpp:257-527): projections over
+   16 rows or more read FP16 row-scaled inputs (orc_half_rows), the rows a
+   layer computes follow trailing-row pruning (engine.cpp:304-323), and
+   attention reads through orc_attention_read_prompt except a full-attention
+   layer left with one row, which reads as a decode row. */
+int orc_session_steps(orc_session* s, const uint32_t* tokens, uint32_t n,
+                      float* logits, float* hidden, int prompt_path);
+/* The same from n caller FP32 input rows (n * hidden floats) in place of
+   the tokens' embedding rows (Session::ForwardEmbeddings). */
+int orc_session_steps_rows(orc_session* s, const float* rows, uint32_t n,
+                           float* logits, float* hidden, int prompt_path);
+/* The prompt path's attention read (hip/ops.hip:1355-1561): q scaled by
+   log2(e)/sqrt(D) and rounded to F16, base-2 scores over the F16 query,
+   probabilities exp2(s - max) rounded to F16, summed and applied as
+   rounded; keys and output as orc_attention_read. */
+void orc_attention_read_prompt(const float* q, const float* gate,
+                               const float* ck, const float* cv,
+                               uint32_t heads, uint32_t kv_heads, uint32_t dim,
+                               uint32_t position, uint32_t capacity,
+                               uint32_t window, float* out);
 
 #ifdef __cplusplus
 }

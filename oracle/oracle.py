@@ -13,6 +13,29 @@ import numpy as np
 
 ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
+LIB_V4_PATH = os.path.join(ORACLE_DIR, "liboracle_v4.so")
+
+
+def _has_avx512() -> bool:
+    """x86-64-v4's AVX-512 subsets, from the kernel's CPU flags."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    return {"avx512f", "avx512bw", "avx512cd", "avx512dq",
+                            "avx512vl"} <= flags
+    except OSError:
+        pass
+    return False
+
+
+def lib_path() -> str:
+    """The oracle build this CPU runs: x86-64-v4 where AVX-512 is present,
+    else x86-64-v3 (identical results; only the speed differs)."""
+    if _has_avx512() and os.path.exists(LIB_V4_PATH):
+        return LIB_V4_PATH
+    return LIB_PATH
 
 F32, F16, Q8_0, BF16 = 0, 1, 8, 30
 CONV, FULL, SLIDING = 0, 1, 2
@@ -64,6 +87,9 @@ _SIGS = {
     "orc_session_v": (C.POINTER(C.c_float), [vp, u32]),
     "orc_session_step": (i32, [vp, u32, vp, vp]),
     "orc_session_step_row": (i32, [vp, vp, vp, vp]),
+    "orc_session_steps": (i32, [vp, vp, u32, vp, vp, i32]),
+    "orc_session_steps_rows": (i32, [vp, vp, u32, vp, vp, i32]),
+    "orc_attention_read_prompt": (None, [vp, vp, vp, vp, u32, u32, u32, u32, u32, u32, vp]),
 }
 
 _lib = None
@@ -78,7 +104,7 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             build()
-        h = C.CDLL(LIB_PATH)
+        h = C.CDLL(lib_path())
         for name, (res, args) in _SIGS.items():
             fn = getattr(h, name)
             fn.restype = res
@@ -209,6 +235,18 @@ def attention_step(q, k, v, gate, q_norm, k_norm, factors, cache_k, cache_v, hea
     return out, q, k
 
 
+def attention_read_prompt(q, gate, cache_k, cache_v, heads, kv_heads, dim, position, capacity,
+                          window) -> np.ndarray:
+    """The prompt path's attention read (F16 scaled query and probabilities)."""
+    out = np.empty(heads * dim, np.float32)
+    lib().orc_attention_read_prompt(_p(np.ascontiguousarray(q, np.float32)),
+                                    _p(np.ascontiguousarray(gate, np.float32)),
+                                    _p(np.ascontiguousarray(cache_k, np.float32)),
+                                    _p(np.ascontiguousarray(cache_v, np.float32)),
+                                    heads, kv_heads, dim, position, capacity, window, _p(out))
+    return out
+
+
 def half_rows(x: np.ndarray):
     """Prompt activations: (effective inputs, exponent per row)."""
     x = np.ascontiguousarray(x, np.float32)
@@ -317,6 +355,31 @@ class Session:
         if lib().orc_session_step(self.handle, token, 0 if out is None else _p(out), 0) != 0:
             raise ValueError("invalid oracle step")
         return out
+
+    def steps(self, tokens, logits: bool = True, prompt_path: bool = False):
+        """A prompt of n tokens, layer-major over the n rows: bit-identical to
+        n calls of step(); returns the last row's logits (or None). With
+        prompt_path, the n rows are one prompt chunk with the reference's
+        prompt-path numerics (FP16 row-scaled projection inputs, F16
+        attention arithmetic, trailing-row pruning)."""
+        toks = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty(self.model.dims.vocab, np.float32) if logits else None
+        if lib().orc_session_steps(self.handle, _p(toks), toks.size,
+                                   0 if out is None else _p(out), 0, int(prompt_path)) != 0:
+            raise ValueError("invalid oracle steps")
+        return out
+
+    def steps_rows(self, rows, logits: bool = True, prompt_path: bool = False):
+        """steps() from FP32 input rows (n, hidden) in place of embedding
+        rows; returns (last logits or None, last final-normed hidden row)."""
+        rows = np.ascontiguousarray(rows, np.float32)
+        n = rows.shape[0]
+        out = np.empty(self.model.dims.vocab, np.float32) if logits else None
+        hidden = np.empty(self.model.dims.hidden, np.float32)
+        if lib().orc_session_steps_rows(self.handle, _p(rows), n, 0 if out is None else _p(out),
+                                        _p(hidden), int(prompt_path)) != 0:
+            raise ValueError("invalid oracle steps")
+        return out, hidden
 
     def step_row(self, row, logits: bool = True):
         """One step from an FP32 input row in place of a token's embedding

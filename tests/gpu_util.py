@@ -90,3 +90,111 @@ def inject_state(gs: L.Session, os_: O.Session, dims: L.Dims, seed: int, sid: in
                 view(l)[:] = O.half_to_float(bits)
     gs.set_position(position)
     os_.set_position(position)
+
+
+def top2_margin(logits) -> float:
+    top = np.sort(np.asarray(logits, np.float32))[-2:]
+    return float(top[1] - top[0])
+
+
+def same_greedy(got, want, label=""):
+    """The greedy id of the GPU logits is the oracle's, unconditionally
+    (std::max_element's first maximum, session_test.cpp:32-34); the oracle's
+    top-2 margin and the largest logit difference are printed beside it."""
+    err = float(np.max(np.abs(np.asarray(got, np.float64) - want)))
+    print(f"{label}: max |logit - oracle| {err:.3g}, oracle top-2 margin "
+          f"{top2_margin(want):.3g}", flush=True)
+    assert int(np.argmax(got)) == O.argmax(want), (label, err, top2_margin(want))
+    return err
+
+
+def kl_divergence(p_logits, q_logits) -> float:
+    """session_test.cpp:19-31 Divergence: KL(softmax(p) || softmax(q)),
+    log-softmax in float64."""
+    def log_softmax(x):
+        x = np.asarray(x, np.float64)
+        m = x.max()
+        return x - m - np.log(np.sum(np.exp(x - m)))
+    lp, lq = log_softmax(p_logits), log_softmax(q_logits)
+    return float(np.sum(np.exp(lp) * (lp - lq)))
+
+
+def prompt_gate(got, want, label=""):
+    """session_test.cpp:120-143's gate between a batched prompt pass and the
+    same tokens stepped one at a time: KL(want || got) < 1e-6, max |Δlogit|
+    < 0.02 and the same argmax, all unconditional."""
+    got = np.asarray(got, np.float32)
+    assert np.all(np.isfinite(got)) and np.all(np.isfinite(want)), label
+    kl = kl_divergence(want, got)
+    err = float(np.max(np.abs(got.astype(np.float64) - want)))
+    print(f"{label}: max |logit - oracle| {err:.3g}, kl {kl:.3g}, oracle top-2 margin "
+          f"{top2_margin(want):.3g}", flush=True)
+    assert kl < 1e-6 and err < 0.02, (label, kl, err)
+    assert int(np.argmax(got)) == O.argmax(want), (label, err, top2_margin(want))
+    return err, kl
+
+
+PROMPT_CHUNK = 512      # engine.hpp:47 kPrefillChunk
+
+
+def oracle_twin(om: O.Model, o: O.Session, context: int, f16: bool = True) -> O.Session:
+    """A second oracle session holding o's state and position."""
+    t = om.session(context, f16=f16)
+    d = om.dims
+    for l in range(d.n_layers):
+        if d.layer_type(l) == L.LAYER_CONV:
+            t.conv(l)[:] = o.conv(l)
+        else:
+            t.k(l)[:] = o.k(l)
+            t.v(l)[:] = o.v(l)
+    t.set_position(o.position)
+    return t
+
+
+def oracle_prompt(o: O.Session, tokens=None, rows=None, prompt: bool = False):
+    """The oracle over a prompt in the engine's 512-row chunks, layer-major
+    (bit-identical to one step per token). With prompt, every chunk of two
+    rows or more takes the reference's prompt-path numerics (FP16
+    row-scaled projection inputs from 16 rows on, F16 attention arithmetic,
+    trailing-row pruning), as the engine runs it; a one-row chunk is a
+    decode row. Returns the last logits."""
+    n = len(tokens) if tokens is not None else len(rows)
+    out = None
+    for i in range(0, n, PROMPT_CHUNK):
+        m = min(PROMPT_CHUNK, n - i)
+        if tokens is not None:
+            out = o.steps(tokens[i:i + m], prompt_path=prompt)
+        else:
+            out, _ = o.steps_rows(rows[i:i + m], prompt_path=prompt)
+    return out
+
+
+def prompt_gate_pair(got, want, want_prompt, label=""):
+    """A prompt pass against the oracle twice, with session_test.cpp:120-143's
+    gate (KL < 1e-6, max |Δ| < 0.02, the same argmax) wherever the prompt
+    path's own formats allow it:
+    * want (reference.cpp's FP32 steps): max |Δ| < 0.02, the same argmax, and
+      a KL above the prompt path's own cost, KL(want || want_prompt), by less
+      than 5e-7 (half the reference gate's budget);
+    * want_prompt (the oracle restating the prompt path's numerics: FP16
+      row-scaled projection inputs, F16 attention query and probabilities,
+      pruned rows in FP32): max |Δ| < 0.02, the same argmax, and KL below
+      1e-6, or below the prompt path's own cost where that is larger. (The
+      kernel rounds each probability against the running maximum of its key
+      span; that rounding noise is independent of any fixed-order
+      restatement, so two faithful implementations of these formats differ
+      by about the formats' own cost.)"""
+    got64 = np.asarray(got, np.float64)
+    assert np.all(np.isfinite(got64)) and np.all(np.isfinite(want_prompt)), label
+    kl_format = kl_divergence(want, want_prompt)
+    err_p = float(np.max(np.abs(got64 - want_prompt)))
+    kl_p = kl_divergence(want_prompt, got)
+    err = float(np.max(np.abs(got64 - want)))
+    kl = kl_divergence(want, got)
+    print(f"{label}: vs prompt-path oracle max |Δ| {err_p:.3g}, kl {kl_p:.3g}; vs FP32 oracle "
+          f"max |Δ| {err:.3g}, kl {kl:.3g}; the prompt path's own kl {kl_format:.3g}; oracle "
+          f"top-2 margin {top2_margin(want):.3g}", flush=True)
+    assert err_p < 0.02 and kl_p < max(1e-6, kl_format), (label, err_p, kl_p, kl_format)
+    assert err < 0.02 and kl < kl_format + 5e-7, (label, err, kl, kl_format)
+    assert int(np.argmax(got)) == O.argmax(want_prompt) == O.argmax(want), \
+        (label, err, top2_margin(want))

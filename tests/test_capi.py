@@ -203,6 +203,10 @@ def test_prompt_attention_rejects_bad_shapes():
     # kernel addresses rings with 32-bit buffer offsets
     assert lib.lfm3_prompt_attention(1, 2048, 1, 1, 1, 16, 1, 1, 1, 2048, 40, 16, 4, 128, 100,
                                      1 << 21, 256, None, 0, None) == L.E_INVALID
+    # a sliding ring shorter than the window - 1 keys the first row reads
+    # (here 254 < min(255, 300)): the older of them would be overwritten
+    assert lib.lfm3_prompt_attention(1, 2048, 1, 1, 1, 16, 1, 1, 1, 2048, 40, 16, 4, 128, 300,
+                                     254, 256, None, 0, None) == L.E_INVALID
     assert b"prompt attention" in lib.lfm3_last_error()
 
 

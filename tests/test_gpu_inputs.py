@@ -14,6 +14,7 @@ import pytest
 
 import lfm3amd as L
 import oracle as O
+from gpu_util import oracle_prompt, oracle_twin, prompt_gate, prompt_gate_pair
 from test_oracle import data, powf
 
 pytestmark = pytest.mark.gpu
@@ -25,11 +26,6 @@ def small_dims(**kw):
                 kv_heads=2, window=32, pattern="CSGCCSCG")
     base.update(kw)
     return L.Dims(**base)
-
-
-def margin(logits):
-    top = np.sort(logits)[-2:]
-    return float(top[1] - top[0])
 
 
 @pytest.mark.parametrize("n", [1, 5, 40, 600])
@@ -48,13 +44,13 @@ def test_forward_rows_matches_oracle(n):
     dev = L.DeviceBuffer.of(np.ascontiguousarray(rows))
     got2 = g2.forward_rows(n, device_addr=dev.addr)
     assert np.array_equal(got, got2)
+    oh = oracle_twin(om, o, 1024)
+    want_prompt = oracle_prompt(oh, rows=rows, prompt=True)
+    oh.close()
     want, hidden = None, None
     for r in rows:
         want, hidden = o.step_row(r)
-    err = float(np.max(np.abs(got - want)))
-    assert err < 0.02, err
-    if margin(want) > 0.05:
-        assert int(np.argmax(got)) == O.argmax(want)
+    prompt_gate_pair(got, want, want_prompt, f"{n} input rows")
     assert g.position == o.position == n
     front = g.read_hidden()
     assert np.max(np.abs(front - hidden)) < 0.02 * max(1.0, float(np.max(np.abs(hidden))))
@@ -259,3 +255,42 @@ def test_pack_kv_rounds_to_nearest_even():
     assert np.array_equal(gk[~nan_k], wk[~nan_k]) and np.array_equal(gv[~nan_v], wv[~nan_v])
     assert np.all((gk[nan_k] & 0x7c00) == 0x7c00) and np.all(gk[nan_k] & 0x3ff)
     assert L.lib().lfm3_pack_kv(None, None, None, None, 0, None) == 0
+
+
+def test_prepare_logits_runs_the_head_on_the_frontier():
+    """Session::PrepareLogits (engine.cpp:1369-1373): after a round and a
+    prompt without the vocabulary head, the device logits row
+    (LFM3_STATE_LOGITS) holds the head on the returned frontier row: the
+    oracle's tied head applied to that row (within(); the GPU's head GEMV
+    reads the row as fp16 hi/lo parts), and exactly what read_logits then
+    returns; logits already current are left as they are; a session at
+    position 0 (no frontier) is refused."""
+    from gpu_util import within
+    dims = small_dims()
+    w = L.synth_weights(dims, seed=56)
+    gm, om = L.Model(w), O.Model(dims, w)
+    a, b = gm.session(256), gm.session(256)
+    with pytest.raises(L.LFM3Error) as e:
+        a.prepare_logits()
+    assert e.value.status == L.E_INVALID
+    head = O.q8_tensor(w.globals[0][0], dims.vocab, dims.hidden)
+    addr, nbytes = a.state(L.STATE_LOGITS)
+    assert nbytes == dims.vocab * 4
+    # a decode round without the head (ForwardBatchInputs, want_logits 0)
+    gm.forward_batch_inputs([a, b], np.array([3, 9], np.uint32), [0, 0], want_logits=False)
+    # a prompt without logits
+    b.forward(np.arange(40, dtype=np.uint32), want_logits=False)
+    for s in (a, b):
+        s.prepare_logits()
+        addr, _ = s.state(L.STATE_LOGITS)
+        dev = L.download_from(addr, np.float32, dims.vocab)
+        want = O.mat(head, s.read_hidden())
+        ok, err = within(dev, want)
+        assert ok, err
+        assert np.array_equal(s.read_logits(), dev)
+        s.prepare_logits()                      # current: unchanged
+        assert np.array_equal(L.download_from(addr, np.float32, dims.vocab), dev)
+    a.close()
+    b.close()
+    gm.close()
+    om.close()

@@ -1,14 +1,16 @@
 """One scheduler round (lfm3_scheduler_round): a decode batch beside a
-prompt pass on two streams gives exactly what the two give one after the
-other (lfm3_forward_batch and lfm3_session_forward on twin sessions), for
-prompts that overlap the round, a prompt whose last chunk is one row (run
-after the round), and rounds with only one of the two; invalid rounds are
-refused before any work."""
+prompt pass on two streams. Its results are checked against the oracle
+(every decode row's logits at 2e-3 with the same greedy id; the pass's last
+logits at session_test.cpp:120-143's prompt gate) and against the two run
+one after the other (lfm3_forward_batch and lfm3_session_forward on twin
+sessions, bit for bit), for prompts that overlap the round, a prompt whose
+last chunk is one row (run after the round), and rounds with only one of the
+two; invalid rounds are refused before any work."""
 import numpy as np
 import pytest
 
 import lfm3amd as L
-from gpu_util import inject_state
+from gpu_util import inject_state, oracle_prompt, prompt_gate_pair, same_greedy
 import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -23,15 +25,19 @@ def small_dims(**kw):
 
 
 def twins(gm, om, dims, positions, seed):
-    a, b = [], []
+    """Two GPU sessions and one oracle session per position, all three at
+    the same injected state."""
+    a, b, o = [], [], []
     for sid, p in enumerate(positions):
         x, y = gm.session(2048), gm.session(2048)
         o1, o2 = om.session(2048), om.session(2048)
         inject_state(x, o1, dims, seed, sid, p)
         inject_state(y, o2, dims, seed, sid, p)
+        o2.close()
         a.append(x)
         b.append(y)
-    return a, b
+        o.append(o1)
+    return a, b, o
 
 
 @pytest.mark.parametrize("n_prompt", [40, 513, 600])
@@ -40,22 +46,35 @@ def test_scheduler_round_equals_serial_work(n_prompt):
     w = L.synth_weights(dims, seed=61)
     gm, om = L.Model(w), O.Model(dims, w)
     positions = [3, 100, 700, 1500]
-    dec, dec2 = twins(gm, om, dims, positions, 61)
+    dec, dec2, orc = twins(gm, om, dims, positions, 61)
     p1, p2 = gm.session(2048), gm.session(2048)
+    po, poh = om.session(2048), om.session(2048)
     ptoks = L.uniform_u32(SEED, f"mixed.p.{n_prompt}", n_prompt, 0, dims.vocab - 1)
     toks = L.uniform_u32(SEED, "mixed.d", 4, 0, dims.vocab - 1)
     for rnd in range(2):
         ids, logits, plog = gm.scheduler_round(dec, toks, p1, ptoks, want_logits=True)
+        # the oracle: each decode row one step, the prompt layer-major steps
+        for i, o in enumerate(orc):
+            want = o.step(int(toks[i]))
+            err = same_greedy(logits[i], want, f"round {rnd} decode row {i}")
+            assert err < 2e-3, (rnd, i, err)
+            assert ids[i] == O.argmax(want)
+        prompt_gate_pair(plog, oracle_prompt(po, ptoks), oracle_prompt(poh, ptoks, prompt=True),
+                         f"round {rnd} {n_prompt}-token pass")
+        # the same work one after the other, bit for bit
         want = gm.forward_batch(dec2, toks)
         pwant = p2.forward(ptoks)
         assert np.array_equal(logits, want), rnd
         assert np.array_equal(ids, np.array([O.argmax(r) for r in want], np.uint32))
         assert np.array_equal(plog, pwant), rnd
-        assert [s.position for s in dec] == [s.position for s in dec2]
-        assert p1.position == p2.position == (rnd + 1) * n_prompt
+        assert [s.position for s in dec] == [s.position for s in dec2] == \
+            [o.position for o in orc]
+        assert p1.position == p2.position == po.position == (rnd + 1) * n_prompt
         toks = ids
     for x in dec + dec2 + [p1, p2]:
         x.close()
+    for o in orc + [po, poh]:
+        o.close()
     gm.close()
     om.close()
 

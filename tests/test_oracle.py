@@ -317,6 +317,236 @@ def test_parallel_rows_and_heads_give_identical_steps():
     model.close()
 
 
+@pytest.mark.parametrize("n,start", [(1, 0), (13, 0), (21, 9)])
+def test_layer_major_prompt_steps_are_the_token_steps(n, start):
+    """orc_session_steps (n rows a layer at a time) against n calls of the
+    token step: the same logits and the same state, bit for bit, across the
+    sliding window (8) and from a session already at a position."""
+    dims = tiny_dims()
+    w = L.synth_weights(dims, seed=15)
+    model = O.Model(dims, w)
+    O.set_threads(3)
+    try:
+        a, b = model.session(64), model.session(64)
+        for tok in range(start):
+            a.step(tok * 11 % dims.vocab, logits=False)
+            b.step(tok * 11 % dims.vocab, logits=False)
+        tokens = L.uniform_u32(15, f"steps.{n}", n, 0, dims.vocab - 1)
+        want = None
+        for tok in tokens:
+            want = a.step(int(tok))
+        got = b.steps(tokens)
+        assert np.array_equal(got, want)
+        assert a.position == b.position == start + n
+        for i in range(dims.n_layers):
+            if dims.layer_type(i) == L.LAYER_CONV:
+                assert np.array_equal(a.conv(i), b.conv(i))
+            else:
+                assert np.array_equal(a.k(i), b.k(i)) and np.array_equal(a.v(i), b.v(i))
+        # refused without moving the state: past the context, a bad token
+        with pytest.raises(ValueError):
+            b.steps(np.zeros(64, np.uint32))
+        with pytest.raises(ValueError):
+            b.steps(np.array([0, dims.vocab], np.uint32))
+        assert b.position == start + n
+        a.close()
+        b.close()
+    finally:
+        O.set_threads(1)
+    model.close()
+
+
+def _tensor(entry):
+    data, typ, cols, rows = entry
+    return O.Tensor(data.ctypes.data, typ, cols, rows)
+
+
+def prune_rows(dims, n):
+    """engine.cpp:304-323 restated: (live_in, live_out) per layer."""
+    live_in, live_out = [n] * dims.n_layers, [n] * dims.n_layers
+    need = 1
+    for i in reversed(range(dims.n_layers)):
+        t = dims.layer_type(i)
+        if t == L.LAYER_SLIDING:
+            break
+        live_out[i] = min(n, need)
+        if t == L.LAYER_FULL:
+            break
+        need = min(n, need + dims.conv_width - 1)
+        live_in[i] = need
+    return live_in, live_out
+
+
+def composed_prompt_chunk(dims, w, state, tokens, position):
+    """A prompt chunk of n rows with the reference's prompt-path numerics,
+    composed in Python from the oracle's pinned primitives (norm, RoPE, mat,
+    conv step, half rows, both attention reads, SwiGLU), layer by layer:
+    projections over 16 rows or more read FP16 row-scaled inputs
+    (hip/ops.hpp:32, q8_prefill.hpp:27-51), the live row counts follow
+    trailing-row pruning (engine.cpp:304-323), attention reads through the
+    prompt read except a full-attention layer left with one row (FP32
+    decode read). state holds per layer the conv history or the FP32 (K, V)
+    rings (binary16 values), updated in place. Returns the last logits."""
+    H, D, n = dims.hidden, dims.head_dim, len(tokens)
+    live_in, live_out = prune_rows(dims, n)
+
+    def inp(rows, live):
+        rows = np.asarray(rows, np.float32)
+        return O.half_rows(rows)[0] if live >= 16 else rows
+
+    norm_rows = lambda rows, wt: np.stack([O.norm(r, wt, dims.eps) for r in rows])
+    x = np.stack([O.decode_row(_tensor(w.globals[0]), int(t)) for t in tokens])
+    for i in range(dims.n_layers):
+        t = w.layers[i]
+        z = inp(norm_rows(x, t[0][0]), live_in[i])
+        if dims.layer_type(i) == L.LAYER_CONV:
+            p = O.mat(_tensor(t[8]), z)
+            y = np.empty((n, H), np.float32)
+            for r in range(n):
+                y[r], state[i] = O.conv_step(p[r], t[7][0], state[i], H, dims.conv_width)
+            out = O.mat(_tensor(t[9]), inp(y, live_out[i]))
+        else:
+            sliding = dims.layer_type(i) == L.LAYER_SLIDING
+            q, k, v, g = (O.mat(_tensor(t[j]), z) for j in (10, 11, 12, 15))
+            ck, cv = state[i]
+            stride = dims.kv_heads * D
+            cap = ck.size // stride
+            theta = dims.theta_swa if sliding else dims.theta
+            prompt_read = not (live_out[i] == 1 and not sliding)
+            a = np.empty((n, dims.heads * D), np.float32)
+            for r in range(n):
+                pos = position + r
+                qr = np.concatenate([O.norm(h, t[13][0], dims.eps)
+                                     for h in q[r].reshape(dims.heads, D)])
+                kr = np.concatenate([O.norm(h, t[14][0], dims.eps)
+                                     for h in k[r].reshape(dims.kv_heads, D)])
+                qr = O.rope(qr, D, pos, theta, sliding, w.globals[3][0])
+                kr = O.rope(kr, D, pos, theta, sliding, w.globals[3][0])
+                slot = pos % cap
+                ck[slot * stride:(slot + 1) * stride] = O.half_to_float(O.float_to_half(kr))
+                cv[slot * stride:(slot + 1) * stride] = O.half_to_float(O.float_to_half(v[r]))
+                read = O.attention_read_prompt if prompt_read else O.attention_read
+                a[r] = read(qr, g[r], ck, cv, dims.heads, dims.kv_heads, D, pos, cap,
+                            dims.window if sliding else 0)
+            out = O.mat(_tensor(t[16]), inp(a, live_out[i]))
+        if t[2] is not None and t[2][0] is not None:
+            out = norm_rows(out, t[2][0])
+        x = (x + out).astype(np.float32)
+        z = inp(norm_rows(x, t[1][0]), live_out[i])
+        h = O.swiglu(O.mat(_tensor(t[4]), z), O.mat(_tensor(t[5]), z))
+        out = O.mat(_tensor(t[6]), inp(h, live_out[i]))
+        if t[3] is not None and t[3][0] is not None:
+            out = norm_rows(out, t[3][0])
+        x = (x + out).astype(np.float32)
+    last = O.norm(x[-1], w.globals[2][0], dims.eps)
+    return O.mat(_tensor(w.globals[0]), last)
+
+
+def test_prompt_read_matches_fp64_with_f16_points():
+    """orc_attention_read_prompt against float64 numpy with the prompt
+    path's three rounding points (F16 of q log2(e)/sqrt(D), F16 probabilities
+    against the row maximum, the sum over the rounded probabilities): within
+    2e-6 of the output scale, while the FP32 read differs by far more."""
+    rng = np.random.default_rng(5)
+    H, KH, D, P, cap = 8, 2, 64, 300, 512
+    q = rng.standard_normal(H * D).astype(np.float32)
+    gate = rng.standard_normal(H).astype(np.float32)
+    ck = O.half_to_float(O.float_to_half(rng.standard_normal(cap * KH * D).astype(np.float32)))
+    cv = O.half_to_float(O.float_to_half(rng.standard_normal(cap * KH * D).astype(np.float32)))
+    for window in (0, 32):
+        got = O.attention_read_prompt(q, gate, ck, cv, H, KH, D, P, cap, window)
+        fp32 = O.attention_read(q, gate, ck, cv, H, KH, D, P, cap, window)
+        first = max(0, P + 1 - window) if window else 0
+        keys = ck.reshape(cap, KH, D).astype(np.float64)
+        vals = cv.reshape(cap, KH, D).astype(np.float64)
+        ts = np.arange(first, P + 1) % cap
+        scale = np.float32(np.float32(1) / np.sqrt(np.float32(D))) * np.float32(1.4426950408889634)
+        want = np.empty(H * D)
+        for h in range(H):
+            kh = h // (H // KH)
+            qs = (q[h * D:(h + 1) * D] * scale).astype(np.float32).astype(np.float16)
+            sc = keys[ts, kh] @ qs.astype(np.float64)
+            p = np.exp2(sc - sc.max()).astype(np.float32).astype(np.float16).astype(np.float64)
+            want[h * D:(h + 1) * D] = (p @ vals[ts, kh] / p.sum()) / (1 + np.exp(-float(gate[h])))
+        sc_out = np.max(np.abs(want))
+        err = np.max(np.abs(got - want)) / sc_out
+        err32 = np.max(np.abs(fp32 - want)) / sc_out
+        assert err < 2e-6 and err32 > 20 * err, (window, err, err32)
+
+
+@pytest.mark.parametrize("n,pattern", [(5, "CSGCG"), (19, "CSGCG"), (40, "CSGCG"),
+                                       (40, "GSCCC"), (2, "CSGCG")])
+def test_prompt_path_steps_are_the_composed_chunk(n, pattern):
+    """orc_session_steps with prompt_path against the same chunk composed in
+    Python from the pinned primitives: the same logits bit for bit. Chunks
+    below 16 rows (FP32 projections, F16 attention), above (FP16 row inputs),
+    a last layer that is global (one live row: FP32 decode read, FP32 FFN)
+    and trailing convolutions (7 then 13 live rows), across the sliding
+    window (8); and different logits from the FP32 steps."""
+    dims = tiny_dims(pattern=pattern)
+    w = L.synth_weights(dims, seed=17)
+    model = O.Model(dims, w)
+    a, b = model.session(64), model.session(64)
+    for tok in range(3):                 # start from position 3
+        a.step(tok, logits=False)
+        b.step(tok, logits=False)
+    state = {}
+    for i in range(dims.n_layers):
+        if dims.layer_type(i) == L.LAYER_CONV:
+            state[i] = a.conv(i).copy()
+        else:
+            state[i] = (a.k(i).copy(), a.v(i).copy())
+    tokens = L.uniform_u32(17, f"prompt.{n}.{pattern}", n, 0, dims.vocab - 1)
+    got = a.steps(tokens, prompt_path=True)
+    full = b.steps(tokens)
+    want = composed_prompt_chunk(dims, w, state, tokens, 3)
+    assert np.array_equal(got, want)
+    assert not np.array_equal(got, full)
+    for i in range(dims.n_layers):
+        if dims.layer_type(i) == L.LAYER_CONV:
+            assert np.array_equal(a.conv(i), state[i])
+        else:
+            assert np.array_equal(a.k(i), state[i][0]) and np.array_equal(a.v(i), state[i][1])
+    model.close()
+
+
+def test_isa_builds_give_identical_steps():
+    """The x86-64-v3 and x86-64-v4 builds of the oracle (vectorized only
+    across independent sums) step to identical logits."""
+    import ctypes
+    if not O._has_avx512() or not __import__("os").path.exists(O.LIB_V4_PATH):
+        pytest.skip("no AVX-512 on this CPU")
+    dims = tiny_dims()
+    w = L.synth_weights(dims, seed=16)
+    model = O.Model(dims, w)
+    outs = []
+    for path in (O.LIB_PATH, O.LIB_V4_PATH):
+        h = ctypes.CDLL(path)
+        h.orc_model_create.restype = ctypes.c_void_p
+        h.orc_model_create.argtypes = [ctypes.POINTER(O.Config), ctypes.POINTER(O.Tensor),
+                                       ctypes.c_size_t]
+        h.orc_session_create.restype = ctypes.c_void_p
+        h.orc_session_create.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int]
+        h.orc_session_step.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+        h.orc_session_destroy.argtypes = [ctypes.c_void_p]
+        h.orc_model_destroy.argtypes = [ctypes.c_void_p]
+        m = h.orc_model_create(ctypes.byref(model.config), model._tensors,
+                               len(model._tensors))
+        s = h.orc_session_create(m, 64, 1)
+        rows = []
+        for tok in range(12):
+            out = np.empty(dims.vocab, np.float32)
+            assert h.orc_session_step(s, tok * 13 % dims.vocab, out.ctypes.data, None) == 0
+            rows.append(out)
+        h.orc_session_destroy(s)
+        h.orc_model_destroy(m)
+        outs.append(rows)
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+    model.close()
+
+
 def test_step_row_with_embedding_row_is_the_token_step():
     """ForwardBatchInputs' row path (engine.cpp:1217-1299 copies the row over
     the embedding): the step from the token's dequantized embedding row is
