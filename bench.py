@@ -60,9 +60,10 @@ MIXED_DECODE, MIXED_LO, MIXED_HI = 7, 16384, 32768
 # plain 256 MiB device-to-device copy in the same program (FETCH_SIZE x 2.0,
 # WRITE_SIZE x 1.0). Re-measure after a change to either kernel.
 GEMV_TRAFFIC = {"read": 18_477_766, "write": 262_144}
-# The same for the SwiGLU operand-image GEMV (2 x 7680 x 2048, 8 rows):
-# 1.017 x its algorithmic bytes.
-SWIGLU_TRAFFIC = {"read": 34_044_181, "write": 245_760}
+# The same for the round's dominant launch, the residual norm (2 K parts)
+# fused with the SwiGLU operand-image GEMV (2 x 7680 x 2048, 8 rows):
+# 1.024 x its algorithmic bytes.
+SWIGLU_TRAFFIC = {"read": 34_394_800, "write": 444_621}
 GEMM_TRAFFIC = {"read": 86_290_594, "write": 15_851_520}
 
 
@@ -187,41 +188,61 @@ def packed_copies(parts, rows_total: int, cols: int, copies: int):
     return [(L.DeviceBuffer.of(codes), L.DeviceBuffer.of(scales)) for _ in range(copies)]
 
 
-def time_launches(launch, copies: int, passes: int) -> float:
+def time_launches(launch, copies: int, passes: int, seqs: bool = False) -> float:
     """Microseconds per launch of launch(copy, stream) replayed from a HIP
     graph (one pass launches every copy once), timed with HIP events on the
-    stream the kernels run on."""
+    stream the kernels run on. With seqs, launch(copy, stream, seq) is a
+    fused norm + GEMV launch, whose rows' flags must see a new sequence
+    number at every launch: two graphs with disjoint numbers (1..copies and
+    copies + 1..2 copies) replay alternately, so no launch finds its own
+    number left in the flags by the one before it."""
     stream = L.Stream()
-
-    def one_pass():
-        for i in range(copies):
-            launch(i, stream.handle)
-
-    graph = L.Graph(stream, one_pass)
-    graph.launch()
+    graphs = []
+    for g in range(2 if seqs else 1):
+        def one_pass(base=g * copies + 1):
+            for i in range(copies):
+                if seqs:
+                    launch(i, stream.handle, base + i)
+                else:
+                    launch(i, stream.handle)
+        graphs.append(L.Graph(stream, one_pass))
+    for graph in graphs:
+        graph.launch()
     stream.synchronize()
     a, b = L.Event(), L.Event()
     a.record(stream.handle)
-    for _ in range(passes):
-        graph.launch()
+    for p in range(passes):
+        graphs[p % len(graphs)].launch()
     b.record(stream.handle)
     b.synchronize()
     us = a.elapsed_ms(b) * 1000.0 / (passes * copies)
-    graph.close()
+    for graph in graphs:
+        graph.close()
     a.close()
     b.close()
     stream.close()
     return us
 
 
+def norm_bytes(d: L.Dims, parts: int) -> int:
+    """Algorithmic bytes of the round's residual norm over 8 rows: x read and
+    written, the branch's K parts read, the norm and post-norm weights (the
+    operand image it hands to the GEMV is not counted, as the GEMV's operand
+    rows are counted once, as FP32 rows)."""
+    return SESSIONS * d.hidden * 4 * (2 + parts) + 2 * d.hidden * 4
+
+
 def round_kernels(d: L.Dims, positions=None, passes: int = 6):
     """Each kind of launch of the decode round alone at its round shape (8
     rows; weight and K/V copies rotated past the 256 MB MALL): microseconds,
     the algorithmic HBM bytes it moves and their fraction of 8 TB/s, and
-    its launches per round. The first entry, the SwiGLU operand-image GEMV,
-    is the round's dominant kernel. With `positions` (the rows' positions)
-    the fused heads + decode attention of a global and of a sliding layer
-    are timed too."""
+    its launches per round. The round runs each residual norm inside the
+    launch of the GEMV that consumes its image (lfm3_q8_gemv_image_norm,
+    lfm3_q8_gemv_conv_image_norm), so those launches are timed fused, their
+    bytes the GEMV's plus the norm's. The first entry, the fused norm +
+    SwiGLU GEMV, is the round's dominant kernel. With `positions` (the rows'
+    positions) the fused heads + decode attention of a global and of a
+    sliding layer are timed too."""
     H, F, V, B = d.hidden, d.intermediate, d.vocab, SESSIONS
     lib = L.lib()
     seed = L.SEED
@@ -241,18 +262,37 @@ def round_kernels(d: L.Dims, positions=None, passes: int = 6):
     exps = L.DeviceBuffer(8 * 4)
     L.check(lib.lfm3_residual_norm_image(branch.addr, 1, B * H, wts.addr, x.addr, wts.addr, None,
                                          image.addr, exps.addr, B, H, d.eps, None))
+    # The fused launches' flags and wait-error word.
+    flags = L.DeviceBuffer(lib.lfm3_norm_flags_bytes())
+    L.hip_check(L.hip().hipMemset(flags.addr, 0, flags.nbytes))
+    werr = L.DeviceBuffer(4)
+    L.hip_check(L.hip().hipMemset(werr.addr, 0, 4))
     L.synchronize()
+
+    def norm_args(parts, seq):
+        return (branch.addr, parts, B * H, wts.addr, x.addr, wts.addr, d.eps, image.addr,
+                exps.addr, flags.addr, seq, werr.addr)
+
     n_conv = sum(1 for i in range(d.n_layers) if d.layer_type(i) == L.LAYER_CONV)
     n_attn = d.n_layers - n_conv
-    # SwiGLU (gate/up interleaved) on the operand image.
+    mixer_parts = lib.lfm3_q8_gemv_parts(H, H)
+    ffn_parts = lib.lfm3_q8_gemv_parts(H, F)
+    # The FFN norm and SwiGLU (gate/up interleaved) on its operand image.
     g, u = L.q8(seed, "rk.gate", F, H), L.q8(seed, "rk.up", F, H)
     mats = packed_copies([(g, F, 0, 2), (u, F, 1, 2)], 2 * F, H, 12)
     hid = L.DeviceBuffer(B * F * 4)
+    us = time_launches(lambda i, s, q: L.check(lib.lfm3_q8_gemv_image_norm(
+        *norm_args(mixer_parts, q), mats[i][0].addr, mats[i][1].addr, F, H, 1, B, hid.addr, F,
+        s)), len(mats), passes, seqs=True)
+    entry(f"residual norm ({mixer_parts} K parts) + SwiGLU GEMV on its image, 2 x 7680 x 2048",
+          us, 2 * q8_bytes(F, H) + B * H * 4 + B * F * 4 + norm_bytes(d, mixer_parts),
+          d.n_layers)
+    # The same GEMV as a launch of its own (its operand image ready).
     us = time_launches(lambda i, s: L.check(lib.lfm3_q8_gemv_swiglu_image(
         mats[i][0].addr, mats[i][1].addr, F, H, image.addr, exps.addr, B, hid.addr, F, s)),
         len(mats), passes)
-    entry("SwiGLU GEMV on the operand image, 2 x 7680 x 2048", us,
-          2 * q8_bytes(F, H) + B * H * 4 + B * F * 4, d.n_layers)
+    entry("(the SwiGLU GEMV alone on a ready image, 2 x 7680 x 2048; not a launch of the round)",
+          us, 2 * q8_bytes(F, H) + B * H * 4 + B * F * 4, 0)
     del mats
     # Down projection in K parts from the FP32 hidden rows.
     mats = packed_copies([(L.q8(seed, "rk.down", H, F), H, 0, 1)], H, F, 20)
@@ -280,11 +320,12 @@ def round_kernels(d: L.Dims, positions=None, passes: int = 6):
              for r in range(B)]
     table = L.DeviceBuffer.of(np.array([h.addr for h in hists], np.uint64))
     a = L.DeviceBuffer(B * H * 4)
-    us = time_launches(lambda i, s: L.check(lib.lfm3_q8_gemv_conv_image(
-        mats[i][0].addr, mats[i][1].addr, H, image.addr, exps.addr, B, taps.addr, table.addr,
-        d.conv_width, a.addr, H, s)), len(mats), passes)
-    entry("convolution in_proj GEMV + step, 6144 x 2048", us,
-          q8_bytes(3 * H, H) + B * H * 4 * (2 + 2 * (d.conv_width - 1)), n_conv)
+    us = time_launches(lambda i, s, q: L.check(lib.lfm3_q8_gemv_conv_image_norm(
+        *norm_args(ffn_parts, q), mats[i][0].addr, mats[i][1].addr, H, B, taps.addr, table.addr,
+        d.conv_width, a.addr, H, s)), len(mats), passes, seqs=True)
+    entry(f"residual norm ({ffn_parts} K parts) + convolution in_proj GEMV + step, 6144 x 2048",
+          us, q8_bytes(3 * H, H) + B * H * 4 * (2 + 2 * (d.conv_width - 1))
+          + norm_bytes(d, ffn_parts), n_conv)
     del mats
     # q | k | v | gate of an attention layer on the operand image.
     qr, kr = d.heads * d.head_dim, d.kv_heads * d.head_dim
@@ -296,27 +337,23 @@ def round_kernels(d: L.Dims, positions=None, passes: int = 6):
                           (L.q8(seed, "rk.g", d.heads, H), d.heads, tq + 2 * tk, 1)],
                          rows, H, 48)
     proj = L.DeviceBuffer(B * rows * 4)
-    us = time_launches(lambda i, s: L.check(lib.lfm3_q8_gemv_image(
-        mats[i][0].addr, mats[i][1].addr, rows, H, image.addr, exps.addr, B, proj.addr, rows,
-        1, s)), len(mats), passes)
-    entry("q | k | v | gate GEMV on the operand image, 3088 x 2048", us,
-          q8_bytes(qr + 2 * kr + d.heads, H) + B * H * 4 + B * rows * 4, n_attn)
+    us = time_launches(lambda i, s, q: L.check(lib.lfm3_q8_gemv_image_norm(
+        *norm_args(ffn_parts, q), mats[i][0].addr, mats[i][1].addr, rows, H, 0, B, proj.addr,
+        rows, s)), len(mats), passes, seqs=True)
+    entry(f"residual norm ({ffn_parts} K parts) + q | k | v | gate GEMV, 3088 x 2048", us,
+          q8_bytes(qr + 2 * kr + d.heads, H) + B * H * 4 + B * rows * 4
+          + norm_bytes(d, ffn_parts), n_attn)
     del mats
     # The vocabulary head (the round's own launch also keeps greedy keys).
     mats = packed_copies([(L.q8(seed, "rk.head", V, H), V, 0, 1)], V, H, 2)
     logits = L.DeviceBuffer(B * V * 4)
-    us = time_launches(lambda i, s: L.check(lib.lfm3_q8_gemv_image(
-        mats[i][0].addr, mats[i][1].addr, V, H, image.addr, exps.addr, B, logits.addr, V, 1,
-        s)), len(mats), max(2, passes // 2))
-    entry("vocabulary head GEMV on the operand image, 128000 x 2048", us,
-          q8_bytes(V, H) + B * H * 4 + B * V * 4, 1)
+    us = time_launches(lambda i, s, q: L.check(lib.lfm3_q8_gemv_image_norm(
+        *norm_args(ffn_parts, q), mats[i][0].addr, mats[i][1].addr, V, H, 0, B, logits.addr, V,
+        s)), len(mats), max(2, passes // 2), seqs=True)
+    entry(f"final norm ({ffn_parts} K parts) + vocabulary head GEMV, 128000 x 2048", us,
+          q8_bytes(V, H) + B * H * 4 + B * V * 4 + norm_bytes(d, ffn_parts), 1)
     del mats
-    # The residual norm writing the next operand image (4 K parts).
-    us = time_launches(lambda i, s: L.check(lib.lfm3_residual_norm_image(
-        branch.addr, 4, B * H, wts.addr, x.addr, wts.addr, None, image.addr, exps.addr, B, H,
-        d.eps, s)), 8, passes)
-    entry("residual norm to the operand image (4 K parts)", us, B * H * 4 * (2 + 4 + 2) + 2 * H * 4,
-          2 * d.n_layers + 1)
+    assert int(werr.download(np.uint32, 1)[0]) == 0, "a fused launch's wait timed out"
     if positions is not None:
         for window in (0, d.window):
             out.append(attention_launch(d, positions, window, proj, rows, passes))
@@ -846,8 +883,9 @@ def main():
     sampled_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
     log(f"sampled round {sampled_ms:.3f} ms")
 
-    # The round's kernels alone at their round shapes; the first (the SwiGLU
-    # operand-image GEMV, the largest share of the round) is the roofline.
+    # The round's kernels alone at their round shapes; the first (the
+    # residual norm fused with the SwiGLU operand-image GEMV, the largest
+    # share of the round) is the roofline.
     kernels = round_kernels(dims, [int(c) - 1 for c in ctx])
     top = kernels[0]
     for k in kernels:

@@ -278,6 +278,45 @@ int lfm3_residual_norm_image(const float* branch, uint32_t parts,
                              float* x, const float* norm, float* z, void* image,
                              int* exps, uint32_t rows, uint32_t hidden,
                              float eps, void* stream);
+/* The decode round's residual norm and the GEMV that consumes its image in
+   one launch: the launch's first `batch` blocks compute
+   lfm3_residual_norm_image(branch, parts, part_stride, post_norm, x, norm,
+   z = NULL, image, exps, batch, cols, eps) and publish each row through a
+   flag; its GEMV blocks issue their weight loads, wait for the rows and
+   compute lfm3_q8_gemv_image (swiglu 0) or lfm3_q8_gemv_swiglu_image
+   (swiglu 1, rows of each of gate and up) on the image. Results equal the
+   two calls made one after the other, bit for bit. flags: a device buffer
+   of lfm3_norm_flags_bytes(), zeroed once; seq: a number no earlier call
+   on these flags used (not 0); wait_error: NULL or a word the GPU can
+   write (device or mapped host memory) that is set to 1 if a block's
+   bounded wait for the rows timed out (its results are then undefined).
+   Calls on the same flags must not overlap. Replaces: the residual_norm
+   lambda of Session::Impl::Run followed by gpu::Project / ProjectSwiGLU
+   (engine.cpp:327-350; hip/ops.hip:905-970, 2170-2204). */
+size_t lfm3_norm_flags_bytes(void);
+int lfm3_q8_gemv_image_norm(const float* branch, uint32_t parts,
+                            size_t part_stride, const float* post_norm,
+                            float* x, const float* norm, float eps,
+                            void* image, int* exps, unsigned* flags,
+                            uint32_t seq, unsigned* wait_error,
+                            const void* codes, const void* scales,
+                            uint32_t rows, uint32_t cols, int swiglu,
+                            uint32_t batch, float* y, uint32_t ldy,
+                            void* stream);
+/* The same for the convolution block's in projection with its step
+   (lfm3_q8_gemv_conv_image): norm, then projection and step, in one
+   launch. Replaces: the residual_norm lambda, then gpu::Project of in_proj
+   and gpu::ShortConv for n == 1 (engine.cpp:327-350, 386-393). */
+int lfm3_q8_gemv_conv_image_norm(const float* branch, uint32_t parts,
+                                 size_t part_stride, const float* post_norm,
+                                 float* x, const float* norm, float eps,
+                                 void* image, int* exps, unsigned* flags,
+                                 uint32_t seq, unsigned* wait_error,
+                                 const void* codes, const void* scales,
+                                 uint32_t hidden, uint32_t batch,
+                                 const float* taps, float* const* history,
+                                 uint32_t width, float* y, uint32_t ldy,
+                                 void* stream);
 /* lfm3_residual_norm_parts whose normed rows also go out as the prompt
    GEMM's FP16 row-scaled activations (lfm3_half_rows of z: a16 rows of lda
    halves, scale per row); z may be NULL. Replaces: the FP16 split branch of

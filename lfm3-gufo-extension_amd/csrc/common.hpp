@@ -144,6 +144,20 @@ __device__ __forceinline__ void StoreB128(BufferResource res, unsigned offset, u
   const u4 w = {v.x, v.y, v.z, v.w};
   __builtin_amdgcn_raw_buffer_store_b128(w, res, offset, 0, 0);
 }
+// Buffer stores with a cache policy: kCachePolicySc1 writes through the
+// XCD's L2 to memory (the coherence point of every XCD); a load with it
+// reads from there.
+constexpr int kCachePolicySc1 = 16;
+template<int kPolicy>
+__device__ __forceinline__ void StoreB32P(BufferResource res, unsigned offset, unsigned v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, res, offset, 0, kPolicy);
+}
+template<int kPolicy>
+__device__ __forceinline__ void StoreB128P(BufferResource res, unsigned offset, uint4 v) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  const u4 w = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(w, res, offset, 0, kPolicy);
+}
 __device__ __forceinline__ void StoreF4(BufferResource res, unsigned offset, float a, float b,
                                         float c, float d) {
   StoreB128(res, offset,

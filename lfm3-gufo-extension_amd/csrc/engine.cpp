@@ -23,6 +23,7 @@
 
 #include "common.hpp"
 #include "internal.hpp"
+#include "norm_image.hpp"
 
 namespace lfm3amd {
 namespace {
@@ -226,6 +227,12 @@ struct lfm3_model {
   Buffer z, head_out;
   std::uint32_t head_groups = 0;
   Buffer image, exps;  // GEMV operand image of the current hidden-wide input
+  // A decode round's norms run inside the GEMV launches that consume their
+  // images (FusedNorm): the rows' flags, the launches' sequence numbers and
+  // a host word that a timed-out wait sets (checked after every round).
+  Buffer norm_flags;
+  std::uint32_t norm_seq = 0;
+  std::unique_ptr<PinnedBuffer> wait_error;
   Buffer one_row;      // a host input row of a one-row chunk, on the device
   std::size_t proj_ld = 0, gemv_ws_bytes = 0;
   // Per-round device tables: RoundTable, per-layer pointer rows, items.
@@ -528,6 +535,10 @@ int lfm3_model_load(const lfm3_config* config, const lfm3_tensor* tensors,
     m->head_keys = Buffer(std::size_t(B) * m->head_groups * sizeof(unsigned long long));
     m->image = Buffer(lfm3_operand_image_bytes(H));
     m->exps = Buffer(kMaxBatch * sizeof(int));
+    m->norm_flags = Buffer(kFlagWords * sizeof(unsigned));
+    m->wait_error = std::make_unique<PinnedBuffer>(sizeof(unsigned),
+                                                   hipHostMallocMapped | hipHostMallocCoherent);
+    *static_cast<unsigned*>(m->wait_error->p) = 0;
     // Mapped and coherent (fine-grained): the last kernel's stores reach
     // host memory without a cache flush; the host reads them after the
     // stream synchronization that ends the round.
@@ -1081,52 +1092,56 @@ void EnqueueRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
   std::uint32_t mixer_parts = 1;
 
   // Normed rows go out as operand images; the convolution and attention
-  // outputs and the FFN hidden state are staged by their GEMVs.
+  // outputs and the FFN hidden state are staged by their GEMVs. Each norm
+  // runs inside the launch of the GEMV that consumes its image: the
+  // launch's first n blocks are the norm (one row each), and its GEMV
+  // blocks stream their weights while they wait for the rows (FusedNorm).
   void* image = m.image.p;
   int* exps = m.exps.as<int>();
-  const auto gemv_image = [&](const Matrix& w, float* y, std::uint32_t ldy) {
-    CheckStatus(lfm3_q8_gemv_image(w.codes.p, w.scales.p, w.rows, w.cols, image,
-                                   exps, n, y, ldy, 1, s));
-  };
-  NormImageArgs na;
-  na.part_stride = std::size_t(n) * H;
-  na.x = x;
-  na.H = int(H);
-  na.eps = c.eps;
-  na.image = static_cast<uint4*>(image);
-  na.exps = exps;
-  const auto norm_image = [&](std::uint32_t parts, const float* post, const float* weight,
-                              float* const* z_rows) {
-    na.branch = parts ? out : nullptr;
-    na.parts = parts ? int(parts) : 1;
-    na.post = parts ? post : nullptr;
-    na.weight = weight;
-    na.z_rows = z_rows;
-    CheckStatus(LaunchNormImage(na, n, s));
+  FusedNorm fn;
+  fn.args.part_stride = std::size_t(n) * H;
+  fn.args.x = x;
+  fn.args.H = int(H);
+  fn.args.eps = c.eps;
+  fn.args.image = static_cast<uint4*>(image);
+  fn.args.exps = exps;
+  fn.flags = m.norm_flags.as<unsigned>();
+  fn.error = static_cast<unsigned*>(m.wait_error->device);
+  // The next fused launch's norm: x += post(branch parts), then norm with
+  // `weight` (and the FP32 rows to z_rows when given).
+  const auto norm = [&](std::uint32_t parts, const float* post, const float* weight,
+                        float* const* z_rows) {
+    fn.args.branch = parts ? out : nullptr;
+    fn.args.parts = parts ? int(parts) : 1;
+    fn.args.post = parts ? post : nullptr;
+    fn.args.weight = weight;
+    fn.args.z_rows = z_rows;
+    if (++m.norm_seq == 0)  // 0 is the flags' initial value
+      m.norm_seq = 1;
+    fn.seq = m.norm_seq;
   };
 
   // The first norm gathers the round's embedding rows into x.
-  na.emb_codes = static_cast<const std::uint8_t*>(m.embedding.codes.p);
-  na.emb_scales = static_cast<const std::uint16_t*>(m.embedding.scales.p);
-  na.tokens = d_rt->tokens;
-  na.inputs = inputs ? d_rt->inputs : nullptr;
-  na.vocab = int(c.vocab);
-  norm_image(0, nullptr, m.layers[0].norm.as<float>(), nullptr);
-  na.tokens = nullptr;
-  na.inputs = nullptr;
+  fn.args.emb_codes = static_cast<const std::uint8_t*>(m.embedding.codes.p);
+  fn.args.emb_scales = static_cast<const std::uint16_t*>(m.embedding.scales.p);
+  fn.args.tokens = d_rt->tokens;
+  fn.args.inputs = inputs ? d_rt->inputs : nullptr;
+  fn.args.vocab = int(c.vocab);
+  norm(0, nullptr, m.layers[0].norm.as<float>(), nullptr);
   for (std::uint32_t il = 0; il < L; ++il) {
     const Layer& l = m.layers[il];
     if (l.type == LFM3_LAYER_CONV) {
       // The in projection with the convolution step in its epilogue; the
       // FP32 output is staged by the out projection.
-      CheckStatus(lfm3_q8_gemv_conv_image(
+      CheckStatus(LaunchConvImage(
           l.in_proj.codes.p, l.in_proj.scales.p, H, image, exps, n, l.conv.as<float>(),
           reinterpret_cast<float* const*>(dev + conv_off) + il * kMaxBatch, c.conv_width, a,
-          H, s));
+          H, &fn, s));
       mixer_parts = partials(l.out_proj, a, H);
     } else {
       const bool swa = l.type == LFM3_LAYER_SLIDING;
-      gemv_image(l.qkvg, proj, pld);
+      CheckStatus(LaunchGemvImageFused(l.qkvg.codes.p, l.qkvg.scales.p, l.qkvg.rows,
+                                       l.qkvg.cols, image, exps, n, proj, pld, false, fn, s));
       const auto* kp = reinterpret_cast<std::uint16_t* const*>(dev + k_off) + il * kMaxBatch;
       const auto* vp = reinterpret_cast<std::uint16_t* const*>(dev + v_off) + il * kMaxBatch;
       const auto* cp = reinterpret_cast<const std::uint32_t*>(dev + cap_off) + il * kMaxBatch;
@@ -1141,28 +1156,46 @@ void EnqueueRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
           c.heads, l.kv, D, c.eps, m.attn_ws.p, m.attn_ws_bytes, s));
       mixer_parts = partials(l.attn_out, a, c.heads * D);
     }
-    norm_image(mixer_parts, l.post_norm.as<float>(), l.ffn_norm.as<float>(), nullptr);
-    CheckStatus(lfm3_q8_gemv_swiglu_image(l.ffn.codes.p, l.ffn.scales.p, F, H,
-                                          image, exps, n, hid, F, s));
+    fn.args.tokens = nullptr;
+    fn.args.inputs = nullptr;
+    norm(mixer_parts, l.post_norm.as<float>(), l.ffn_norm.as<float>(), nullptr);
+    CheckStatus(LaunchGemvImageFused(l.ffn.codes.p, l.ffn.scales.p, F, H, image, exps, n, hid,
+                                     F, true, fn, s));
     const std::uint32_t ffn_parts = partials(l.down, hid, F);
     const bool last = il + 1 == L;
     // The last norm's FP32 rows are the sessions' frontier rows
     // (engine.cpp:505-511), written in place.
-    norm_image(ffn_parts, l.post_ffn_norm.as<float>(),
-               last ? m.output_norm.as<float>() : m.layers[il + 1].norm.as<float>(),
-               last ? d_rt->frontier : nullptr);
+    norm(ffn_parts, l.post_ffn_norm.as<float>(),
+         last ? m.output_norm.as<float>() : m.layers[il + 1].norm.as<float>(),
+         last ? d_rt->frontier : nullptr);
   }
   // LM head over the final-normed rows into each session's logits row, with
   // per-block greedy candidates; then the greedy ids from the candidates.
+  // Without the head the final norm runs alone (the frontier rows).
   if (head) {
     const Matrix& w = m.head();
     auto* keys = m.head_keys.as<unsigned long long>();
     CheckStatus(LaunchHeadGemv(w.codes.p, w.scales.p, w.rows, w.cols, image, exps, n,
-                               d_rt->logits, keys, nullptr, s));
+                               d_rt->logits, keys, nullptr, s, &fn));
     if (greedy)
       CheckStatus(LaunchArgmaxKeys(keys, n, m.head_groups, m.ids(), s));
+  } else {
+    CheckStatus(LaunchNormImage(fn.args, n, s));
   }
   Check(hipGetLastError(), "round launch");
+}
+
+// A fused launch's wait that timed out (FusedNorm) leaves the round's
+// results undefined: the round fails as a device error. Call after the
+// model stream has been synchronized.
+void CheckRoundWaits(lfm3_model& m) {
+  if (!m.wait_error)
+    return;
+  auto* word = static_cast<volatile unsigned*>(m.wait_error->p);
+  if (*word) {
+    *word = 0;
+    throw Error(LFM3_E_HIP, "LFM3 decode round: a GEMV block's wait for its norm timed out");
+  }
 }
 
 void FinishRound(lfm3_session* const* sessions, std::uint32_t n, bool head) {
@@ -1177,6 +1210,7 @@ void RunRound(lfm3_model& m, lfm3_session* const* sessions, std::uint32_t n,
               bool head = true) {
   EnqueueRound(m, sessions, n, tokens, greedy, inputs, head);
   Check(hipStreamSynchronize(m.stream), "round");
+  CheckRoundWaits(m);
   FinishRound(sessions, n, head);
 }
 
@@ -1752,6 +1786,7 @@ int BatchEntry(lfm3_session* const* sessions, std::size_t n,
       EnqueueSample(m, std::uint32_t(n), *sample);
     EnqueueReadback(m, sessions, std::uint32_t(n), logits != nullptr);
     Check(hipStreamSynchronize(m.stream), "round");
+    CheckRoundWaits(m);
     FinishRound(sessions, std::uint32_t(n), head);
     DeliverReadback(m, std::uint32_t(n), ids, logits);
     return LFM3_OK;
@@ -1976,6 +2011,7 @@ int lfm3_scheduler_round(lfm3_session* const* sessions, std::size_t n,
       enqueued = true;
       if (!overlap) {
         Check(hipStreamSynchronize(m.stream), "round");
+        CheckRoundWaits(m);
         FinishRound(sessions, std::uint32_t(n), true);
         enqueued = false;
       }
@@ -1996,6 +2032,7 @@ int lfm3_scheduler_round(lfm3_session* const* sessions, std::size_t n,
     }
     if (enqueued) {
       Check(hipStreamSynchronize(m.stream), "round");
+      CheckRoundWaits(m);
       FinishRound(sessions, std::uint32_t(n), true);
       enqueued = false;
     }

@@ -39,13 +39,33 @@ struct NormImageArgs {
   float* a_scale = nullptr;
 };
 int LaunchNormImage(const NormImageArgs& a, std::uint32_t rows, hipStream_t stream);
+// An operand-image GEMV launch that takes its norm along: its first `batch`
+// blocks run the residual norm of `args` (one row each) and publish the
+// image rows; its GEMV blocks wait for them (flags: kFlagWords words,
+// norm_image.hpp; seq: a number no earlier launch on these flags used;
+// error: a host-visible word set to 1 if a wait timed out).
+struct FusedNorm {
+  NormImageArgs args;
+  unsigned* flags = nullptr;
+  unsigned seq = 0;
+  unsigned* error = nullptr;
+};
+int LaunchGemvImageFused(const void* codes, const void* scales, std::uint32_t rows,
+                         std::uint32_t cols, const void* image, const int* exps,
+                         std::uint32_t batch, float* y, std::uint32_t ldy, bool swiglu,
+                         const FusedNorm& fused, hipStream_t stream);
+// lfm3_q8_gemv_conv_image, fused with the norm when `fused` is not null.
+int LaunchConvImage(const void* codes, const void* scales, std::uint32_t hidden,
+                    const void* image, const int* exps, std::uint32_t batch, const float* taps,
+                    float* const* history, std::uint32_t width, float* y, std::uint32_t ldy,
+                    const FusedNorm* fused, hipStream_t stream);
 // The vocabulary head on the final operand image: row t of the logits goes
 // to y_rows[t], and keys[t * groups + j] gets the best ArgKey of block j's
 // rows; returns the number of groups through *groups.
 int LaunchHeadGemv(const void* codes, const void* scales, std::uint32_t rows,
                    std::uint32_t cols, const void* image, const int* exps, std::uint32_t batch,
                    float* const* y_rows, unsigned long long* keys, std::uint32_t* groups,
-                   hipStream_t stream);
+                   hipStream_t stream, const FusedNorm* fused = nullptr);
 std::uint32_t HeadGemvGroups(std::uint32_t rows, std::uint32_t cols);
 // ids[t] = the first index of token t's maximum from the head's keys.
 int LaunchArgmaxKeys(const unsigned long long* keys, std::uint32_t rows, std::uint32_t groups,

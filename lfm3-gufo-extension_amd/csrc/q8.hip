@@ -12,6 +12,7 @@
 
 #include "common.hpp"
 #include "internal.hpp"
+#include "norm_image.hpp"
 
 namespace lfm3amd {
 namespace {
@@ -170,7 +171,8 @@ template<int W, int RT, bool kSwiGLU>
 __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int group,
                                              int B, float* __restrict__ y, int ldy,
                                              int rows_out, float* const* y_rows = nullptr,
-                                             unsigned long long* keys = nullptr) {
+                                             unsigned long long* keys = nullptr,
+                                             int groups = 0) {
   constexpr int T = W * 64;
   const int tid = threadIdx.x;
   // With T a multiple of 128 a thread stores one token's outputs; its row
@@ -199,7 +201,7 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
         key = other > key ? other : key;
       }
       if (tid < 8 * R && tid % R == 0 && tok < B)
-        keys[std::size_t(tok) * gridDim.x + group] = key;
+        keys[std::size_t(tok) * groups + group] = key;
     } else if (tid < B) {  // small blocks: one lane per token
       unsigned long long best = 0;
       for (int i = 0; i < R; ++i) {
@@ -208,7 +210,7 @@ __device__ __forceinline__ void GemvEpilogue(f4 (&total)[RT], float* red, int gr
             SumOverWaves<W, RT>(red, i / kTileRows, tid * 16 + i % kTileRows), unsigned(row));
         best = row < rows_out && k > best ? k : best;
       }
-      keys[std::size_t(tid) * gridDim.x + group] = best;
+      keys[std::size_t(tid) * groups + group] = best;
     }
   }
   if constexpr (kSwiGLU) {
@@ -419,12 +421,18 @@ __global__ void Q8Gemv(const std::uint8_t* __restrict__ codes,
 // The operand-image GEMV's main loop: tile r of the block is tile_of(r);
 // returns each lane's un-scaled sums (D layout: lane L holds A rows
 // 4 (L / 16) + i of weight row L % 16) with the rows' powers of two undone.
-template<int W, int RT, int SPW, typename TileOf>
+// With kAwait (a fused launch) the image is written by this launch's norm
+// blocks: each compute wave issues its first round's weight loads, waits
+// for its block's watcher wave (AwaitReady: the rows are published), then
+// loads the image, so the weights stream in while the norm runs.
+template<int W, int RT, int SPW, bool kAwait = false, typename TileOf>
 __device__ __forceinline__ void ImageGemvCore(const std::uint8_t* __restrict__ codes,
                                               const Half* __restrict__ scales, int row_tiles,
                                               int nchunks, const uint4* __restrict__ image,
                                               const int* __restrict__ exps, int B, int c_begin,
-                                              int nloc, TileOf tile_of, f4 (&total)[RT]) {
+                                              int nloc, TileOf tile_of, f4 (&total)[RT],
+                                              const unsigned* ready = nullptr,
+                                              unsigned seq = 0) {
   constexpr int ROUND = W * SPW;  // chunks per wave per round
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool a_live = (lane & 7) < B;
@@ -438,10 +446,21 @@ __device__ __forceinline__ void ImageGemvCore(const std::uint8_t* __restrict__ c
   const BufferResource c_res = MakeBuffer(codes, tiles_bytes * kTileCodeBytes);
   const BufferResource s_res = MakeBuffer(scales, tiles_bytes * kTileScales * 2);
   const BufferResource a_res = MakeBuffer(image, unsigned(nchunks) * 2 * 64 * 16);
+  if constexpr (kAwait) {
+    if (nloc <= 0)
+      AwaitReady(ready, seq);  // no round: the exponents still wait
+  }
   for (int base = 0; base < nloc; base += ROUND) {
     uint4 q[RT][SPW];
     unsigned sc[RT][SPW];
     uint4 a[SPW][2];
+    const auto load_a = [&](int j) {
+      const int chunk = base + wave + W * j;
+      const bool live = chunk < nloc;
+      const unsigned at = (unsigned(c_begin + chunk) * 2 * 64 + lane) * 16;
+      a[j][0] = LoadB128(a_res, live && a_live ? at : kOutOfRange);
+      a[j][1] = LoadB128(a_res, live && a_live ? at + 64 * 16 : kOutOfRange);
+    };
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
       const int chunk = base + wave + W * j;
@@ -454,9 +473,15 @@ __device__ __forceinline__ void ImageGemvCore(const std::uint8_t* __restrict__ c
         q[r][j] = LoadB128(c_res, ok ? off * kTileCodeBytes + lane * 16 : kOutOfRange);
         sc[r][j] = LoadB32(s_res, ok ? off * (kTileScales * 2) + (lane & 15) * 4 : kOutOfRange);
       }
-      const unsigned at = (unsigned(c_begin + chunk) * 2 * 64 + lane) * 16;
-      a[j][0] = LoadB128(a_res, live && a_live ? at : kOutOfRange);
-      a[j][1] = LoadB128(a_res, live && a_live ? at + 64 * 16 : kOutOfRange);
+      if constexpr (!kAwait)
+        load_a(j);
+    }
+    if constexpr (kAwait) {
+      if (base == 0)
+        AwaitReady(ready, seq);
+#pragma unroll
+      for (int j = 0; j < SPW; ++j)
+        load_a(j);
     }
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
@@ -491,24 +516,46 @@ __device__ __forceinline__ void ImageGemvCore(const std::uint8_t* __restrict__ c
   }
 }
 
-template<int W, int RT, bool kSwiGLU, int SPW>
-__launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(RT >= 4 ? 2 : 4)))
+// A fused launch (kNorm) has W + 1 waves a block: wave W loads the image
+// into LDS (dynamic shared memory, 2 KB a chunk of the K range) and leaves.
+template<int W, int RT, bool kSwiGLU, int SPW, bool kNorm = false>
+__launch_bounds__((W + kNorm) * 64)
+__attribute__((amdgpu_waves_per_eu(RT >= 4 ? 2 : kNorm ? 5 : 4)))
 __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
                             const Half* __restrict__ scales, int row_tiles,
                             int nchunks, const uint4* __restrict__ image,
                             const int* __restrict__ exps, int B,
                             float* __restrict__ y, int ldy, int rows_out,
                             std::size_t part_stride, float* const* __restrict__ y_rows,
-                            unsigned long long* __restrict__ keys) {
+                            unsigned long long* __restrict__ keys, const FusedNorm fused) {
   __shared__ float red[W * RT * 128 + RT * 128];
-  const int group = blockIdx.x;
+  // A fused launch's first B blocks are the norm of its B rows.
+  const int lead = kNorm ? B : 0;
   const int c_begin = int(blockIdx.y) * nchunks / int(gridDim.y);
   const int nloc = (int(blockIdx.y) + 1) * nchunks / int(gridDim.y) - c_begin;
+  __shared__ unsigned s_ready;
+  if constexpr (kNorm) {
+    if (int(blockIdx.x) < B) {
+      NormImageRow<(W + 1) * 64, 1, true>(fused.args, blockIdx.x, fused.flags, fused.seq);
+      return;
+    }
+    // s_ready starts cleared for every wave (LDS is not initialized).
+    if (threadIdx.x == 0)
+      s_ready = 0;
+    __syncthreads();
+    if ((threadIdx.x >> 6) == W) {
+      WatchRows(fused.flags, fused.seq, fused.error, B, &s_ready);
+      return;
+    }
+  }
+  const int group = int(blockIdx.x) - lead;
   y += std::size_t(blockIdx.y) * part_stride;
   f4 total[RT];
-  ImageGemvCore<W, RT, SPW>(codes, scales, row_tiles, nchunks, image, exps, B, c_begin, nloc,
-                            [=](int r) { return group * RT + r; }, total);
-  GemvEpilogue<W, RT, kSwiGLU>(total, red, group, B, y, ldy, rows_out, y_rows, keys);
+  ImageGemvCore<W, RT, SPW, kNorm>(codes, scales, row_tiles, nchunks, image, exps, B, c_begin,
+                                   nloc, [=](int r) { return group * RT + r; }, total, &s_ready,
+                                   fused.seq);
+  GemvEpilogue<W, RT, kSwiGLU>(total, red, group, B, y, ldy, rows_out, y_rows, keys,
+                               int(gridDim.x) - lead);
 }
 
 // The convolution block's in projection with the decode convolution step
@@ -517,20 +564,36 @@ __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
 // X of channels 16 g .. 16 g + 15, then applies ConvStepKernel's
 // expressions to them, in the same order (for the same projection values,
 // outputs and history equal lfm3_conv_step_ragged's bit for bit).
-template<int W>
-__launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2)))
+template<int W, bool kNorm = false>
+__launch_bounds__((W + kNorm) * 64) __attribute__((amdgpu_waves_per_eu(2)))
 __global__ void Q8GemvConvImage(const std::uint8_t* __restrict__ codes,
                                 const Half* __restrict__ scales, int third_tiles,
                                 int nchunks, const uint4* __restrict__ image,
                                 const int* __restrict__ exps, int B,
                                 const float* __restrict__ taps,
                                 float* const* __restrict__ history, int L, int H,
-                                float* __restrict__ y, int ldy) {
+                                float* __restrict__ y, int ldy, const FusedNorm fused) {
   constexpr int RT = 3, T = W * 64, kMaxWidth = 32;
   __shared__ float red[W * RT * 128 + RT * 128];
   __shared__ float s_hist[128][kMaxWidth - 1];
   __shared__ float s_taps[kTileRows][kMaxWidth];
-  const int group = blockIdx.x;
+  __shared__ unsigned s_ready;
+  // A fused launch's first B blocks are the norm of its B rows; then wave W
+  // of each block watches the rows' flags and leaves.
+  if constexpr (kNorm) {
+    if (int(blockIdx.x) < B) {
+      NormImageRow<(W + 1) * 64, 1, true>(fused.args, blockIdx.x, fused.flags, fused.seq);
+      return;
+    }
+    if (threadIdx.x == 0)
+      s_ready = 0;
+    __syncthreads();
+    if ((threadIdx.x >> 6) == W) {
+      WatchRows(fused.flags, fused.seq, fused.error, B, &s_ready);
+      return;
+    }
+  }
+  const int group = int(blockIdx.x) - (kNorm ? B : 0);
   // The step's history rows and taps do not depend on the projection: they
   // are staged before the weights stream, so the epilogue reads LDS only.
   for (int e = threadIdx.x; e < 128 * (L - 1); e += T) {
@@ -545,9 +608,9 @@ __global__ void Q8GemvConvImage(const std::uint8_t* __restrict__ codes,
       s_taps[n][t] = taps[std::size_t(ch) * L + t];
   }
   f4 total[RT];
-  ImageGemvCore<W, RT, W >= 16 ? 2 : 4>(codes, scales, 3 * third_tiles, nchunks, image, exps, B,
-                                         0, nchunks,
-                                         [=](int r) { return group + r * third_tiles; }, total);
+  ImageGemvCore<W, RT, W >= 16 ? 2 : 4, kNorm>(
+      codes, scales, 3 * third_tiles, nchunks, image, exps, B, 0, nchunks,
+      [=](int r) { return group + r * third_tiles; }, total, &s_ready, fused.seq);
   const float* fin = ReduceWaves<W, RT>(total, red);  // its barriers publish s_hist
   for (int o = threadIdx.x; o < 128; o += T) {
 #pragma clang fp contract(off)
@@ -624,30 +687,46 @@ int LaunchGemv(const void* codes, const void* scales, std::uint32_t rows,
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 GEMV launch");
 }
 
+// A fused launch's norm blocks have the GEMV's block size: one thread per 8
+// columns (NormImageRow with G = 1) needs hidden / 8 <= threads; its
+// operand image and flags must be given.
+bool FusedNormFits(const FusedNorm& f, std::uint32_t cols, unsigned threads) {
+  return f.flags && f.args.image && f.args.exps && f.args.x && f.args.weight &&
+         f.args.H == int(cols) && Chunks(cols) * 8 <= threads;
+}
+
 template<int W, int RT, bool kSwiGLU>
 void LaunchImagePlan(const GemvPlan& p, const std::uint8_t* c, const Half* s,
                      const uint4* image, const int* exps, int B, float* y,
                      int ldy, int rows_out, hipStream_t stream, float* const* y_rows,
-                     unsigned long long* keys) {
-  Q8GemvImage<W, RT, kSwiGLU, W >= 16 ? 2 : 4><<<dim3(p.groups, p.parts), W * 64, 0, stream>>>(
-      c, s, p.row_tiles, p.nchunks, image, exps, B, y, ldy, rows_out,
-      std::size_t(ldy) * B, y_rows, keys);
+                     unsigned long long* keys, const FusedNorm* fused) {
+  constexpr int SPW = W >= 16 ? 2 : 4;
+  if (fused)
+    Q8GemvImage<W, RT, kSwiGLU, SPW, true>
+        <<<dim3(p.groups + B, p.parts), (W + 1) * 64, 0, stream>>>(
+            c, s, p.row_tiles, p.nchunks, image, exps, B, y, ldy, rows_out,
+            std::size_t(ldy) * B, y_rows, keys, *fused);
+  else
+    Q8GemvImage<W, RT, kSwiGLU, SPW><<<dim3(p.groups, p.parts), W * 64, 0, stream>>>(
+        c, s, p.row_tiles, p.nchunks, image, exps, B, y, ldy, rows_out,
+        std::size_t(ldy) * B, y_rows, keys, FusedNorm{});
 }
 
 template<int W, bool kSwiGLU>
 void LaunchImageRT(const GemvPlan& p, const std::uint8_t* c, const Half* s,
                    const uint4* image, const int* exps, int B, float* y, int ldy,
                    int rows_out, hipStream_t stream, float* const* y_rows,
-                   unsigned long long* keys) {
+                   unsigned long long* keys, const FusedNorm* fused) {
   if constexpr (kSwiGLU) {
-    LaunchImagePlan<W, 2, true>(p, c, s, image, exps, B, y, ldy, rows_out, stream, y_rows, keys);
+    LaunchImagePlan<W, 2, true>(p, c, s, image, exps, B, y, ldy, rows_out, stream, y_rows, keys,
+                                fused);
   } else {
     if (p.RT == 1)
       LaunchImagePlan<W, 1, false>(p, c, s, image, exps, B, y, ldy, rows_out, stream, y_rows,
-                                   keys);
+                                   keys, fused);
     else
       LaunchImagePlan<W, 2, false>(p, c, s, image, exps, B, y, ldy, rows_out, stream, y_rows,
-                                   keys);
+                                   keys, fused);
   }
 }
 
@@ -669,27 +748,30 @@ int LaunchGemvImage(const void* codes, const void* scales, std::uint32_t rows,
                     std::uint32_t cols, const void* image, const int* exps,
                     std::uint32_t batch, float* y, std::uint32_t ldy,
                     std::uint32_t parts, hipStream_t stream, float* const* y_rows = nullptr,
-                    unsigned long long* keys = nullptr) {
+                    unsigned long long* keys = nullptr, const FusedNorm* fused = nullptr) {
   if (!codes || !scales || !image || !exps || (!y && !y_rows) || rows == 0 || cols == 0 ||
       cols % 32 || batch == 0 || batch > 8 || (!y_rows && ldy < rows) || parts < 1 ||
       parts > Chunks(cols) || (kSwiGLU && parts != 1) || ((y_rows || keys) && parts != 1) ||
+
       (reinterpret_cast<std::uintptr_t>(image) & 15) ||
       !BufferFits(std::size_t(RowTiles(rows) * (kSwiGLU ? 2 : 1)) * Chunks(cols) *
                   kTileCodeBytes))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 operand-image GEMV");
   const GemvPlan p = PlanImage(rows, cols, kSwiGLU, parts);
+  if (fused && (parts != 1 || !FusedNormFits(*fused, cols, unsigned(p.W + 1) * 64)))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 fused norm + operand-image GEMV");
   const auto* c = static_cast<const std::uint8_t*>(codes);
   const auto* s = static_cast<const Half*>(scales);
   const auto* im = static_cast<const uint4*>(image);
   const int B = int(batch), ly = int(ldy), ro = int(rows);
   if (p.W == 8)
-    LaunchImageRT<8, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys);
+    LaunchImageRT<8, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys, fused);
   else if (p.W == 4)
-    LaunchImageRT<4, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys);
+    LaunchImageRT<4, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys, fused);
   else if (p.W == 2)
-    LaunchImageRT<2, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys);
+    LaunchImageRT<2, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys, fused);
   else
-    LaunchImageRT<1, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys);
+    LaunchImageRT<1, kSwiGLU>(p, c, s, im, exps, B, y, ly, ro, stream, y_rows, keys, fused);
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 operand-image GEMV launch");
 }
 
@@ -726,13 +808,77 @@ std::uint32_t HeadGemvGroups(std::uint32_t rows, std::uint32_t cols) {
 int LaunchHeadGemv(const void* codes, const void* scales, std::uint32_t rows,
                    std::uint32_t cols, const void* image, const int* exps, std::uint32_t batch,
                    float* const* y_rows, unsigned long long* keys, std::uint32_t* groups,
-                   hipStream_t stream) {
+                   hipStream_t stream, const FusedNorm* fused) {
   if (!y_rows || !keys)
     return Fail(LFM3_E_INVALID, "LFM3 head GEMV needs its row table and key buffer");
   if (groups)
     *groups = HeadGemvGroups(rows, cols);
   return LaunchGemvImage<false>(codes, scales, rows, cols, image, exps, batch, nullptr, 0, 1,
-                                stream, y_rows, keys);
+                                stream, y_rows, keys, fused);
+}
+
+// A fused launch runs at most 8 compute waves a block (with its loader
+// wave, at most 9 of the 16 a block may have).
+template<int W>
+void LaunchConvPlan(dim3 grid, const std::uint8_t* c, const Half* s, int third, int nchunks,
+                    const uint4* im, const int* exps, int B, const float* taps,
+                    float* const* history, int L, int H, float* y, int ly,
+                    const FusedNorm* fused, hipStream_t st) {
+  constexpr int WF = W > 8 ? 8 : W;
+  if (fused)
+    Q8GemvConvImage<WF, true><<<dim3(grid.x + B), (WF + 1) * 64, 0, st>>>(
+        c, s, third, nchunks, im, exps, B, taps, history, L, H, y, ly, *fused);
+  else
+    Q8GemvConvImage<W><<<grid, W * 64, 0, st>>>(c, s, third, nchunks, im, exps, B, taps, history,
+                                               L, H, y, ly, FusedNorm{});
+}
+
+int LaunchConvImage(const void* codes, const void* scales, std::uint32_t hidden,
+                    const void* image, const int* exps, std::uint32_t batch, const float* taps,
+                    float* const* history, std::uint32_t width, float* y, std::uint32_t ldy,
+                    const FusedNorm* fused, hipStream_t st) {
+  if (!codes || !scales || !image || !exps || !taps || !history || !y || !hidden ||
+      hidden % kTileRows || batch == 0 || batch > 8 || width < 2 || width > 32 ||
+      ldy < hidden || (reinterpret_cast<std::uintptr_t>(image) & 15) ||
+      !BufferFits(std::size_t(RowTiles(3 * hidden)) * Chunks(hidden) * kTileCodeBytes))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 projection + convolution shape");
+  const int third = int(hidden / kTileRows), nchunks = int(Chunks(hidden));
+  // One block per 16 channels: few blocks, so each takes 16 waves (two
+  // chunks each of a 32-chunk round) for more loads in flight per CU.
+  const int W = nchunks <= 4 ? 1 : nchunks <= 8 ? 2 : nchunks <= 16 ? 4 : nchunks <= 24 ? 8 : 16;
+  if (fused && !FusedNormFits(*fused, hidden, unsigned(std::min(W, 8) + 1) * 64))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 fused norm + convolution projection");
+  const auto* c = static_cast<const std::uint8_t*>(codes);
+  const auto* s = static_cast<const Half*>(scales);
+  const auto* im = static_cast<const uint4*>(image);
+  const dim3 grid(third);
+  const int B = int(batch), L = int(width), H = int(hidden), ly = int(ldy);
+  if (W == 16)
+    LaunchConvPlan<16>(grid, c, s, third, nchunks, im, exps, B, taps, history, L, H, y, ly,
+                       fused, st);
+  else if (W == 8)
+    LaunchConvPlan<8>(grid, c, s, third, nchunks, im, exps, B, taps, history, L, H, y, ly, fused,
+                      st);
+  else if (W == 4)
+    LaunchConvPlan<4>(grid, c, s, third, nchunks, im, exps, B, taps, history, L, H, y, ly, fused,
+                      st);
+  else if (W == 2)
+    LaunchConvPlan<2>(grid, c, s, third, nchunks, im, exps, B, taps, history, L, H, y, ly, fused,
+                      st);
+  else
+    LaunchConvPlan<1>(grid, c, s, third, nchunks, im, exps, B, taps, history, L, H, y, ly, fused,
+                      st);
+  return HipStatus(hipGetLastError(), "LFM3 projection + convolution launch");
+}
+
+int LaunchGemvImageFused(const void* codes, const void* scales, std::uint32_t rows,
+                         std::uint32_t cols, const void* image, const int* exps,
+                         std::uint32_t batch, float* y, std::uint32_t ldy, bool swiglu,
+                         const FusedNorm& fused, hipStream_t stream) {
+  return swiglu ? LaunchGemvImage<true>(codes, scales, rows, cols, image, exps, batch, y, ldy, 1,
+                                        stream, nullptr, nullptr, &fused)
+                : LaunchGemvImage<false>(codes, scales, rows, cols, image, exps, batch, y, ldy, 1,
+                                         stream, nullptr, nullptr, &fused);
 }
 }  // namespace lfm3amd
 
@@ -863,37 +1009,70 @@ int lfm3_q8_gemv_conv_image(const void* codes, const void* scales, std::uint32_t
                             const void* image, const int* exps, std::uint32_t batch,
                             const float* taps, float* const* history, std::uint32_t width,
                             float* y, std::uint32_t ldy, void* stream) {
-  if (!codes || !scales || !image || !exps || !taps || !history || !y || !hidden ||
-      hidden % kTileRows || batch == 0 || batch > 8 || width < 2 || width > 32 ||
-      ldy < hidden || (reinterpret_cast<std::uintptr_t>(image) & 15) ||
-      !BufferFits(std::size_t(RowTiles(3 * hidden)) * Chunks(hidden) * kTileCodeBytes))
-    return Fail(LFM3_E_INVALID, "unsupported LFM3 projection + convolution shape");
-  const int third = int(hidden / kTileRows), nchunks = int(Chunks(hidden));
-  // One block per 16 channels: few blocks, so each takes 16 waves (two
-  // chunks each of a 32-chunk round) for more loads in flight per CU.
-  const int W = nchunks <= 4 ? 1 : nchunks <= 8 ? 2 : nchunks <= 16 ? 4 : nchunks <= 24 ? 8 : 16;
-  const auto* c = static_cast<const std::uint8_t*>(codes);
-  const auto* s = static_cast<const Half*>(scales);
-  const auto* im = static_cast<const uint4*>(image);
-  const auto st = static_cast<hipStream_t>(stream);
-  const dim3 grid(third);
-  const int B = int(batch), L = int(width), H = int(hidden), ly = int(ldy);
-  if (W == 16)
-    Q8GemvConvImage<16><<<grid, 1024, 0, st>>>(c, s, third, nchunks, im, exps, B, taps, history,
-                                               L, H, y, ly);
-  else if (W == 8)
-    Q8GemvConvImage<8><<<grid, 512, 0, st>>>(c, s, third, nchunks, im, exps, B, taps, history,
-                                             L, H, y, ly);
-  else if (W == 4)
-    Q8GemvConvImage<4><<<grid, 256, 0, st>>>(c, s, third, nchunks, im, exps, B, taps, history,
-                                             L, H, y, ly);
-  else if (W == 2)
-    Q8GemvConvImage<2><<<grid, 128, 0, st>>>(c, s, third, nchunks, im, exps, B, taps, history,
-                                             L, H, y, ly);
-  else
-    Q8GemvConvImage<1><<<grid, 64, 0, st>>>(c, s, third, nchunks, im, exps, B, taps, history,
-                                            L, H, y, ly);
-  return HipStatus(hipGetLastError(), "LFM3 projection + convolution launch");
+  return LaunchConvImage(codes, scales, hidden, image, exps, batch, taps, history, width, y, ldy,
+                         nullptr, static_cast<hipStream_t>(stream));
+}
+
+std::size_t lfm3_norm_flags_bytes(void) { return kFlagWords * sizeof(unsigned); }
+
+namespace {
+// The C-ABI's fused norm arguments (lfm3_residual_norm_image's), checked as
+// that call checks them.
+int FusedArgs(const float* branch, std::uint32_t parts, std::size_t part_stride,
+              const float* post_norm, float* x, const float* norm, float eps, void* image,
+              int* exps, unsigned* flags, std::uint32_t seq, unsigned* wait_error,
+              std::uint32_t batch, std::uint32_t hidden, FusedNorm& f) {
+  if (!x || !norm || !image || !exps || !flags || !seq || !batch || batch > 8 || !hidden ||
+      hidden % 32 || !parts || parts > std::uint32_t(kNormParts) ||
+      (branch && parts > 1 && part_stride < std::size_t(batch) * hidden))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 fused norm arguments");
+  f.args.branch = branch;
+  f.args.parts = int(parts);
+  f.args.part_stride = part_stride;
+  f.args.post = branch ? post_norm : nullptr;
+  f.args.x = x;
+  f.args.weight = norm;
+  f.args.H = int(hidden);
+  f.args.eps = eps;
+  f.args.image = static_cast<uint4*>(image);
+  f.args.exps = exps;
+  f.flags = flags;
+  f.seq = seq;
+  f.error = wait_error;
+  return LFM3_OK;
+}
+}  // namespace
+
+int lfm3_q8_gemv_image_norm(const float* branch, std::uint32_t parts, std::size_t part_stride,
+                            const float* post_norm, float* x, const float* norm, float eps,
+                            void* image, int* exps, unsigned* flags, std::uint32_t seq,
+                            unsigned* wait_error, const void* codes, const void* scales,
+                            std::uint32_t rows, std::uint32_t cols, int swiglu,
+                            std::uint32_t batch, float* y, std::uint32_t ldy, void* stream) {
+  FusedNorm f;
+  const int e = FusedArgs(branch, parts, part_stride, post_norm, x, norm, eps, image, exps, flags,
+                          seq, wait_error, batch, cols, f);
+  if (e)
+    return e;
+  return LaunchGemvImageFused(codes, scales, rows, cols, image, exps, batch, y, ldy, swiglu != 0,
+                              f, static_cast<hipStream_t>(stream));
+}
+
+int lfm3_q8_gemv_conv_image_norm(const float* branch, std::uint32_t parts,
+                                 std::size_t part_stride, const float* post_norm, float* x,
+                                 const float* norm, float eps, void* image, int* exps,
+                                 unsigned* flags, std::uint32_t seq, unsigned* wait_error,
+                                 const void* codes, const void* scales, std::uint32_t hidden,
+                                 std::uint32_t batch, const float* taps, float* const* history,
+                                 std::uint32_t width, float* y, std::uint32_t ldy,
+                                 void* stream) {
+  FusedNorm f;
+  const int e = FusedArgs(branch, parts, part_stride, post_norm, x, norm, eps, image, exps, flags,
+                          seq, wait_error, batch, hidden, f);
+  if (e)
+    return e;
+  return LaunchConvImage(codes, scales, hidden, image, exps, batch, taps, history, width, y, ldy,
+                         &f, static_cast<hipStream_t>(stream));
 }
 
 int lfm3_q8_gemv_swiglu_image(const void* codes, const void* scales,

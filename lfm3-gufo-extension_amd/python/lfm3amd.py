@@ -91,6 +91,11 @@ _SIGS = {
     "lfm3_q8_gemv_swiglu_image": (i32, [vp, vp, u32, u32, vp, vp, u32, vp, u32, vp]),
     "lfm3_q8_gemv_conv_image": (i32, [vp, vp, u32, vp, vp, u32, vp, vp, u32, vp, u32, vp]),
     "lfm3_residual_norm_image": (i32, [vp, u32, sz, vp, vp, vp, vp, vp, vp, u32, u32, f32, vp]),
+    "lfm3_norm_flags_bytes": (sz, []),
+    "lfm3_q8_gemv_image_norm": (i32, [vp, u32, sz, vp, vp, vp, f32, vp, vp, vp, u32, vp,
+                                      vp, vp, u32, u32, i32, u32, vp, u32, vp]),
+    "lfm3_q8_gemv_conv_image_norm": (i32, [vp, u32, sz, vp, vp, vp, f32, vp, vp, vp, u32, vp,
+                                           vp, vp, u32, u32, vp, vp, u32, vp, u32, vp]),
     "lfm3_conv_step_ragged_image": (i32, [vp, u32, vp, vp, vp, u32, vp, vp, u32, u32, u32, vp]),
     "lfm3_half_rows": (i32, [vp, u32, vp, u32, vp, u32, vp, u32, u32, vp]),
     "lfm3_q8_gemm_swiglu_max_blocks": (u32, [u32]),

@@ -313,3 +313,19 @@ def test_batch_entries_refuse_empty_and_oversized_batches():
     # null session pointers are refused too
     assert lib.lfm3_forward_batch_greedy(sessions, 2, toks, ids) == L.E_INVALID
     assert b"null" in lib.lfm3_last_error()
+
+
+def test_fused_norm_gemv_refusals():
+    """The fused norm + GEMV entries refuse a zero sequence number, missing
+    flags, more than 8 rows and an unsupported GEMV shape before any launch."""
+    lib = L.lib()
+    assert lib.lfm3_norm_flags_bytes() >= 8 * 8 * 4
+    args = lambda seq, flags, batch, cols: (None, 1, 0, None, 1, 1, 1e-5, 16, 16, flags, seq, None,
+                                            16, 16, 64, cols, 0, batch, 16, 64, None)
+    assert lib.lfm3_q8_gemv_image_norm(*args(0, 16, 8, 256)) == L.E_INVALID     # seq 0
+    assert lib.lfm3_q8_gemv_image_norm(*args(1, None, 8, 256)) == L.E_INVALID   # no flags
+    assert lib.lfm3_q8_gemv_image_norm(*args(1, 16, 9, 256)) == L.E_INVALID     # 9 rows
+    assert lib.lfm3_q8_gemv_image_norm(*args(1, 16, 8, 200)) == L.E_INVALID     # cols % 32
+    assert lib.lfm3_q8_gemv_conv_image_norm(None, 1, 0, None, 1, 1, 1e-5, 16, 16, 16, 0, None,
+                                            16, 16, 256, 8, 16, 16, 7, 16, 256,
+                                            None) == L.E_INVALID
