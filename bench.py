@@ -417,6 +417,141 @@ def attention_launch(d: L.Dims, positions, window: int, proj, ld: int, passes: i
             "frac": round(gbs / HBM_PEAK_GBS, 4), "per_round": n_layers}
 
 
+def config_attention(ctx, heads: int, kv: int, D: int, window: int, passes: int, sets: int = 8):
+    """Config 2: the fused heads + ragged decode attention of one layer over
+    8 sessions at contexts `ctx` (positions ctx - 1), Q/K RMSNorm, paired
+    RoPE at theta 1e6, the sigmoid per-head gate; F16 K/V rings of N(0, 1)
+    values, capacity 4096 (global) or 256 (sliding, window 256); at least
+    `sets` independent cache sets rotated per timed pass. Bytes: the K/V
+    rows read (keys [first, position]), the current row written, and the
+    q / k / v / gate rows read and the output written."""
+    lib = L.lib()
+    B = len(ctx)
+    stride = kv * D
+    cap = window if window else 4096
+    pos = (np.asarray(ctx, np.uint32) - 1).astype(np.uint32)
+    keys = sum(min(int(p) + 1, window) if window else int(p) + 1 for p in pos)
+    ld = (heads + 2 * kv) * D + heads
+    nbytes = keys * stride * 2 * 2 + B * stride * 2 * 2 + B * ld * 4 + B * heads * D * 4
+    ring_bytes = cap * stride * 2
+    copies = max(sets, min(64, (300 << 20) // max(B * 2 * ring_bytes, 1)))
+    cap_items = lib.lfm3_attention_max_items(B, int(pos.max()))
+    items = (L.AttentionItem * cap_items)()
+    count = L.check(lib.lfm3_attention_plan(L.ptr(pos), B, window, items, cap_items))
+    ditems = L.DeviceBuffer(count * L.C.sizeof(L.AttentionItem))
+    L.hip_check(L.hip().hipMemcpy(ditems.addr, L.C.addressof(items),
+                                  count * L.C.sizeof(L.AttentionItem), L.H2D))
+    ws_bytes = lib.lfm3_attention_workspace_bytes(count, B, heads, kv, D)
+    ws = L.DeviceBuffer(max(ws_bytes, 4))
+    dpos = L.DeviceBuffer.of(pos)
+    dcap = L.DeviceBuffer.of(np.full(B, cap, np.uint32))
+    qn = L.DeviceBuffer.of(L.normal(L.SEED, f"c2.qn{D}", D, 1, 0.02))
+    kn = L.DeviceBuffer.of(L.normal(L.SEED, f"c2.kn{D}", D, 1, 0.02))
+    i = np.arange(D // 2, dtype=np.float64)
+    freq = L.DeviceBuffer.of(np.power(1e6, -2.0 * i / D).astype(np.float32))
+    factors = L.DeviceBuffer.of(np.ones(D // 2, np.float32))
+    proj = L.DeviceBuffer.of(L.normal(L.SEED, f"c2.proj{heads}.{D}", B * ld))
+    outb = L.DeviceBuffer(B * heads * D * 4)
+    # one ring of N(0, 1) halves, copied into every ring of every set
+    src = L.DeviceBuffer.of(L.half_normal(L.SEED, f"c2.kv{D}.{window}", cap * stride))
+    rings = []
+    for c in range(copies):
+        ks = [L.DeviceBuffer(ring_bytes) for _ in range(B)]
+        vs = [L.DeviceBuffer(ring_bytes) for _ in range(B)]
+        for b in ks + vs:
+            L.hip_check(L.hip().hipMemcpy(b.addr, src.addr, ring_bytes, 3))  # D2D
+        tk = L.DeviceBuffer.of(np.array([b.addr for b in ks], np.uint64))
+        tv = L.DeviceBuffer.of(np.array([b.addr for b in vs], np.uint64))
+        rings.append((ks, vs, tk, tv))
+    L.synchronize()
+    k_off, v_off, g_off = heads * D, heads * D + stride, heads * D + 2 * stride
+
+    def launch(c, stream):
+        _, _, tk, tv = rings[c]
+        L.check(lib.lfm3_decode_heads_attention_ragged(
+            proj.addr, proj.addr + 4 * k_off, proj.addr + 4 * v_off, ld, proj.addr + 4 * g_off,
+            ld, qn.addr, kn.addr, freq.addr, 0 if window else factors.addr, tk.addr, tv.addr,
+            dpos.addr, dcap.addr, ditems.addr, count, outb.addr, heads * D, B, heads, kv, D,
+            1e-5, ws.addr, ws_bytes, stream))
+
+    us = time_launches(launch, copies, passes)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    kind = f"sliding-{window}" if window else "global"
+    return {"kernel": f"heads + decode attention, {heads}q/{kv}kv x {D}, {kind}, 8 rows "
+                      f"({count} spans; {copies} cache sets rotated)",
+            "us": round(us, 3), "bytes": int(nbytes), "GBps": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def config_conv(passes: int):
+    """Config 3: the gated width-7 short-convolution block of 8 sessions
+    (hidden 2048; in projection 6144 x 2048 with the step in its epilogue,
+    from the normed rows' operand image; out projection 2048 x 2048 in K
+    parts; FP32 histories [8][2048][6] N(0, 1), taps N(0, 0.1)), two launches
+    a block, 24 rotated weight copies; and the prefill variant, the packed
+    prompt convolution over segments of {512, 37, 300, 1} rows (850 rows,
+    each continuing its own session's history), from their in-projection
+    rows."""
+    lib = L.lib()
+    seed = L.SEED
+    H, B, W = 2048, SESSIONS, 7
+    x = L.DeviceBuffer.of(L.normal(seed, "c3.x", B * H))
+    wts = L.DeviceBuffer.of(np.ones(H, np.float32))
+    image = L.DeviceBuffer(lib.lfm3_operand_image_bytes(H))
+    exps = L.DeviceBuffer(32)
+    L.check(lib.lfm3_residual_norm_image(None, 1, 0, None, x.addr, wts.addr, None, image.addr,
+                                         exps.addr, B, H, 1e-5, None))
+    taps = L.DeviceBuffer.of(L.normal(seed, "c3.taps", H * W, 0, 0.1))
+    hists = [L.DeviceBuffer.of(L.normal(seed, f"c3.h{r}", H * (W - 1))) for r in range(B)]
+    table = L.DeviceBuffer.of(np.array([h.addr for h in hists], np.uint64))
+    copies = 24
+    ins = packed_copies([(L.q8(seed, "c3.in", 3 * H, H), 3 * H, 0, 1)], 3 * H, H, copies)
+    outs = packed_copies([(L.q8(seed, "c3.out", H, H), H, 0, 1)], H, H, copies)
+    a = L.DeviceBuffer(B * H * 4)
+    parts = lib.lfm3_q8_gemv_parts(H, H)
+    y = L.DeviceBuffer(parts * B * H * 4)
+
+    def block(i, s):
+        L.check(lib.lfm3_q8_gemv_conv_image(ins[i][0].addr, ins[i][1].addr, H, image.addr,
+                                            exps.addr, B, taps.addr, table.addr, W, a.addr, H,
+                                            s))
+        L.check(lib.lfm3_q8_gemv_partials(outs[i][0].addr, outs[i][1].addr, H, H, a.addr, H,
+                                          y.addr, H, B, parts, s))
+
+    us = time_launches(block, copies, passes)
+    nbytes = (q8_bytes(3 * H, H) + q8_bytes(H, H) + B * H * 4  # weights, normed rows
+              + B * H * (W - 1) * 4 * 2                        # histories read and written
+              + B * H * 4 * 2 + parts * B * H * 4)             # y written and read, out parts
+    gbs = nbytes / (us * 1e-6) / 1e9
+    block_line = {"kernel": f"convolution block, 8 rows: in projection 6144 x 2048 + step, out "
+                            f"projection 2048 x 2048 in {parts} K parts (two launches)",
+                  "us": round(us, 3), "bytes": int(nbytes), "GBps": round(gbs, 1),
+                  "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    del ins, outs
+    # the packed prompt convolution
+    seg = [512, 37, 300, 1]
+    n = sum(seg)
+    begins = np.cumsum([0] + seg[:-1]).astype(np.uint32)
+    p = L.DeviceBuffer.of(L.normal(seed, "c3.p", n * 3 * H))
+    yp = L.DeviceBuffer(n * H * 4)
+    phist = [L.DeviceBuffer.of(L.normal(seed, f"c3.ph{r}", H * (W - 1))) for r in range(4)]
+    hp = (L.C.c_void_p * 4)(*[h.addr for h in phist])
+    rows = np.asarray(seg, np.uint32)
+
+    def conv(i, s):
+        L.check(lib.lfm3_conv_prompt(p.addr, 3 * H, taps.addr, hp, L.ptr(begins), L.ptr(rows), 4,
+                                     yp.addr, H, H, W, 0, s))
+
+    us = time_launches(conv, 8, passes)
+    nbytes = n * H * 4 * 4 + 4 * H * (W - 1) * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    prefill_line = {"kernel": "packed prompt convolution, segments {512, 37, 300, 1} (850 rows), "
+                              "hidden 2048, width 7",
+                    "us": round(us, 3), "bytes": int(nbytes), "GBps": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return block_line, prefill_line
+
+
 def projection_weights(d: L.Dims) -> int:
     """Weight elements of every projection a token's row goes through (the
     vocabulary head excluded)."""
@@ -683,6 +818,32 @@ def prefill_and_mixed(model, dims, seed, reps: int, warmup: int):
     return pass_ms, times, [int(c) for c in ctx]
 
 
+def usable_cores(hw: int) -> int:
+    """The cores this process may run on: its CPU affinity, capped by a
+    cgroup CPU quota where one is set (cgroup v2 cpu.max, or v1
+    cfs_quota_us / cfs_period_us)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else hw
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+            if q != "max":
+                quota = int(q) / int(period)
+    except (OSError, ValueError):
+        try:
+            with open("/sys/fs/cgroup/cpu/cpu.cfs_quota_us") as f:
+                q = int(f.read())
+            with open("/sys/fs/cgroup/cpu/cpu.cfs_period_us") as f:
+                period = int(f.read())
+            if q > 0:
+                quota = q / period
+        except (OSError, ValueError):
+            pass
+    if quota is not None:
+        n = min(n, max(1, int(quota)))
+    return max(1, n)
+
+
 def cpu_model() -> str:
     """The host CPU's model name from /proc/cpuinfo."""
     try:
@@ -714,9 +875,8 @@ def cpu_baseline(dims, weights, ctx, tokens, seed):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     hw = O.hardware_concurrency()
-    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else hw
-    # The GPU host grants this process a share of its cores (16 a GPU).
-    cores = max(1, min(usable, 16))
+    usable = usable_cores(hw)
+    cores = usable
     om = O.Model(dims, weights)
 
     def fresh_sessions(extra):
@@ -896,6 +1056,15 @@ def main():
     for g in sweep:
         log(f"gemv B={g['batch']}: {g['us']:.2f} us/launch, "
             f"{g['bytes'] / (g['us'] * 1e-6) / 1e9:.0f} GB/s")
+    # Config 2: one layer's ragged decode attention at contexts U[1, 4096],
+    # both head shapes, global and sliding; config 3: the convolution block
+    # and the packed prompt convolution.
+    ctx2 = L.uniform_u32(seed, "bench.attn.ctx", SESSIONS, 1, 4096)
+    config2 = [config_attention(ctx2, h, kv, D, w, 6)
+               for h, kv, D in ((32, 8, 64), (16, 4, 128)) for w in (0, 256)]
+    conv_block, conv_prompt = config_conv(6)
+    for k in config2 + [conv_block, conv_prompt]:
+        log(f"{k['kernel']}: {k['us']:.2f} us, {k['GBps']:.0f} GB/s ({100 * k['frac']:.1f}%)")
 
     result = {
         "metric": "decode tok/s @8 sessions (HBM GB/s % peak); 512-tok prefill pass ms (MFMA %)",
@@ -956,6 +1125,15 @@ def main():
                       for g in sweep],
             "traffic_read_write": [GEMV_TRAFFIC["read"], GEMV_TRAFFIC["write"]],
         },
+        "attention_one_layer": {
+            "workload": ("one layer's fused Q/K norm, RoPE (theta 1e6), gate and ragged decode "
+                         "attention, 8 sessions at contexts uniform in [1, 4096], F16 K/V rings "
+                         "(capacity 4096 global, 256 sliding)"),
+            "contexts": [int(c) for c in ctx2],
+            "lines": config2,
+        },
+        "conv_block": conv_block,
+        "conv_prompt_packed": conv_prompt,
     }
     ceilings = device_ceilings()
     log(f"measured ceilings: streaming read {ceilings['stream_read_GBps']:.0f} GB/s, "
