@@ -520,6 +520,19 @@ int lfm3_conv_prompt(const float* p, uint32_t ldp, const float* taps,
                      const uint32_t* rows, uint32_t segments, float* y,
                      uint32_t ldy, uint32_t hidden, uint32_t width,
                      int update_history, void* stream);
+/* lfm3_conv_prompt over one segment of `rows` rows fused with
+   lfm3_half_rows of its output: rows r >= skip of the convolution output go
+   to out + (r - skip) * lda as FP16 row-scaled activations with scale[r -
+   skip] (bit-identical to the two calls; chunk tails zeroed), and no FP32
+   output is written. Rows before skip only feed the windows. hidden % 4 ==
+   0 and at most 2048, width 2..7, lda % 64 == 0. Replaces: gpu::ShortConv
+   with n > 1 (hip/ops.hip:2250-2264) followed by the out projection's
+   HalfRows (q8_prefill.hpp:30-51), for prompts of 16 rows or more. */
+int lfm3_conv_prompt_half(const float* p, uint32_t ldp, const float* taps,
+                          float* history, uint32_t rows, uint32_t skip,
+                          uint16_t* out, uint32_t lda, float* scale,
+                          uint32_t hidden, uint32_t width, int update_history,
+                          void* stream);
 /* Per-head Q/K RMSNorm and paired RoPE of `rows` chunk rows at positions
    position + r (q/k/v rows of stride ld floats, rotated in place), and the
    F16 K/V of row r stored to row r of k16/v16 (kv_heads * dim halves a
@@ -584,6 +597,26 @@ int lfm3_prompt_attention(const float* q, uint32_t ldq, const uint16_t* k,
                           uint32_t position, uint32_t capacity,
                           uint32_t window, void* workspace,
                           size_t workspace_bytes, void* stream);
+/* lfm3_prompt_attention with its output written as the output projection's
+   FP16 row-scaled activations: row r's heads * dim outputs (the same FP32
+   values) go to out + r * lda as fp16(out 2^e) with scale[r] = 2^-e, e =
+   14 - ilogb(max |row|) (lfm3_half_rows of the FP32 output, bit for bit).
+   Every call keeps per-span partial sums in the workspace
+   (lfm3_prompt_attention_half_workspace_bytes, at least one span); a
+   per-row merge writes the rows. lda % 64 == 0, lda >= heads * dim.
+   Replaces: gpu::Attention with n > 1 (hip/ops.hip:2316-2332) followed by
+   the out projection's HalfRows (q8_prefill.hpp:30-51). */
+size_t lfm3_prompt_attention_half_workspace_bytes(uint32_t rows, uint32_t heads,
+                                                  uint32_t dim, uint32_t position,
+                                                  uint32_t window);
+int lfm3_prompt_attention_half(const float* q, uint32_t ldq, const uint16_t* k,
+                               const uint16_t* v, const float* gate, uint32_t ldg,
+                               const uint16_t* cache_k, const uint16_t* cache_v,
+                               uint16_t* out, uint32_t lda, float* scale,
+                               uint32_t rows, uint32_t heads, uint32_t kv_heads,
+                               uint32_t dim, uint32_t position, uint32_t capacity,
+                               uint32_t window, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------
  * Engine: Model / Session (engine.hpp:17-163).

@@ -1284,8 +1284,10 @@ PromptBuffers& EnsurePromptBuffers(lfm3_model& m) {
   b->chunk_k = Buffer(R * std::max<std::size_t>(kv_max, 1) * D * 2);
   b->chunk_v = Buffer(R * std::max<std::size_t>(kv_max, 1) * D * 2);
   b->attn_ws_bytes = std::max<std::size_t>(
-      lfm3_prompt_attention_workspace_bytes(std::uint32_t(R), c.heads, std::uint32_t(D),
-                                            c.context, 0),
+      std::max(lfm3_prompt_attention_workspace_bytes(std::uint32_t(R), c.heads,
+                                                     std::uint32_t(D), c.context, 0),
+               lfm3_prompt_attention_half_workspace_bytes(std::uint32_t(R), c.heads,
+                                                          std::uint32_t(D), c.context, 0)),
       256);
   b->attn_ws = Buffer(b->attn_ws_bytes);
   b->one_items = lfm3_attention_max_items(1, c.context);
@@ -1509,10 +1511,17 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
       // Rows before the first live one are not read: outputs that would
       // need them are not live either (engine.cpp:386-393).
       float* hist = state.conv.as<float>();
-      const std::uint32_t begin = 0;
-      CheckStatus(lfm3_conv_prompt(proj, 3 * H, l.conv.as<float>(), &hist, &begin, &rows_in, 1,
-                                   mix, H, H, c.conv_width, 1, s));
-      parts = dense(l.out_proj, mix + std::size_t(o - o_in) * H, H, rows_out, nullptr);
+      if (rows_out >= mfma_rows && c.conv_width <= 7 && H % 4 == 0 && H <= 2048) {
+        // The output projection's FP16 rows straight from the convolution.
+        CheckStatus(lfm3_conv_prompt_half(proj, 3 * H, l.conv.as<float>(), hist, rows_in,
+                                          o - o_in, a16, lda, scale, H, c.conv_width, 1, s));
+        parts = gemm(l.out_proj, 0, rows_out, out, H);
+      } else {
+        const std::uint32_t begin = 0;
+        CheckStatus(lfm3_conv_prompt(proj, 3 * H, l.conv.as<float>(), &hist, &begin, &rows_in,
+                                     1, mix, H, H, c.conv_width, 1, s));
+        parts = dense(l.out_proj, mix + std::size_t(o - o_in) * H, H, rows_out, nullptr);
+      }
     } else {
       const bool swa = l.type == LFM3_LAYER_SLIDING;
       const std::uint32_t stride = l.kv * D;
@@ -1565,6 +1574,12 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
             b.one_ws_bytes, s));
         // The staging buffer is reused by the next layer's row.
         Check(hipStreamSynchronize(s), "decode attention row");
+      } else if (rows_out >= mfma_rows) {
+        // The output projection's FP16 rows straight from the attention.
+        CheckStatus(lfm3_prompt_attention_half(
+            q_rows, pld, kc + std::size_t(skip) * stride, vc + std::size_t(skip) * stride,
+            g_rows, pld, ck, cv, a16, lda, scale, n - skip, c.heads, l.kv, D, position + skip,
+            state.capacity, swa ? c.window : 0, b.attn_ws.p, b.attn_ws_bytes, s));
       } else {
         CheckStatus(lfm3_prompt_attention(
             q_rows, pld, kc + std::size_t(skip) * stride, vc + std::size_t(skip) * stride,
@@ -1574,8 +1589,11 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
       }
       if (swa)
         CheckStatus(lfm3_store_kv(kc, vc, ck, cv, n, stride, position, state.capacity, s));
-      parts = dense(l.attn_out, mix + std::size_t(o) * c.heads * D, c.heads * D, rows_out,
-                    nullptr);
+      if (rows_out >= mfma_rows)
+        parts = gemm(l.attn_out, 0, rows_out, out, H);
+      else
+        parts = dense(l.attn_out, mix + std::size_t(o) * c.heads * D, c.heads * D, rows_out,
+                      nullptr);
     }
     residual_norm(parts, &l.post_norm, &l.ffn_norm, rows_out, rows_out);
     // FFN over the live rows: SwiGLU (with each row's max |y| per block of

@@ -325,7 +325,6 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
       h8 w[RT];
-      float d[RT];
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
         if constexpr (Shape::kHalfTiles)
@@ -333,57 +332,59 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
                                               blk * kTileCodeBytes + lane * 16);
         else
           w[r] = blk ? EightCodes(q[r].z, q[r].w) : EightCodes(q[r].x, q[r].y);
-        // An opaque conversion keeps the scale FMAs as in-place v_fmac_f32
-        // (a v_fma_mix_f32 reading the half would write a fresh register).
-        asm("v_cvt_f32_f16 %0, %1" : "=v"(d[r]) : "v"(blk ? sc[r] >> 16 : sc[r]));
       }
+      // acc += d * p, with d the block's fp16 scale (the low half of the
+      // tile's scale dword for block 0, the high half for block 1) read by
+      // v_fma_mix_f32 as an exact FP32 value: one rounding, as the
+      // conversion followed by an FMA, without the conversion and shift.
+      // Written as assembly tied to the accumulator so it updates in place.
+      const auto scale_fma = [&](float& a, int r, float p) {
+        if (blk)
+          asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+              : "+v"(a) : "v"(sc[r]), "v"(p));
+        else
+          asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
+              : "+v"(a) : "v"(sc[r]), "v"(p));
+      };
       const int slot = (blk * 4 + (lane >> 4)) ^ (lane & 7);
       const auto a_frag = [&](int t) {
         return *reinterpret_cast<const h8*>(stage + (t * 16 + a_row) * 128 + slot * 16);
       };
       // Software pipeline over token groups: the MFMAs of group t issue
-      // beside the scale FMAs of group t - 1; a scheduling barrier per
-      // group and the register pins keep the compiler from hoisting every
-      // MFMA of the chunk (which would hold 4 RT TT result registers).
+      // beside the scale FMAs of group t - 1, in a fixed order (the A read
+      // for t + 1, then each MFMA of t followed by the 4 FMAs of t - 1 on
+      // the previous MFMA's tile), so the matrix pipe runs while the VALU
+      // works; the scheduling barriers also keep the compiler from
+      // hoisting every MFMA of the chunk (which would hold 4 RT TT result
+      // registers).
       h8 av = a_frag(0);
       f4 prev[RT];
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
         const h8 next = a_frag(t + 1 < TT ? t + 1 : t);
         f4 cur[RT];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int r = 0; r < RT; ++r)
+        for (int r = 0; r < RT; ++r) {
           cur[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, w[r], zero, 0, 0, 0);
-        if (t > 0) {
-#pragma unroll
-          for (int r = 0; r < RT; ++r)
+          __builtin_amdgcn_sched_barrier(0);
+          if (t > 0) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              acc[r][t - 1][i] = fmaf(d[r], prev[r][i], acc[r][t - 1][i]);
-          asm volatile("" : LFM3_PIN4(acc[0][t - 1]), LFM3_PIN4(acc[1][t - 1]),
-                       LFM3_PIN4(acc[2][t - 1]), LFM3_PIN4(acc[3][t - 1]));
+              scale_fma(acc[r][t - 1][i], r, prev[r][i]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int r = 0; r < RT; ++r)
           prev[r] = cur[r];
         av = next;
-        // Issue order: the A read for t + 1, then each MFMA of t followed
-        // by 4 FMAs of t - 1, so the matrix pipe runs while the VALU works.
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        if (t > 0) {
-#pragma unroll
-          for (int r = 0; r < RT; ++r) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int r = 0; r < RT; ++r)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          acc[r][TT - 1][i] = fmaf(d[r], prev[r][i], acc[r][TT - 1][i]);
+          scale_fma(acc[r][TT - 1][i], r, prev[r][i]);
       asm volatile("" : LFM3_PIN4(acc[0][TT - 1]), LFM3_PIN4(acc[1][TT - 1]),
                    LFM3_PIN4(acc[2][TT - 1]), LFM3_PIN4(acc[3][TT - 1]));
     }

@@ -458,6 +458,80 @@ __launch_bounds__(D) __global__
   out[std::size_t(row) * ldo + head * D + d] = (acc / sum) / (1.0f + expf(-g));
 }
 
+// The span merge of one query row over all its heads, fused with the FP16
+// row-scaled activations of the attention output (the output projection's
+// GEMM input, hip/q8_prefill.hpp:27-51): a thread takes 4 dimensions of one
+// head, merges the spans with CombineSpansKernel's expressions and order
+// (a single span reduces to the tile kernel's own (acc / sum) / (1 +
+// e^-gate)), the block reduces the row's max |out|, and the row is stored
+// as fp16(out 2^e) with scale 2^-e (HalfRowsKernel's expressions).
+constexpr int kCombineDims = 4;
+
+template<int D>
+__launch_bounds__(1024) __global__
+    void CombineRowsHalfKernel(const float* __restrict__ partial, const float* __restrict__ gate,
+                               int ldg, Half* __restrict__ out, int lda,
+                               float* __restrict__ scale, int n, int heads, int splits) {
+  __shared__ float s_max[16];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  constexpr int kPerHead = D / kCombineDims;
+  const bool live = tid < heads * kPerHead;
+  const int head = live ? tid / kPerHead : 0, d0 = (tid % kPerHead) * kCombineDims;
+  const std::size_t rh = std::size_t(row) * heads + head, rows = std::size_t(n) * heads;
+  float m[kMaxSpans], l[kMaxSpans], a[kMaxSpans][kCombineDims];
+#pragma unroll
+  for (int s = 0; s < kMaxSpans; ++s) {
+    const float* part = partial + (s * rows + rh) * (D + 2);
+    const bool on = live && s < splits;
+    // Records are D + 2 floats: 8-byte aligned pairs.
+    const float2 ml = on ? *reinterpret_cast<const float2*>(part) : make_float2(-INFINITY, 0.0f);
+    const float2 v0 = on ? *reinterpret_cast<const float2*>(part + 2 + d0) : make_float2(0, 0);
+    const float2 v1 = on ? *reinterpret_cast<const float2*>(part + 4 + d0) : make_float2(0, 0);
+    m[s] = ml.x;
+    l[s] = ml.y;
+    a[s][0] = v0.x;
+    a[s][1] = v0.y;
+    a[s][2] = v1.x;
+    a[s][3] = v1.y;
+  }
+  const float g = live ? gate[std::size_t(row) * ldg + head] : 0.0f;
+  float maximum = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kMaxSpans; ++s)
+    maximum = fmaxf(maximum, m[s]);
+  float sum = 0.0f, acc[kCombineDims] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < kMaxSpans; ++s) {
+    if (s < splits) {
+      const float w = __builtin_amdgcn_exp2f(m[s] - maximum);
+      sum = fmaf(l[s], w, sum);
+#pragma unroll
+      for (int i = 0; i < kCombineDims; ++i)
+        acc[i] = fmaf(a[s][i], w, acc[i]);
+    }
+  }
+  float o[kCombineDims], largest = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kCombineDims; ++i) {
+    o[i] = (acc[i] / sum) / (1.0f + expf(-g));
+    largest = live ? fmaxf(largest, fabsf(o[i])) : largest;
+  }
+  largest = WaveMax(largest);
+  if ((tid & 63) == 0)
+    s_max[tid >> 6] = largest;
+  __syncthreads();
+  float row_max = 0.0f;
+  for (int w = 0; w < int(blockDim.x) / 64; ++w)
+    row_max = fmaxf(row_max, s_max[w]);
+  const int e = RowExponent(row_max);
+  if (tid == 0)
+    scale[row] = ldexpf(1.0f, -e);
+  if (live)
+    *reinterpret_cast<uint2*>(out + std::size_t(row) * lda + head * D + d0) =
+        make_uint2(unsigned(ScaledHalf(o[0], e)) | (unsigned(ScaledHalf(o[1], e)) << 16),
+                   unsigned(ScaledHalf(o[2], e)) | (unsigned(ScaledHalf(o[3], e)) << 16));
+}
+
 struct PromptArgs {
   const float* q;
   int ldq;
@@ -471,6 +545,10 @@ struct PromptArgs {
   int ldo;
   float* partial;
   int n, heads, kv_heads, position, capacity, window, span, splits;
+  // FP16 rows out (partials for every span, merged by CombineRowsHalfKernel).
+  Half* out16 = nullptr;
+  int lda = 0;
+  float* scale = nullptr;
 };
 
 // Long histories: two column tiles a wave (each K / V operand read feeds two
@@ -503,7 +581,8 @@ void LaunchTiles(const PromptArgs& a, hipStream_t s) {
   const int blocks = (pairs + 7) / 8 * 8 * row_blocks;
   PromptAttentionKernel<D, G, CT><<<blocks, kPAThreads, 0, s>>>(
       a.q, a.ldq, a.k, a.v, a.gate, a.ldg, a.ck, a.cv, a.out, a.ldo,
-      a.splits > 1 ? a.partial : nullptr, a.n, a.heads, a.kv_heads, a.position, a.capacity,
+      a.splits > 1 || a.out16 ? a.partial : nullptr, a.n, a.heads, a.kv_heads, a.position,
+      a.capacity,
       a.window, a.span, row_blocks, a.splits);
 }
 
@@ -513,9 +592,14 @@ void LaunchPrompt(const PromptArgs& a, hipStream_t s) {
     LaunchTiles<D, G, 2>(a, s);
   else
     LaunchTiles<D, G, 1>(a, s);
-  if (a.splits > 1)
+  if (a.out16) {
+    const int threads = (a.heads * (D / kCombineDims) + 63) / 64 * 64;
+    CombineRowsHalfKernel<D><<<a.n, threads, 0, s>>>(a.partial, a.gate, a.ldg, a.out16, a.lda,
+                                                     a.scale, a.n, a.heads, a.splits);
+  } else if (a.splits > 1) {
     CombineSpansKernel<D><<<a.n * a.heads, D, 0, s>>>(a.partial, a.gate, a.ldg, a.out, a.ldo,
                                                        a.n, a.heads, a.splits);
+  }
 }
 
 template<int D>
@@ -550,18 +634,35 @@ std::size_t lfm3_prompt_attention_workspace_bytes(std::uint32_t rows, std::uint3
   return spans > 1 ? std::size_t(spans) * rows * heads * (dim + 2) * sizeof(float) : 0;
 }
 
-int lfm3_prompt_attention(const float* q, std::uint32_t ldq, const std::uint16_t* k,
-                          const std::uint16_t* v, const float* gate, std::uint32_t ldg,
-                          const std::uint16_t* cache_k, const std::uint16_t* cache_v,
-                          float* out, std::uint32_t ldo, std::uint32_t rows,
-                          std::uint32_t heads, std::uint32_t kv_heads, std::uint32_t dim,
-                          std::uint32_t position, std::uint32_t capacity,
-                          std::uint32_t window, void* workspace, std::size_t workspace_bytes,
-                          void* stream) {
+std::size_t lfm3_prompt_attention_half_workspace_bytes(std::uint32_t rows, std::uint32_t heads,
+                                                       std::uint32_t dim, std::uint32_t position,
+                                                       std::uint32_t window) {
+  return std::size_t(MostSpans(position, rows, window)) * rows * heads * (dim + 2) *
+         sizeof(float);
+}
+
+}  // extern "C"
+
+namespace lfm3amd {
+namespace {
+// lfm3_prompt_attention (out, ldo) and lfm3_prompt_attention_half (out16,
+// lda, scale): one check and plan.
+int PromptAttention(const float* q, std::uint32_t ldq, const std::uint16_t* k,
+                    const std::uint16_t* v, const float* gate, std::uint32_t ldg,
+                    const std::uint16_t* cache_k, const std::uint16_t* cache_v, float* out,
+                    std::uint32_t ldo, std::uint16_t* out16, std::uint32_t lda, float* scale,
+                    std::uint32_t rows, std::uint32_t heads, std::uint32_t kv_heads,
+                    std::uint32_t dim, std::uint32_t position, std::uint32_t capacity,
+                    std::uint32_t window, void* workspace, std::size_t workspace_bytes,
+                    void* stream) {
   const std::uint32_t group = kv_heads ? heads / kv_heads : 0;
-  if (!q || !k || !v || !gate || !out || !rows || !heads || !kv_heads || heads % kv_heads ||
+  const bool half = out16 != nullptr;
+  if (half ? (!scale || lda % kChunk || lda < heads * dim || heads * dim / kCombineDims > 1024)
+           : (!out || ldo < heads * dim || ldo % 4))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt attention output");
+  if (!q || !k || !v || !gate || !rows || !heads || !kv_heads || heads % kv_heads ||
       (group != 2 && group != 4 && group != 8) || (dim != 64 && dim != 128) ||
-      ldq < heads * dim || ldo < heads * dim || ldg < heads || ldq % 4 || ldo % 4 ||
+      ldq < heads * dim || ldg < heads || ldq % 4 ||
       (position && (!cache_k || !cache_v || !capacity)) ||
       (!window && position && capacity < position) ||
       // A sliding row at `position` reads the ring's last min(window - 1,
@@ -573,8 +674,9 @@ int lfm3_prompt_attention(const float* q, std::uint32_t ldq, const std::uint16_t
     return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt attention shape");
   PromptArgs a{};
   a.splits = PlanCall(int(rows), int(position), int(window), int(group), int(kv_heads), a.span);
-  const std::size_t need =
-      a.splits > 1 ? std::size_t(a.splits) * rows * heads * (dim + 2) * sizeof(float) : 0;
+  const std::size_t need = a.splits > 1 || half
+                               ? std::size_t(a.splits) * rows * heads * (dim + 2) * sizeof(float)
+                               : 0;
   if (need && (!workspace || workspace_bytes < need))
     return Fail(LFM3_E_INVALID, "LFM3 prompt attention workspace too small");
   a.q = q;
@@ -587,6 +689,9 @@ int lfm3_prompt_attention(const float* q, std::uint32_t ldq, const std::uint16_t
   a.cv = cache_v;
   a.out = out;
   a.ldo = int(ldo);
+  a.out16 = out16;
+  a.lda = int(lda);
+  a.scale = scale;
   a.partial = static_cast<float*>(workspace);
   a.n = int(rows);
   a.heads = int(heads);
@@ -600,6 +705,40 @@ int lfm3_prompt_attention(const float* q, std::uint32_t ldq, const std::uint16_t
   else
     LaunchPromptGroup<64>(a, int(group), s);
   return HipStatus(hipGetLastError(), "LFM3 prompt attention launch");
+}
+}  // namespace
+}  // namespace lfm3amd
+
+extern "C" {
+
+int lfm3_prompt_attention(const float* q, std::uint32_t ldq, const std::uint16_t* k,
+                          const std::uint16_t* v, const float* gate, std::uint32_t ldg,
+                          const std::uint16_t* cache_k, const std::uint16_t* cache_v,
+                          float* out, std::uint32_t ldo, std::uint32_t rows,
+                          std::uint32_t heads, std::uint32_t kv_heads, std::uint32_t dim,
+                          std::uint32_t position, std::uint32_t capacity,
+                          std::uint32_t window, void* workspace, std::size_t workspace_bytes,
+                          void* stream) {
+  if (!out)
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt attention output");
+  return PromptAttention(q, ldq, k, v, gate, ldg, cache_k, cache_v, out, ldo, nullptr, 0,
+                         nullptr, rows, heads, kv_heads, dim, position, capacity, window,
+                         workspace, workspace_bytes, stream);
+}
+
+int lfm3_prompt_attention_half(const float* q, std::uint32_t ldq, const std::uint16_t* k,
+                               const std::uint16_t* v, const float* gate, std::uint32_t ldg,
+                               const std::uint16_t* cache_k, const std::uint16_t* cache_v,
+                               std::uint16_t* out, std::uint32_t lda, float* scale,
+                               std::uint32_t rows, std::uint32_t heads, std::uint32_t kv_heads,
+                               std::uint32_t dim, std::uint32_t position, std::uint32_t capacity,
+                               std::uint32_t window, void* workspace,
+                               std::size_t workspace_bytes, void* stream) {
+  if (!out)
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt attention output");
+  return PromptAttention(q, ldq, k, v, gate, ldg, cache_k, cache_v, nullptr, 0, out, lda, scale,
+                         rows, heads, kv_heads, dim, position, capacity, window, workspace,
+                         workspace_bytes, stream);
 }
 
 }  // extern "C"

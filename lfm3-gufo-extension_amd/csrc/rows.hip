@@ -527,6 +527,213 @@ __global__ void PromptConvKernel(const float* __restrict__ p, int ldp,
     WriteConvHistory<L>(ps, ldp, H, ch, rows, hist, L);
 }
 
+// The prompt convolution of one segment fused with the FP16 row-scaled
+// activations of its output (the output projection's GEMM input,
+// hip/q8_prefill.hpp:27-51): a block owns kConvHalfRows consecutive rows and
+// every channel, so each output row is whole in the block. A thread takes V
+// consecutive channels, keeps PromptConvKernel's expressions and order for
+// every output, the block reduces each row's max |y|, and the row is stored
+// as fp16(y 2^e) with scale 2^-e (HalfRowsKernel's expressions), so the FP16
+// rows equal lfm3_conv_prompt followed by lfm3_half_rows bit for bit.
+// Outputs of rows before `skip` are not stored (no later layer reads
+// them); their products still feed the windows of the live rows. Block 0
+// holds the lowest rows: it alone reads the old history (kConvHalfRows >=
+// L - 1, so later blocks' windows start at row 0 or after), and it writes
+// the new one after the block barrier that follows every thread's reads.
+// Six rows a block (86 blocks for 512 rows; 8 rows: 9.5 us against 8.5
+// for the 512-row pass shape) and four channels a thread (two: 9.5 us).
+constexpr int kConvHalfRows = 6, kConvHalfV = 4;
+constexpr int kConvHalfMaxHidden = 2048, kConvHalfMaxThreads = kConvHalfMaxHidden / kConvHalfV;
+// Widths past 7 hold more than the 256 registers a lane has here.
+constexpr int kConvHalfMaxWidth = 7;
+static_assert(kConvHalfMaxWidth <= kConvHalfRows + 1, "window within the block's reach");
+
+// V consecutive floats at a 4 V-byte aligned offset (zeros out of range).
+template<int V>
+__device__ __forceinline__ void LoadVec(BufferResource res, unsigned offset, float* v) {
+  if constexpr (V == 4) {
+    const float4 f = LoadF4(res, offset);
+    v[0] = f.x;
+    v[1] = f.y;
+    v[2] = f.z;
+    v[3] = f.w;
+  } else if constexpr (V == 2) {
+    typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    const u2 f = __builtin_amdgcn_raw_buffer_load_b64(res, offset, 0, 0);
+    v[0] = __uint_as_float(f.x);
+    v[1] = __uint_as_float(f.y);
+  } else {
+    v[0] = __uint_as_float(LoadB32(res, offset));
+  }
+}
+
+template<int L, int V>
+__launch_bounds__(kConvHalfMaxThreads) __global__ void PromptConvHalfKernel(
+    const float* __restrict__ p, int ldp, const float* __restrict__ taps,
+    float* __restrict__ history, int rows, int skip, int first0, Half* __restrict__ out,
+    int lda, float* __restrict__ scale, int H, int update_history) {
+#pragma clang fp contract(off)
+  static_assert(L >= 2 && L <= kConvHalfMaxWidth, "supported width");
+  constexpr int R = kConvHalfRows;
+  __shared__ float s_max[R][kConvHalfMaxThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int waves = int(blockDim.x) / 64;
+  const int first = first0 + int(blockIdx.x) * R;
+  const int padded = (H + kChunk - 1) / kChunk * kChunk;
+  const bool live = tid * V < H;
+  const int c0 = live ? tid * V : 0;
+  // Buffer loads throughout: a row outside its range reads zeros without a
+  // branch, and every load of a thread is issued before the first product.
+  const BufferResource p_res = MakeBuffer(p, unsigned(std::size_t(rows) * ldp * 4));
+  const BufferResource t_res = MakeBuffer(taps, unsigned(H * L * 4));
+  const BufferResource h_res = MakeBuffer(history, unsigned(H * (L - 1) * 4));
+  const bool history_block = update_history && blockIdx.x == 0;
+  // The thread's taps (V L consecutive floats).
+  float tw[V * L];
+#pragma unroll
+  for (int i = 0; i < L; ++i)
+    LoadVec<V>(t_res, unsigned((c0 * L + V * i) * 4), tw + V * i);
+  // The L - 1 products before the block's first row: for the block at row 0
+  // the old history (every such row is before the segment; V (L - 1)
+  // consecutive floats), taken as the entry times an exact 1; for any other
+  // block (first >= kConvHalfRows >= L - 1) B x of rows of p.
+  float pb[L - 1][V], px[L - 1][V], hv[V * (L - 1)];
+  if (first == 0) {
+#pragma unroll
+    for (int i = 0; i < L - 1; ++i)
+      LoadVec<V>(h_res, unsigned((c0 * (L - 1) + V * i) * 4), hv + V * i);
+  } else {
+#pragma unroll
+    for (int t = 0; t < L - 1; ++t) {
+      const unsigned at = unsigned((std::size_t(first - (L - 1) + t) * ldp + c0) * 4);
+      LoadVec<V>(p_res, at, pb[t]);
+      LoadVec<V>(p_res, at + unsigned(2 * H) * 4u, px[t]);
+    }
+  }
+  // B, C, x of the block's rows (rows past the segment read zeros and are
+  // not stored).
+  float bv[R][V], cv[R][V], xv[R][V];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int r = first + i;
+    const unsigned at = r < rows ? unsigned((std::size_t(r) * ldp + c0) * 4) : kOutOfRange;
+    LoadVec<V>(p_res, at, bv[i]);
+    LoadVec<V>(p_res, r < rows ? at + unsigned(H) * 4u : kOutOfRange, cv[i]);
+    LoadVec<V>(p_res, r < rows ? at + unsigned(2 * H) * 4u : kOutOfRange, xv[i]);
+  }
+  // Block 0's new history (the segment's last L - 1 B x products, or old
+  // entries for rows before the segment): B and x of those rows.
+  float nb[L - 1][V], nx[L - 1][V];
+  if (history_block) {
+#pragma unroll
+    for (int t = 0; t < L - 1; ++t) {
+      const int r = rows - (L - 1) + t;
+      const unsigned at = r >= 0 ? unsigned((std::size_t(r) * ldp + c0) * 4) : kOutOfRange;
+      LoadVec<V>(p_res, at, nb[t]);
+      LoadVec<V>(p_res, r >= 0 ? at + unsigned(2 * H) * 4u : kOutOfRange, nx[t]);
+    }
+  }
+  // Keeps the products below every load: one memory round trip.
+  __builtin_amdgcn_sched_barrier(0);
+  if (first == 0) {
+#pragma unroll
+    for (int t = 0; t < L - 1; ++t)
+#pragma unroll
+      for (int c = 0; c < V; ++c) {
+        pb[t][c] = hv[c * (L - 1) + t];
+        px[t][c] = 1.0f;
+      }
+  }
+  float win[L][V];
+#pragma unroll
+  for (int t = 0; t < L - 1; ++t)
+#pragma unroll
+    for (int c = 0; c < V; ++c)
+      win[t + 1][c] = pb[t][c] * px[t][c];
+  float y[R][V], row_max[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+#pragma unroll
+    for (int t = 0; t < L - 1; ++t)
+#pragma unroll
+      for (int c = 0; c < V; ++c)
+        win[t][c] = win[t + 1][c];
+#pragma unroll
+    for (int c = 0; c < V; ++c)
+      win[L - 1][c] = bv[i][c] * xv[i][c];
+    row_max[i] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < V; ++c) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int t = 0; t < L; ++t)
+        sum += tw[c * L + t] * win[t][c];
+      y[i][c] = sum * cv[i][c];
+      row_max[i] = fmaxf(row_max[i], fabsf(y[i][c]));
+    }
+    if (!live)
+      row_max[i] = 0.0f;
+  }
+  // Each row's maximum over the block (rows past the segment are unused).
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const float m = WaveMax(row_max[i]);
+    if (lane == 0)
+      s_max[i][wave] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    float m = 0.0f;
+    for (int w = 0; w < waves; ++w)
+      m = fmaxf(m, s_max[i][w]);
+    row_max[i] = m;
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int r = first + i;
+    if (r < skip || r >= rows)
+      continue;
+    const int e = RowExponent(row_max[i]);
+    Half* dst = out + std::size_t(r - skip) * lda;
+    if (tid == 0)
+      scale[r - skip] = ldexpf(1.0f, -e);
+    if (live) {
+      unsigned h[(V + 1) / 2];
+#pragma unroll
+      for (int c = 0; c < V; c += 2)
+        h[c / 2] = unsigned(ScaledHalf(y[i][c], e)) |
+                   (c + 1 < V ? unsigned(ScaledHalf(y[i][c + 1], e)) << 16 : 0u);
+      if constexpr (V == 4)
+        *reinterpret_cast<uint2*>(dst + c0) = make_uint2(h[0], h[1]);
+      else if constexpr (V == 2)
+        *reinterpret_cast<unsigned*>(dst + c0) = h[0];
+      else
+        dst[c0] = Half(h[0]);
+    }
+    for (int k = H + tid; k < padded; k += int(blockDim.x))  // the chunk's zero tail
+      dst[k] = Half(0);
+  }
+  if (history_block && live) {
+    // WriteConvHistory's entries for the thread's channels: entry t of
+    // channel c is the B x product of row rows - (L - 1) + t, or for a row
+    // before the segment the old entry rows + t (loaded above: this block's
+    // first row is 0 whenever rows < L - 1). Every old entry of these
+    // channels was read by this thread.
+    float e[V * (L - 1)];
+#pragma unroll
+    for (int t = 0; t < L - 1; ++t) {
+      const int r = rows - (L - 1) + t;
+#pragma unroll
+      for (int c = 0; c < V; ++c)
+        e[c * (L - 1) + t] = r >= 0 ? nb[t][c] * nx[t][c] : hv[c * (L - 1) + (rows + t)];
+    }
+#pragma unroll
+    for (int i = 0; i < V * (L - 1); ++i)
+      StoreF32(h_res, unsigned((c0 * (L - 1) + i) * 4), e[i]);
+  }
+}
+
 // Any width: each output recomputes its window's products (same values and
 // order as PromptConvKernel).
 __global__ void PromptConvAnyKernel(const float* __restrict__ p, int ldp,
@@ -908,6 +1115,37 @@ int lfm3_store_kv(const std::uint16_t* k16, const std::uint16_t* v16, std::uint1
   StoreRingKernel<<<(count + 255) / 256, 256, 0, static_cast<hipStream_t>(stream)>>>(
       k16, v16, cache_k, cache_v, int(rows), int(stride), position, capacity);
   return HipStatus(hipGetLastError(), "LFM3 K/V ring store launch");
+}
+
+int lfm3_conv_prompt_half(const float* p, std::uint32_t ldp, const float* taps,
+                          float* history, std::uint32_t rows, std::uint32_t skip,
+                          std::uint16_t* out, std::uint32_t lda, float* scale,
+                          std::uint32_t hidden, std::uint32_t width, int update_history,
+                          void* stream) {
+  if (!p || !taps || !history || !out || !scale || !rows || skip >= rows || !hidden ||
+      hidden % kConvHalfV || width < 2 || width > std::uint32_t(kConvHalfMaxWidth) ||
+      ldp < 3 * hidden || lda % kChunk || lda < hidden ||
+      hidden > std::uint32_t(kConvHalfMaxHidden) ||
+      !BufferFits(std::size_t(rows) * ldp * 4))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt convolution (FP16 rows) shape");
+  const auto s = static_cast<hipStream_t>(stream);
+  const std::uint32_t first0 = skip / kConvHalfRows * kConvHalfRows;
+  const unsigned blocks = (rows - first0 + kConvHalfRows - 1) / kConvHalfRows;
+  const unsigned threads = (hidden / kConvHalfV + 63) / 64 * 64;
+  const auto go = [&](auto kernel) {
+    kernel<<<blocks, threads, 0, s>>>(p, int(ldp), taps, history, int(rows), int(skip),
+                                      int(first0), out, int(lda), scale, int(hidden),
+                                      update_history);
+  };
+  switch (width) {
+    case 2: go(PromptConvHalfKernel<2, kConvHalfV>); break;
+    case 3: go(PromptConvHalfKernel<3, kConvHalfV>); break;
+    case 4: go(PromptConvHalfKernel<4, kConvHalfV>); break;
+    case 5: go(PromptConvHalfKernel<5, kConvHalfV>); break;
+    case 6: go(PromptConvHalfKernel<6, kConvHalfV>); break;
+    default: go(PromptConvHalfKernel<7, kConvHalfV>); break;
+  }
+  return HipStatus(hipGetLastError(), "LFM3 prompt convolution (FP16 rows) launch");
 }
 
 int lfm3_conv_prompt(const float* p, std::uint32_t ldp, const float* taps,

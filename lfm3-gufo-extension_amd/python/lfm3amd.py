@@ -129,12 +129,16 @@ _SIGS = {
                                        u32, u32, u32, u32, f32, vp]),
     "lfm3_sum_parts": (i32, [vp, sz, u32, u32, u32, u32, vp]),
     "lfm3_conv_prompt": (i32, [vp, u32, vp, vp, vp, vp, u32, vp, u32, u32, u32, i32, vp]),
+    "lfm3_conv_prompt_half": (i32, [vp, u32, vp, vp, u32, u32, vp, u32, vp, u32, u32, i32, vp]),
     "lfm3_prompt_heads": (i32, [vp, vp, vp, u32, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32,
                                 u32, f32, vp]),
     "lfm3_store_kv": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, vp]),
     "lfm3_prompt_attention_workspace_bytes": (sz, [u32, u32, u32, u32, u32]),
     "lfm3_prompt_attention": (i32, [vp, u32, vp, vp, vp, u32, vp, vp, vp, u32, u32, u32, u32,
                                     u32, u32, u32, u32, vp, sz, vp]),
+    "lfm3_prompt_attention_half_workspace_bytes": (sz, [u32, u32, u32, u32, u32]),
+    "lfm3_prompt_attention_half": (i32, [vp, u32, vp, vp, vp, u32, vp, vp, vp, u32, vp, u32, u32,
+                                         u32, u32, u32, u32, u32, vp, sz, vp]),
     "lfm3_attention_plan": (i32, [vp, u32, u32, vp, u32]),
     "lfm3_attention_max_items": (sz, [u32, u32]),
     "lfm3_attention_workspace_bytes": (sz, [u32, u32, u32, u32, u32]),

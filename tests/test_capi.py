@@ -234,6 +234,31 @@ def test_projection_conv_rejects_bad_shapes():
                                        None) == L.E_INVALID  # 2056 % 16
 
 
+def test_conv_prompt_half_rejects_bad_shapes():
+    """The convolution with FP16 rows out refuses, before any launch: skip
+    not below rows, a hidden size that is not a multiple of 4 or past 2048,
+    a width outside [2, 7], a row stride that is not a whole number of
+    64-column chunks."""
+    lib = L.lib()
+    f = 64
+    ok = dict(p=f, ldp=3 * 2048, taps=f, hist=f, rows=40, skip=3, out=f, lda=2048, scale=f,
+              hidden=2048, width=7)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return lib.lfm3_conv_prompt_half(a["p"], a["ldp"], a["taps"], a["hist"], a["rows"],
+                                         a["skip"], a["out"], a["lda"], a["scale"], a["hidden"],
+                                         a["width"], 1, None)
+    assert call(skip=40) == L.E_INVALID
+    assert call(hidden=2050, ldp=3 * 2050, lda=2112) == L.E_INVALID
+    assert call(hidden=2052, ldp=3 * 2052, lda=2112) == L.E_INVALID
+    assert call(width=8) == L.E_INVALID
+    assert call(width=1) == L.E_INVALID
+    assert call(lda=2080) == L.E_INVALID
+    assert call(ldp=3 * 2048 - 1) == L.E_INVALID
+    assert call(out=None) == L.E_INVALID
+
+
 def test_snapshot_signature_is_fnv1a32():
     """The snapshot's configuration signature is 32-bit FNV-1a
     (engine.cpp ConfigSignature): the published test vectors, and the word

@@ -103,6 +103,46 @@ def test_conv_prompt_without_history_update_leaves_it():
         assert np.array_equal(y[i], want)
 
 
+@pytest.mark.parametrize("H,n,skip,Lw", [(2048, 512, 0, 7), (2048, 300, 13, 7), (2048, 37, 0, 7),
+                                          (256, 20, 5, 7), (256, 5, 2, 7), (2048, 100, 50, 4),
+                                          (2048, 40, 9, 5), (96, 17, 0, 2)])
+def test_conv_prompt_half_is_conv_then_half_rows(H, n, skip, Lw):
+    """The convolution fused with its output's FP16 row-scaled activations
+    against the oracle's decode steps followed by its FP16 row conversion
+    (hip/q8_prefill.hpp:27-51): rows skip.. of the FP16 output, their
+    scales and the new history bit-exact; chunk tails zero; nothing written
+    past the live rows or the chunk tail. Covers a prompt shorter than the
+    window (the history moves within it), a skip past the first row block,
+    other widths and a hidden size that is not a whole chunk."""
+    p = L.normal(SEED, f"pch.p.{H}.{n}", n * 3 * H).reshape(n, 3 * H)
+    taps = L.normal(SEED, f"pch.t.{H}.{Lw}", H * Lw, 0, 0.1)
+    hist = L.normal(SEED, f"pch.h.{H}.{Lw}", H * (Lw - 1))
+    lda = (H + 63) // 64 * 64 + 64
+    live = n - skip
+    dp, dt, dh = L.DeviceBuffer.of(p), L.DeviceBuffer.of(taps), L.DeviceBuffer.of(hist)
+    sentinel = np.full((live + 1) * lda, 0x7e00, np.uint16)
+    da = L.DeviceBuffer.of(sentinel)
+    ds = L.DeviceBuffer.of(np.full(live + 1, -1.0, np.float32))
+    L.check(L.lib().lfm3_conv_prompt_half(dp.addr, 3 * H, dt.addr, dh.addr, n, skip, da.addr,
+                                          lda, ds.addr, H, Lw, 1, None))
+    L.synchronize()
+    a = da.download(np.uint16, (live + 1) * lda).reshape(live + 1, lda)
+    scale = ds.download(np.float32, live + 1)
+    y = np.zeros((n, H), np.float32)
+    h = hist
+    for i in range(n):
+        y[i], h = O.conv_step(p[i], taps, h, H, Lw)
+    inputs, exps = O.half_rows(y[skip:])
+    want = O.float_to_half(np.ldexp(y[skip:], exps[:, None]).astype(np.float32))
+    assert np.array_equal(a[:live, :H], want)
+    assert np.array_equal(scale[:live], np.ldexp(np.float32(1), -exps).astype(np.float32))
+    padded = (H + 63) // 64 * 64
+    assert not a[:live, H:padded].any()
+    assert np.all(a[:live, padded:] == 0x7e00) and np.all(a[live] == 0x7e00)
+    assert scale[live] == -1.0
+    assert np.array_equal(dh.download(np.float32, H * (Lw - 1)), h)
+
+
 # ------------------------------------------------------------------ heads
 
 @pytest.mark.parametrize("heads,kv,D", [(16, 4, 128), (32, 8, 64)])
@@ -268,6 +308,51 @@ def test_prompt_attention_reference_vectors(n, window, P, H, KH):
         for r in range(n):
             ring_k[(P + r) % cap] = kbits.reshape(n, stride)[r]
         assert np.array_equal(dck.download(np.uint16, cap * stride).reshape(cap, stride), ring_k)
+
+
+@pytest.mark.parametrize("n,window,P,H,KH,D", [(512, 0, 24576, 16, 4, 128), (512, 256, 24576, 16, 4, 128),
+                                               (77, 0, 3000, 16, 4, 128), (16, 0, 259, 4, 2, 128),
+                                               (37, 256, 300, 32, 8, 64), (200, 0, 0, 32, 8, 64)])
+def test_prompt_attention_half_is_attention_then_half_rows(n, window, P, H, KH, D):
+    """The attention output as the output projection's FP16 rows: every
+    row equals lfm3_prompt_attention's FP32 row converted by the oracle's
+    FP16 row rule (hip/q8_prefill.hpp:27-51) bit for bit, with its scale,
+    for a global history split into spans (depth 24576), the sliding
+    window (one span), a short history and the 32 x 64 head shape; nothing
+    is written past the row's heads x dim halves."""
+    cap = window if window else P + n
+    stride = KH * D
+    tag = f"{n}.{window}.{P}.{H}.{D}"
+    q = L.normal(SEED, f"pah.q.{tag}", n * H * D).reshape(n, H * D)
+    gates = L.normal(SEED, f"pah.g.{tag}", n * H).reshape(n, H)
+    kbits = L.half_normal(SEED, f"pah.k.{tag}", n * stride)
+    vbits = L.half_normal(SEED, f"pah.v.{tag}", n * stride)
+    ckbits = L.half_normal(SEED, f"pah.ck.{tag}", cap * stride)
+    cvbits = L.half_normal(SEED, f"pah.cv.{tag}", cap * stride)
+    print(f"[prompt attention half] {tag}", flush=True)
+    out, _ = run_prompt_attention(q, gates, kbits, vbits, ckbits, cvbits, n, H, KH, D, P, cap,
+                                  window)
+    lda = H * D + 64
+    dq = L.DeviceBuffer.of(np.ascontiguousarray(q, np.float32))
+    dg = L.DeviceBuffer.of(np.ascontiguousarray(gates, np.float32))
+    dk, dv = L.DeviceBuffer.of(kbits), L.DeviceBuffer.of(vbits)
+    dck, dcv = L.DeviceBuffer.of(ckbits), L.DeviceBuffer.of(cvbits)
+    ws_bytes = L.lib().lfm3_prompt_attention_half_workspace_bytes(n, H, D, P, window)
+    assert ws_bytes >= n * H * (D + 2) * 4
+    ws = L.DeviceBuffer(ws_bytes)
+    da = L.DeviceBuffer.of(np.full((n + 1) * lda, 0x7e00, np.uint16))
+    ds = L.DeviceBuffer.of(np.full(n + 1, -1.0, np.float32))
+    L.check(L.lib().lfm3_prompt_attention_half(dq.addr, H * D, dk.addr, dv.addr, dg.addr, H,
+                                               dck.addr, dcv.addr, da.addr, lda, ds.addr, n, H,
+                                               KH, D, P, cap, window, ws.addr, ws_bytes, None))
+    L.synchronize()
+    a = da.download(np.uint16, (n + 1) * lda).reshape(n + 1, lda)
+    scale = ds.download(np.float32, n + 1)
+    _, exps = O.half_rows(out)
+    want = O.float_to_half(np.ldexp(out, exps[:, None]).astype(np.float32))
+    assert np.array_equal(a[:n, :H * D], want)
+    assert np.array_equal(scale[:n], np.ldexp(np.float32(1), -exps).astype(np.float32))
+    assert np.all(a[:n, H * D:] == 0x7e00) and np.all(a[n] == 0x7e00) and scale[n] == -1.0
 
 
 @pytest.mark.parametrize("n,window,P,cap,D", [(9, 256, 37, 46, 128), (8, 0, 40, 50, 128),
