@@ -48,6 +48,90 @@ def test_gemv_decode_shape_8192x2048(B):
     assert np.max(np.abs(y - want64)) < 2e-5
 
 
+def wide_range_rows(B, K, tag):
+    """Rows whose magnitudes span 2^-20..1 inside every 64-column chunk:
+    |x| = 2^(-20 u) with u uniform in [0, 1), random signs, and one entry of
+    magnitude 1 per chunk, so every chunk's (and slice's) maximum is 1."""
+    rng = np.random.default_rng(zlib.crc32(f"{SEED}.{tag}".encode()))
+    u = rng.random((B, K))
+    x = np.exp2(-20.0 * u) * rng.choice([-1.0, 1.0], (B, K))
+    for c in range(0, K, 64):
+        x[:, c + rng.integers(0, 64)] = rng.choice([-1.0, 1.0], B)
+    return x.astype(np.float32)
+
+
+def truncate_to_fp16_grid(x, e):
+    """fp16(x 2^e) 2^-e truncated toward zero, for x 2^e in fp16's normal
+    range: the float32 significand cut to 11 bits (the operand's hi plane)."""
+    bits = (np.asarray(x, np.float32) * np.float32(2.0 ** e)).view(np.uint32) & np.uint32(0xffffe000)
+    return bits.view(np.float32).astype(np.float64) * 2.0 ** -e
+
+
+@pytest.mark.parametrize("B", [1, 2, 4, 8])
+def test_gemv_operand_keeps_two_fp16_planes_over_a_wide_range(B):
+    """The decode operand's precision (q8.hip SplitPair, norm_image.hpp) on
+    the config-1 matrix (W 8192 x 2048 Q8_0) with rows spanning 2^-20..1
+    inside every chunk, against FP64.
+
+    Bound: with the slice's maximum in [2^14, 2^15) after scaling by 2^e, hi
+    = fp16(x 2^e) truncated keeps 11 bits (|r| < 2^-10 |X|, X = x 2^e) and
+    lo = fp16(r 2^11) truncated keeps 11 bits of r (an error below 2^-10
+    |r|); X >= 2^-6 keeps both planes normal, so the operand is within
+    2^-20 |x| of x. The FP32 sums add at most 128 u (u = 2^-24: 31
+    roundings in a block's 32 exact products, 64 block FMAs, the hi + lo
+    sum), so |y - y64| <= (2^-20 + 2^-17) S per output, S = sum |w| |x|.
+
+    Tight check: the error's RMS stays within twice that of the reference's
+    FP32 path (the oracle, reference.cpp's order) on the same rows; the same
+    rows with the lo plane dropped (hi alone) are about 400 times worse, so
+    a lost or shortened lo plane fails here.
+
+    Both the FP32-row GEMV (an exponent per wave slice: every slice's
+    maximum is 1, e = 14) and the image GEMV fed by the residual norm (an
+    exponent per row) are checked."""
+    M, K = 8192, 2048
+    w = L.q8(SEED, "prec.W", M, K)
+    wd = L.q8_dequant(w, M, K)
+    x = wide_range_rows(B, K, f"prec.x{B}")
+    m = DeviceMatrix(w, M, K)
+    tensor = O.q8_tensor(w, M, K)
+
+    def check(y, xin, label, e=None):
+        x64 = np.asarray(xin, np.float64)
+        want = x64 @ wd.T
+        err = np.asarray(y, np.float64) - want
+        bound = (2.0 ** -20 + 2.0 ** -17) * (np.abs(x64) @ np.abs(wd).T)
+        ref = O.mat(tensor, xin) - want
+        rms = lambda v: float(np.sqrt(np.mean(np.square(v))))
+        print(f"[{label}] B={B} max |err| / bound {np.max(np.abs(err) / bound):.4f}, "
+              f"rms err {rms(err):.3g} (FP32 reference {rms(ref):.3g})", flush=True)
+        assert np.all(np.abs(err) <= bound), label
+        assert rms(err) <= 2.0 * rms(ref), label
+        if e is not None:
+            hi_only = truncate_to_fp16_grid(xin, e) @ wd.T - want
+            assert rms(hi_only) > 100.0 * rms(ref), label
+
+    check(gemv(m, x), x, "fp32 rows", e=14)
+    # The image path: the residual norm (no branch, unit weights) writes z
+    # and its operand image; the GEMV reads the image.
+    H = K
+    dx = L.DeviceBuffer.of(x)
+    dwn = L.DeviceBuffer.of(np.ones(H, np.float32))
+    dz = L.DeviceBuffer(B * H * 4)
+    img = L.DeviceBuffer(L.lib().lfm3_operand_image_bytes(H))
+    ex = L.DeviceBuffer(32)
+    L.check(L.lib().lfm3_residual_norm_image(None, 1, 0, None, dx.addr, dwn.addr, dz.addr,
+                                             img.addr, ex.addr, B, H, 1e-5, None))
+    dy = L.DeviceBuffer(B * M * 4)
+    L.check(L.lib().lfm3_q8_gemv_image(m.codes.addr, m.scales.addr, M, H, img.addr, ex.addr, B,
+                                       dy.addr, M, 1, None))
+    L.synchronize()
+    gz = dz.download(np.float32, B * H).reshape(B, H)
+    zmax = np.abs(gz).max(axis=1)
+    assert np.all(np.abs(gz).min(axis=1) >= zmax * 2.0 ** -21)  # the range survives the norm
+    check(dy.download(np.float32, B * M).reshape(B, M), gz, "image")
+
+
 @pytest.mark.parametrize("M,K,B", [(2048, 7680, 8), (128000, 2048, 4), (16, 2048, 5),
                                    (3088, 2048, 8), (48, 96, 7), (512, 64, 8), (64, 64, 1), (6144, 2048, 8)])
 def test_gemv_model_shapes(M, K, B):
