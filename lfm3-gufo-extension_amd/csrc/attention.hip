@@ -473,6 +473,19 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
       __shared__ int s_last;
       __shared__ float s_w[kMaxParts][G], s_lv[kMaxParts][G], s_top[G], s_den[G];
       // Every thread's partial stores have completed before the arrival.
+      // The hand-over is relaxed on purpose, and is ordered by how gfx950
+      // carries out agent-scope accesses rather than by C++ release /
+      // acquire: AgentStore writes through the XCD's L2 to the device's
+      // coherence point, vmcnt(0) returns only once every store of this
+      // thread is acknowledged there, the block barrier makes that true
+      // for every thread before the atomic is issued, the atomic itself is
+      // performed at that point, and the merging block issues its
+      // AgentLoads (which read from that point, not from its own L2) only
+      // after its atomic returned the final count (through LDS and a
+      // block barrier, which the compiler does not move loads across). A
+      // release / acquire pair would add an L2 write-back and an
+      // invalidate to every arrival. The multi-span parity tests at
+      // 16K-32K keys (many spans a row) would see a stale partial.
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (tid == 0) {

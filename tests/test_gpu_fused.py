@@ -48,8 +48,11 @@ def norm_inputs(tag, B, H, parts):
 
 @pytest.mark.parametrize("M,H,swiglu", [(3088, 2048, False), (7680, 2048, True),
                                         (2048, 2048, False), (64, 256, False),
-                                        (512, 512, True)])
+                                        (512, 512, True), (8192, 2048, True)])
 def test_fused_norm_gemv_equals_the_two_launches(M, H, swiglu):
+    """The fused entry against the norm launch followed by the GEMV launch.
+    8192 x 2048 SwiGLU (512 GEMV blocks + the norm's, more than two blocks
+    a CU) takes the entry's own fallback to the two launches."""
     lib = L.lib()
     w = L.q8(SEED, f"fu.W.{M}.{H}", M, H)
     if swiglu:
