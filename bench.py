@@ -1077,7 +1077,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q8_0 x f32 (activations as fp16 hi/lo pairs, about 22 bits; fp32 accumulate)",
+        "dtype": "q8_0 x f32 (activations as two fp16 planes, hi and lo each truncated to 11 "
+                 "bits: within 2^-20 of each value; fp32 accumulate)",
         "data": "synthetic (random-init Q8_0 weights, synthesized session state)",
         "config": {
             "workload": ("LFM3 decode round, 8 ragged sessions: 24 layers (13 conv7, 5 sliding-256, "
