@@ -233,6 +233,28 @@ int lfm3_q8_gemm_swiglu(const void* codes, const void* scales, uint32_t rows,
                         uint32_t cols, const uint16_t* a, uint32_t lda,
                         const float* a_scale, uint32_t tokens, float* y,
                         uint32_t ldy, unsigned* row_max, void* stream);
+/* lfm3_q8_gemm_swiglu_h16 with the down projection's input in the same
+   launch: after the GEMM blocks, trailing blocks convert the SwiGLU output
+   rows (y, FP32, still written) into FP16 row-scaled activations, out +
+   t * out_ld with out_scale[t] (lfm3_half_rows of y with these row maxima,
+   bit for bit; chunk tails zeroed). A GEMM block writes y and its row
+   maxima through to memory and then stores `seq` in its flag; a trailing
+   block waits for the flags of its token block's GEMM blocks (bounded: a
+   timeout stores 1 to *error, which may be NULL, and the block goes on).
+   flags: lfm3_q8_gemm_swiglu_flags_bytes(rows, tokens), zeroed once; seq:
+   nonzero and different from the previous call's on the same flags; calls
+   on the same flags must not overlap. out must not alias a (the GEMM reads
+   a while trailing blocks write out). rows % 4 == 0 and rows <= 8192, ldy
+   % 4 == 0, out_ld % 64 == 0. Replaces: gpu::ProjectFfn's gate/up GEMM
+   and the down projection's HalfRowsFromMax (q8_prefill.hpp:53-74;
+   hip/ops.hip:2205-2222). */
+size_t lfm3_q8_gemm_swiglu_flags_bytes(uint32_t rows, uint32_t tokens);
+int lfm3_q8_gemm_swiglu_h16_rows(const void* halves, const void* scales, uint32_t rows,
+                                 uint32_t cols, const uint16_t* a, uint32_t lda,
+                                 const float* a_scale, uint32_t tokens, float* y,
+                                 uint32_t ldy, unsigned* row_max, uint16_t* out,
+                                 uint32_t out_ld, float* out_scale, unsigned* flags,
+                                 uint32_t seq, unsigned* error, void* stream);
 /* FP16 tiles of a tiled Q8_0 matrix: each code decoded exactly to fp16 in
    the order the prompt GEMM's MFMA takes it (2 KB per 16-row x 64-column
    tile; lfm3_q8_half_tiles_bytes). The scales stay in the Q8_0 scale

@@ -184,6 +184,14 @@ inline std::size_t SampleTableBytes() {
 // prompt and shared by the model's prompts (under the model's lock).
 struct PromptBuffers {
   Buffer tokens, x, z, a16, scale, proj, mix, hid, out, row_max, chunk_k, chunk_v, attn_ws;
+  // The FFN hidden rows as the down projection's FP16 rows (written by the
+  // SwiGLU launch's trailing blocks), with the flags its GEMM blocks
+  // publish (zeroed once) and the launch counter (0 skipped).
+  Buffer hid16, hid_scale, swiglu_flags;
+  std::uint32_t swiglu_seq = 0;
+  // Set to 1 by a trailing block whose wait timed out (host-mapped; the
+  // prompt checks it after its synchronization).
+  std::unique_ptr<PinnedBuffer> wait_error;
   Buffer one_table;  // one decode-attention row: ring pointers, capacity, position, items
   Buffer one_ws;     // that row's span partials (apart from the decode round's)
   std::unique_ptr<PinnedBuffer> one_staging;
@@ -1276,6 +1284,12 @@ PromptBuffers& EnsurePromptBuffers(lfm3_model& m) {
   b->z = Buffer(R * H * 4);
   b->a16 = Buffer(R * b->lda * 2);
   b->scale = Buffer(R * 4);
+  b->hid16 = Buffer(R * ((F + 63) / 64 * 64) * 2, false);
+  b->hid_scale = Buffer(R * 4, false);
+  b->swiglu_flags = Buffer(lfm3_q8_gemm_swiglu_flags_bytes(std::uint32_t(F), std::uint32_t(R)));
+  b->wait_error = std::make_unique<PinnedBuffer>(sizeof(unsigned),
+                                                 hipHostMallocMapped | hipHostMallocCoherent);
+  *static_cast<unsigned*>(b->wait_error->p) = 0;
   b->proj = Buffer(8 * R * b->proj_ld * 4);  // up to 8 K parts
   b->mix = Buffer(R * std::max<std::size_t>(H, std::size_t(c.heads) * D) * 4);
   b->hid = Buffer(R * F * 4);
@@ -1602,10 +1616,23 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
       gemv(l.ffn, z + std::size_t(o) * H, H, hid, F, rows_out, true);
       parts = dense(l.down, hid, F, rows_out, nullptr);
     } else {
-      CheckStatus(lfm3_q8_gemm_swiglu_h16(l.ffn.halves.p, l.ffn.scales.p, F, H,
-                                      a16 + std::size_t(o) * lda, lda, scale + o, rows_out, hid,
-                                      F, row_max, s));
-      parts = dense(l.down, hid, F, rows_out, row_max);
+      // The hidden rows' FP16 conversion runs in the SwiGLU launch's
+      // trailing blocks, into their own buffer (the launch still reads
+      // a16).
+      if (++b.swiglu_seq == 0)
+        b.swiglu_seq = 1;
+      const std::uint32_t hld = (F + 63) / 64 * 64;
+      auto* h16 = b.hid16.as<std::uint16_t>();
+      float* hscale = b.hid_scale.as<float>();
+      CheckStatus(lfm3_q8_gemm_swiglu_h16_rows(
+          l.ffn.halves.p, l.ffn.scales.p, F, H, a16 + std::size_t(o) * lda, lda, scale + o,
+          rows_out, hid, F, row_max, h16, hld, hscale, b.swiglu_flags.as<unsigned>(),
+          b.swiglu_seq, static_cast<unsigned*>(b.wait_error->device), s));
+      const Matrix& w = l.down;
+      const std::uint32_t dparts = lfm3_q8_gemm_parts(w.rows, w.cols, rows_out, 0);
+      CheckStatus(lfm3_q8_gemm(w.codes.p, w.scales.p, w.rows, w.cols, h16, hld, hscale,
+                               rows_out, out, H, dparts, s));
+      parts = dparts;
     }
     const bool last = il + 1 == L;
     residual_norm(parts, &l.post_ffn_norm, last ? nullptr : &m.layers[il + 1].norm, rows_out,
@@ -1619,6 +1646,11 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
     HeadRow(m, se.frontier.as<float>(), se.logits.as<float>(), s);
   Check(hipGetLastError(), "prompt launch");
   Check(hipStreamSynchronize(s), "prompt");
+  auto* word = static_cast<volatile unsigned*>(b.wait_error->p);
+  if (*word) {
+    *word = 0;
+    throw Error(LFM3_E_HIP, "LFM3 prompt: a SwiGLU conversion block's wait timed out");
+  }
   se.position += n;
   se.logits_ready = want_logits;
 }

@@ -200,6 +200,126 @@ __device__ __forceinline__ int XcdMajorItem(int b, int blocks) {
   return (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + i;
 }
 
+// The SwiGLU GEMM's trailing blocks (lfm3_q8_gemm_swiglu_h16_rows): after
+// the GEMM blocks of a launch (blockIdx.x < gemm_blocks), each further
+// block converts kHiddenRows rows of the FFN hidden output into the down
+// projection's FP16 row-scaled activations (HalfRowsKernel's expressions,
+// the row maximum from the epilogue's partial maxima). A GEMM block stores
+// its outputs and partial maxima through to memory (sc1), waits for them,
+// and then stores `seq` into its flag (flags[tb * row_blocks + rb]); a
+// converter block waits for the flags of every GEMM block of its token
+// block. The converters come after every GEMM block in dispatch order and
+// the GEMM blocks wait on nothing, so every wait ends; each is bounded
+// (kGemmSpinLimit polls, then error set to 1 and the block goes on).
+struct HiddenHalves {
+  Half* out = nullptr;  // null: a plain SwiGLU launch
+  int lda = 0;
+  float* scale = nullptr;
+  unsigned* flags = nullptr;
+  unsigned seq = 0;
+  unsigned* error = nullptr;
+  int gemm_blocks = 0;
+};
+// Two rows a trailing block (256 blocks for 512 rows): the 512-token pass
+// at 4.59 ms against 4.60 with 4 rows, 4.61 with 8 or 1, and 4.65 with the
+// conversion as a launch of its own (three runs each, one box).
+constexpr int kHiddenRows = 2, kHiddenLoads = 4;
+constexpr int kGemmSpinLimit = 1 << 20;
+
+// A trailing block of the SwiGLU GEMM: rows r0 .. r0 + kHiddenRows - 1 of
+// y (cols = the FFN width) once every GEMM block of their token block has
+// published. Loads read memory (sc1), where the GEMM blocks wrote.
+template<int T, int kTokens>
+__device__ __forceinline__ void ConvertHidden(const HiddenHalves& t, const float* y, int ldy,
+                                              int cols, int n, const unsigned* row_max,
+                                              int row_blocks) {
+  static_assert(kTokens % kHiddenRows == 0, "a converter's rows lie in one token block");
+  __shared__ float s_rmax[kHiddenRows][T / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r0 = (int(blockIdx.x) - t.gemm_blocks) * kHiddenRows;
+  const int tb = r0 / kTokens;
+  if (wave == 0) {
+    const BufferResource f_res =
+        MakeBuffer(t.flags + std::size_t(tb) * row_blocks, unsigned(row_blocks) * 4u);
+    int spins = 0;
+    for (;;) {
+      bool mine = true;
+      for (int k = lane; k < row_blocks; k += 64)
+        mine = mine && __builtin_amdgcn_raw_buffer_load_b32(f_res, unsigned(k) * 4u, 0,
+                                                            kCachePolicySc1) == t.seq;
+      if (__all(mine))
+        break;
+      if (++spins >= kGemmSpinLimit) {
+        if (lane == 0 && t.error)
+          __hip_atomic_store(t.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(4);
+    }
+  }
+  __syncthreads();
+  // Each row's maximum over the partial maxima of the row blocks.
+  const BufferResource m_res = MakeBuffer(row_max, unsigned(row_blocks) * unsigned(n) * 4u);
+  float part[kHiddenRows];
+#pragma unroll
+  for (int i = 0; i < kHiddenRows; ++i) {
+    const int r = r0 + i;
+    float m = 0.0f;
+    for (int b = tid; b < row_blocks; b += T)
+      m = fmaxf(m, __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                       m_res, r < n ? unsigned(b * n + r) * 4u : kOutOfRange, 0,
+                       kCachePolicySc1)));
+    part[i] = WaveMax(m);
+  }
+  if (lane == 0)
+#pragma unroll
+    for (int i = 0; i < kHiddenRows; ++i)
+      s_rmax[i][wave] = part[i];
+  __syncthreads();
+  // Every row's values are loaded before the first conversion (at most
+  // kHiddenLoads 16-byte loads a row and thread: cols <= 16 T), so the
+  // block waits on memory once.
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  const BufferResource y_res = MakeBuffer(y, unsigned(n) * unsigned(ldy) * 4u);
+  u4 w[kHiddenRows][kHiddenLoads];
+#pragma unroll
+  for (int i = 0; i < kHiddenRows; ++i)
+#pragma unroll
+    for (int j = 0; j < kHiddenLoads; ++j) {
+      const int r = r0 + i, v = tid + T * j;
+      w[i][j] = __builtin_amdgcn_raw_buffer_load_b128(
+          y_res, r < n && v < cols / 4 ? unsigned(std::size_t(r) * ldy + 4 * v) * 4u : kOutOfRange,
+          0, kCachePolicySc1);
+    }
+  const int padded = (cols + kChunk - 1) / kChunk * kChunk;
+#pragma unroll
+  for (int i = 0; i < kHiddenRows; ++i) {
+    const int r = r0 + i;
+    if (r >= n)
+      break;
+    float maximum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < T / 64; ++q)
+      maximum = fmaxf(maximum, s_rmax[i][q]);
+    const int e = RowExponent(maximum);
+    if (tid == 0)
+      t.scale[r] = ldexpf(1.0f, -e);
+    Half* dst = t.out + std::size_t(r) * t.lda;
+#pragma unroll
+    for (int j = 0; j < kHiddenLoads; ++j) {
+      const int v = tid + T * j;
+      if (v < cols / 4)
+        *reinterpret_cast<uint2*>(dst + 4 * v) = make_uint2(
+            unsigned(ScaledHalf(__uint_as_float(w[i][j].x), e)) |
+                (unsigned(ScaledHalf(__uint_as_float(w[i][j].y), e)) << 16),
+            unsigned(ScaledHalf(__uint_as_float(w[i][j].z), e)) |
+                (unsigned(ScaledHalf(__uint_as_float(w[i][j].w), e)) << 16));
+    }
+    for (int k = cols + tid; k < padded; k += T)  // the zero tail of the last chunk
+      dst[k] = Half(0);
+  }
+}
+
 // Pins 16 accumulators at this point: the FMAs producing them run before
 // it and the values stay in their registers.
 #define LFM3_PIN4(a) "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3])
@@ -213,7 +333,7 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
                              float* __restrict__ y, int ldy, int rows_out,
                              int row_blocks, int token_blocks, int parts,
                              std::size_t part_stride,
-                             unsigned* __restrict__ row_max) {
+                             unsigned* __restrict__ row_max, const HiddenHalves tail) {
   constexpr int RT = kGemmRT, TT = kGemmTT;
   using Stage = Shape;
   constexpr int A_LOADS = Shape::kTokens * 8 / Shape::kThreads;  // 16-byte loads a lane
@@ -230,7 +350,15 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   __shared__ __attribute__((aligned(16))) std::uint8_t s_st2[Shape::kStages == 3 ? Stage::kBytes : 16];
   static_assert(Shape::kStages == 2 || Shape::kStages == 3, "two or three stage arrays");
 
-  const int item = XcdMajorItem(blockIdx.x, gridDim.x);
+  const bool publish = kSwiGLU && tail.out != nullptr;
+  if constexpr (kSwiGLU) {
+    if (publish && int(blockIdx.x) >= tail.gemm_blocks) {
+      ConvertHidden<Shape::kThreads, Shape::kTokens>(tail, y, ldy, rows_out, n, row_max,
+                                                     row_blocks);
+      return;
+    }
+  }
+  const int item = XcdMajorItem(blockIdx.x, publish ? tail.gemm_blocks : int(gridDim.x));
   const int tb = item % token_blocks, rb = (item / token_blocks) % row_blocks;
   const int part = item / (token_blocks * row_blocks);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -489,7 +617,11 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
           const float g = acc[2 * pr][t][i] * s[t][i], u = acc[2 * pr + 1][t][i] * s[t][i];
           const float value = (g * (1.0f / (1.0f + expf(-g)))) * u;
           const bool inside = token_off[t][i] != kOutOfRange && row_off[pr] != kOutOfRange;
-          StoreF32(y_res, inside ? token_off[t][i] + row_off[pr] : kOutOfRange, value);
+          const unsigned at = inside ? token_off[t][i] + row_off[pr] : kOutOfRange;
+          if (publish)  // uniform
+            StoreB32P<kCachePolicySc1>(y_res, at, __float_as_uint(value));
+          else
+            StoreF32(y_res, at, value);
           m = inside ? fmaxf(m, fabsf(value)) : m;
         }
         m = fmaxf(m, __shfl_xor(m, 8, 64));
@@ -501,10 +633,23 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
       }
     }
     __syncthreads();
-    if (row_max)
+    if (publish) {
+      // The outputs and partial maxima through to memory, then the flag.
+      const BufferResource m_res =
+          MakeBuffer(row_max + std::size_t(rb) * n, unsigned(n) * 4u);
+      for (int i = tid; i < Shape::kTokens; i += Shape::kThreads)
+        StoreB32P<kCachePolicySc1>(m_res, tok0 + i < n ? unsigned(tok0 + i) * 4u : kOutOfRange,
+                                   s_max[i]);
+      __builtin_amdgcn_s_waitcnt(WaitVm(0));
+      __syncthreads();
+      if (tid == 0)
+        __hip_atomic_store(tail.flags + tb * row_blocks + rb, tail.seq, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    } else if (row_max) {
       for (int i = tid; i < Shape::kTokens; i += Shape::kThreads)
         if (tok0 + i < n)
           row_max[std::size_t(rb) * n + tok0 + i] = s_max[i];
+    }
   } else {
     unsigned row_off[RT];
 #pragma unroll
@@ -598,13 +743,20 @@ template<bool kSwiGLU, class Shape>
 void LaunchGemm(const void* codes, const void* scales, int row_tiles, int nchunks,
                 const std::uint16_t* a, std::uint32_t lda, const float* a_scale,
                 std::uint32_t tokens, float* y, std::uint32_t ldy, std::uint32_t rows,
-                int parts, std::size_t part_stride, unsigned* row_max, hipStream_t stream) {
+                int parts, std::size_t part_stride, unsigned* row_max, hipStream_t stream,
+                HiddenHalves tail = HiddenHalves{}) {
   const int row_blocks = (row_tiles + Shape::kTiles - 1) / Shape::kTiles;
   const int token_blocks = (int(tokens) + Shape::kTokens - 1) / Shape::kTokens;
-  Q8GemmKernel<kSwiGLU, Shape><<<row_blocks * token_blocks * parts, Shape::kThreads, 0, stream>>>(
+  const int gemm_blocks = row_blocks * token_blocks * parts;
+  int blocks = gemm_blocks;
+  if (tail.out) {
+    tail.gemm_blocks = gemm_blocks;
+    blocks += (int(tokens) + kHiddenRows - 1) / kHiddenRows;
+  }
+  Q8GemmKernel<kSwiGLU, Shape><<<blocks, Shape::kThreads, 0, stream>>>(
       static_cast<const std::uint8_t*>(codes), static_cast<const Half*>(scales), row_tiles,
       nchunks, reinterpret_cast<const Half*>(a), int(lda), a_scale, int(tokens), y, int(ldy),
-      int(rows), row_blocks, token_blocks, parts, part_stride, row_max);
+      int(rows), row_blocks, token_blocks, parts, part_stride, row_max, tail);
 }
 
 }  // namespace
@@ -686,14 +838,15 @@ int Gemm(const void* tiles, bool half, const void* scales, std::uint32_t rows,
                            : (narrow ? LaunchGemm<false, NarrowShape>
                                      : LaunchGemm<false, WideShape>);
   launch(tiles, scales, int(RowTiles(rows)), int(Chunks(cols)), a, lda, a_scale, tokens, y, ldy,
-         rows, int(parts), std::size_t(ldy) * tokens, nullptr, static_cast<hipStream_t>(stream));
+         rows, int(parts), std::size_t(ldy) * tokens, nullptr, static_cast<hipStream_t>(stream),
+         HiddenHalves{});
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 prompt GEMM launch");
 }
 
 int GemmSwiGLU(const void* tiles, bool half, const void* scales, std::uint32_t rows,
                std::uint32_t cols, const std::uint16_t* a, std::uint32_t lda,
                const float* a_scale, std::uint32_t tokens, float* y, std::uint32_t ldy,
-               unsigned* row_max, void* stream) {
+               unsigned* row_max, void* stream, const HiddenHalves& tail = HiddenHalves{}) {
   if (!tiles || !scales || !a || !a_scale || !y || !rows || !cols ||
       cols % 32 || !tokens || lda % 64 || lda < Chunks(cols) * kChunk ||
       ldy < rows || (reinterpret_cast<std::uintptr_t>(a) & 15) ||
@@ -701,8 +854,16 @@ int GemmSwiGLU(const void* tiles, bool half, const void* scales, std::uint32_t r
     return Fail(LFM3_E_INVALID, "unsupported LFM3 Q8_0 prompt SwiGLU shape");
   const auto launch = half ? LaunchGemm<true, WideHalfShape> : LaunchGemm<true, WideShape>;
   launch(tiles, scales, int(2 * RowTiles(rows)), int(Chunks(cols)), a, lda, a_scale, tokens, y,
-         ldy, rows, 1, 0, row_max, static_cast<hipStream_t>(stream));
+         ldy, rows, 1, 0, row_max, static_cast<hipStream_t>(stream), tail);
   return HipStatus(hipGetLastError(), "LFM3 Q8_0 prompt SwiGLU launch");
+}
+
+// Flags of a SwiGLU launch with trailing conversion blocks: one per GEMM block.
+std::size_t SwiGLUFlags(std::uint32_t rows, std::uint32_t tokens) {
+  const std::size_t row_blocks = (2 * RowTiles(rows) + WideHalfShape::kTiles - 1) /
+                                 WideHalfShape::kTiles;
+  const std::size_t token_blocks = (tokens + WideHalfShape::kTokens - 1) / WideHalfShape::kTokens;
+  return row_blocks * token_blocks;
 }
 
 }  // namespace
@@ -714,6 +875,31 @@ int lfm3_q8_gemm(const void* codes, const void* scales, std::uint32_t rows,
                  const float* a_scale, std::uint32_t tokens, float* y,
                  std::uint32_t ldy, std::uint32_t parts, void* stream) {
   return Gemm(codes, false, scales, rows, cols, a, lda, a_scale, tokens, y, ldy, parts, stream);
+}
+
+std::size_t lfm3_q8_gemm_swiglu_flags_bytes(std::uint32_t rows, std::uint32_t tokens) {
+  return rows && tokens ? SwiGLUFlags(rows, tokens) * sizeof(unsigned) : 0;
+}
+
+int lfm3_q8_gemm_swiglu_h16_rows(const void* halves, const void* scales, std::uint32_t rows,
+                                 std::uint32_t cols, const std::uint16_t* a, std::uint32_t lda,
+                                 const float* a_scale, std::uint32_t tokens, float* y,
+                                 std::uint32_t ldy, unsigned* row_max, std::uint16_t* out,
+                                 std::uint32_t out_ld, float* out_scale, unsigned* flags,
+                                 std::uint32_t seq, unsigned* error, void* stream) {
+  if (!out || !out_scale || !row_max || !flags || !seq || rows % 4 || ldy % 4 ||
+      out_ld % 64 || out_ld < rows || rows > std::uint32_t(16 * WideHalfShape::kThreads) ||
+      (reinterpret_cast<std::uintptr_t>(y) & 15) || (reinterpret_cast<std::uintptr_t>(out) & 7))
+    return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt SwiGLU with FP16 hidden rows");
+  HiddenHalves tail;
+  tail.out = reinterpret_cast<Half*>(out);
+  tail.lda = int(out_ld);
+  tail.scale = out_scale;
+  tail.flags = flags;
+  tail.seq = seq;
+  tail.error = error;
+  return GemmSwiGLU(halves, true, scales, rows, cols, a, lda, a_scale, tokens, y, ldy, row_max,
+                    stream, tail);
 }
 
 int lfm3_q8_gemm_h16(const void* halves, const void* scales, std::uint32_t rows,

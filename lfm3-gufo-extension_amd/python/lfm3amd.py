@@ -108,6 +108,9 @@ _SIGS = {
     "lfm3_q8_half_tiles": (i32, [vp, u32, u32, vp, vp]),
     "lfm3_q8_gemm_h16": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, vp, u32, u32, vp]),
     "lfm3_q8_gemm_swiglu_h16": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, vp, u32, vp, vp]),
+    "lfm3_q8_gemm_swiglu_flags_bytes": (sz, [u32, u32]),
+    "lfm3_q8_gemm_swiglu_h16_rows": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, vp, u32, vp, vp,
+                                           u32, vp, vp, u32, vp, vp]),
     "lfm3_q8_gemv_swiglu": (i32, [vp, vp, u32, u32, vp, u32, vp, u32, u32, vp, sz, vp]),
     "lfm3_bf16_tiled_bytes": (sz, [u32, u32]),
     "lfm3_bf16_pack_host": (i32, [vp, u32, u32, vp, u32, u32]),

@@ -259,6 +259,33 @@ def test_conv_prompt_half_rejects_bad_shapes():
     assert call(out=None) == L.E_INVALID
 
 
+def test_swiglu_rows_rejects_bad_arguments():
+    """The SwiGLU GEMM with FP16 hidden rows refuses, before any launch: a
+    missing output, scale, row-maximum or flags buffer, sequence number 0,
+    rows not a multiple of 4 or past 8192, an output stride that is not a
+    whole number of 64-column chunks."""
+    lib = L.lib()
+    f = 4096
+    ok = dict(h=f, s=f, rows=7680, cols=2048, a=f, lda=2048, asc=f, tokens=512, y=f, ldy=7680,
+              rm=f, out=f, out_ld=7680, osc=f, flags=f, seq=1)
+
+    def call(**kw):
+        a = dict(ok, **kw)
+        return lib.lfm3_q8_gemm_swiglu_h16_rows(a["h"], a["s"], a["rows"], a["cols"], a["a"],
+                                                a["lda"], a["asc"], a["tokens"], a["y"],
+                                                a["ldy"], a["rm"], a["out"], a["out_ld"],
+                                                a["osc"], a["flags"], a["seq"], None, None)
+    assert call(out=None) == L.E_INVALID
+    assert call(osc=None) == L.E_INVALID
+    assert call(rm=None) == L.E_INVALID
+    assert call(flags=None) == L.E_INVALID
+    assert call(seq=0) == L.E_INVALID
+    assert call(rows=7682, ldy=7682, out_ld=7744) == L.E_INVALID
+    assert call(rows=8196, ldy=8196, out_ld=8256) == L.E_INVALID
+    assert call(out_ld=7700) == L.E_INVALID
+    assert lib.lfm3_q8_gemm_swiglu_flags_bytes(7680, 512) == 60 * 4 * 4
+
+
 def test_snapshot_signature_is_fnv1a32():
     """The snapshot's configuration signature is 32-bit FNV-1a
     (engine.cpp ConfigSignature): the published test vectors, and the word

@@ -178,3 +178,49 @@ def test_gemm_half_tiles_identical(M, K, n, parts, swiglu):
     inputs, _ = O.half_rows(x)
     ok, err = within(b, inputs.astype(np.float64) @ L.q8_dequant(g, M, K).T)
     assert ok, err
+
+
+@pytest.mark.parametrize("F,K,ns", [(7680, 2048, (512, 300)), (192, 128, (20, 133)),
+                                    (7680, 2048, (16, 512))])
+def test_gemm_swiglu_rows_is_gemm_then_half_rows(F, K, ns):
+    """The SwiGLU GEMM whose trailing blocks write the down projection's
+    FP16 rows (lfm3_q8_gemm_swiglu_h16_rows) against the plain SwiGLU GEMM
+    followed by lfm3_half_rows with its row maxima: y, the row maxima, the
+    FP16 rows and their scales bit-exact, chunk tails zero, nothing past the
+    last row; two calls in a row on the same flags (the second with another
+    row count and the next sequence number), and no wait timed out."""
+    lib = L.lib()
+    g, u = L.q8(SEED, f"sr.g{F}", F, K), L.q8(SEED, f"sr.u{F}", F, K)
+    m = DeviceMatrix(g, F, K, interleave_with=u)
+    halves = half_tiles(m, 2 * F)
+    flags = L.DeviceBuffer(lib.lfm3_q8_gemm_swiglu_flags_bytes(F, 512))
+    L.hip_check(L.hip().hipMemset(flags.addr, 0, flags.nbytes))
+    err = L.DeviceBuffer.of(np.zeros(1, np.uint32))
+    blocks = lib.lfm3_q8_gemm_swiglu_max_blocks(F)
+    out_ld = (F + 63) // 64 * 64 + 64
+    for seq, n in enumerate(ns, start=1):
+        print(f"[swiglu rows] F {F} K {K} n {n} seq {seq}", flush=True)
+        x = L.normal(SEED, f"sr.x.{F}.{n}", n * K).reshape(n, K)
+        da, ds, lda = half_rows_gpu(x)
+        want_y, want_rm = gemm(m, x, swiglu=True, half=True)
+        dy = L.DeviceBuffer(n * F * 4)
+        rm = L.DeviceBuffer(blocks * n * 4)
+        out = L.DeviceBuffer.of(np.full((n + 1) * out_ld, 0x7e00, np.uint16))
+        sc = L.DeviceBuffer.of(np.full(n + 1, -1.0, np.float32))
+        L.check(lib.lfm3_q8_gemm_swiglu_h16_rows(halves.addr, m.scales.addr, F, K, da.addr, lda,
+                                                 ds.addr, n, dy.addr, F, rm.addr, out.addr,
+                                                 out_ld, sc.addr, flags.addr, seq, err.addr,
+                                                 None))
+        L.synchronize()
+        y = dy.download(np.float32, n * F).reshape(n, F)
+        assert np.array_equal(y, want_y)
+        assert np.array_equal(rm.download(np.uint32, blocks * n).reshape(blocks, n), want_rm)
+        wa, ws, wlda = half_rows_gpu(want_y, row_max=want_rm.reshape(-1), max_blocks=blocks)
+        want = wa.download(np.uint16, n * wlda).reshape(n, wlda)
+        got = out.download(np.uint16, (n + 1) * out_ld).reshape(n + 1, out_ld)
+        padded = (F + 63) // 64 * 64
+        assert np.array_equal(got[:n, :padded], want[:, :padded])
+        assert np.all(got[:n, padded:] == 0x7e00) and np.all(got[n] == 0x7e00)
+        scale = sc.download(np.float32, n + 1)
+        assert np.array_equal(scale[:n], ws.download(np.float32, n)) and scale[n] == -1.0
+    assert err.download(np.uint32, 1)[0] == 0
