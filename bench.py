@@ -63,8 +63,12 @@ GEMV_TRAFFIC = {"read": 18_477_766, "write": 262_144}
 # The same for the round's dominant launch, the residual norm (2 K parts)
 # fused with the SwiGLU operand-image GEMV (2 x 7680 x 2048, 8 rows):
 # 1.024 x its algorithmic bytes.
-SWIGLU_TRAFFIC = {"read": 34_394_800, "write": 444_621}
-GEMM_TRAFFIC = {"read": 86_290_594, "write": 15_851_520}
+SWIGLU_TRAFFIC = {"read": 34_396_745, "write": 444_621}
+# The prompt pass's gate/up SwiGLU GEMM as the pass launches it, with the
+# trailing blocks that write the FP16 hidden rows: 1.40 x its algorithmic
+# bytes (the trailing blocks re-read the 15.7 MB of FP32 outputs; the GEMM
+# alone moves 1.23 x, as each XCD fetches the activation block).
+GEMM_TRAFFIC = {"read": 103_201_906, "write": 23_731_712}
 
 
 def log(msg: str):
@@ -589,62 +593,68 @@ def pass_flops(d: L.Dims, n: int, depth: int, pruned: bool) -> int:
 
 def gemm_roofline(copies: int, passes: int):
     """The prompt pass's dominant kernel: the gate/up SwiGLU GEMM (7680 gate
-    + 7680 up rows x 2048, Q8_0) on 512 FP16 rows with its row maxima for the
-    down projection, as the pass runs it, over `copies` rotated
-    weight buffers, replayed from a HIP graph and timed with HIP events on
-    the stream it runs on."""
+    + 7680 up rows x 2048, Q8_0 on FP16 tiles) on 512 FP16 rows, launched as
+    the pass launches it (lfm3_q8_gemm_swiglu_h16_rows: its trailing blocks
+    write the down projection's FP16 rows), over `copies` rotated weight
+    buffers, replayed from HIP graphs and timed with HIP events on the
+    stream it runs on. The same GEMM without the trailing blocks
+    (lfm3_q8_gemm_swiglu_h16, its row maxima for a separate conversion) is
+    timed beside it."""
     import ctypes as C
+    lib = L.lib()
     F, H, n = 7680, 2048, PASS_ROWS
     cb, sb = C.c_size_t(), C.c_size_t()
-    L.lib().lfm3_q8_tiled_bytes(2 * F, H, C.byref(cb), C.byref(sb))
+    lib.lfm3_q8_tiled_bytes(2 * F, H, C.byref(cb), C.byref(sb))
     codes = np.zeros(cb.value, np.uint8)
     scales = np.zeros(sb.value, np.uint8)
     g = L.q8(L.SEED, "gemm.gate", F, H)
     u = L.q8(L.SEED, "gemm.up", F, H)
-    L.check(L.lib().lfm3_q8_pack_host(L.ptr(g), F, H, L.ptr(codes), L.ptr(scales), 0, 2))
-    L.check(L.lib().lfm3_q8_pack_host(L.ptr(u), F, H, L.ptr(codes), L.ptr(scales), 1, 2))
+    L.check(lib.lfm3_q8_pack_host(L.ptr(g), F, H, L.ptr(codes), L.ptr(scales), 0, 2))
+    L.check(lib.lfm3_q8_pack_host(L.ptr(u), F, H, L.ptr(codes), L.ptr(scales), 1, 2))
     # The pass reads FP16 tiles: decoded once from the codes, as the model does.
     dcodes = L.DeviceBuffer.of(codes)
     mats = []
     for _ in range(copies):
-        halves = L.DeviceBuffer(L.lib().lfm3_q8_half_tiles_bytes(2 * F, H))
-        L.check(L.lib().lfm3_q8_half_tiles(dcodes.addr, 2 * F, H, halves.addr, None))
+        halves = L.DeviceBuffer(lib.lfm3_q8_half_tiles_bytes(2 * F, H))
+        L.check(lib.lfm3_q8_half_tiles(dcodes.addr, 2 * F, H, halves.addr, None))
         mats.append((halves, L.DeviceBuffer.of(scales)))
     L.synchronize()
     dcodes.close()
     x = L.DeviceBuffer.of(L.normal(L.SEED, "gemm.x", n * H))
     a16 = L.DeviceBuffer(n * H * 2)
     scale = L.DeviceBuffer(n * 4)
-    L.check(L.lib().lfm3_half_rows(x.addr, H, None, 0, a16.addr, H, scale.addr, n, H, None))
+    L.check(lib.lfm3_half_rows(x.addr, H, None, 0, a16.addr, H, scale.addr, n, H, None))
     y = L.DeviceBuffer(n * F * 4)
-    row_max = L.DeviceBuffer(L.lib().lfm3_q8_gemm_swiglu_max_blocks(F) * n * 4)
-    stream = L.Stream()
-
-    def one_pass():
-        for c, s in mats:
-            L.check(L.lib().lfm3_q8_gemm_swiglu_h16(c.addr, s.addr, F, H, a16.addr, H, scale.addr,
-                                                    n, y.addr, F, row_max.addr, stream.handle))
-
-    graph = L.Graph(stream, one_pass)
-    graph.launch()
-    stream.synchronize()
-    a, b = L.Event(), L.Event()
-    a.record(stream.handle)
-    for _ in range(passes):
-        graph.launch()
-    b.record(stream.handle)
-    b.synchronize()
-    us = a.elapsed_ms(b) * 1000.0 / (passes * copies)
-    graph.close()
-    a.close()
-    b.close()
-    stream.close()
+    max_blocks = lib.lfm3_q8_gemm_swiglu_max_blocks(F)
+    row_max = L.DeviceBuffer(max_blocks * n * 4)
+    hld = (F + 63) // 64 * 64
+    hid16 = L.DeviceBuffer(n * hld * 2)
+    hscale = L.DeviceBuffer(n * 4)
+    flags = L.DeviceBuffer(lib.lfm3_q8_gemm_swiglu_flags_bytes(F, n))
+    L.hip_check(L.hip().hipMemset(flags.addr, 0, flags.nbytes))
+    err = L.DeviceBuffer(4)
+    L.hip_check(L.hip().hipMemset(err.addr, 0, 4))
+    L.synchronize()
+    us = time_launches(lambda i, s, q: L.check(lib.lfm3_q8_gemm_swiglu_h16_rows(
+        mats[i][0].addr, mats[i][1].addr, F, H, a16.addr, H, scale.addr, n, y.addr, F,
+        row_max.addr, hid16.addr, hld, hscale.addr, flags.addr, q, err.addr, s)),
+        copies, passes, seqs=True)
+    if int(err.download(np.uint32, 1)[0]):
+        raise RuntimeError("the SwiGLU GEMM's trailing blocks timed out waiting")
+    gemm_us = time_launches(lambda i, s: L.check(lib.lfm3_q8_gemm_swiglu_h16(
+        mats[i][0].addr, mats[i][1].addr, F, H, a16.addr, H, scale.addr, n, y.addr, F,
+        row_max.addr, s)), copies, passes)
     flops = 2 * n * 2 * F * H
     # FP16 weights (2 bytes each) and their fp16 block scales, the FP16
-    # rows with their scales, the outputs and the row maxima.
-    nbytes = (2 * F * H * 2 + 2 * F * (H // 32) * 2 + n * H * 2 + n * 4 + n * F * 4
-              + L.lib().lfm3_q8_gemm_swiglu_max_blocks(F) * n * 4)
-    return {"flops": flops, "bytes": nbytes, "us": us, "tflops": flops / (us * 1e-6) / 1e12}
+    # rows with their scales, the FP32 outputs and row maxima, and the FP16
+    # hidden rows with their scales (the trailing blocks' re-read of the
+    # FP32 outputs is not counted).
+    gemm_bytes = (2 * F * H * 2 + 2 * F * (H // 32) * 2 + n * H * 2 + n * 4 + n * F * 4
+                  + max_blocks * n * 4)
+    nbytes = gemm_bytes + n * hld * 2 + n * 4
+    return {"flops": flops, "bytes": nbytes, "us": us, "tflops": flops / (us * 1e-6) / 1e12,
+            "gemm_only_us": gemm_us, "gemm_only_bytes": gemm_bytes,
+            "gemm_only_tflops": flops / (gemm_us * 1e-6) / 1e12}
 
 
 def copy_calibration(nbytes: int, reps: int):
@@ -1171,7 +1181,8 @@ def main():
         gemm = gemm_roofline(8, 4)
         log(f"pass {pass_ms:.2f} ms, {tflops:.0f} TFLOP/s; mixed round {mixed_ms:.2f} ms "
             f"(serial {mixed['serial']:.2f}, decode alone {mixed['decode']:.2f}); "
-            f"swiglu GEMM {gemm['us']:.1f} us, {gemm['tflops']:.0f} TFLOP/s")
+            f"swiglu GEMM {gemm['us']:.1f} us, {gemm['tflops']:.0f} TFLOP/s "
+            f"(without its trailing blocks {gemm['gemm_only_us']:.1f} us)")
         result["prefill"] = {
             "workload": (f"one {PASS_ROWS}-token prompt pass (Session::Forward) at depth "
                          f"{PASS_DEPTH} of a synthesized session, same model"),
@@ -1184,7 +1195,8 @@ def main():
             "reps": args.prefill_reps,
             "roofline": {
                 "bound": "mfma",
-                "kernel": "Q8_0 x FP16 SwiGLU GEMM, 15360 x 2048 on 512 rows",
+                "kernel": ("Q8_0 x FP16 SwiGLU GEMM, 15360 x 2048 on 512 rows, with its "
+                           "trailing blocks writing the 512 x 7680 FP16 hidden rows"),
                 "achieved": round(gemm["tflops"], 1),
                 "peak": MFMA_PEAK_TFLOPS,
                 "unit": "TFLOP/s",
@@ -1195,6 +1207,8 @@ def main():
                 "algorithmic_bytes": gemm["bytes"],
                 "flops_per_launch": gemm["flops"],
                 "us_per_launch": round(gemm["us"], 2),
+                "gemm_only_us_per_launch": round(gemm["gemm_only_us"], 2),
+                "gemm_only_frac": round(gemm["gemm_only_tflops"] / MFMA_PEAK_TFLOPS, 4),
             },
         }
         result["mixed_round"] = {
