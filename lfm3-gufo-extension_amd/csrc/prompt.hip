@@ -447,77 +447,108 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
         q[r] = *reinterpret_cast<const uint4*>(stage + Stage::kW +
                                                (wr * RT + r) * kTileW + lane * 16);
     }
+    // Q8_0 block blk's operands: the B operand of tile r, and the A operand
+    // of token group t (lane L: row wt 16 TT + 16 t + L % 16, segment
+    // 4 blk + L / 16, stored in slot segment ^ (L & 7)).
+    const auto w_frag = [&](int blk, int r) -> h8 {
+      if constexpr (Shape::kHalfTiles)
+        return *reinterpret_cast<const h8*>(stage + Stage::kW + (wr * RT + r) * kTileW +
+                                            blk * kTileCodeBytes + lane * 16);
+      else
+        return blk ? EightCodes(q[r].z, q[r].w) : EightCodes(q[r].x, q[r].y);
+    };
+    const auto a_frag = [&](int blk, int t) {
+      const int slot = (blk * 4 + (lane >> 4)) ^ (lane & 7);
+      return *reinterpret_cast<const h8*>(stage + (t * 16 + a_row) * 128 + slot * 16);
+    };
+    // acc += d * p, with d the block's fp16 scale (the low half of the
+    // tile's scale dword for block 0, the high half for block 1) read by
+    // v_fma_mix_f32 as an exact FP32 value: one rounding, as the
+    // conversion followed by an FMA, without the conversion and shift.
+    // Written as assembly tied to the accumulator so it updates in place.
+    unsigned sc[4];
+    const auto scale_fma = [&](float& a, int r, float p, int blk) {
+      if (blk)
+        asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "+v"(a) : "v"(sc[r]), "v"(p));
+      else
+        asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
+            : "+v"(a) : "v"(sc[r]), "v"(p));
+    };
+    // The first step's operands are read first, in the order the MFMAs
+    // take them (the first MFMA waits for its A fragment and tile 0 only),
+    // then the scales.
+    h8 av = a_frag(0, 0);
+    h8 w[RT], wn[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      __builtin_amdgcn_sched_barrier(0);
+      w[r] = w_frag(0, r);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     const uint4 sc4 = *reinterpret_cast<const uint4*>(
         stage + Stage::kS + wr * RT * kTileScales * 2 + (lane & 15) * 16);
-    const unsigned sc[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+    sc[0] = sc4.x;
+    sc[1] = sc4.y;
+    sc[2] = sc4.z;
+    sc[3] = sc4.w;
+    // One software pipeline over the chunk's 2 TT steps (block 0's token
+    // groups, then block 1's): the MFMAs of step s issue beside the scale
+    // FMAs of step s - 1, in a fixed order (the A read for s + 1, then each
+    // MFMA of s followed by the 4 FMAs of s - 1 on the previous MFMA's
+    // tile), so the matrix pipe runs while the VALU works; block 1's tiles
+    // are read during block 0's second step. The scheduling barriers also
+    // keep the compiler from hoisting every MFMA of the chunk (which would
+    // hold 8 RT TT result registers).
+    f4 prev[RT];
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      h8 w[RT];
-#pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        if constexpr (Shape::kHalfTiles)
-          w[r] = *reinterpret_cast<const h8*>(stage + Stage::kW + (wr * RT + r) * kTileW +
-                                              blk * kTileCodeBytes + lane * 16);
-        else
-          w[r] = blk ? EightCodes(q[r].z, q[r].w) : EightCodes(q[r].x, q[r].y);
-      }
-      // acc += d * p, with d the block's fp16 scale (the low half of the
-      // tile's scale dword for block 0, the high half for block 1) read by
-      // v_fma_mix_f32 as an exact FP32 value: one rounding, as the
-      // conversion followed by an FMA, without the conversion and shift.
-      // Written as assembly tied to the accumulator so it updates in place.
-      const auto scale_fma = [&](float& a, int r, float p) {
-        if (blk)
-          asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-              : "+v"(a) : "v"(sc[r]), "v"(p));
-        else
-          asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
-              : "+v"(a) : "v"(sc[r]), "v"(p));
-      };
-      const int slot = (blk * 4 + (lane >> 4)) ^ (lane & 7);
-      const auto a_frag = [&](int t) {
-        return *reinterpret_cast<const h8*>(stage + (t * 16 + a_row) * 128 + slot * 16);
-      };
-      // Software pipeline over token groups: the MFMAs of group t issue
-      // beside the scale FMAs of group t - 1, in a fixed order (the A read
-      // for t + 1, then each MFMA of t followed by the 4 FMAs of t - 1 on
-      // the previous MFMA's tile), so the matrix pipe runs while the VALU
-      // works; the scheduling barriers also keep the compiler from
-      // hoisting every MFMA of the chunk (which would hold 4 RT TT result
-      // registers).
-      h8 av = a_frag(0);
-      f4 prev[RT];
-#pragma unroll
-      for (int t = 0; t < TT; ++t) {
-        const h8 next = a_frag(t + 1 < TT ? t + 1 : t);
-        f4 cur[RT];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int r = 0; r < RT; ++r) {
-          cur[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, w[r], zero, 0, 0, 0);
-          __builtin_amdgcn_sched_barrier(0);
-          if (t > 0) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              scale_fma(acc[r][t - 1][i], r, prev[r][i]);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
+    for (int step = 0; step < 2 * TT; ++step) {
+      const int blk = step / TT, t = step % TT;
+      const int pblk = (step - 1) / TT, pt = (step + TT - 1) % TT;  // step - 1
+      const h8 next = step + 1 < 2 * TT ? a_frag((step + 1) / TT, (step + 1) % TT) : av;
+      if (step == 1) {
 #pragma unroll
         for (int r = 0; r < RT; ++r)
-          prev[r] = cur[r];
-        av = next;
+          wn[r] = w_frag(1, r);
+      }
+      if (step == TT) {
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+          w[r] = wn[r];
+      }
+      f4 cur[RT];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        cur[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, w[r], zero, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (step > 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            scale_fma(acc[r][pt][i], r, prev[r][i], pblk);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int r = 0; r < RT; ++r)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          scale_fma(acc[r][TT - 1][i], r, prev[r][i]);
-      asm volatile("" : LFM3_PIN4(acc[0][TT - 1]), LFM3_PIN4(acc[1][TT - 1]),
-                   LFM3_PIN4(acc[2][TT - 1]), LFM3_PIN4(acc[3][TT - 1]));
+        prev[r] = cur[r];
+      av = next;
+      (void)blk;
+      (void)t;
     }
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        scale_fma(acc[r][TT - 1][i], r, prev[r][i], 1);
+    asm volatile("" : LFM3_PIN4(acc[0][TT - 1]), LFM3_PIN4(acc[1][TT - 1]),
+                 LFM3_PIN4(acc[2][TT - 1]), LFM3_PIN4(acc[3][TT - 1]));
   };
 
+  // No scalar load (kernel arguments for the epilogue) is left in flight
+  // into the loop: with one pending, the wait before each chunk's first
+  // MFMA would have to drain every LDS read, not just its own operands.
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   // Three-stage pipeline, unrolled so each stage is a fixed array. Step c:
   // wait until chunk c's loads are done (chunk c + 1's may remain in
   // flight), barrier (chunk c visible to every wave, and every wave done
@@ -553,6 +584,10 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
       wait_all_but_one_chunk();
     else
       __builtin_amdgcn_s_waitcnt(WaitVm(0));
+    // Nothing counted by lgkmcnt is in flight here; the wait says so to the
+    // compiler's wait insertion on every path into the step, so the step's
+    // first MFMA waits for its own LDS operands, not for all of them.
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
     BlockBarrier();
     if (c + 2 < c_end)
       issue(c + 2, refill);
