@@ -439,6 +439,30 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   // A read of lane L: row wt 16 TT + 16 t + L % 16, segment 4 blk + L / 16,
   // stored in slot segment ^ (L & 7).
   const int a_row = wt * TT * 16 + (lane & 15);
+  // The previous chunk's last MFMA results and block scales, scaled into
+  // acc[.][TT - 1] at the next chunk's first step (before the first chunk:
+  // zero products at scale 0, which leave the zero accumulators as they
+  // are).
+  f4 last[RT];
+  unsigned last_sc[RT];
+  // acc += d * p, with d the block's fp16 scale (the low half of the
+  // tile's scale dword d2 for block 0, the high half for block 1) read by
+  // v_fma_mix_f32 as an exact FP32 value: one rounding, as the conversion
+  // followed by an FMA, without the conversion and shift. Written as
+  // assembly tied to the accumulator so it updates in place.
+  const auto scale_fma = [](float& a, unsigned d2, float p, int blk) {
+    if (blk)
+      asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+          : "+v"(a) : "v"(d2), "v"(p));
+    else
+      asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
+          : "+v"(a) : "v"(d2), "v"(p));
+  };
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    last[r] = zero;
+    last_sc[r] = 0u;
+  }
   const auto compute = [&](const std::uint8_t* stage) {
     uint4 q[RT];
     if constexpr (!Shape::kHalfTiles) {
@@ -461,20 +485,7 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
       const int slot = (blk * 4 + (lane >> 4)) ^ (lane & 7);
       return *reinterpret_cast<const h8*>(stage + (t * 16 + a_row) * 128 + slot * 16);
     };
-    // acc += d * p, with d the block's fp16 scale (the low half of the
-    // tile's scale dword for block 0, the high half for block 1) read by
-    // v_fma_mix_f32 as an exact FP32 value: one rounding, as the
-    // conversion followed by an FMA, without the conversion and shift.
-    // Written as assembly tied to the accumulator so it updates in place.
     unsigned sc[4];
-    const auto scale_fma = [&](float& a, int r, float p, int blk) {
-      if (blk)
-        asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-            : "+v"(a) : "v"(sc[r]), "v"(p));
-      else
-        asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
-            : "+v"(a) : "v"(sc[r]), "v"(p));
-    };
     // The first step's operands are read first, in the order the MFMAs
     // take them (the first MFMA waits for its A fragment and tile 0 only),
     // then the scales.
@@ -497,7 +508,10 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
     // FMAs of step s - 1, in a fixed order (the A read for s + 1, then each
     // MFMA of s followed by the 4 FMAs of s - 1 on the previous MFMA's
     // tile), so the matrix pipe runs while the VALU works; block 1's tiles
-    // are read during block 0's second step. The scheduling barriers also
+    // are read during block 0's second step. The FMAs of the chunk's last
+    // step run in the next chunk's first step (last, last_sc), after the
+    // block barrier, beside that chunk's first MFMAs; each accumulator still
+    // takes its block products in K order. The scheduling barriers also
     // keep the compiler from hoisting every MFMA of the chunk (which would
     // hold 8 RT TT result registers).
     f4 prev[RT];
@@ -525,7 +539,11 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
         if (step > 0) {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            scale_fma(acc[r][pt][i], r, prev[r][i], pblk);
+            scale_fma(acc[r][pt][i], sc[r], prev[r][i], pblk);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            scale_fma(acc[r][TT - 1][i], last_sc[r], last[r][i], 1);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -537,18 +555,11 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
       (void)t;
     }
 #pragma unroll
-    for (int r = 0; r < RT; ++r)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        scale_fma(acc[r][TT - 1][i], r, prev[r][i], 1);
-    asm volatile("" : LFM3_PIN4(acc[0][TT - 1]), LFM3_PIN4(acc[1][TT - 1]),
-                 LFM3_PIN4(acc[2][TT - 1]), LFM3_PIN4(acc[3][TT - 1]));
+    for (int r = 0; r < RT; ++r) {
+      last[r] = prev[r];
+      last_sc[r] = sc[r];
+    }
   };
-
-  // No scalar load (kernel arguments for the epilogue) is left in flight
-  // into the loop: with one pending, the wait before each chunk's first
-  // MFMA would have to drain every LDS read, not just its own operands.
-  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   // Three-stage pipeline, unrolled so each stage is a fixed array. Step c:
   // wait until chunk c's loads are done (chunk c + 1's may remain in
   // flight), barrier (chunk c visible to every wave, and every wave done
@@ -607,6 +618,13 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
   if (c + 1 < c_end)
     step(c + 1, s_st1, s_st0);
   }
+
+  // The last chunk's last step.
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      scale_fma(acc[r][TT - 1][i], last_sc[r], last[r][i], 1);
 
   // D layout: lane L holds tokens 16 t + 4 (L / 16) + i of weight row L % 16.
   const int sub = lane & 15, quad = lane >> 4;
