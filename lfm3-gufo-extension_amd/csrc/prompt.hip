@@ -45,14 +45,14 @@ constexpr int kGemmRT = 4, kGemmTT = 4, kGemmStages = 3;
 // holds, decoded once at load into block 0's eight halves at byte 16 L and
 // block 1's at 1024 + 16 L), so the loop feeds them to the MFMA without the
 // per-chunk decode; the operands, and so every product, are the same.
-template<int WR, int WT, bool kHalf = false, int kStageCount = kGemmStages>
+template<int WR, int WT, bool kHalf = false, int kStageCount = kGemmStages, int TT = kGemmTT>
 struct GemmShape {
-  static constexpr int kWR = WR, kWT = WT;
+  static constexpr int kWR = WR, kWT = WT, kTT = TT;
   static constexpr bool kHalfTiles = kHalf;
   static constexpr int kStages = kStageCount;  // LDS pipeline stages: 2 or 3
   static constexpr int kWaves = WR * WT, kThreads = 64 * kWaves;
   static constexpr int kTiles = WR * kGemmRT;  // weight tiles a block
-  static constexpr int kTokens = WT * kGemmTT * 16;
+  static constexpr int kTokens = WT * TT * 16;
   static constexpr int kTileW = kHalf ? 2 * kTileCodeBytes : kTileCodeBytes;
   static constexpr int kW = kTokens * 128;
   static constexpr int kS = kW + kTiles * kTileW;
@@ -223,7 +223,7 @@ struct HiddenHalves {
 // Two rows a trailing block (256 blocks for 512 rows): the 512-token pass
 // at 4.59 ms against 4.60 with 4 rows, 4.61 with 8 or 1, and 4.65 with the
 // conversion as a launch of its own (three runs each, one box).
-constexpr int kHiddenRows = 2, kHiddenLoads = 4;
+constexpr int kHiddenRows = 2, kHiddenMaxCols = 8192;
 constexpr int kGemmSpinLimit = 1 << 20;
 
 // A trailing block of the SwiGLU GEMM: rows r0 .. r0 + kHiddenRows - 1 of
@@ -234,6 +234,7 @@ __device__ __forceinline__ void ConvertHidden(const HiddenHalves& t, const float
                                               int cols, int n, const unsigned* row_max,
                                               int row_blocks) {
   static_assert(kTokens % kHiddenRows == 0, "a converter's rows lie in one token block");
+  constexpr int kHiddenLoads = kHiddenMaxCols / 4 / T;
   __shared__ float s_rmax[kHiddenRows][T / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r0 = (int(blockIdx.x) - t.gemm_blocks) * kHiddenRows;
@@ -277,8 +278,8 @@ __device__ __forceinline__ void ConvertHidden(const HiddenHalves& t, const float
       s_rmax[i][wave] = part[i];
   __syncthreads();
   // Every row's values are loaded before the first conversion (at most
-  // kHiddenLoads 16-byte loads a row and thread: cols <= 16 T), so the
-  // block waits on memory once.
+  // kHiddenLoads 16-byte loads a row and thread: cols <= kHiddenMaxCols), so
+  // the block waits on memory once.
   typedef unsigned u4 __attribute__((ext_vector_type(4)));
   const BufferResource y_res = MakeBuffer(y, unsigned(n) * unsigned(ldy) * 4u);
   u4 w[kHiddenRows][kHiddenLoads];
@@ -334,7 +335,7 @@ __global__ void Q8GemmKernel(const std::uint8_t* __restrict__ codes,
                              int row_blocks, int token_blocks, int parts,
                              std::size_t part_stride,
                              unsigned* __restrict__ row_max, const HiddenHalves tail) {
-  constexpr int RT = kGemmRT, TT = kGemmTT;
+  constexpr int RT = kGemmRT, TT = Shape::kTT;
   using Stage = Shape;
   constexpr int A_LOADS = Shape::kTokens * 8 / Shape::kThreads;  // 16-byte loads a lane
   constexpr int W_LOADS = Shape::kTiles / Shape::kWaves;         // tiles a wave loads
@@ -941,7 +942,7 @@ int lfm3_q8_gemm_swiglu_h16_rows(const void* halves, const void* scales, std::ui
                                  std::uint32_t out_ld, float* out_scale, unsigned* flags,
                                  std::uint32_t seq, unsigned* error, void* stream) {
   if (!out || !out_scale || !row_max || !flags || !seq || rows % 4 || ldy % 4 ||
-      out_ld % 64 || out_ld < rows || rows > std::uint32_t(16 * WideHalfShape::kThreads) ||
+      out_ld % 64 || out_ld < rows || rows > std::uint32_t(kHiddenMaxCols) ||
       (reinterpret_cast<std::uintptr_t>(y) & 15) || (reinterpret_cast<std::uintptr_t>(out) & 7))
     return Fail(LFM3_E_INVALID, "unsupported LFM3 prompt SwiGLU with FP16 hidden rows");
   HiddenHalves tail;
