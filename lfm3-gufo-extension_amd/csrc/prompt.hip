@@ -11,10 +11,11 @@
 // code x half products summed in FP32 (A operand = 16 tokens' activations,
 // B operand = 16 weight rows decoded exactly from the tiled layout), and
 // the block scale applies as acc = fma(d, dot, acc) (q8_prefill.hpp:
-// 538-560). A block of 4 waves owns 64 RT weight rows (16 RT per wave) and
-// 16 TT tokens. Each chunk's activations, weight tiles and scales arrive
-// by direct-to-LDS loads into a two-stage pipeline, so registers hold only
-// the accumulators and the chunk being multiplied. Narrow outputs split K
+// 538-560). A block of WR x WT waves owns 16 RT WR weight rows and 16 TT WT
+// tokens (16 RT rows and 16 TT tokens a wave). Each chunk's activations,
+// weight tiles and scales arrive by direct-to-LDS loads into a two- or
+// three-stage pipeline, so registers hold only the accumulators and the
+// operands being multiplied. Narrow outputs split K
 // across blockIdx.z into parts written separately; their consumer adds the
 // parts in part order, so no launch merges blocks through memory.
 #include <algorithm>
@@ -26,13 +27,13 @@ namespace lfm3amd {
 namespace {
 
 // Block shapes: WR x WT waves; each wave owns kGemmRT weight tiles (16
-// rows each) and 16 kGemmTT tokens. The wide shape (4 x 2 waves) covers 256
-// weight rows and 128 tokens: 128 FLOP per staged byte (2 M N / (M + 2 N)
-// for 1-byte codes and 2-byte activations), about one block per CU for the
-// 512-token pass. The narrow shape (2 x 2 waves, 128 rows x 128 tokens)
-// does a quarter of that work a block and two blocks fit a CU: projections
-// with few output rows fill the 256 CUs with fewer K parts, and each part
-// costs a full FP32 output pass.
+// rows each) and 16 TT tokens (kGemmTT unless the shape says otherwise).
+// The wide shape (4 x 2 waves) covers 256 weight rows and 128 tokens: 128
+// FLOP per staged byte (2 M N / (M + 2 N) for 1-byte codes and 2-byte
+// activations), about one block per CU for the 512-token pass. The narrow
+// shape (2 x 2 waves, 128 rows x 128 tokens) does a quarter of that work a
+// block and two blocks fit a CU: projections with few output rows fill the
+// 256 CUs with fewer K parts, and each part costs a full FP32 output pass.
 constexpr int kGemmRT = 4, kGemmTT = 4, kGemmStages = 3;
 
 // A block shape and its pipeline stage: the block's activation rows for
@@ -60,7 +61,13 @@ struct GemmShape {
 };
 using WideShape = GemmShape<4, 2>;
 using NarrowShape = GemmShape<2, 2>;
-using WideHalfShape = GemmShape<4, 2, true>;
+// The same 256 x 128 block tile on FP16 tiles in 16 waves of 64 rows x 32
+// tokens: four waves a SIMD instead of two hide more of the LDS and MFMA
+// latency, for half again the LDS operand reads a MFMA (the SwiGLU GEMM
+// 54.9-56.8 us against 57.6-59.5 with 8 waves of 64 x 64, the pass 0.7-1.2%
+// faster). The code-tile shapes stay at 8 and 4 waves: 16 and 8 waves made
+// their projections slower (6144 x 2048: 31.2 us against 28.0).
+using WideHalfShape = GemmShape<4, 4, true, kGemmStages, 2>;
 // Two stages, so that two blocks (2 x 65 KB) fit a CU.
 using NarrowHalfShape = GemmShape<2, 2, true, 2>;
 
