@@ -516,8 +516,10 @@ __device__ __forceinline__ void ImageGemvCore(const std::uint8_t* __restrict__ c
   }
 }
 
-// A fused launch (kNorm) has W + 1 waves a block: wave W loads the image
-// into LDS (dynamic shared memory, 2 KB a chunk of the K range) and leaves.
+// A fused launch (kNorm) has W + 1 waves a block: its first B blocks run
+// the norm rows and publish them (NormImageRow); in every other block wave
+// W watches the rows' flags (WatchRows) and hands over through an LDS word
+// while waves 0 .. W - 1 have their weight loads in flight, then leaves.
 template<int W, int RT, bool kSwiGLU, int SPW, bool kNorm = false>
 __launch_bounds__((W + kNorm) * 64)
 __attribute__((amdgpu_waves_per_eu(RT >= 4 ? 2 : kNorm ? 5 : 4)))
