@@ -63,12 +63,12 @@ GEMV_TRAFFIC = {"read": 18_477_766, "write": 262_144}
 # The same for the round's dominant launch, the residual norm (2 K parts)
 # fused with the SwiGLU operand-image GEMV (2 x 7680 x 2048, 8 rows):
 # 1.024 x its algorithmic bytes.
-SWIGLU_TRAFFIC = {"read": 34_396_745, "write": 444_621}
+SWIGLU_TRAFFIC = {"read": 34_396_183, "write": 444_621}
 # The prompt pass's gate/up SwiGLU GEMM as the pass launches it, with the
 # trailing blocks that write the FP16 hidden rows: 1.40 x its algorithmic
 # bytes (the trailing blocks re-read the 15.7 MB of FP32 outputs; the GEMM
 # alone moves 1.23 x, as each XCD fetches the activation block).
-GEMM_TRAFFIC = {"read": 103_201_906, "write": 23_731_712}
+GEMM_TRAFFIC = {"read": 103_034_560, "write": 23_731_712}
 
 
 def log(msg: str):
