@@ -93,8 +93,8 @@ struct PinnedBuffer {
 };
 
 // A tiled Q8_0 matrix of rows x cols (several sources may share it). The
-// gate/up prompt GEMM reads `halves`, the codes decoded to FP16 tiles,
-// made with the model's prompt scratch.
+// prompt GEMMs read `halves`, the codes decoded to FP16 tiles, made with
+// the model's prompt scratch; the decode GEMVs read the codes.
 // A float matrix (BF16, F16 or F32: `exact` set, `type` its format) keeps
 // its tiles in `codes` (lfm3_float_pack_host layout) and has no scales.
 struct Matrix {
@@ -1313,20 +1313,20 @@ PromptBuffers& EnsurePromptBuffers(lfm3_model& m) {
       256);
   b->one_ws = Buffer(b->one_ws_bytes);
   b->one_staging = std::make_unique<PinnedBuffer>(b->one_bytes);
-  // FP16 tiles of the gate/up matrices (every stored tile: two per 16
-  // output rows). Their GEMM runs in the wide block shape, where dropping
-  // the per-chunk code decode pays for the doubled tile bytes (about 9% on
-  // the 512-token gate/up GEMM). The other projections run in the narrow
-  // shape, two blocks a CU, where FP16 tiles gain under 1% of the pass (two
-  // LDS stages instead of three) for 1.4 GB more memory: they stay on code
-  // tiles.
+  // FP16 tiles of every Q8_0 matrix the prompt GEMMs multiply (every
+  // stored tile: gate/up two per 16 output rows), 2 bytes a weight: 2.9 GB
+  // at the reference dims. Dropping the per-chunk code decode pays for the
+  // doubled tile bytes: about 9% on the 512-token gate/up GEMM, 3% of the
+  // pass on the other projections.
   for (auto& l : m.layers) {
-    Matrix& w = l.ffn;
-    if (w.exact)
-      continue;
-    const std::uint32_t rows = w.tiles * kTileRows;
-    w.halves = Buffer(lfm3_q8_half_tiles_bytes(rows, w.cols), false);
-    CheckStatus(lfm3_q8_half_tiles(w.codes.p, rows, w.cols, w.halves.p, m.stream));
+    for (Matrix* wp : {&l.ffn, &l.down, &l.in_proj, &l.out_proj, &l.qkvg, &l.attn_out}) {
+      Matrix& w = *wp;
+      if (w.exact || !w.codes.p)
+        continue;
+      const std::uint32_t rows = w.tiles * kTileRows;
+      w.halves = Buffer(lfm3_q8_half_tiles_bytes(rows, w.cols), false);
+      CheckStatus(lfm3_q8_half_tiles(w.codes.p, rows, w.cols, w.halves.p, m.stream));
+    }
   }
   Check(hipStreamSynchronize(m.stream), "FP16 tiles");
   m.prompt = std::move(b);
@@ -1427,9 +1427,9 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
   };
   const auto gemm_parts = [&](const Matrix& w, std::uint32_t a_row, std::uint32_t rows,
                               float* y, std::uint32_t ldy, std::uint32_t parts) {
-    CheckStatus(lfm3_q8_gemm(w.codes.p, w.scales.p, w.rows, w.cols,
-                             a16 + std::size_t(a_row) * lda, lda, scale + a_row, rows, y, ldy,
-                             parts, s));
+    CheckStatus(lfm3_q8_gemm_h16(w.halves.p, w.scales.p, w.rows, w.cols,
+                                 a16 + std::size_t(a_row) * lda, lda, scale + a_row, rows, y,
+                                 ldy, parts, s));
   };
   const auto gemm = [&](const Matrix& w, std::uint32_t a_row, std::uint32_t rows, float* y,
                         std::uint32_t ldy) -> std::uint32_t {
@@ -1630,8 +1630,8 @@ void RunPrompt(lfm3_model& m, lfm3_session& se, const std::vector<ChunkPart>& in
           b.swiglu_seq, static_cast<unsigned*>(b.wait_error->device), s));
       const Matrix& w = l.down;
       const std::uint32_t dparts = lfm3_q8_gemm_parts(w.rows, w.cols, rows_out, 0);
-      CheckStatus(lfm3_q8_gemm(w.codes.p, w.scales.p, w.rows, w.cols, h16, hld, hscale,
-                               rows_out, out, H, dparts, s));
+      CheckStatus(lfm3_q8_gemm_h16(w.halves.p, w.scales.p, w.rows, w.cols, h16, hld, hscale,
+                                   rows_out, out, H, dparts, s));
       parts = dparts;
     }
     const bool last = il + 1 == L;

@@ -68,8 +68,13 @@ using NarrowShape = GemmShape<2, 2>;
 // faster). The code-tile shapes stay at 8 and 4 waves: 16 and 8 waves made
 // their projections slower (6144 x 2048: 31.2 us against 28.0).
 using WideHalfShape = GemmShape<4, 4, true, kGemmStages, 2>;
-// Two stages, so that two blocks (2 x 65 KB) fit a CU.
-using NarrowHalfShape = GemmShape<2, 2, true, 2>;
+// The narrow 128 x 128 block tile on FP16 tiles in 8 waves of 64 rows x 32
+// tokens and three stages (100 KB of LDS: one block a CU). With every
+// narrow projection of the 512-token pass on it the pass takes 4.22-4.30 ms
+// against 4.35-4.41 on code tiles in 4-wave blocks (two a CU); the same
+// 8 waves with two stages (two blocks a CU) 4.45-4.47, the 8-wave shape on
+// code tiles 4.48.
+using NarrowHalfShape = GemmShape<2, 4, true, kGemmStages, 2>;
 
 // One block per row: row maximum (scanned, or the maximum of max_blocks
 // partial maxima), then fp16(x 2^e) and the scale 2^-e. The vector form
