@@ -124,7 +124,7 @@ GemvPlan PlanGemv(std::uint32_t rows, std::uint32_t cols, bool swiglu,
 // + n] holds tile r's row n for token tok when the block's barrier returns.
 // GemvEpilogue then writes the block's rows (SwiGLU: tile 2j is gate,
 // 2j + 1 up, rows j * 16 + n).
-template<int W, int RT>
+template<int W, int RT, bool kLdsOnly = false>
 __device__ __forceinline__ void StoreWaveSums(f4 (&total)[RT], float* red);
 template<int W, int RT>
 __device__ __forceinline__ float SumOverWaves(const float* red, int r, int idx);
@@ -143,7 +143,16 @@ __device__ __forceinline__ float* ReduceWaves(f4 (&total)[RT], float* red) {
 // Each lane's hi + lo sums go to red[(wave * RT + r) * 128 + tok * 16 + n]
 // (lanes L and L ^ 32 hold a token's hi and lo parts); after the block
 // barrier, SumOverWaves adds one output's W wave sums in wave order.
-template<int W, int RT>
+// A block barrier that orders LDS only: the waves' LDS stores complete,
+// then s_barrier; vector memory loads and stores in flight stay in flight
+// (__syncthreads would wait for them too).
+__device__ __forceinline__ void LdsBarrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+template<int W, int RT, bool kLdsOnly>
 __device__ __forceinline__ void StoreWaveSums(f4 (&total)[RT], float* red) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tok0 = ((lane >> 4) & 1) * 4;
@@ -156,7 +165,10 @@ __device__ __forceinline__ void StoreWaveSums(f4 (&total)[RT], float* red) {
         red[(wave * RT + r) * 128 + (tok0 + i) * 16 + (lane & 15)] = val;
     }
   }
-  __syncthreads();
+  if constexpr (kLdsOnly)
+    LdsBarrier();
+  else
+    __syncthreads();
 }
 template<int W, int RT>
 __device__ __forceinline__ float SumOverWaves(const float* red, int r, int idx) {
@@ -560,6 +572,189 @@ __global__ void Q8GemvImage(const std::uint8_t* __restrict__ codes,
                                int(gridDim.x) - lead);
 }
 
+// The operand-image GEMV over many row groups (the vocabulary head: 4000
+// groups of two tiles) as a grid-stride loop over one block a CU: each
+// wave stages its image operands in LDS once, and issues the next group's
+// weight loads before it computes and writes the current one, so its
+// weight stream does not stop at group boundaries (one block a group
+// drains its loads before its epilogue, and the next block starts behind
+// it: the head 59.7 us against 54.8 with this loop). K is one round of
+// chunks (nchunks <= W * SPW); parts = 1. Per group, tile and chunk the
+// same loads, products and reductions as Q8GemvImage, so the outputs and
+// greedy keys are bit-identical to it. Block barriers in the loop order
+// LDS only, so the next group's loads stay in flight across them.
+template<int W, int RT, int SPW, bool kNorm>
+__launch_bounds__((W + kNorm) * 64)
+__global__ void Q8GemvImageLoop(const std::uint8_t* __restrict__ codes,
+                                const Half* __restrict__ scales, int row_tiles, int nchunks,
+                                int groups, const uint4* __restrict__ image,
+                                const int* __restrict__ exps, int B, float* __restrict__ y,
+                                int ldy, int rows_out, float* const* __restrict__ y_rows,
+                                unsigned long long* __restrict__ keys, const FusedNorm fused) {
+  __shared__ float red[W * RT * 128 + RT * 128];
+  __shared__ uint4 s_img[W][SPW * 2][64];
+  __shared__ unsigned s_ready;
+  const int lead = kNorm ? B : 0;
+  if constexpr (kNorm) {
+    if (int(blockIdx.x) < B) {
+      NormImageRow<(W + 1) * 64, 1, true>(fused.args, blockIdx.x, fused.flags, fused.seq);
+      return;
+    }
+    if (threadIdx.x == 0)
+      s_ready = 0;
+    __syncthreads();
+    if ((threadIdx.x >> 6) == W) {
+      WatchRows(fused.flags, fused.seq, fused.error, B, &s_ready);
+      return;
+    }
+  }
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool a_live = (lane & 7) < B;
+  const int part = lane >> 5, tok0 = ((lane >> 4) & 1) * 4;
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  const unsigned tiles_bytes = unsigned(row_tiles) * unsigned(nchunks);
+  const BufferResource c_res = MakeBuffer(codes, tiles_bytes * kTileCodeBytes);
+  const BufferResource s_res = MakeBuffer(scales, tiles_bytes * kTileScales * 2);
+  const BufferResource a_res = MakeBuffer(image, unsigned(nchunks) * 2 * 64 * 16);
+  // Empty resources: every load through them reads zeros.
+  const BufferResource c_none = MakeBuffer(codes, 0), s_none = MakeBuffer(scales, 0);
+  // The lanes' VGPR offsets are fixed for the whole loop (a VGPR that an
+  // in-flight load still reads is never rewritten, so no wait drains the
+  // loads in flight); the group and chunk offsets ride in the SGPR offset.
+  unsigned c_off[SPW], s_off[SPW];
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    const bool live = wave + W * j < nchunks;
+    c_off[j] = live ? unsigned(wave) * kTileCodeBytes + unsigned(lane) * 16 : kOutOfRange;
+    s_off[j] = live ? unsigned(wave) * (kTileScales * 2) + unsigned(lane & 15) * 4 : kOutOfRange;
+  }
+  const int stride = int(gridDim.x) - lead;
+  using Codes = uint4[RT][SPW];
+  using Scales = unsigned[RT][SPW];
+  const auto fetch = [&](int g, Codes& q, Scales& sc) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      // Block-uniform: a tile past the matrix (or a group past the last)
+      // reads through the empty resources.
+      const int tile = g * RT + r;
+      const bool in = g < groups && tile < row_tiles;
+      const BufferResource cr = in ? c_res : c_none, sr = in ? s_res : s_none;
+#pragma unroll
+      for (int j = 0; j < SPW; ++j) {
+        const unsigned at = in ? unsigned(tile) * unsigned(nchunks) + unsigned(W * j) : 0u;
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(cr, c_off[j], at * kTileCodeBytes, 0);
+        q[r][j] = make_uint4(v.x, v.y, v.z, v.w);
+        sc[r][j] = __builtin_amdgcn_raw_buffer_load_b32(sr, s_off[j], at * (kTileScales * 2), 0);
+      }
+    }
+  };
+  int group = int(blockIdx.x) - lead;
+  Codes q0, q1;
+  Scales s0, s1;
+  fetch(group, q0, s0);
+  if constexpr (kNorm)
+    AwaitReady(&s_ready, fused.seq);
+  // The wave's image chunks (wave + W j) into its own LDS rows; it reads
+  // only what its own lanes wrote, in order.
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    const int chunk = wave + W * j;
+    const unsigned at = (unsigned(chunk) * 2 * 64 + lane) * 16;
+    const bool live = chunk < nchunks && a_live;
+    s_img[wave][2 * j][lane] = LoadB128(a_res, live ? at : kOutOfRange);
+    s_img[wave][2 * j + 1][lane] = LoadB128(a_res, live ? at + 64 * 16 : kOutOfRange);
+  }
+  int ex[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = tok0 + i;
+    ex[i] = -((t < B ? exps[t] : 0) + (part ? 11 : 0));
+  }
+  // Thread tid stores token (tid % 128) / 16's outputs: its row pointer is
+  // loaded once, before any group's weight loads are in flight behind it.
+  using GlobalFloat = __attribute__((address_space(1))) float;
+  static_assert(W * 64 % 128 == 0, "a thread stores one token's outputs");
+  const int my_tok = (tid % 128) / 16;
+  GlobalFloat* yrow = nullptr;
+  if (my_tok < B)
+    yrow = (GlobalFloat*)(y_rows ? y_rows[my_tok] : y + std::size_t(my_tok) * ldy);
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const auto step = [&](int g, const Codes& q, const Scales& sc) {
+    f4 acc[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+      acc[r] = zero;
+    // Chunks past nchunks (and groups past the last) loaded zeros: their
+    // products add exactly 0, so every MFMA runs unconditionally.
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      const h8 a0 = __builtin_bit_cast(h8, s_img[wave][2 * j][lane]);
+      const h8 a1 = __builtin_bit_cast(h8, s_img[wave][2 * j + 1][lane]);
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        const h8 w0 = EightCodes(q[r][j].x, q[r][j].y);
+        const h8 w1 = EightCodes(q[r][j].z, q[r][j].w);
+        const f4 p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, w0, zero, 0, 0, 0);
+        const f4 p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, w1, zero, 0, 0, 0);
+        const float d0 = HalfBitsToFloat(sc[r][j] & 0xffffu);
+        const float d1 = HalfBitsToFloat(sc[r][j] >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[r][i] = fmaf(d0, p0[i], acc[r][i]);
+          acc[r][i] = fmaf(d1, p1[i], acc[r][i]);
+        }
+      }
+    }
+    f4 total[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        total[r][i] = ldexpf(acc[r][i], ex[i]);
+    // GemvEpilogue's reductions and stores, with the row pointer above.
+    StoreWaveSums<W, RT, true>(total, red);
+    if (keys) {
+      constexpr int R = RT * kTileRows, T = W * 64;
+      static_assert(8 * R <= T, "one (token, row) a lane");
+      const int tok = tid / R, r = (tid % R) / kTileRows, n = tid % kTileRows;
+      const int row = (g * RT + r) * kTileRows + n;
+      unsigned long long key = 0;
+      if (tid < 8 * R && row < rows_out)
+        key = ArgKey(SumOverWaves<W, RT>(red, r, tok * 16 + n), unsigned(row));
+#pragma unroll
+      for (int m = R / 2; m; m >>= 1) {
+        const unsigned long long other = __shfl_xor(key, m, 64);
+        key = other > key ? other : key;
+      }
+      if (tid < 8 * R && tid % R == 0 && tok < B)
+        keys[std::size_t(tok) * groups + g] = key;
+    }
+    for (int o = tid; o < RT * 128; o += W * 64) {
+      const int r = o / 128, idx = o % 128, n = idx % 16;
+      const int row = (g * RT + r) * kTileRows + n;
+      if (my_tok < B && row < rows_out)
+        yrow[row] = SumOverWaves<W, RT>(red, r, idx);
+    }
+    LdsBarrier();  // red is rewritten by the next group
+  };
+  // Two register sets, alternating, so no copy waits on the loads in flight;
+  // the next group's loads issue before the current group's first MFMA.
+  while (group < groups) {
+    fetch(group + stride, q1, s1);
+    __builtin_amdgcn_sched_barrier(0);
+    step(group, q0, s0);
+    group += stride;
+    if (group >= groups)
+      break;
+    fetch(group + stride, q0, s0);
+    __builtin_amdgcn_sched_barrier(0);
+    step(group, q1, s1);
+    group += stride;
+  }
+}
+
 // The convolution block's in projection with the decode convolution step
 // (reference.cpp:85-101) in its epilogue: block g computes tiles g, g + T
 // and g + 2T (T = hidden / 16) of the [B | C | X] projection, i.e. B, C and
@@ -697,12 +892,47 @@ bool FusedNormFits(const FusedNorm& f, std::uint32_t cols, unsigned threads) {
          f.args.H == int(cols) && Chunks(cols) * 8 <= threads;
 }
 
+// The device's CU count (the first device queried; 256 on MI355X).
+int CuCount() {
+  static const int cus = [] {
+    int device = 0, n = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    return n;
+  }();
+  return cus;
+}
+
+// Past this many two-tile groups an operand-image GEMV whose K is one round
+// runs as Q8GemvImageLoop (the vocabulary head: 4000 groups).
+constexpr int kLoopGroups = 1024;
+
 template<int W, int RT, bool kSwiGLU>
 void LaunchImagePlan(const GemvPlan& p, const std::uint8_t* c, const Half* s,
                      const uint4* image, const int* exps, int B, float* y,
                      int ldy, int rows_out, hipStream_t stream, float* const* y_rows,
                      unsigned long long* keys, const FusedNorm* fused) {
   constexpr int SPW = W >= 16 ? 2 : 4;
+  if constexpr (!kSwiGLU && RT == 2 && W == 8) {
+    if (p.parts == 1 && p.nchunks <= W * SPW && p.groups >= kLoopGroups) {
+      // One block a CU (its 152 VGPRs a lane allow one), the norm blocks
+      // included: a block past that would start only when a whole block
+      // has finished its groups.
+      const int lead = fused ? B : 0;
+      const int blocks = std::min(p.groups, std::max(1, CuCount() - lead));
+      if (fused)
+        Q8GemvImageLoop<W, RT, SPW, true><<<blocks + lead, (W + 1) * 64, 0, stream>>>(
+            c, s, p.row_tiles, p.nchunks, p.groups, image, exps, B, y, ldy, rows_out, y_rows,
+            keys, *fused);
+      else
+        Q8GemvImageLoop<W, RT, SPW, false><<<blocks, W * 64, 0, stream>>>(
+            c, s, p.row_tiles, p.nchunks, p.groups, image, exps, B, y, ldy, rows_out, y_rows,
+            keys, FusedNorm{});
+      return;
+    }
+  }
   if (fused)
     Q8GemvImage<W, RT, kSwiGLU, SPW, true>
         <<<dim3(p.groups + B, p.parts), (W + 1) * 64, 0, stream>>>(
@@ -877,16 +1107,7 @@ int LaunchConvImage(const void* codes, const void* scales, std::uint32_t hidden,
 // blocks a CU. Past that the last blocks wait for a second dispatch wave
 // behind blocks that spin on the norm, and the norm in its own launch is
 // faster (at FFN 8192: 512 + 8 blocks, round 1.177 ms fused against 1.160).
-static int FusedSlots() {
-  static const int slots = [] {
-    int device = 0, cus = 0;
-    if (hipGetDevice(&device) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
-      cus = 256;
-    return 2 * cus;
-  }();
-  return slots;
-}
+static int FusedSlots() { return 2 * CuCount(); }
 
 int LaunchGemvImageFused(const void* codes, const void* scales, std::uint32_t rows,
                          std::uint32_t cols, const void* image, const int* exps,

@@ -132,6 +132,49 @@ def test_gemv_operand_keeps_two_fp16_planes_over_a_wide_range(B):
     check(dy.download(np.float32, B * M).reshape(B, M), gz, "image")
 
 
+@pytest.mark.parametrize("M,B", [(128000, 8), (128000, 3), (32784, 5)])
+def test_image_gemv_loop_equals_group_blocks(M, B):
+    """Past 1024 two-tile groups (the vocabulary head, 128000 x 2048) the
+    operand-image GEMV runs as a grid-stride loop over one block a CU, each
+    block issuing its next group's loads before it reduces the current one;
+    per group it takes the loads, products and reductions of the one-group
+    blocks that smaller matrices run. Its first and last 2048 rows equal,
+    bit for bit, the same rows computed as 2048-row matrices (64 groups:
+    one block a group) over the same tiles, and every row is within the
+    FP64 gate. 32784 rows: 1025 groups, the last one a single tile."""
+    K = 2048
+    lib = L.lib()
+    w = L.q8(SEED, f"loop.W.{M}", M, K)
+    m = DeviceMatrix(w, M, K)
+    x = L.normal(SEED, f"loop.x.{M}.{B}", B * K, 0, 2).reshape(B, K)
+    dx = L.DeviceBuffer.of(x)
+    dwn = L.DeviceBuffer.of(np.ones(K, np.float32))
+    dz = L.DeviceBuffer(B * K * 4)
+    img = L.DeviceBuffer(lib.lfm3_operand_image_bytes(K))
+    ex = L.DeviceBuffer(32)
+    L.check(lib.lfm3_residual_norm_image(None, 1, 0, None, dx.addr, dwn.addr, dz.addr, img.addr,
+                                         ex.addr, B, K, 1e-5, None))
+    print(f"[loop] M {M} B {B}", flush=True)
+    dy = L.DeviceBuffer(B * M * 4)
+    L.check(lib.lfm3_q8_gemv_image(m.codes.addr, m.scales.addr, M, K, img.addr, ex.addr, B,
+                                   dy.addr, M, 1, None))
+    L.synchronize()
+    y = dy.download(np.float32, B * M).reshape(B, M)
+    nchunks, sub = K // 64, 2048
+    for first in (0, M - sub):
+        tile = first // 16
+        ds = L.DeviceBuffer(B * sub * 4)
+        L.check(lib.lfm3_q8_gemv_image(m.codes.addr + tile * nchunks * 1024,
+                                       m.scales.addr + tile * nchunks * 64, sub, K, img.addr,
+                                       ex.addr, B, ds.addr, sub, 1, None))
+        L.synchronize()
+        assert np.array_equal(ds.download(np.float32, B * sub).reshape(B, sub),
+                              y[:, first:first + sub]), first
+    gz = dz.download(np.float32, B * K).reshape(B, K)
+    ok, err = within(y, O.mat(O.q8_tensor(w, M, K), gz))
+    assert ok, err
+
+
 @pytest.mark.parametrize("M,K,B", [(2048, 7680, 8), (128000, 2048, 4), (16, 2048, 5),
                                    (3088, 2048, 8), (48, 96, 7), (512, 64, 8), (64, 64, 1), (6144, 2048, 8)])
 def test_gemv_model_shapes(M, K, B):
