@@ -820,7 +820,12 @@ __launch_bounds__(kArgmaxThreads) __global__
 }
 
 // ids[t] from per-block candidate keys: keys[t * groups + j] is the best
-// ArgKey of block j's rows for token t.
+// ArgKey of block j's rows for token t. A thread's keys (j = tid + 256 i)
+// are loaded kKeysPer at a time, all in flight together: one memory round
+// trip for up to 4096 groups (the vocabulary head's 4000), where a load
+// per loop step waited for each in turn (5.2 us a launch). Keys are
+// distinct (they hold the row), so the maximum does not depend on order.
+constexpr int kKeysPer = 16;
 __launch_bounds__(256) __global__
     void ArgmaxKeysKernel(const unsigned long long* __restrict__ keys, int groups,
                           std::uint32_t* __restrict__ ids) {
@@ -828,8 +833,17 @@ __launch_bounds__(256) __global__
   const int t = blockIdx.x, tid = threadIdx.x;
   const unsigned long long* kr = keys + std::size_t(t) * groups;
   unsigned long long key = 0;
-  for (int j = tid; j < groups; j += 256)
-    key = kr[j] > key ? kr[j] : key;
+  for (int j0 = tid; j0 < groups; j0 += 256 * kKeysPer) {
+    unsigned long long v[kKeysPer];
+#pragma unroll
+    for (int i = 0; i < kKeysPer; ++i) {
+      const int j = j0 + 256 * i;
+      v[i] = j < groups ? kr[j] : 0ull;
+    }
+#pragma unroll
+    for (int i = 0; i < kKeysPer; ++i)
+      key = v[i] > key ? v[i] : key;
+  }
 #pragma unroll
   for (int m = 32; m; m >>= 1) {
     const unsigned long long other = __shfl_xor(key, m, 64);
