@@ -27,15 +27,18 @@
 //
 // With the heads fused in (lfm3_decode_heads_attention_ragged), every block
 // also applies the per-head Q/K RMSNorm and paired RoPE of its row
-// (hip/ops.hip:1072-1134) in its prologue. Exactly one block of a row
-// writes the ring: the one whose span ends at the current position. It
-// stores the row's F16 K/V to slot position % capacity, waits for its
-// stores (vmcnt 0) and the block barrier, and then reads that key back
-// through the ring with the rest of its span. No other span of the row
-// covers the current position, so no other block reads the slot being
-// written; on a sliding layer this relies on the ring holding at least the
-// window (capacity = min(context, window) >= keys of any span), so the
-// current slot is not an earlier key of another span.
+// (hip/ops.hip:1072-1134) in its prologue. Each wave's first K/V group is
+// issued right after the prologue's own loads, so it arrives while the
+// norms and rotations compute. Exactly one block of a row writes the
+// ring: the one whose span ends at the current position. It stores the
+// row's F16 K/V to slot position % capacity for later rounds and takes
+// that key from LDS for this one (the ring loads skip it, and the group
+// holding it selects the LDS row in its place), so nothing waits for the
+// store. No other span of the row covers the current position, so no
+// other block reads the slot being written; on a sliding layer this
+// relies on the ring holding at least the window (capacity = min(context,
+// window) >= keys of any span), so the current slot is not an earlier key
+// of another span.
 //
 // A row with several spans needs the merge. The 8-wave whole-row path runs
 // only when the item count equals the row count (every row one item); an
@@ -194,10 +197,10 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
   const lfm3_attention_item item = items[blockIdx.x];
   const int g = blockIdx.y, row = int(item.row);
   const int tid = threadIdx.x, lane = tid & 63;
-  // The output gate's divisor, loaded before any store (a load after
-  // stores waits for them) and read from LDS by the epilogue or the merge.
-  if (tid < G)
-    s_gate[tid] = 1.0f + expf(-gate[std::size_t(row) * ldg + g * G + tid]);
+  // The output gate, loaded before any store (a load after stores waits
+  // for them); its divisor goes to LDS for the epilogue or the merge once
+  // the first K/V group is in flight.
+  const float gate_x = tid < G ? gate[std::size_t(row) * ldg + g * G + tid] : 0.0f;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int stride = kv_heads * D;
   const std::uint32_t cap = capacity[row];
@@ -206,28 +209,108 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
   Half* ck = cache_k[row];
   Half* cv = cache_v[row];
 
-  // Prologue: queries of the group (normed and rotated when fused).
+  // The span holds the current position (fused: this block writes its
+  // key to the ring); that key is never read back through the ring.
+  const int held = kFused && ke == pos + 1 ? 1 : 0;
+  // P V layout: lane L owns dimensions 8 (L % DL) .. + 7 of keys
+  // L / DL + KG i (i < KPL) of each 16-key group, one 16-byte V load per key.
+  constexpr int DL = D / 8, KG = 64 / DL, KPL = 16 / KG;
+  const int dg = lane % DL, kq = lane / DL;
+  // The rings as buffers: a key past the span reads zeros, without a branch.
+  const unsigned ring_bytes = cap * unsigned(stride) * 2;
+  const BufferResource k_res = MakeBuffer(ck, ring_bytes);
+  const BufferResource v_res = MakeBuffer(cv, ring_bytes);
+  const int n = lane & 15, kg = lane >> 4;
+  // Ring slots of keys base + o (o < 16) for the lane's K row (o = n) and V
+  // rows (o = kq + KG i): one wave-uniform division per group, then the
+  // wrap as an unsigned minimum (rings of 16 slots or more; smaller rings
+  // take the remainder). Keys past the span, and groups past the wave's
+  // last, read zeros from an offset the hardware drops (no traffic). The
+  // offsets are selects, not branches around the loads.
+  const int ngroups = ngroups_of(kb, ke);
+  const unsigned row_bytes = unsigned(stride) * 2;
+  const unsigned k_lane = unsigned(g * D + 8 * kg) * 2, v_lane = unsigned(g * D + 8 * dg) * 2;
+  const auto fetch = [&](int j, uint4 (&kr)[S], uint4 (&vr)[KPL]) {
+    const int base = kb + kGroupKeys * j;
+    // Keys of the group inside the span; the current position's key (the
+    // span's last when it holds it) comes from LDS instead (patch below).
+    const int rem = j < ngroups ? ke - held - base : 0;
+    const unsigned b0 = unsigned(base) % cap;
+    unsigned sk = b0 + unsigned(n), sv[KPL];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i)
+      sv[i] = b0 + unsigned(kq + KG * i);
+    if (cap >= 16) {
+      sk = min(sk, sk - cap);
+#pragma unroll
+      for (int i = 0; i < KPL; ++i)
+        sv[i] = min(sv[i], sv[i] - cap);
+    } else {
+      sk %= cap;
+#pragma unroll
+      for (int i = 0; i < KPL; ++i)
+        sv[i] %= cap;
+    }
+    const unsigned koff = n < rem ? sk * row_bytes + k_lane : kOutOfRange;
+#pragma unroll
+    for (int s2 = 0; s2 < S; ++s2)
+      kr[s2] = LoadB128(k_res, koff + 64 * s2);
+#pragma unroll
+    for (int i = 0; i < KPL; ++i)
+      vr[i] = LoadB128(v_res, kq + KG * i < rem ? sv[i] * row_bytes + v_lane : kOutOfRange);
+  };
+
+  uint4 kr[S], vr[KPL];
+
+  // Prologue: queries of the group (normed and rotated when fused). Its
+  // own loads go out first, then the wave's first K/V group, so the
+  // group's loads are in flight while the prologue computes (loads return
+  // in issue order: issued the other way round, the prologue would wait
+  // for the group).
   if constexpr (kFused) {
 #pragma clang fp contract(off)
-    constexpr int P = D / 2, SLOTS = (NW * 64) / P;
+    constexpr int P = D / 2, SLOTS = (NW * 64) / P, ROUNDS = (G + SLOTS) / SLOTS;
     const int slot = tid / P, pair = tid % P;
     const float fp = frequencies[pair];
-    for (int h0 = 0; h0 <= G; h0 += SLOTS) {
-      const int h = h0 + slot;
-      if (h <= G) {  // h == G is the key head
-        const float* src = h < G ? q + std::size_t(row) * ld + (g * G + h) * D
-                                 : k + std::size_t(row) * ld + g * D;
-        const float* w = h < G ? q_norm : k_norm;
-        const float x0 = src[pair], x1 = src[pair + P];
+    const float fac = factors ? factors[pair] : 1.0f;
+    // Loaded without a branch (a slot past the key head reads the key row
+    // again and drops it): values loaded under a branch are copied at its
+    // join, and each copy waits for its load.
+    float x0s[ROUNDS], x1s[ROUNDS], w0s[ROUNDS], w1s[ROUNDS];
+#pragma unroll
+    for (int r = 0; r < ROUNDS; ++r) {
+      const int h = r * SLOTS + slot;  // h == G is the key head
+      const float* src = h < G ? q + std::size_t(row) * ld + (g * G + h) * D
+                               : k + std::size_t(row) * ld + g * D;
+      const float* w = h < G ? q_norm : k_norm;
+      x0s[r] = src[pair];
+      x1s[r] = src[pair + P];
+      w0s[r] = w[pair];
+      w1s[r] = w[pair + P];
+    }
+    // A buffer load (zero past the row), not a branch: the compiler would
+    // sink the F16 conversion into the branch and wait for the load there.
+    const float vrow = __uint_as_float(
+        LoadB32(MakeBuffer(v + std::size_t(row) * ld + g * D, D * 4),
+                tid < D ? unsigned(tid) * 4 : kOutOfRange));
+    fetch(wave, kr, vr);
+    __builtin_amdgcn_sched_barrier(0);  // nothing that waits on a load moves above
+    if (tid < G)
+      s_gate[tid] = 1.0f + expf(-gate_x);
+#pragma unroll
+    for (int r = 0; r < ROUNDS; ++r) {
+      const int h = r * SLOTS + slot;
+      if (h <= G) {
+        const float x0 = x0s[r], x1 = x1s[r];
         float squares = x0 * x0 + x1 * x1;
 #pragma unroll
         for (int m = P / 2; m; m >>= 1)
           squares += __shfl_xor(squares, m, 64);
         const float inv = 1.0f / sqrtf(squares / float(D) + eps);
-        const float a = (x0 * inv) * w[pair], b = (x1 * inv) * w[pair + P];
+        const float a = (x0 * inv) * w0s[r], b = (x1 * inv) * w1s[r];
         float angle = float(pos) * fp;
         if (factors)
-          angle /= factors[pair];
+          angle /= fac;
         float sn, cs;
         sincosf(angle, &sn, &cs);
         const float r0 = a * cs - b * sn, r1 = b * cs + a * sn;
@@ -240,25 +323,39 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
         }
       }
     }
-    for (int d = tid; d < D; d += (NW * 64))
-      s_kv[1][d] = FloatToHalfBits(v[std::size_t(row) * ld + g * D + d]);
+    static_assert(D <= NW * 64, "a thread per dimension of the V row");
+    if (tid < D)
+      s_kv[1][tid] = FloatToHalfBits(vrow);
     __syncthreads();
-    if (ke == pos + 1) {  // this span holds the current position
-      // The row goes to the ring and has landed (the store counter at
-      // zero) before any wave of the block reads it back with the other
-      // keys; the block's waves share the CU's L1, and stores write
-      // through it.
-      if (tid < D) {
-        const std::size_t at = std::size_t(std::uint32_t(pos) % cap) * stride + g * D + tid;
-        ck[at] = s_kv[0][tid];
-        cv[at] = s_kv[1][tid];
-      }
-      __builtin_amdgcn_s_waitcnt(WaitVm(0));
-      __syncthreads();
+    if (held && tid < D) {
+      // The row goes to the ring for later rounds; this launch takes the
+      // key from s_kv (no other span of the row covers the position, so no
+      // block reads the slot being written). Global stores, not flat ones:
+      // a flat store in flight makes the compiler wait for every load
+      // before the next LDS read.
+      using GlobalHalf = __attribute__((address_space(1))) Half;
+      const std::size_t at = std::size_t(std::uint32_t(pos) % cap) * stride + g * D + tid;
+      ((GlobalHalf*)ck)[at] = s_kv[0][tid];
+      ((GlobalHalf*)cv)[at] = s_kv[1][tid];
     }
   } else {
-    for (int e = tid; e < G * D; e += (NW * 64))
-      s_q[e / D][e % D] = q[std::size_t(row) * ld + (g * G + e / D) * D + e % D];
+    constexpr int QPT = (G * D + NW * 64 - 1) / (NW * 64);
+    float qv[QPT];
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int e = tid + NW * 64 * i;
+      qv[i] = e < G * D ? q[std::size_t(row) * ld + (g * G + e / D) * D + e % D] : 0.0f;
+    }
+    fetch(wave, kr, vr);
+    __builtin_amdgcn_sched_barrier(0);  // nothing that waits on a load moves above
+    if (tid < G)
+      s_gate[tid] = 1.0f + expf(-gate_x);
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int e = tid + NW * 64 * i;
+      if (e < G * D)
+        s_q[e / D][e % D] = qv[i];
+    }
     __syncthreads();
   }
 
@@ -285,10 +382,6 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
     m_own[r] = -INFINITY;
     l_own[r] = 0.0f;
   }
-  // P V layout: lane L owns dimensions 8 (L % DL) .. + 7 of keys
-  // L / DL + KG i (i < KPL) of each 16-key group, one 16-byte V load per key.
-  constexpr int DL = D / 8, KG = 64 / DL, KPL = 16 / KG;
-  const int dg = lane % DL, kq = lane / DL;
   float acc[G][8];
 #pragma unroll
   for (int h = 0; h < G; ++h)
@@ -297,53 +390,25 @@ __launch_bounds__(NW * 64) __global__ void DecodeAttentionKernel(
       acc[h][i] = 0.0f;
   const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 
-  // The rings as buffers: a key past the span reads zeros, without a branch.
-  const unsigned ring_bytes = cap * unsigned(stride) * 2;
-  const BufferResource k_res = MakeBuffer(ck, ring_bytes);
-  const BufferResource v_res = MakeBuffer(cv, ring_bytes);
-  const int n = lane & 15, kg = lane >> 4;
-  // Ring slots of keys base + o (o < 16) for the lane's K row (o = n) and V
-  // rows (o = kq + KG i): one wave-uniform division per group, then the
-  // wrap as an unsigned minimum (rings of 16 slots or more; smaller rings
-  // take the remainder). Keys past the span, and groups past the wave's
-  // last, read zeros from an offset the hardware drops (no traffic). The
-  // offsets are selects, not branches around the loads.
-  const int ngroups = ngroups_of(kb, ke);
-  const unsigned row_bytes = unsigned(stride) * 2;
-  const unsigned k_lane = unsigned(g * D + 8 * kg) * 2, v_lane = unsigned(g * D + 8 * dg) * 2;
-  const auto fetch = [&](int j, uint4 (&kr)[S], uint4 (&vr)[KPL]) {
-    const int base = kb + kGroupKeys * j;
-    const int rem = j < ngroups ? ke - base : 0;  // keys of the group inside the span
-    const unsigned b0 = unsigned(base) % cap;
-    unsigned sk = b0 + unsigned(n), sv[KPL];
-#pragma unroll
-    for (int i = 0; i < KPL; ++i)
-      sv[i] = b0 + unsigned(kq + KG * i);
-    if (cap >= 16) {
-      sk = min(sk, sk - cap);
-#pragma unroll
-      for (int i = 0; i < KPL; ++i)
-        sv[i] = min(sv[i], sv[i] - cap);
-    } else {
-      sk %= cap;
-#pragma unroll
-      for (int i = 0; i < KPL; ++i)
-        sv[i] %= cap;
-    }
-    const unsigned koff = n < rem ? sk * row_bytes + k_lane : kOutOfRange;
-#pragma unroll
-    for (int s2 = 0; s2 < S; ++s2)
-      kr[s2] = LoadB128(k_res, koff + 64 * s2);
-#pragma unroll
-    for (int i = 0; i < KPL; ++i)
-      vr[i] = LoadB128(v_res, kq + KG * i < rem ? sv[i] * row_bytes + v_lane : kOutOfRange);
-  };
-
-  uint4 kr[S], vr[KPL], kn[S], vn[KPL];
-  fetch(wave, kr, vr);
+  uint4 kn[S], vn[KPL];
   for (int j = wave; j < ngroups; j += NW) {
     const int base = kb + kGroupKeys * j;
     fetch(j + NW, kn, vn);  // past the span: zeros, no traffic
+    if constexpr (kFused) {
+      // The current key (key o of the group holding it; no lane matches in
+      // other groups) from LDS, as selects: a branch here would leave the
+      // compiler's wait counts for the loads in flight inexact, and it
+      // then waits for all of them.
+      const int o = held ? pos - base : -1;
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2)
+        kr[s2] = SelectU4(n == o, *reinterpret_cast<const uint4*>(&s_kv[0][32 * s2 + 8 * kg]),
+                          kr[s2]);
+      const uint4 cur_v = *reinterpret_cast<const uint4*>(&s_kv[1][8 * dg]);
+#pragma unroll
+      for (int i = 0; i < KPL; ++i)
+        vr[i] = SelectU4(kq + KG * i == o, cur_v, vr[i]);
+    }
     f4 sacc = zero;
 #pragma unroll
     for (int s2 = 0; s2 < S; ++s2)
