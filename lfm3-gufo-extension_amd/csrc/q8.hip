@@ -755,6 +755,163 @@ __global__ void Q8GemvImageLoop(const std::uint8_t* __restrict__ codes,
   }
 }
 
+// Q8Gemv over many row groups (the vocabulary head on FP32 rows: 4000
+// groups of two tiles) as the same grid-stride loop as Q8GemvImageLoop:
+// each wave stages its chunks of x once (Q8Gemv's one-slice staging: the
+// same exponents and hi/lo operands), then issues the next group's weight
+// loads before it computes and writes the current one. Per group the
+// loads, products and reductions are Q8Gemv's, so the outputs are
+// bit-identical to it. K is one slice (nchunks <= W * SPW); parts = 1.
+template<int W, int RT, int SPW>
+__launch_bounds__(W * 64)
+__global__ void Q8GemvLoop(const std::uint8_t* __restrict__ codes,
+                           const Half* __restrict__ scales, int row_tiles, int nchunks,
+                           int groups, int K, const float* __restrict__ x, int ldx, int B,
+                           float* __restrict__ y, int ldy, int rows_out) {
+  __shared__ uint4 s_a[W][SPW * 2 * 64];
+  __shared__ float red[W * RT * 128 + RT * 128];
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  const unsigned tiles_bytes = unsigned(row_tiles) * unsigned(nchunks);
+  const BufferResource c_res = MakeBuffer(codes, tiles_bytes * kTileCodeBytes);
+  const BufferResource s_res = MakeBuffer(scales, tiles_bytes * kTileScales * 2);
+  const BufferResource c_none = MakeBuffer(codes, 0), s_none = MakeBuffer(scales, 0);
+  const BufferResource x_res = MakeBuffer(x, unsigned(((B - 1) * ldx + K) * 4));
+  // Fixed lane offsets, group and chunk in the SGPR offset (as in
+  // Q8GemvImageLoop).
+  unsigned c_off[SPW], s_off[SPW];
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    const bool live = wave + W * j < nchunks;
+    c_off[j] = live ? unsigned(wave) * kTileCodeBytes + unsigned(lane) * 16 : kOutOfRange;
+    s_off[j] = live ? unsigned(wave) * (kTileScales * 2) + unsigned(lane & 15) * 4 : kOutOfRange;
+  }
+  const int stride = int(gridDim.x);
+  using Codes = uint4[RT][SPW];
+  using Scales = unsigned[RT][SPW];
+  const auto fetch = [&](int g, Codes& q, Scales& sc) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      const int tile = g * RT + r;
+      const bool in = g < groups && tile < row_tiles;
+      const BufferResource cr = in ? c_res : c_none, sr = in ? s_res : s_none;
+#pragma unroll
+      for (int j = 0; j < SPW; ++j) {
+        const unsigned at = in ? unsigned(tile) * unsigned(nchunks) + unsigned(W * j) : 0u;
+        const u4 v = __builtin_amdgcn_raw_buffer_load_b128(cr, c_off[j], at * kTileCodeBytes, 0);
+        q[r][j] = make_uint4(v.x, v.y, v.z, v.w);
+        sc[r][j] = __builtin_amdgcn_raw_buffer_load_b32(sr, s_off[j], at * (kTileScales * 2), 0);
+      }
+    }
+  };
+  // Q8Gemv's staging of the wave's chunks (token t = L % 8, columns
+  // 8 (L / 8) .. + 7 of each chunk), x first so it returns before the
+  // weights.
+  const int t = lane & 7, g8 = lane >> 3;
+  float v[SPW][8];
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    const int chunk = wave + W * j;
+    const int k = chunk * kChunk + g8 * 8;
+    const unsigned off = t < B && chunk < nchunks && k < K ? unsigned(t * ldx + k) * 4 : kOutOfRange;
+    const float4 lo4 = LoadF4(x_res, off), hi4 = LoadF4(x_res, off + 16);
+    v[j][0] = lo4.x; v[j][1] = lo4.y; v[j][2] = lo4.z; v[j][3] = lo4.w;
+    v[j][4] = hi4.x; v[j][5] = hi4.y; v[j][6] = hi4.z; v[j][7] = hi4.w;
+  }
+  int group = int(blockIdx.x);
+  Codes q0, q1;
+  Scales s0, s1;
+  fetch(group, q0, s0);
+  __builtin_amdgcn_sched_barrier(0);
+  const int part = lane >> 5, tok0 = ((lane >> 4) & 1) * 4;
+  float maximum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < SPW; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      maximum = fmaxf(maximum, fabsf(v[j][i]));
+  maximum = MaxXor32(MaxXor16(MaxXor8(maximum)));
+  const int e = RowExponent(maximum);
+  int ex[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int lo_tok = __builtin_amdgcn_readlane(e, i), hi_tok = __builtin_amdgcn_readlane(e, 4 + i);
+    ex[i] = -((tok0 ? hi_tok : lo_tok) + (part ? 11 : 0));
+  }
+  uint4* s_own = s_a[wave];
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    unsigned hw[4], lw[4];
+#pragma unroll
+    for (int i = 0; i < 8; i += 2)
+      SplitPair(v[j][i], v[j][i + 1], e, hw[i / 2], lw[i / 2]);
+    const int idx = (j * 2 + (g8 >> 2)) * 64 + 16 * (g8 & 3) + t;
+    s_own[idx] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    s_own[idx + 8] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  }
+  // The wave reads what its own lanes wrote: LDS keeps a wave's operations
+  // in order; the fence keeps the compiler's order too.
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const auto step = [&](int g, const Codes& q, const Scales& sc) {
+    f4 acc[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+      acc[r] = zero;
+    // Chunks past nchunks (and groups past the last) loaded zeros: their
+    // products add exactly 0, so every MFMA runs unconditionally.
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      const h8 a0 = __builtin_bit_cast(h8, s_own[(j * 2) * 64 + lane]);
+      const h8 a1 = __builtin_bit_cast(h8, s_own[(j * 2 + 1) * 64 + lane]);
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        const h8 w0 = EightCodes(q[r][j].x, q[r][j].y);
+        const h8 w1 = EightCodes(q[r][j].z, q[r][j].w);
+        const f4 p0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, w0, zero, 0, 0, 0);
+        const f4 p1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, w1, zero, 0, 0, 0);
+        const float d0 = HalfBitsToFloat(sc[r][j] & 0xffffu);
+        const float d1 = HalfBitsToFloat(sc[r][j] >> 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[r][i] = fmaf(d0, p0[i], acc[r][i]);
+          acc[r][i] = fmaf(d1, p1[i], acc[r][i]);
+        }
+      }
+    }
+    f4 total[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        total[r][i] = ldexpf(acc[r][i], ex[i]);
+    // GemvEpilogue's reductions and stores (y is a global pointer: no
+    // load behind the next group's weights).
+    StoreWaveSums<W, RT, true>(total, red);
+    for (int o = tid; o < RT * 128; o += W * 64) {
+      const int r = o / 128, idx = o % 128, tok = idx / 16, n = idx % 16;
+      const int row = (g * RT + r) * kTileRows + n;
+      if (tok < B && row < rows_out)
+        y[std::size_t(tok) * ldy + row] = SumOverWaves<W, RT>(red, r, idx);
+    }
+    LdsBarrier();  // red is rewritten by the next group
+  };
+  while (group < groups) {
+    fetch(group + stride, q1, s1);
+    __builtin_amdgcn_sched_barrier(0);
+    step(group, q0, s0);
+    group += stride;
+    if (group >= groups)
+      break;
+    fetch(group + stride, q0, s0);
+    __builtin_amdgcn_sched_barrier(0);
+    step(group, q1, s1);
+    group += stride;
+  }
+}
+
 // The convolution block's in projection with the decode convolution step
 // (reference.cpp:85-101) in its epilogue: block g computes tiles g, g + T
 // and g + 2T (T = hidden / 16) of the [B | C | X] projection, i.e. B, C and
@@ -830,10 +987,36 @@ __global__ void Q8GemvConvImage(const std::uint8_t* __restrict__ codes,
   }
 }
 
+// The device's CU count (the first device queried; 256 on MI355X).
+int CuCount() {
+  static const int cus = [] {
+    int device = 0, n = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    return n;
+  }();
+  return cus;
+}
+
+// Past this many two-tile groups an operand-image GEMV whose K is one round
+// runs as Q8GemvImageLoop, and a Q8Gemv whose K is one slice as Q8GemvLoop
+// (the vocabulary head: 4000 groups).
+constexpr int kLoopGroups = 1024;
+
 template<int W, int SPW, int RT, bool kSwiGLU>
 void LaunchPlan(const GemvPlan& p, const std::uint8_t* c, const Half* s, int K,
                 const float* x, int ldx, int B, float* y, int ldy, int rows_out,
                 hipStream_t stream) {
+  if constexpr (!kSwiGLU && RT == 2 && W == 8 && SPW == 4) {
+    if (p.parts == 1 && p.nchunks <= W * SPW && p.groups >= kLoopGroups) {
+      // One block a CU, as the operand-image loop.
+      Q8GemvLoop<W, RT, SPW><<<std::min(p.groups, CuCount()), W * 64, 0, stream>>>(
+          c, s, p.row_tiles, p.nchunks, p.groups, K, x, ldx, B, y, ldy, rows_out);
+      return;
+    }
+  }
   Q8Gemv<W, SPW, RT, kSwiGLU><<<dim3(p.groups, p.parts), W * 64, 0, stream>>>(
       c, s, p.row_tiles, p.nchunks, K, x, ldx, B, y, ldy, rows_out,
       std::size_t(ldy) * B);
@@ -891,23 +1074,6 @@ bool FusedNormFits(const FusedNorm& f, std::uint32_t cols, unsigned threads) {
   return f.flags && f.args.image && f.args.exps && f.args.x && f.args.weight &&
          f.args.H == int(cols) && Chunks(cols) * 8 <= threads;
 }
-
-// The device's CU count (the first device queried; 256 on MI355X).
-int CuCount() {
-  static const int cus = [] {
-    int device = 0, n = 0;
-    if (hipGetDevice(&device) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
-        n <= 0)
-      n = 256;
-    return n;
-  }();
-  return cus;
-}
-
-// Past this many two-tile groups an operand-image GEMV whose K is one round
-// runs as Q8GemvImageLoop (the vocabulary head: 4000 groups).
-constexpr int kLoopGroups = 1024;
 
 template<int W, int RT, bool kSwiGLU>
 void LaunchImagePlan(const GemvPlan& p, const std::uint8_t* c, const Half* s,

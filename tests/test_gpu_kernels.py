@@ -175,6 +175,37 @@ def test_image_gemv_loop_equals_group_blocks(M, B):
     assert ok, err
 
 
+@pytest.mark.parametrize("M,B", [(128000, 1), (128000, 8), (32784, 3)])
+def test_fp32_row_gemv_loop_equals_group_blocks(M, B):
+    """The FP32-row GEMV (lfm3_q8_gemv) past 1024 two-tile groups with K in
+    one slice (the prompt's vocabulary head on its frontier row) runs the
+    same grid-stride loop as the operand-image GEMV; each wave stages its
+    chunks of x once with the one-block-a-group kernel's exponents and
+    operands. Its first and last 2048 rows equal, bit for bit, the same
+    rows computed as 2048-row matrices (64 groups: one block a group) over
+    the same tiles, and every row is within the FP32 gate of the oracle."""
+    K = 2048
+    lib = L.lib()
+    w = L.q8(SEED, f"floop.W.{M}", M, K)
+    m = DeviceMatrix(w, M, K)
+    x = (3.0 * L.normal(SEED, f"floop.x.{M}.{B}", B * K)).reshape(B, K)
+    print(f"[fp32 loop] M {M} B {B}", flush=True)
+    y = gemv(m, x)
+    dx = L.DeviceBuffer.of(np.ascontiguousarray(x, np.float32))
+    nchunks, sub = K // 64, 2048
+    for first in (0, M - sub):
+        tile = first // 16
+        ds = L.DeviceBuffer(B * sub * 4)
+        L.check(lib.lfm3_q8_gemv(m.codes.addr + tile * nchunks * 1024,
+                                 m.scales.addr + tile * nchunks * 64, sub, K, dx.addr, K,
+                                 ds.addr, sub, B, None, 0, None))
+        L.synchronize()
+        assert np.array_equal(ds.download(np.float32, B * sub).reshape(B, sub),
+                              y[:, first:first + sub]), first
+    ok, err = within(y, O.mat(O.q8_tensor(w, M, K), x))
+    assert ok, err
+
+
 @pytest.mark.parametrize("M,K,B", [(2048, 7680, 8), (128000, 2048, 4), (16, 2048, 5),
                                    (3088, 2048, 8), (48, 96, 7), (512, 64, 8), (64, 64, 1), (6144, 2048, 8)])
 def test_gemv_model_shapes(M, K, B):
