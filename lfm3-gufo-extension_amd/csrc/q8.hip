@@ -1135,7 +1135,9 @@ GemvPlan PlanImage(std::uint32_t rows, std::uint32_t cols, bool swiglu, std::uin
   // staging, a second tile only shares the cross-wave reduction, which
   // pays once the tiles outnumber the CUs: at 193 tiles (q | k | v | gate,
   // 3088 x 2048, 8 rows) one tile a block takes 4.8 us against 5.8 us with
-  // two; at 8000 tiles (the vocabulary head) two take 60 us against 73 us.
+  // two; at 8000 tiles (the vocabulary head) two take 60 us against 73 us
+  // as one block a group (past kLoopGroups groups they run in
+  // Q8GemvImageLoop).
   p.RT = swiglu ? 2 : p.row_tiles > 256 ? 2 : 1;
   p.groups = (p.row_tiles + p.RT - 1) / p.RT;
   return p;
